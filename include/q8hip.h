@@ -1,0 +1,211 @@
+/*
+ * q8hip.h -- C ABI of the MI355X (gfx950) int8 quantized-inference library
+ * (libq8hip.so).
+ *
+ * This is the boundary the host side binds: the Node N-API addon
+ * (mlfw_amd/node/q8hip_napi.c) and the Python ctypes binding
+ * (mlfw_amd/_lib.py).  Plain C types only; every device pointer is a raw
+ * address in the current HIP device's memory, every `stream` is a
+ * hipStream_t (NULL = the null stream).
+ *
+ * Reference interfaces replaced (paths relative to the slexisvn/mlfw tree):
+ *   - the CUDA runtime backend's per-kernel launch path for the int8 ops,
+ *     runCudaKernelSync (src/runtime/node/cuda_runtime.ts:85-121) and
+ *     launchKernel (src/runtime/node/cuda/launcher.ts:34-54), which run the
+ *     NVRTC-compiled kernels CUDACodegen emits for `quantize`,
+ *     `quantized_dot` and `dequantize`;
+ *   - the device-memory and error conventions of the reference's other
+ *     native C ABI, terac (terac/include/Tera/CAPI/Execution.h:40-81:
+ *     status codes, teraLastError, teraDeviceAlloc/Upload/Download).
+ *
+ * Conventions (all entry points):
+ *   - return Q8_OK (0) on success, a Q8_ERR_* code otherwise; the message of
+ *     the last failure on the calling thread is q8_last_error();
+ *   - arguments are validated on the host before anything is launched; a
+ *     call that fails validation launches nothing;
+ *   - work is enqueued on `stream` and is asynchronous with respect to the
+ *     host, except q8_h2d / q8_d2h / q8_stream_sync which block;
+ *   - the arithmetic of every op is the reference CPU backend's, bit for bit
+ *     (int8 codes, int32 accumulators and fp32 outputs), see each entry.
+ */
+#ifndef Q8HIP_H
+#define Q8HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q8HIP_VERSION 1
+
+/* status codes */
+#define Q8_OK               0
+#define Q8_ERR_INVALID      1   /* bad argument: null pointer, shape, enum, scale <= 0 */
+#define Q8_ERR_DEVICE       2   /* no usable HIP device, or a HIP runtime error */
+#define Q8_ERR_UNSUPPORTED  3   /* valid request this build does not implement */
+#define Q8_ERR_OOM          4   /* device allocation failed */
+
+/* element types */
+#define Q8_I8   0
+#define Q8_U8   1
+#define Q8_I32  2
+#define Q8_F32  3
+
+/* scale granularity */
+#define Q8_PER_TENSOR  0   /* one scale */
+#define Q8_PER_TOKEN   1   /* one scale per row of an [M,K] tensor */
+#define Q8_PER_CHANNEL 2   /* one scale per output channel (weights) */
+
+/* epilogue forms of the GEMM */
+#define Q8_EPI_PT      0   /* y = fround(acc * s_out), s_out an f64 scalar (E-pt) */
+#define Q8_EPI_ROWCOL  1   /* y = fround(acc * fround(sA[m] * sB[n])) (E-pc / E-rowcol) */
+
+/* activations applied after the optional bias */
+#define Q8_ACT_NONE 0
+#define Q8_ACT_RELU 1      /* Math.max(v, 0): NaN stays NaN, -0 -> +0 */
+#define Q8_ACT_SILU 2      /* v * (1 / (1 + exp(-v))), every step rounded to f32 */
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Library version (Q8HIP_VERSION). */
+int q8_version(void);
+
+/* Message of the last failed call on this thread ("" if none).
+ * Mirrors teraLastError (terac/include/Tera/CAPI/Execution.h:55). */
+const char* q8_last_error(void);
+
+/* Number of HIP devices; 0 (and Q8_OK) on a machine without a GPU. */
+int q8_device_count(int* count);
+
+/* Make `device` current for this thread and prepare it (checks the device is
+ * gfx950, allocates the library's small per-device work area).  Entry points
+ * below call it for the current device on first use.  Replaces the CUDA
+ * backend's context/stream set-up (src/runtime/node/cuda/device.ts:14-35). */
+int q8_init(int device);
+
+/* Device memory that outlives a call: teraDeviceAlloc / Upload / Download
+ * (terac/include/Tera/CAPI/Execution.h:62-81), and the reference's pooled
+ * device buffers (src/runtime/node/cuda/memory.ts:92-127). */
+int q8_alloc(void** dptr, size_t bytes);
+int q8_free(void* dptr);
+int q8_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int q8_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int q8_memset(void* dst, int value, size_t bytes, void* stream);
+int q8_stream_sync(void* stream);
+
+/* ---------------------------------------------------------------- inputs */
+
+/* Seeded synthetic inputs, counter-based form of mulberry32
+ * (src/util/random.ts:5-14): draw i of seed s is a function of
+ * s + (i + 1) * 0x6D2B79F5 alone, so the stream is generated in parallel.
+ * `offset` = number of draws of the stream already consumed.
+ * q8_fill_normal follows normal_ (src/nn/init.ts:40-52: Box-Muller on
+ * pairs, 2*ceil(n/2) draws); q8_fill_uniform follows uniform_
+ * (src/nn/init.ts:31-37, n draws). */
+int q8_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
+                   double mean, double std, void* stream);
+int q8_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset,
+                    double a, double b, void* stream);
+
+/* ---------------------------------------------------------------- quantize */
+
+/* The compiled `quantize` op with a static scale: the CUDA kernel CUDACodegen
+ * emits for the lowering of quant_math.ts:16-27 (rule
+ * src/compiler/passes/lowering/rules/quantization.ts:6-12).  Bit-exact with
+ * the CPU backend's form
+ *   q = (Math.min(Math.max(Math.round(Math.fround(x / s)), lo), hi) | 0)
+ * and, for zero_point != 0, Math.round(Math.fround(Math.fround(x/s) + zp)).
+ * target Q8_I8 ([-128,127]) or Q8_U8 ([0,255]); scale must be > 0
+ * (op verifier, src/compiler/ir/graph/ops/quantization.ts:44-47). */
+int q8_quantize_static(const float* x, int64_t n, double scale, double zero_point,
+                       int target, void* q, void* stream);
+
+/* Dynamic symmetric int8 quantize of an [M,K] row-major fp32 tensor.
+ * mode Q8_PER_TOKEN: scales[m] = S-abs of row m, mode Q8_PER_TENSOR:
+ * scales[0] = S-abs of the whole tensor, where S-abs is the reference's
+ * calibration scale: ValueObserver min/max (src/compiler/analysis/
+ * calibration.ts:24-34, NaN never taken) fed to QuantizationParams.fromRange
+ * (src/compiler/ir/graph/quantization_types.ts:248-254):
+ *   s = max(|min|, |max|) / 127 || 1e-10   (f64; an empty row gets 6/127).
+ * Codes are then the compiled quantize above with that scale.  The
+ * reference has this scale only as a static, calibrated one; the dynamic
+ * per-token / per-tensor op is this library's composition of the two.
+ * scales: f64 device array of M (per token) or 1 (per tensor) entries. */
+int q8_quantize_rows(const float* x, int64_t M, int64_t K, int mode,
+                     int8_t* q, double* scales, void* stream);
+
+/* ---------------------------------------------------------------- dequantize */
+
+/* The compiled `dequantize` op (quant_math.ts:29-34, rule
+ * rules/quantization.ts:14-21): y = Math.fround((+q) * s), and for
+ * zero_point != 0 y = Math.fround(Math.fround((+q) - zp) * s).
+ * src: Q8_I8, Q8_U8 or Q8_I32 (the int32 form is the per-tensor GEMM
+ * epilogue).  granularity Q8_PER_TENSOR uses scales[0] for all M*K
+ * elements, Q8_PER_TOKEN uses scales[m] for row m.  scales: f64 device. */
+int q8_dequantize(const void* q, int src, int64_t M, int64_t K,
+                  const double* scales, int granularity, double zero_point,
+                  float* y, void* stream);
+
+/* ---------------------------------------------------------------- weights */
+
+/* Host weight quantization moved to the device: QuantizationPass's
+ * per-channel weight path (src/compiler/passes/quantization/
+ * quantization_pass.ts:390-400) = fromConstantArrayPerChannel
+ * (quantization_types.ts:299-317) + quantizeArrayPerChannel (:118-130),
+ * all in f64, clamp [-128,127]; or, with granularity Q8_PER_TENSOR,
+ * fromConstantArray (:287-297) + quantizeArray (:85-97), clamp [-127,127].
+ * W is a row-major [rows, cols] fp32 array.  axis 0: channel = row (the
+ * nn.Linear weight [N,K]); axis 1: channel = column (a [K,N] weight).
+ * Output Wq is always [N, K] (channel-major, K contiguous: the GEMM's B
+ * layout), i.e. W itself for axis 0 and its transpose for axis 1.
+ * scales: f64 device array of N entries (per channel) or 1 (per tensor). */
+int q8_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int granularity,
+                   int8_t* Wq, double* scales, void* stream);
+
+/* ---------------------------------------------------------------- matmul */
+
+/* quantized_dot (src/compiler/ir/graph/ops/quantization.ts:103-155, lowering
+ * src/compiler/passes/lowering/rules/quantization.ts:57-76) with its
+ * dequant epilogue fused:
+ *   acc[m,n] = sum_k (A[m,k] - zpA) * (B[n,k] - zpB)   (int32, wraps mod 2^32
+ *              exactly like the JS double accumulator stored to an Int32Array)
+ * A: [M,K] int8 row-major; B: [N,K] int8 (rhs_contracting = [1], the
+ * nn.Linear weight as packed by q8_pack_weight).
+ * out_kind Q8_I32: out = acc (the bare quantized_dot result).
+ * out_kind Q8_F32: out = act(bias + epilogue(acc)), with
+ *   epi Q8_EPI_PT:     fround(acc * s_out)                 (quantization_pass.ts:335-355)
+ *   epi Q8_EPI_ROWCOL: fround(acc * fround(sA[m] * sB[n])) (quantization_pass.ts:431-446;
+ *                      sA_mode / sB_mode Q8_PER_TENSOR read element 0,
+ *                      Q8_PER_TOKEN / Q8_PER_CHANNEL index by m / n)
+ *   bias (may be NULL): fround(y + bias[n]); act: Q8_ACT_*.
+ * zpA / zpB must be 0 in this build (Q8_ERR_UNSUPPORTED otherwise).
+ * Routes M <= 16 to the GEMV kernel. */
+int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+            int32_t zpA, int32_t zpB,
+            const double* sA, int sA_mode, const double* sB, int sB_mode,
+            int epi, double s_out, const float* bias, int act,
+            int out_kind, void* out, void* stream);
+
+/* The skinny (decode) form of q8_gemm for 1 <= M <= 16: same contract,
+ * HBM-bound kernel (packed int8 dot products, no matrix cores). */
+int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+            const double* sA, int sA_mode, const double* sB, int sB_mode,
+            int epi, double s_out, const float* bias, int act,
+            int out_kind, void* out, void* stream);
+
+/* ---------------------------------------------------------------- fused */
+
+/* h = fround(silu(g) * u) for the gated MLP (SiLU decomposition
+ * src/compiler/passes/decompose/decomposition_pass.ts:197-203,224-230 and a
+ * `mul`), followed by the per-token dynamic quantize of h (as
+ * q8_quantize_rows with Q8_PER_TOKEN).  g, u: [M,K] fp32.  h_out may be
+ * NULL (the fp32 h is then not written). */
+int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K,
+                              float* h_out, int8_t* q, double* scales, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q8HIP_H */

@@ -1,0 +1,76 @@
+"""Build step for the gfx950 library (libq8hip.so) and the Node addon.
+
+`python -m mlfw_amd.build` (or __graft_entry__.build()) compiles every HIP
+source under mlfw_amd/csrc with hipcc for gfx950 only, in-tree, so the
+built shared object travels with the source tree.  The Node N-API addon
+(mlfw_amd/node/q8hip.node) is built with gcc against the Node headers when
+they are installed.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libq8hip.so")
+NODE_DIR = os.path.join(HERE, "node")
+NODE_ADDON = os.path.join(NODE_DIR, "q8hip.node")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip"]
+
+# IEEE arithmetic everywhere (the kernels reproduce the reference's f64 /
+# f32 rounding bit for bit), no packed-FP32 instructions, gfx950 only.
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-fno-gpu-rdc",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def build_hip(verbose: bool = False) -> str:
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_node_addon(verbose: bool = False) -> str | None:
+    inc = "/usr/include/node"
+    src = os.path.join(NODE_DIR, "q8hip_napi.c")
+    if not (os.path.isdir(inc) and os.path.exists(src) and shutil.which("gcc")):
+        return None
+    cmd = ["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+           "-I", inc, "-I", os.path.join(ROOT, "include"),
+           "-o", NODE_ADDON, src,
+           "-L", HERE, "-lq8hip", "-Wl,-rpath,$ORIGIN/.."]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    return NODE_ADDON
+
+
+def build_all(verbose: bool = False) -> None:
+    build_hip(verbose)
+    build_node_addon(verbose)
+
+
+if __name__ == "__main__":
+    build_all(verbose="-v" in sys.argv)

@@ -1,0 +1,325 @@
+// q8_capi.hip -- the extern "C" boundary (include/q8hip.h).
+//
+// Every entry point validates its arguments on the host before launching
+// anything, reports failures as a status code plus a thread-local message
+// (the terac convention, terac/include/Tera/CAPI/Execution.h:55), and
+// enqueues its kernels on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/q8hip.h"
+#include "q8_internal.h"
+
+namespace {
+
+thread_local char g_err[1024] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(e == hipErrorOutOfMemory ? Q8_ERR_OOM : Q8_ERR_DEVICE, "%s: %s (%d)", what,
+              hipGetErrorString(e), (int)e);
+}
+
+// Per-device state: initialised once, holds the small work area used by
+// the two-phase per-tensor reductions (a few int32 keys).
+constexpr int kMaxDevices = 64;
+struct DevState {
+  std::atomic<int> ready{0};
+  int* work = nullptr;
+};
+DevState g_dev[kMaxDevices];
+std::mutex g_init_mu;
+
+int init_device(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(Q8_ERR_INVALID, "device %d out of range", dev);
+  if (g_dev[dev].ready.load(std::memory_order_acquire)) return Q8_OK;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_dev[dev].ready.load(std::memory_order_relaxed)) return Q8_OK;
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(Q8_ERR_DEVICE, "device %d is %s; this library is built for gfx950 only", dev,
+                prop.gcnArchName);
+  int cur = 0;
+  e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+  e = q8::setup_kernel_attributes();
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&g_dev[dev].work), 256);
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return hip_fail(e, "device set-up");
+  g_dev[dev].ready.store(1, std::memory_order_release);
+  return Q8_OK;
+}
+
+// Initialise the calling thread's current device on first use.
+int ensure_current(int** work) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice (no HIP device?)");
+  int rc = init_device(dev);
+  if (rc != Q8_OK) return rc;
+  if (work) *work = g_dev[dev].work;
+  return Q8_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return hip_fail(e, what);
+  g_err[0] = '\0';
+  return Q8_OK;
+}
+
+bool mul_ok(int64_t a, int64_t b) { return a >= 0 && b >= 0 && (b == 0 || a <= INT64_MAX / b); }
+
+#define Q8_REQUIRE(cond, ...) \
+  do {                        \
+    if (!(cond)) return fail(Q8_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int q8_version(void) { return Q8HIP_VERSION; }
+
+const char* q8_last_error(void) { return g_err; }
+
+int q8_device_count(int* count) {
+  Q8_REQUIRE(count != nullptr, "q8_device_count: count is NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) n = 0;
+  else if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  *count = n;
+  return Q8_OK;
+}
+
+int q8_init(int device) {
+  int n = 0;
+  int rc = q8_device_count(&n);
+  if (rc != Q8_OK) return rc;
+  if (n == 0) return fail(Q8_ERR_DEVICE, "q8_init: no HIP device is visible");
+  if (device < 0 || device >= n)
+    return fail(Q8_ERR_INVALID, "q8_init: device %d out of range (%d visible)", device, n);
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  return init_device(device);
+}
+
+int q8_alloc(void** dptr, size_t bytes) {
+  Q8_REQUIRE(dptr != nullptr, "q8_alloc: dptr is NULL");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  *dptr = nullptr;
+  if (bytes == 0) return Q8_OK;
+  hipError_t e = hipMalloc(dptr, bytes);
+  return launched(e, "hipMalloc");
+}
+
+int q8_free(void* dptr) {
+  if (dptr == nullptr) return Q8_OK;
+  return launched(hipFree(dptr), "hipFree");
+}
+
+int q8_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return Q8_OK;
+  Q8_REQUIRE(dst && src, "q8_h2d: NULL pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream));
+  if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+  return launched(e, "q8_h2d");
+}
+
+int q8_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return Q8_OK;
+  Q8_REQUIRE(dst && src, "q8_d2h: NULL pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream));
+  if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+  return launched(e, "q8_d2h");
+}
+
+int q8_memset(void* dst, int value, size_t bytes, void* stream) {
+  if (bytes == 0) return Q8_OK;
+  Q8_REQUIRE(dst != nullptr, "q8_memset: dst is NULL");
+  return launched(hipMemsetAsync(dst, value, bytes, as_stream(stream)), "q8_memset");
+}
+
+int q8_stream_sync(void* stream) {
+  return launched(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+}
+
+int q8_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset, double mean,
+                   double std, void* stream) {
+  Q8_REQUIRE(n >= 0, "q8_fill_normal: n < 0");
+  Q8_REQUIRE(n == 0 || out, "q8_fill_normal: out is NULL");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_fill_normal(out, n, seed, offset, mean, std, as_stream(stream)),
+                  "q8_fill_normal launch");
+}
+
+int q8_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset, double a, double b,
+                    void* stream) {
+  Q8_REQUIRE(n >= 0, "q8_fill_uniform: n < 0");
+  Q8_REQUIRE(n == 0 || out, "q8_fill_uniform: out is NULL");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_fill_uniform(out, n, seed, offset, a, b, as_stream(stream)),
+                  "q8_fill_uniform launch");
+}
+
+int q8_quantize_static(const float* x, int64_t n, double scale, double zero_point, int target,
+                       void* q, void* stream) {
+  Q8_REQUIRE(n >= 0, "q8_quantize_static: n < 0");
+  Q8_REQUIRE(n == 0 || (x && q), "q8_quantize_static: NULL pointer");
+  Q8_REQUIRE(target == Q8_I8 || target == Q8_U8,
+             "q8_quantize_static: target must be Q8_I8 or Q8_U8 (got %d)", target);
+  // quantize op verifier: `scale <= 0` is rejected (ops/quantization.ts:44-47)
+  Q8_REQUIRE(!(scale <= 0.0), "q8_quantize_static: quantize scale must be positive (got %g)", scale);
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_quant_static(x, n, scale, zero_point, target == Q8_U8, q,
+                                          as_stream(stream)),
+                  "q8_quantize_static launch");
+}
+
+int q8_quantize_rows(const float* x, int64_t M, int64_t K, int mode, int8_t* q, double* scales,
+                     void* stream) {
+  Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_quantize_rows: bad shape [%lld,%lld]",
+             (long long)M, (long long)K);
+  Q8_REQUIRE(mode == Q8_PER_TOKEN || mode == Q8_PER_TENSOR,
+             "q8_quantize_rows: mode must be Q8_PER_TOKEN or Q8_PER_TENSOR (got %d)", mode);
+  Q8_REQUIRE(scales != nullptr || (mode == Q8_PER_TOKEN && M == 0), "q8_quantize_rows: scales is NULL");
+  Q8_REQUIRE(M * K == 0 || (x && q), "q8_quantize_rows: NULL pointer");
+  int* work = nullptr;
+  int rc = ensure_current(&work);
+  if (rc != Q8_OK) return rc;
+  hipError_t e = mode == Q8_PER_TOKEN
+                     ? q8::launch_quant_rows(x, M, K, q, scales, as_stream(stream))
+                     : q8::launch_quant_tensor(x, M * K, q, scales, work, as_stream(stream));
+  return launched(e, "q8_quantize_rows launch");
+}
+
+int q8_dequantize(const void* q, int src, int64_t M, int64_t K, const double* scales,
+                  int granularity, double zero_point, float* y, void* stream) {
+  Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_dequantize: bad shape [%lld,%lld]",
+             (long long)M, (long long)K);
+  Q8_REQUIRE(src == Q8_I8 || src == Q8_U8 || src == Q8_I32,
+             "q8_dequantize: src must be Q8_I8, Q8_U8 or Q8_I32 (got %d)", src);
+  Q8_REQUIRE(granularity == Q8_PER_TENSOR || granularity == Q8_PER_TOKEN,
+             "q8_dequantize: granularity must be Q8_PER_TENSOR or Q8_PER_TOKEN (got %d)", granularity);
+  Q8_REQUIRE(M * K == 0 || (q && y && scales), "q8_dequantize: NULL pointer");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_dequant(q, src, M, K, scales, granularity == Q8_PER_TOKEN,
+                                     zero_point, y, as_stream(stream)),
+                  "q8_dequantize launch");
+}
+
+int q8_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int granularity,
+                   int8_t* Wq, double* scales, void* stream) {
+  Q8_REQUIRE(rows >= 0 && cols >= 0 && mul_ok(rows, cols), "q8_pack_weight: bad shape [%lld,%lld]",
+             (long long)rows, (long long)cols);
+  Q8_REQUIRE(axis == 0 || axis == 1, "q8_pack_weight: axis must be 0 or 1 (got %d)", axis);
+  Q8_REQUIRE(granularity == Q8_PER_CHANNEL || granularity == Q8_PER_TENSOR,
+             "q8_pack_weight: granularity must be Q8_PER_CHANNEL or Q8_PER_TENSOR (got %d)",
+             granularity);
+  Q8_REQUIRE(rows * cols == 0 || (W && Wq), "q8_pack_weight: NULL pointer");
+  Q8_REQUIRE(scales != nullptr, "q8_pack_weight: scales is NULL");
+  int* work = nullptr;
+  int rc = ensure_current(&work);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_pack_weight(W, rows, cols, axis, granularity == Q8_PER_TENSOR, Wq,
+                                         scales, work, as_stream(stream)),
+                  "q8_pack_weight launch");
+}
+
+static int gemm_common(const char* who, const int8_t* A, const int8_t* B, int64_t M, int64_t N,
+                       int64_t K, int32_t zpA, int32_t zpB, const double* sA, int sA_mode,
+                       const double* sB, int sB_mode, int epi, double s_out, const float* bias,
+                       int act, int out_kind, void* out, q8::GemmEpi* e) {
+  Q8_REQUIRE(M >= 0 && N >= 0 && K >= 0 && mul_ok(M, N) && mul_ok(M, K) && mul_ok(N, K),
+             "%s: bad shape M=%lld N=%lld K=%lld", who, (long long)M, (long long)N, (long long)K);
+  Q8_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31),
+             "%s: dimensions must be below 2^31", who);
+  Q8_REQUIRE(out_kind == Q8_F32 || out_kind == Q8_I32, "%s: out_kind must be Q8_F32 or Q8_I32", who);
+  Q8_REQUIRE(act == Q8_ACT_NONE || act == Q8_ACT_RELU || act == Q8_ACT_SILU, "%s: bad act %d", who, act);
+  Q8_REQUIRE(epi == Q8_EPI_PT || epi == Q8_EPI_ROWCOL, "%s: bad epi %d", who, epi);
+  Q8_REQUIRE(M * N == 0 || out, "%s: out is NULL", who);
+  Q8_REQUIRE(M * N * K == 0 || (A && B), "%s: NULL operand", who);
+  if (zpA != 0 || zpB != 0)
+    return fail(Q8_ERR_UNSUPPORTED, "%s: non-zero zero points are not supported by this build", who);
+  e->sA = sA;
+  e->sB = sB;
+  e->sA_stride = 0;
+  e->sB_stride = 0;
+  e->s_out = s_out;
+  e->bias = bias;
+  e->mode = epi == Q8_EPI_ROWCOL ? 1 : 0;
+  e->act = act;
+  e->out_i32 = out_kind == Q8_I32;
+  if (out_kind == Q8_F32 && epi == Q8_EPI_ROWCOL) {
+    Q8_REQUIRE(sA && sB, "%s: ROWCOL epilogue needs sA and sB", who);
+    Q8_REQUIRE(sA_mode == Q8_PER_TENSOR || sA_mode == Q8_PER_TOKEN, "%s: bad sA_mode %d", who, sA_mode);
+    Q8_REQUIRE(sB_mode == Q8_PER_TENSOR || sB_mode == Q8_PER_CHANNEL, "%s: bad sB_mode %d", who, sB_mode);
+    e->sA_stride = sA_mode == Q8_PER_TOKEN ? 1 : 0;
+    e->sB_stride = sB_mode == Q8_PER_CHANNEL ? 1 : 0;
+  }
+  if (out_kind == Q8_I32)
+    Q8_REQUIRE(bias == nullptr && act == Q8_ACT_NONE, "%s: Q8_I32 output takes no bias or activation", who);
+  return Q8_OK;
+}
+
+int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, int32_t zpA,
+            int32_t zpB, const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
+            double s_out, const float* bias, int act, int out_kind, void* out, void* stream) {
+  q8::GemmEpi e;
+  int rc = gemm_common("q8_gemm", A, B, M, N, K, zpA, zpB, sA, sA_mode, sB, sB_mode, epi, s_out,
+                       bias, act, out_kind, out, &e);
+  if (rc != Q8_OK) return rc;
+  rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  hipError_t err = (M <= 16) ? q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream))
+                             : q8::launch_gemm(A, B, M, N, K, e, out, as_stream(stream));
+  return launched(err, "q8_gemm launch");
+}
+
+int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, const double* sA,
+            int sA_mode, const double* sB, int sB_mode, int epi, double s_out, const float* bias,
+            int act, int out_kind, void* out, void* stream) {
+  Q8_REQUIRE(M >= 0 && M <= 16, "q8_gemv: M must be in [0, 16] (got %lld)", (long long)M);
+  q8::GemmEpi e;
+  int rc = gemm_common("q8_gemv", A, B, M, N, K, 0, 0, sA, sA_mode, sB, sB_mode, epi, s_out, bias,
+                       act, out_kind, out, &e);
+  if (rc != Q8_OK) return rc;
+  rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream)), "q8_gemv launch");
+}
+
+int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K, float* h_out,
+                              int8_t* q, double* scales, void* stream) {
+  Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_silu_mul_quantize_rows: bad shape");
+  Q8_REQUIRE(M == 0 || scales, "q8_silu_mul_quantize_rows: scales is NULL");
+  Q8_REQUIRE(M * K == 0 || (g && u && q), "q8_silu_mul_quantize_rows: NULL pointer");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_silu_mul_quant_rows(g, u, M, K, h_out, q, scales, as_stream(stream)),
+                  "q8_silu_mul_quantize_rows launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+// q8_device.h -- device-side arithmetic shared by the gfx950 kernels.
+//
+// All helpers reproduce the reference CPU backend's JavaScript arithmetic
+// (src/backend/cpu/codegen.ts): f64 evaluation, Math.fround = one RNE
+// conversion to binary32, Math.round = nearest integer with ties toward +inf,
+// `| 0` = NaN -> 0.  The library is compiled with -ffp-contract=off and no
+// fast-math so that every f64 / f32 operation below is a single IEEE op.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ECMA-262 Math.round for an exact double.  y - floor(y) is exact.
+__device__ __forceinline__ double js_round(double y) {
+  double r = floor(y);
+  return (y - r >= 0.5) ? r + 1.0 : r;
+}
+
+// (Math.min(Math.max(r, lo), hi) | 0) for an already-rounded r.
+__device__ __forceinline__ int clamp_to_int(double r, int lo, int hi) {
+  if (r != r) return 0;
+  r = r < (double)lo ? (double)lo : r;
+  r = r > (double)hi ? (double)hi : r;
+  return (int)r;
+}
+
+// R1, exact form: quant_math.ts:16-27 evaluated as the CPU backend does.
+__device__ __forceinline__ int quant_exact(float x, double s, double zp, int lo, int hi) {
+  double y = (double)(float)((double)x / s);          // Math.fround(x / s)
+  if (zp != 0.0) y = (double)(float)(y + zp);          // Math.fround(.. + zp)
+  return clamp_to_int(js_round(y), lo, hi);
+}
+
+// R1 for the symmetric int8 case (zp = 0, clamp [-128,127]) with an f32
+// fast path.  r32 = (float)(1/s).  t = x*r32 differs from y = x/s by at most
+// 2^-22.9 relative, i.e. < 2^-15 for |y| < 256, and fround(y) differs from y
+// by at most 2^-17 there; Math.round only changes value across a
+// half-integer, so when t's fraction is more than 2^-13 away from 0.5 the
+// integer is decided by t.  |t| >= 256 implies |y| > 128.5 (clamped).
+// Everything else (near-ties, NaN) takes the exact f64 path, so the result
+// is always the exact one.  Callers guarantee s is a normal double in
+// [2^-100, 2^100] (else they use quant_exact for every element).
+__device__ __forceinline__ int quant_sym_fast(float x, float r32, double s) {
+  float t = x * r32;
+  float at = __builtin_fabsf(t);
+  if (at < 256.0f) {
+    float fl = __builtin_floorf(t);
+    float fr = t - fl;
+    if (__builtin_fabsf(fr - 0.5f) > 0x1p-13f) {
+      int r = (int)fl + (fr > 0.5f ? 1 : 0);
+      r = r < -128 ? -128 : r;
+      return r > 127 ? 127 : r;
+    }
+  } else if (at >= 256.0f) {          // false for NaN
+    return t > 0.0f ? 127 : -128;
+  }
+  return quant_exact(x, s, 0.0, -128, 127);
+}
+
+// Order key of |x| for a NaN-ignoring absmax: the bit pattern of |x| (an
+// integer order equal to the float order for non-negative floats), -1 for NaN.
+__device__ __forceinline__ int absmax_key(float x) {
+  unsigned u = __float_as_uint(x) & 0x7fffffffu;
+  return u > 0x7f800000u ? -1 : (int)u;
+}
+
+// Scale from a reduced absmax key (fromRange symmetric, quantization_types.ts:
+// 249-253): s = absmax/127 || 1e-10.  key -1 = only NaNs were seen: the
+// observer's min/max stayed (+inf, -inf), so absmax = +inf.
+__device__ __forceinline__ double scale_from_key(int key) {
+  double amax = key < 0 ? __builtin_inf() : (double)__uint_as_float((unsigned)key);
+  double s = amax / 127.0;
+  return (s == 0.0 || s != s) ? 1e-10 : s;
+}
+
+// Whether the f32 fast path of quant_sym_fast is valid for scale s.
+__device__ __forceinline__ bool fast_scale_ok(double s) {
+  return s >= 0x1p-100 && s <= 0x1p100;
+}
+
+// D1: Math.fround((+q) * s), zero point form Math.fround(Math.fround(q - zp) * s).
+__device__ __forceinline__ float dequant(double q, double s, double zp) {
+  if (zp != 0.0) q = (double)(float)(q - zp);
+  return (float)(q * s);
+}
+
+// Math.max(v, 0) on f32: NaN stays NaN, -0 and negatives give +0.
+__device__ __forceinline__ float relu_js(float v) {
+  return (v > 0.0f || v != v) ? v : 0.0f;
+}
+
+// SiLU decomposed (decomposition_pass.ts:197-203, 224-230), each op rounded:
+// fround(x * fround(1 / fround(1 + fround(exp(-x))))), exp evaluated in f64.
+__device__ __noinline__ float silu_js(float x) {
+  float e = (float)exp(-(double)x);
+  float d = (float)(1.0 + (double)e);
+  float r = (float)(1.0 / (double)d);
+  return (float)((double)x * (double)r);
+}
+
+// Wave64 reductions.
+__device__ __forceinline__ int wave_max_i32(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    int w = __shfl_xor(v, o, 64);
+    v = v > w ? v : w;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Key of a float for an order-preserving signed-int min/max (NaN excluded by
+// the caller): non-negative floats keep their bits, negative ones flip the
+// magnitude bits so that more negative is smaller.
+__device__ __forceinline__ int order_key(float x) {
+  int b = __float_as_int(x);
+  return b >= 0 ? b : (int)(b ^ 0x7fffffff);
+}
+__device__ __forceinline__ float from_order_key(int k) {
+  return __int_as_float(k >= 0 ? k : (int)(k ^ 0x7fffffff));
+}
+
+}  // namespace q8

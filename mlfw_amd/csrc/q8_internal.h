@@ -1,0 +1,49 @@
+// q8_internal.h -- launchers shared between the kernel files and the C ABI.
+// Every launcher assumes its arguments were validated by q8_capi.hip and
+// returns the hipError_t of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q8 {
+
+// Epilogue description passed by value to the GEMM / GEMV kernels.
+struct GemmEpi {
+  const double* sA;     // per-row (stride 1) or scalar (stride 0); ROWCOL only
+  const double* sB;     // per-column (stride 1) or scalar (stride 0); ROWCOL only
+  int64_t sA_stride;
+  int64_t sB_stride;
+  double s_out;         // PT only
+  const float* bias;    // may be null
+  int mode;             // 0 = PT, 1 = ROWCOL
+  int act;              // 0 none, 1 relu, 2 silu
+  int out_i32;          // 1: write the raw int32 accumulator
+};
+
+hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
+                              double mean, double std, hipStream_t st);
+hipError_t launch_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset,
+                               double a, double b, hipStream_t st);
+hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, int is_u8,
+                               void* q, hipStream_t st);
+hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, double* scales,
+                             hipStream_t st);
+hipError_t launch_quant_tensor(const float* x, int64_t n, int8_t* q, double* scales,
+                               int* work, hipStream_t st);
+hipError_t launch_dequant(const void* q, int src, int64_t M, int64_t K, const double* scales,
+                          int per_row, double zp, float* y, hipStream_t st);
+hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int axis,
+                              int per_tensor, int8_t* Wq, double* scales, int* work,
+                              hipStream_t st);
+hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M, int64_t K,
+                                      float* h, int8_t* q, double* scales, hipStream_t st);
+hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                       const GemmEpi& e, void* out, hipStream_t st);
+hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                       const GemmEpi& e, void* out, hipStream_t st);
+
+// One-time per-device kernel attribute set-up (dynamic LDS limits).
+hipError_t setup_kernel_attributes();
+
+}  // namespace q8

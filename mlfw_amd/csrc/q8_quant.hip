@@ -1,0 +1,659 @@
+// q8_quant.hip -- HBM-bound kernels of the int8 path for gfx950:
+// seeded input fill, static / per-token / per-tensor quantize, dequantize,
+// per-channel weight packing and the fused SiLU*up + per-token quantize.
+//
+// Layout: every fp32 / int8 tensor is row-major in HBM.  Rows are read with
+// 128-bit coalesced loads (float4 = 16 B per lane, 1 KiB per wave64
+// instruction) when the row length is a multiple of 4 elements and the base
+// is 16-byte aligned; a scalar grid-stride form handles everything else.
+// Per-row absmax reductions run in registers: a row of up to 12 KiB floats
+// stays in VGPRs (VPT float4 per thread) so the row is read from HBM once.
+#include "q8_device.h"
+#include "q8_internal.h"
+
+namespace q8 {
+
+static constexpr int NT = 256;   // threads per block for the streaming kernels
+
+// ------------------------------------------------------------------ inputs
+// mulberry32 (src/util/random.ts:5-14) in counter form: the generator state
+// after draw i is seed + (i+1) * 0x6D2B79F5 (mod 2^32), so every draw is
+// independent of the others.
+__device__ __forceinline__ double mb32(uint32_t seed, uint64_t i) {
+  uint32_t a = seed + (uint32_t)(i + 1) * 0x6D2B79F5u;
+  uint32_t t = (a ^ (a >> 15)) * (1u | a);
+  t = (t + ((t ^ (t >> 7)) * (61u | t))) ^ t;
+  return (double)(t ^ (t >> 14)) / 4294967296.0;
+}
+
+// normal_ (src/nn/init.ts:40-52): element pair p uses draws 2p, 2p+1.
+__global__ __launch_bounds__(NT) void k_fill_normal(float* __restrict__ out, int64_t n,
+                                                    uint32_t seed, uint64_t offset,
+                                                    double mean, double std) {
+  int64_t pairs = (n + 1) >> 1;
+  for (int64_t p = blockIdx.x * (int64_t)NT + threadIdx.x; p < pairs;
+       p += (int64_t)gridDim.x * NT) {
+    double u1 = mb32(seed, offset + 2 * p);
+    if (u1 == 0.0) u1 = 1e-10;
+    double u2 = mb32(seed, offset + 2 * p + 1);
+    double r = sqrt(-2.0 * log(u1));
+    double theta = 6.283185307179586 * u2;
+    out[2 * p] = (float)(mean + std * r * cos(theta));
+    if (2 * p + 1 < n) out[2 * p + 1] = (float)(mean + std * r * sin(theta));
+  }
+}
+
+// uniform_ (src/nn/init.ts:31-37)
+__global__ __launch_bounds__(NT) void k_fill_uniform(float* __restrict__ out, int64_t n,
+                                                     uint32_t seed, uint64_t offset,
+                                                     double a, double b) {
+  double range = b - a;
+  for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * NT)
+    out[i] = (float)(a + mb32(seed, offset + i) * range);
+}
+
+static int grid_for(int64_t work, int64_t per_block, int cap) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  return (int)(g > cap ? cap : g);
+}
+
+hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
+                              double mean, double std, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_normal, dim3(grid_for((n + 1) / 2, NT, 65536)), dim3(NT), 0, st,
+                     out, n, seed, offset, mean, std);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset,
+                               double a, double b, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_uniform, dim3(grid_for(n, NT, 65536)), dim3(NT), 0, st,
+                     out, n, seed, offset, a, b);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ helpers
+__device__ __forceinline__ int pack4(int b0, int b1, int b2, int b3) {
+  return (b0 & 0xff) | ((b1 & 0xff) << 8) | ((b2 & 0xff) << 16) | ((b3 & 0xff) << 24);
+}
+
+__device__ __forceinline__ int key4(float4 v) {
+  int a = absmax_key(v.x), b = absmax_key(v.y), c = absmax_key(v.z), d = absmax_key(v.w);
+  a = a > b ? a : b;
+  c = c > d ? c : d;
+  return a > c ? a : c;
+}
+
+__device__ __forceinline__ int quant4_sym(float4 v, bool fast, float r32, double s) {
+  if (fast)
+    return pack4(quant_sym_fast(v.x, r32, s), quant_sym_fast(v.y, r32, s),
+                 quant_sym_fast(v.z, r32, s), quant_sym_fast(v.w, r32, s));
+  return pack4(quant_exact(v.x, s, 0.0, -128, 127), quant_exact(v.y, s, 0.0, -128, 127),
+               quant_exact(v.z, s, 0.0, -128, 127), quant_exact(v.w, s, 0.0, -128, 127));
+}
+
+// Block-wide max of an int key (256 threads = 4 waves).  `red` is LDS.
+__device__ __forceinline__ int block_max_i32(int key, int* red) {
+  key = wave_max_i32(key);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = key;
+  __syncthreads();
+  int k = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) k = k > red[w] ? k : red[w];
+  __syncthreads();   // red is reused by the next row
+  return k;
+}
+
+// ------------------------------------------------------------------ static quantize
+// R1 with a compile-time scale (quant_math.ts:16-27), any n, any alignment.
+__global__ __launch_bounds__(NT) void k_quant_static(const float* __restrict__ x, int64_t n,
+                                                     double s, double zp, int is_u8,
+                                                     uint8_t* __restrict__ q) {
+  const int lo = is_u8 ? 0 : -128, hi = is_u8 ? 255 : 127;
+  const bool fast = (zp == 0.0) && !is_u8 && fast_scale_ok(s);
+  const float r32 = (float)(1.0 / s);
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  const int64_t i0 = blockIdx.x * (int64_t)NT + threadIdx.x;
+  const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
+  if (vec) {
+    const int64_t n4 = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    int* q4 = reinterpret_cast<int*>(q);
+    for (int64_t i = i0; i < n4; i += stride) {
+      float4 v = x4[i];
+      int p;
+      if (fast) {
+        p = quant4_sym(v, true, r32, s);
+      } else {
+        p = pack4(quant_exact(v.x, s, zp, lo, hi), quant_exact(v.y, s, zp, lo, hi),
+                  quant_exact(v.z, s, zp, lo, hi), quant_exact(v.w, s, zp, lo, hi));
+      }
+      q4[i] = p;
+    }
+    for (int64_t i = (n4 << 2) + i0; i < n; i += stride)
+      q[i] = (uint8_t)(fast ? quant_sym_fast(x[i], r32, s) : quant_exact(x[i], s, zp, lo, hi));
+  } else {
+    for (int64_t i = i0; i < n; i += stride)
+      q[i] = (uint8_t)(fast ? quant_sym_fast(x[i], r32, s) : quant_exact(x[i], s, zp, lo, hi));
+  }
+}
+
+hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, int is_u8,
+                               void* q, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_quant_static, dim3(grid_for((n + 3) / 4, NT, 8192)), dim3(NT), 0, st,
+                     x, n, s, zp, is_u8, static_cast<uint8_t*>(q));
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ per-token quantize
+// One block per row (grid-stride over rows).  The first VPT*1024 elements
+// of the row stay in registers between the absmax reduction and the
+// quantize, so such rows are read once; longer rows re-read the tail.
+template <int VPT>
+__global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t M,
+                                                   int64_t K, int8_t* __restrict__ q,
+                                                   double* __restrict__ scales) {
+  __shared__ int red[NT / 64];
+  const int tid = threadIdx.x;
+  const int64_t K4 = K >> 2;
+  for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
+    const float4* xr = reinterpret_cast<const float4*>(x + row * K);
+    int* qr = reinterpret_cast<int*>(q + row * K);
+    float4 v[VPT];
+    int key = -1;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int64_t i = tid + (int64_t)j * NT;
+      if (i < K4) {
+        v[j] = xr[i];
+        int k = key4(v[j]);
+        key = key > k ? key : k;
+      }
+    }
+    for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
+      int k = key4(xr[i]);
+      key = key > k ? key : k;
+    }
+    key = block_max_i32(key, red);
+    const double s = K == 0 ? 6.0 / 127.0 : scale_from_key(key);
+    if (tid == 0) scales[row] = s;
+    const bool fast = fast_scale_ok(s);
+    const float r32 = (float)(1.0 / s);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int64_t i = tid + (int64_t)j * NT;
+      if (i < K4) qr[i] = quant4_sym(v[j], fast, r32, s);
+    }
+    for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) qr[i] = quant4_sym(xr[i], fast, r32, s);
+  }
+}
+
+// Any K / alignment: two passes over the row with scalar loads.
+__global__ __launch_bounds__(NT) void k_quant_rows_scalar(const float* __restrict__ x, int64_t M,
+                                                          int64_t K, int8_t* __restrict__ q,
+                                                          double* __restrict__ scales) {
+  __shared__ int red[NT / 64];
+  for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
+    const float* xr = x + row * K;
+    int key = -1;
+    for (int64_t i = threadIdx.x; i < K; i += NT) {
+      int k = absmax_key(xr[i]);
+      key = key > k ? key : k;
+    }
+    key = block_max_i32(key, red);
+    const double s = K == 0 ? 6.0 / 127.0 : scale_from_key(key);
+    if (threadIdx.x == 0) scales[row] = s;
+    const bool fast = fast_scale_ok(s);
+    const float r32 = (float)(1.0 / s);
+    for (int64_t i = threadIdx.x; i < K; i += NT)
+      q[row * K + i] = (int8_t)(fast ? quant_sym_fast(xr[i], r32, s)
+                                     : quant_exact(xr[i], s, 0.0, -128, 127));
+  }
+}
+
+hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, double* scales,
+                             hipStream_t st) {
+  if (M == 0) return hipSuccess;
+  const int grid = (int)(M < 1048576 ? M : 1048576);
+  const bool vec = (K % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
+  if (!vec) {
+    hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+    return hipGetLastError();
+  }
+  const int64_t K4 = K / 4;
+  if (K4 <= 1 * NT)
+    hipLaunchKernelGGL(k_quant_rows<1>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+  else if (K4 <= 2 * NT)
+    hipLaunchKernelGGL(k_quant_rows<2>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+  else if (K4 <= 4 * NT)
+    hipLaunchKernelGGL(k_quant_rows<4>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+  else if (K4 <= 8 * NT)
+    hipLaunchKernelGGL(k_quant_rows<8>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+  else
+    hipLaunchKernelGGL(k_quant_rows<12>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ per-tensor quantize
+// Phase 1: NaN-ignoring absmax of the whole tensor into work[0] (an int key,
+// combined with a vector atomic max).  Phase 2: every block derives the
+// scale from the key and quantizes its share.
+__global__ void k_set_i32(int* p, int v) { p[0] = v; }
+
+__global__ __launch_bounds__(NT) void k_absmax_tensor(const float* __restrict__ x, int64_t n,
+                                                      int* __restrict__ work) {
+  __shared__ int red[NT / 64];
+  int key = -1;
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  const int64_t i0 = blockIdx.x * (int64_t)NT + threadIdx.x;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const int64_t n4 = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (int64_t i = i0; i < n4; i += stride) {
+      int k = key4(x4[i]);
+      key = key > k ? key : k;
+    }
+    for (int64_t i = (n4 << 2) + i0; i < n; i += stride) {
+      int k = absmax_key(x[i]);
+      key = key > k ? key : k;
+    }
+  } else {
+    for (int64_t i = i0; i < n; i += stride) {
+      int k = absmax_key(x[i]);
+      key = key > k ? key : k;
+    }
+  }
+  key = block_max_i32(key, red);
+  if (threadIdx.x == 0 && key >= 0) atomicMax(work, key);
+}
+
+__global__ __launch_bounds__(NT) void k_quant_tensor(const float* __restrict__ x, int64_t n,
+                                                     const int* __restrict__ work,
+                                                     int8_t* __restrict__ q,
+                                                     double* __restrict__ scales) {
+  const double s = n == 0 ? 6.0 / 127.0 : scale_from_key(work[0]);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scales[0] = s;
+  const bool fast = fast_scale_ok(s);
+  const float r32 = (float)(1.0 / s);
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  const int64_t i0 = blockIdx.x * (int64_t)NT + threadIdx.x;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(q) & 3) == 0) {
+    const int64_t n4 = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    int* q4 = reinterpret_cast<int*>(q);
+    for (int64_t i = i0; i < n4; i += stride) q4[i] = quant4_sym(x4[i], fast, r32, s);
+    for (int64_t i = (n4 << 2) + i0; i < n; i += stride)
+      q[i] = (int8_t)(fast ? quant_sym_fast(x[i], r32, s) : quant_exact(x[i], s, 0.0, -128, 127));
+  } else {
+    for (int64_t i = i0; i < n; i += stride)
+      q[i] = (int8_t)(fast ? quant_sym_fast(x[i], r32, s) : quant_exact(x[i], s, 0.0, -128, 127));
+  }
+}
+
+hipError_t launch_quant_tensor(const float* x, int64_t n, int8_t* q, double* scales, int* work,
+                               hipStream_t st) {
+  // The key starts at -1 ("only NaNs seen"); blocks that saw a non-NaN
+  // value raise it.  A fill kernel (not a memset) keeps the sequence
+  // capturable in a HIP graph.
+  hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, work, -1);
+  const int grid = grid_for((n + 3) / 4, NT * 4, 2048);
+  if (n > 0) hipLaunchKernelGGL(k_absmax_tensor, dim3(grid), dim3(NT), 0, st, x, n, work);
+  hipLaunchKernelGGL(k_quant_tensor, dim3(grid), dim3(NT), 0, st, x, n, work, q, scales);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ dequantize
+// D1 (quant_math.ts:29-34).  grid.y walks rows, grid.x 16-element chunks of
+// a row; one f64 multiply and one f64->f32 conversion per element.
+template <int SRC>  // 0 i8, 1 u8, 2 i32
+__global__ __launch_bounds__(NT) void k_dequant_vec(const void* __restrict__ qv, int64_t M,
+                                                    int64_t K, const double* __restrict__ scales,
+                                                    int per_row, double zp,
+                                                    float* __restrict__ y) {
+  constexpr int EPC = SRC == 2 ? 4 : 16;           // elements per 16-byte chunk
+  const int64_t chunks = K / EPC;
+  for (int64_t row = blockIdx.y; row < M; row += gridDim.y) {
+    const double s = scales[per_row ? row : 0];
+    for (int64_t c = blockIdx.x * (int64_t)NT + threadIdx.x; c < chunks;
+         c += (int64_t)gridDim.x * NT) {
+      const int64_t base = row * K + c * EPC;
+      float o[EPC];
+      if (SRC == 2) {
+        int4 w = *reinterpret_cast<const int4*>(static_cast<const int32_t*>(qv) + base);
+        o[0] = dequant((double)w.x, s, zp);
+        o[1] = dequant((double)w.y, s, zp);
+        o[2] = dequant((double)w.z, s, zp);
+        o[3] = dequant((double)w.w, s, zp);
+      } else {
+        int4 w = *reinterpret_cast<const int4*>(static_cast<const int8_t*>(qv) + base);
+        int words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          int b = (words[t >> 2] >> ((t & 3) * 8)) & 0xff;
+          if (SRC == 0) b = (int)(int8_t)b;
+          o[t] = dequant((double)b, s, zp);
+        }
+      }
+      float4* yp = reinterpret_cast<float4*>(y + base);
+#pragma unroll
+      for (int t = 0; t < EPC / 4; ++t) yp[t] = make_float4(o[4 * t], o[4 * t + 1], o[4 * t + 2], o[4 * t + 3]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(NT) void k_dequant_scalar(const void* __restrict__ qv, int src,
+                                                       int64_t M, int64_t K,
+                                                       const double* __restrict__ scales,
+                                                       int per_row, double zp,
+                                                       float* __restrict__ y) {
+  const int64_t n = M * K;
+  for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+    const double s = scales[per_row ? i / K : 0];
+    double v;
+    if (src == 0) v = (double)static_cast<const int8_t*>(qv)[i];
+    else if (src == 1) v = (double)static_cast<const uint8_t*>(qv)[i];
+    else v = (double)static_cast<const int32_t*>(qv)[i];
+    y[i] = dequant(v, s, zp);
+  }
+}
+
+hipError_t launch_dequant(const void* q, int src, int64_t M, int64_t K, const double* scales,
+                          int per_row, double zp, float* y, hipStream_t st) {
+  if (M == 0 || K == 0) return hipSuccess;
+  const int epc = src == 2 ? 4 : 16;
+  const bool vec = (K % epc == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
+  if (!vec) {
+    hipLaunchKernelGGL(k_dequant_scalar, dim3(grid_for(M * K, NT, 65536)), dim3(NT), 0, st,
+                       q, src, M, K, scales, per_row, zp, y);
+    return hipGetLastError();
+  }
+  const int64_t chunks = K / epc;
+  dim3 grid(grid_for(chunks, NT, 1024), (unsigned)(M < 65535 ? M : 65535));
+  if (src == 0)
+    hipLaunchKernelGGL(k_dequant_vec<0>, grid, dim3(NT), 0, st, q, M, K, scales, per_row, zp, y);
+  else if (src == 1)
+    hipLaunchKernelGGL(k_dequant_vec<1>, grid, dim3(NT), 0, st, q, M, K, scales, per_row, zp, y);
+  else
+    hipLaunchKernelGGL(k_dequant_vec<2>, grid, dim3(NT), 0, st, q, M, K, scales, per_row, zp, y);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ weight packing
+// fromConstantArrayPerChannel's per-channel fix-ups on a (min, max) pair,
+// then fromRangePerChannel's scale (quantization_types.ts:266-281, 311-316).
+__device__ __forceinline__ double channel_scale(double mn, double mx) {
+  if (!isfinite(mn)) mn = -1.0;
+  if (!isfinite(mx)) mx = 1.0;
+  if (mn == mx) { mn -= 0.5; mx += 0.5; }
+  double a = fabs(mn) > fabs(mx) ? fabs(mn) : fabs(mx);
+  double s = a / 127.0;
+  return (s == 0.0 || s != s) ? 1e-10 : s;
+}
+
+// axis 0: one block per row (channel).  fminf / fmaxf ignore NaN exactly
+// like the reference's `v < min` / `v > max` updates.
+__global__ __launch_bounds__(NT) void k_wscale_rows(const float* __restrict__ W, int64_t rows,
+                                                    int64_t cols, double* __restrict__ scales) {
+  __shared__ float rmn[NT / 64], rmx[NT / 64];
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    float mn = __builtin_inff(), mx = -__builtin_inff();
+    for (int64_t c = threadIdx.x; c < cols; c += NT) {
+      float v = W[r * cols + c];
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      mn = fminf(mn, __shfl_xor(mn, o, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) { rmn[threadIdx.x >> 6] = mn; rmx[threadIdx.x >> 6] = mx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < NT / 64; ++w) { mn = fminf(mn, rmn[w]); mx = fmaxf(mx, rmx[w]); }
+      mn = fminf(rmn[0], mn);
+      mx = fmaxf(rmx[0], mx);
+      scales[r] = channel_scale((double)mn, (double)mx);
+    }
+    __syncthreads();
+  }
+}
+
+// axis 1: a block owns 64 columns; 4 row phases stride the rows.
+__global__ __launch_bounds__(NT) void k_wscale_cols(const float* __restrict__ W, int64_t rows,
+                                                    int64_t cols, double* __restrict__ scales) {
+  __shared__ float smn[NT], smx[NT];
+  const int col_in = threadIdx.x & 63, phase = threadIdx.x >> 6;
+  const int64_t c = blockIdx.x * 64LL + col_in;
+  float mn = __builtin_inff(), mx = -__builtin_inff();
+  if (c < cols)
+    for (int64_t r = phase; r < rows; r += NT / 64) {
+      float v = W[r * cols + c];
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+  smn[threadIdx.x] = mn;
+  smx[threadIdx.x] = mx;
+  __syncthreads();
+  if (phase == 0 && c < cols) {
+    for (int p = 1; p < NT / 64; ++p) {
+      mn = fminf(mn, smn[p * 64 + col_in]);
+      mx = fmaxf(mx, smx[p * 64 + col_in]);
+    }
+    scales[c] = channel_scale((double)mn, (double)mx);
+  }
+}
+
+// per tensor: order-key min / max of the whole array into work[0], work[1].
+__global__ void k_set_minmax_init(int* work) {
+  work[0] = 0x7fffffff;             // key of +NaN-free max -> min starts high
+  work[1] = (int)0x80000000;        // max starts low
+}
+
+__global__ __launch_bounds__(NT) void k_wminmax_tensor(const float* __restrict__ W, int64_t n,
+                                                       int* __restrict__ work) {
+  __shared__ int rmn[NT / 64], rmx[NT / 64];
+  int mn = 0x7fffffff, mx = (int)0x80000000;
+  for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+    float v = W[i];
+    if (v == v) {
+      int k = order_key(v);
+      mn = mn < k ? mn : k;
+      mx = mx > k ? mx : k;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    int a = __shfl_xor(mn, o, 64), b = __shfl_xor(mx, o, 64);
+    mn = mn < a ? mn : a;
+    mx = mx > b ? mx : b;
+  }
+  if ((threadIdx.x & 63) == 0) { rmn[threadIdx.x >> 6] = mn; rmx[threadIdx.x >> 6] = mx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < NT / 64; ++w) { mn = mn < rmn[w] ? mn : rmn[w]; mx = mx > rmx[w] ? mx : rmx[w]; }
+    atomicMin(&work[0], mn);
+    atomicMax(&work[1], mx);
+  }
+}
+
+// fromConstantArray (quantization_types.ts:287-297) on the reduced keys.
+__global__ void k_wscale_tensor(const int* __restrict__ work, double* __restrict__ scales) {
+  const bool none = work[0] == 0x7fffffff && work[1] == (int)0x80000000;
+  double mn = none ? __builtin_inf() : (double)from_order_key(work[0]);
+  double mx = none ? -__builtin_inf() : (double)from_order_key(work[1]);
+  scales[0] = channel_scale(mn, mx);
+}
+
+// R2 (quantization_types.ts:75-79, 118-130): q = clamp(JSround(w/s + 0)), f64.
+__device__ __forceinline__ int wquant(float w, double s, int lo, int hi) {
+  return clamp_to_int(js_round((double)w / s + 0.0), lo, hi);
+}
+
+// axis 0 / per tensor: same layout in and out.
+__global__ __launch_bounds__(NT) void k_wquant_rows(const float* __restrict__ W, int64_t rows,
+                                                    int64_t cols, const double* __restrict__ scales,
+                                                    int per_tensor, int8_t* __restrict__ Wq) {
+  const int lo = per_tensor ? -127 : -128, hi = 127;
+  const int64_t n = rows * cols;
+  for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+    const double s = scales[per_tensor ? 0 : i / cols];
+    Wq[i] = (int8_t)wquant(W[i], s, lo, hi);
+  }
+}
+
+// axis 1: W is [K=rows, N=cols]; Wq is [N, K].  64x64 tiles transposed
+// through LDS so both the fp32 reads and the int8 writes are coalesced.
+__global__ __launch_bounds__(NT) void k_wquant_cols_t(const float* __restrict__ W, int64_t rows,
+                                                      int64_t cols, const double* __restrict__ scales,
+                                                      int per_tensor, int8_t* __restrict__ Wq) {
+  __shared__ int8_t tile[64][65];
+  const int lo = per_tensor ? -127 : -128, hi = 127;
+  const int64_t k0 = blockIdx.y * 64LL, n0 = blockIdx.x * 64LL;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t n = n0 + tx;
+  const double s = n < cols ? scales[per_tensor ? 0 : n] : 1.0;
+  for (int r = ty; r < 64; r += NT / 64) {
+    const int64_t k = k0 + r;
+    int8_t v = 0;
+    if (k < rows && n < cols) v = (int8_t)wquant(W[k * cols + n], s, lo, hi);
+    tile[tx][r] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += NT / 64) {
+    const int64_t nn = n0 + r, kk = k0 + tx;
+    if (nn < cols && kk < rows) Wq[nn * rows + kk] = tile[r][tx];
+  }
+}
+
+hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int per_tensor,
+                              int8_t* Wq, double* scales, int* work, hipStream_t st) {
+  // An empty channel keeps the (inf, -inf) start values, which the fix-ups
+  // turn into (-1, 1) -> 1/127; the scale kernels below produce that too.
+  const int64_t nch = per_tensor ? 1 : (axis == 0 ? rows : cols);
+  if (nch == 0) return hipSuccess;
+  if (per_tensor) {
+    hipLaunchKernelGGL(k_set_minmax_init, dim3(1), dim3(1), 0, st, work);
+    hipLaunchKernelGGL(k_wminmax_tensor, dim3(grid_for(rows * cols, NT * 8, 2048)), dim3(NT), 0, st,
+                       W, rows * cols, work);
+    hipLaunchKernelGGL(k_wscale_tensor, dim3(1), dim3(1), 0, st, work, scales);
+  } else if (axis == 0) {
+    hipLaunchKernelGGL(k_wscale_rows, dim3((unsigned)(rows < 1048576 ? rows : 1048576)), dim3(NT),
+                       0, st, W, rows, cols, scales);
+  } else {
+    hipLaunchKernelGGL(k_wscale_cols, dim3((unsigned)((cols + 63) / 64)), dim3(NT), 0, st,
+                       W, rows, cols, scales);
+  }
+  if (rows == 0 || cols == 0) return hipGetLastError();
+  if (axis == 0) {
+    hipLaunchKernelGGL(k_wquant_rows, dim3(grid_for(rows * cols, NT, 65536)), dim3(NT), 0, st,
+                       W, rows, cols, scales, per_tensor, Wq);
+  } else {
+    dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+    hipLaunchKernelGGL(k_wquant_cols_t, grid, dim3(NT), 0, st, W, rows, cols, scales, per_tensor, Wq);
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ SiLU(g)*u + per-token quantize
+template <int VPT>
+__global__ __launch_bounds__(NT) void k_silu_mul_quant_rows(const float* __restrict__ g,
+                                                            const float* __restrict__ u,
+                                                            int64_t M, int64_t K,
+                                                            float* __restrict__ h,
+                                                            int8_t* __restrict__ q,
+                                                            double* __restrict__ scales) {
+  __shared__ int red[NT / 64];
+  const int tid = threadIdx.x;
+  const int64_t K4 = K >> 2;
+  for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
+    const float4* gr = reinterpret_cast<const float4*>(g + row * K);
+    const float4* ur = reinterpret_cast<const float4*>(u + row * K);
+    float4 v[VPT];
+    int key = -1;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int64_t i = tid + (int64_t)j * NT;
+      if (i < K4) {
+        float4 a = gr[i], b = ur[i];
+        v[j] = make_float4((float)((double)silu_js(a.x) * (double)b.x),
+                           (float)((double)silu_js(a.y) * (double)b.y),
+                           (float)((double)silu_js(a.z) * (double)b.z),
+                           (float)((double)silu_js(a.w) * (double)b.w));
+        if (h) reinterpret_cast<float4*>(h + row * K)[i] = v[j];
+        int k = key4(v[j]);
+        key = key > k ? key : k;
+      }
+    }
+    key = block_max_i32(key, red);
+    const double s = K == 0 ? 6.0 / 127.0 : scale_from_key(key);
+    if (tid == 0) scales[row] = s;
+    const bool fast = fast_scale_ok(s);
+    const float r32 = (float)(1.0 / s);
+    int* qr = reinterpret_cast<int*>(q + row * K);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int64_t i = tid + (int64_t)j * NT;
+      if (i < K4) qr[i] = quant4_sym(v[j], fast, r32, s);
+    }
+  }
+}
+
+// Fallback for K % 4 != 0, misaligned pointers or rows above 12 Ki elements:
+// h is formed twice (scan, then quantize) from g and u.
+__global__ __launch_bounds__(NT) void k_silu_mul_quant_rows_scalar(
+    const float* __restrict__ g, const float* __restrict__ u, int64_t M, int64_t K,
+    float* __restrict__ h, int8_t* __restrict__ q, double* __restrict__ scales) {
+  __shared__ int red[NT / 64];
+  for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
+    int key = -1;
+    for (int64_t i = threadIdx.x; i < K; i += NT) {
+      float v = (float)((double)silu_js(g[row * K + i]) * (double)u[row * K + i]);
+      if (h) h[row * K + i] = v;
+      int k = absmax_key(v);
+      key = key > k ? key : k;
+    }
+    key = block_max_i32(key, red);
+    const double s = K == 0 ? 6.0 / 127.0 : scale_from_key(key);
+    if (threadIdx.x == 0) scales[row] = s;
+    const bool fast = fast_scale_ok(s);
+    const float r32 = (float)(1.0 / s);
+    for (int64_t i = threadIdx.x; i < K; i += NT) {
+      float v = (float)((double)silu_js(g[row * K + i]) * (double)u[row * K + i]);
+      q[row * K + i] = (int8_t)(fast ? quant_sym_fast(v, r32, s) : quant_exact(v, s, 0.0, -128, 127));
+    }
+  }
+}
+
+hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M, int64_t K,
+                                      float* h, int8_t* q, double* scales, hipStream_t st) {
+  if (M == 0) return hipSuccess;
+  const int grid = (int)(M < 1048576 ? M : 1048576);
+  const bool vec = (K % 4 == 0) && (K / 4 <= 12 * NT) &&
+                   ((reinterpret_cast<uintptr_t>(g) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(u) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(h) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
+  if (!vec) {
+    hipLaunchKernelGGL(k_silu_mul_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    return hipGetLastError();
+  }
+  const int64_t K4 = K / 4;
+  if (K4 <= 4 * NT)
+    hipLaunchKernelGGL(k_silu_mul_quant_rows<4>, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+  else if (K4 <= 8 * NT)
+    hipLaunchKernelGGL(k_silu_mul_quant_rows<8>, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+  else
+    hipLaunchKernelGGL(k_silu_mul_quant_rows<12>, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+  return hipGetLastError();
+}
+
+}  // namespace q8

@@ -1,0 +1,228 @@
+"""Device ops of the int8 path, on torch tensors, computed by libq8hip.so.
+
+PyTorch only provides device memory and the stream: every op below is one
+call through the C ABI (include/q8hip.h) on torch's current stream.  Each
+op mirrors a reference operator (src/compiler/ir/graph/ops/quantization.ts)
+and reproduces the reference CPU backend's arithmetic bit for bit.
+
+Tensors must be contiguous and live on the current HIP device; the ops
+check dtype, shape and device before calling, and the C ABI validates again.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib as L
+
+
+def _stream() -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t) -> C.c_void_p:
+    return C.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _need(t: torch.Tensor, dtype: torch.dtype, name: str, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: tensor must be on a HIP device (got {t.device})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name}: expected {ndim}-D, got shape {tuple(t.shape)}")
+
+
+def _rows(x: torch.Tensor):
+    """[..., K] viewed as [M, K] with M the product of the leading dims."""
+    if x.dim() == 0:
+        return 1, 1
+    M = 1
+    for d in x.shape[:-1]:
+        M *= d
+    return M, x.shape[-1]
+
+
+# ---------------------------------------------------------------- inputs
+def fill_normal(t: torch.Tensor, seed: int, offset: int = 0, mean: float = 0.0,
+                std: float = 1.0) -> int:
+    """normal_ (src/nn/init.ts:40-52) on the device; returns draws consumed."""
+    _need(t, torch.float32, "fill_normal")
+    L.call("q8_fill_normal", _ptr(t), t.numel(), seed & 0xFFFFFFFF, offset, mean, std, _stream())
+    return 2 * ((t.numel() + 1) // 2)
+
+
+def fill_uniform(t: torch.Tensor, seed: int, offset: int = 0, a: float = 0.0,
+                 b: float = 1.0) -> int:
+    """uniform_ (src/nn/init.ts:31-37) on the device; returns draws consumed."""
+    _need(t, torch.float32, "fill_uniform")
+    L.call("q8_fill_uniform", _ptr(t), t.numel(), seed & 0xFFFFFFFF, offset, a, b, _stream())
+    return t.numel()
+
+
+# ---------------------------------------------------------------- quantize
+def quantize(x: torch.Tensor, scale: float, zero_point: float = 0.0,
+             target_dtype: str = "i8") -> torch.Tensor:
+    """The `quantize` op with its static attrs (ops/quantization.ts:12-59,
+    lowering quant_math.ts:16-27).  target_dtype 'i8' or 'ui8'."""
+    _need(x, torch.float32, "quantize")
+    if target_dtype not in ("i8", "ui8"):
+        raise ValueError(f"quantize target_dtype must be i8 or ui8, got {target_dtype}")
+    q = torch.empty(x.shape, dtype=torch.int8 if target_dtype == "i8" else torch.uint8,
+                    device=x.device)
+    L.call("q8_quantize_static", _ptr(x), x.numel(), float(scale), float(zero_point),
+           L.Q8_I8 if target_dtype == "i8" else L.Q8_U8, _ptr(q), _stream())
+    return q
+
+
+def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
+                       scales: torch.Tensor | None = None):
+    """Dynamic symmetric int8 quantize with one f64 scale per row of the last
+    dimension (calibration scale of each row, calibration.ts:24-34 +
+    quantization_types.ts:248-254).  Returns (int8 codes, f64 scales[M])."""
+    _need(x, torch.float32, "quantize_per_token")
+    M, K = _rows(x)
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
+    scales = torch.empty(M, dtype=torch.float64, device=x.device) if scales is None else scales
+    L.call("q8_quantize_rows", _ptr(x), M, K, L.Q8_PER_TOKEN, _ptr(q), _ptr(scales), _stream())
+    return q, scales
+
+
+def quantize_per_tensor(x: torch.Tensor, q: torch.Tensor | None = None,
+                        scales: torch.Tensor | None = None):
+    """Dynamic symmetric int8 quantize with one scale for the whole tensor.
+    Returns (int8 codes, f64 scale tensor of one element)."""
+    _need(x, torch.float32, "quantize_per_tensor")
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
+    scales = torch.empty(1, dtype=torch.float64, device=x.device) if scales is None else scales
+    L.call("q8_quantize_rows", _ptr(x), 1, x.numel(), L.Q8_PER_TENSOR, _ptr(q), _ptr(scales),
+           _stream())
+    return q, scales
+
+
+# ---------------------------------------------------------------- dequantize
+_SRC = {torch.int8: L.Q8_I8, torch.uint8: L.Q8_U8, torch.int32: L.Q8_I32}
+
+
+def dequantize(q: torch.Tensor, scale, zero_point: float = 0.0,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """The `dequantize` op (quant_math.ts:29-34).  `scale` is a python float
+    (the op's static attr), a 1-element f64 tensor (per tensor) or an f64
+    tensor with one scale per row (per token)."""
+    if q.dtype not in _SRC:
+        raise TypeError(f"dequantize: input must be int8, uint8 or int32, got {q.dtype}")
+    _need(q, q.dtype, "dequantize")
+    M, K = _rows(q)
+    if isinstance(scale, torch.Tensor):
+        _need(scale, torch.float64, "dequantize scale")
+        gran = L.Q8_PER_TENSOR if scale.numel() == 1 else L.Q8_PER_TOKEN
+        if gran == L.Q8_PER_TOKEN and scale.numel() != M:
+            raise ValueError(f"dequantize: {scale.numel()} scales for {M} rows")
+        s = scale
+    else:
+        gran = L.Q8_PER_TENSOR
+        s = torch.tensor([float(scale)], dtype=torch.float64, device=q.device)
+    y = torch.empty(q.shape, dtype=torch.float32, device=q.device) if out is None else out
+    L.call("q8_dequantize", _ptr(q), _SRC[q.dtype], M, K, _ptr(s), gran, float(zero_point),
+           _ptr(y), _stream())
+    return y
+
+
+# ---------------------------------------------------------------- weights
+def pack_weight(W: torch.Tensor, axis: int = 0, granularity: str = "per_channel"):
+    """Quantize an fp32 weight on the device the way QuantizationPass does on
+    the host (quantization_pass.ts:390-400; quantization_types.ts:299-317,
+    :118-130).  axis 0: W is [N,K] (nn.Linear); axis 1: W is [K,N].
+    Returns (int8 [N,K], f64 scales[N] or [1])."""
+    _need(W, torch.float32, "pack_weight", ndim=2)
+    rows, cols = W.shape
+    N, K = (rows, cols) if axis == 0 else (cols, rows)
+    if granularity not in ("per_channel", "per_tensor"):
+        raise ValueError(f"pack_weight: unknown granularity {granularity}")
+    per_tensor = granularity == "per_tensor"
+    Wq = torch.empty((N, K), dtype=torch.int8, device=W.device)
+    scales = torch.empty(1 if per_tensor else N, dtype=torch.float64, device=W.device)
+    L.call("q8_pack_weight", _ptr(W), rows, cols, axis,
+           L.Q8_PER_TENSOR if per_tensor else L.Q8_PER_CHANNEL, _ptr(Wq), _ptr(scales), _stream())
+    return Wq, scales
+
+
+# ---------------------------------------------------------------- matmul
+_ACT = {None: L.Q8_ACT_NONE, "none": L.Q8_ACT_NONE, "relu": L.Q8_ACT_RELU, "silu": L.Q8_ACT_SILU}
+
+
+def _mk(A, B):
+    _need(A, torch.int8, "A", ndim=2)
+    _need(B, torch.int8, "B", ndim=2)
+    M, K = A.shape
+    N, K2 = B.shape
+    if K != K2:
+        raise ValueError(f"contraction mismatch: A is {tuple(A.shape)}, B is {tuple(B.shape)} ([N,K])")
+    return M, N, K
+
+
+def quantized_dot(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """quantized_dot (ops/quantization.ts:103-155) with lhs_contracting=[1],
+    rhs_contracting=[1]: int32 acc[m,n] = sum_k A[m,k] * B[n,k]."""
+    M, N, K = _mk(A, B)
+    out = torch.empty((M, N), dtype=torch.int32, device=A.device) if out is None else out
+    L.call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT, 0.0,
+           None, L.Q8_ACT_NONE, L.Q8_I32, _ptr(out), _stream())
+    return out
+
+
+def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor,
+            bias: torch.Tensor | None = None, act: str | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """int8 linear with the per-channel epilogue fused:
+    y = act(fround(fround(acc * fround(sA[m] * sB[n])) + bias[n])).
+    sA: f64 [M] (per token) or [1] (per tensor); sB: f64 [N] or [1]."""
+    M, N, K = _mk(A, B)
+    _need(sA, torch.float64, "sA")
+    _need(sB, torch.float64, "sB")
+    if sA.numel() not in (1, M) or sB.numel() not in (1, N):
+        raise ValueError("qlinear: scale sizes must be 1 or M (sA) and 1 or N (sB)")
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.numel() != N:
+            raise ValueError("qlinear: bias must have N elements")
+    out = torch.empty((M, N), dtype=torch.float32, device=A.device) if out is None else out
+    L.call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0,
+           _ptr(sA), L.Q8_PER_TOKEN if sA.numel() == M and M != 1 else L.Q8_PER_TENSOR,
+           _ptr(sB), L.Q8_PER_CHANNEL if sB.numel() == N and N != 1 else L.Q8_PER_TENSOR,
+           L.Q8_EPI_ROWCOL, 0.0, _ptr(bias), _ACT[act], L.Q8_F32, _ptr(out), _stream())
+    return out
+
+
+def qlinear_pt(A: torch.Tensor, B: torch.Tensor, s_out: float,
+               bias: torch.Tensor | None = None, act: str | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-tensor form (quantization_pass.ts:335-355): y = fround(acc * s_out),
+    s_out = lhs_scale * rhs_scale in f64."""
+    M, N, K = _mk(A, B)
+    out = torch.empty((M, N), dtype=torch.float32, device=A.device) if out is None else out
+    L.call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT,
+           float(s_out), _ptr(bias), _ACT[act], L.Q8_F32, _ptr(out), _stream())
+    return out
+
+
+def silu_mul_quantize(g: torch.Tensor, u: torch.Tensor, h_out: torch.Tensor | None = None):
+    """h = fround(silu(g) * u), then per-token int8 quantize of h.
+    Returns (int8 codes, f64 scales[M])."""
+    _need(g, torch.float32, "g")
+    _need(u, torch.float32, "u")
+    if g.shape != u.shape:
+        raise ValueError("silu_mul_quantize: g and u shapes differ")
+    M, K = _rows(g)
+    q = torch.empty(g.shape, dtype=torch.int8, device=g.device)
+    scales = torch.empty(M, dtype=torch.float64, device=g.device)
+    if h_out is not None:
+        _need(h_out, torch.float32, "h_out")
+    L.call("q8_silu_mul_quantize_rows", _ptr(g), _ptr(u), M, K, _ptr(h_out), _ptr(q),
+           _ptr(scales), _stream())
+    return q, scales

@@ -1,0 +1,330 @@
+"""GPU parity of every primitive of the int8 path against the CPU oracle.
+
+All comparisons are bit-exact (int8 codes, int32 accumulators, f64 scales and
+fp32 outputs compared as bit patterns), except the Box-Muller fill, whose
+log/cos/sin come from different libms (see test_fill_normal_matches_oracle).
+Inputs come from the oracle's seeded generator and are uploaded, so both
+sides see identical bits.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from mlfw_amd import ops as O
+    from mlfw_amd import _lib
+    _lib.call("q8_init", 0)
+    return O
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    av = a.view(np.uint8).reshape(-1, a.itemsize)
+    bv = b.view(np.uint8).reshape(-1, b.itemsize)
+    bad = np.nonzero(np.any(av != bv, axis=1))[0]
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(f"{bad.size} of {a.size} differ; first at flat {i}: "
+                             f"{a.reshape(-1)[i]!r} vs {b.reshape(-1)[i]!r}")
+
+
+def edge_rows(oracle, K=4096):
+    """Rows that exercise the rounding and the scale corner cases."""
+    rng = oracle.Rng(123)
+    rows = []
+    base = rng.normal((K,))
+    rows.append(base)                                   # plain
+    r = base.copy(); r[7] = 50.0; rows.append(r)        # outlier
+    rows.append(np.zeros(K, np.float32))                # all zero -> scale 1e-10
+    r = np.full(K, np.nan, np.float32); rows.append(r)  # all NaN -> scale inf
+    r = base.copy(); r[::97] = np.nan; rows.append(r)   # some NaN
+    r = base.copy(); r[3] = np.inf; rows.append(r)      # +inf -> scale inf
+    r = base.copy(); r[5] = -np.inf; r[6] = np.inf; rows.append(r)
+    r = base.copy(); r[:10] = -0.0; rows.append(r)      # negative zeros
+    r = (base * 1e-30).astype(np.float32); rows.append(r)   # subnormal-ish range
+    r = (base * 1e30).astype(np.float32); rows.append(r)
+    # exact ties: x / s = k + 0.5 for s = 1 (absmax 127)
+    t = np.arange(-127, 128, 1, dtype=np.float32) * 0.5
+    r = np.resize(t, K).astype(np.float32); r[0] = 127.0; rows.append(r)
+    # values one ulp around ties for s = 127/127 = 1
+    t = np.float32(2.5)
+    r = np.resize(np.array([np.nextafter(t, np.float32(3)), t, np.nextafter(t, np.float32(2)),
+                            -t, np.nextafter(-t, np.float32(0))], np.float32), K)
+    r[0] = 127.0
+    rows.append(r.astype(np.float32))
+    return np.stack(rows).astype(np.float32)
+
+
+# ------------------------------------------------------------------ quantize
+@pytest.mark.parametrize("shape", [(1, 1), (3, 5), (7, 4096), (33, 1000), (16, 11008),
+                                   (2, 12289), (5, 0)])
+def test_quantize_per_token_random(ops, oracle, shape):
+    x = oracle.Rng(1).normal(shape)
+    if x.size:
+        x.reshape(-1)[:: max(1, x.size // 17)] *= 40.0
+    q, s = ops.quantize_per_token(dev(x))
+    s_ref = oracle.scales_per_token(x)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(x, s_ref))
+
+
+def test_quantize_per_token_edges(ops, oracle):
+    x = edge_rows(oracle)
+    q, s = ops.quantize_per_token(dev(x))
+    s_ref = oracle.scales_per_token(x)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(x, s_ref))
+
+
+def test_quantize_per_token_unaligned(ops, oracle):
+    # K % 4 != 0 and a misaligned view take the scalar kernel
+    x = oracle.Rng(5).normal((9, 1023))
+    q, s = ops.quantize_per_token(dev(x))
+    s_ref = oracle.scales_per_token(x)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(x, s_ref))
+
+
+@pytest.mark.parametrize("n", [0, 1, 4095, 1 << 20])
+def test_quantize_per_tensor(ops, oracle, n):
+    x = oracle.Rng(2).normal((n,))
+    if n > 10:
+        x[7] = -33.0
+        x[9] = np.nan
+    q, s = ops.quantize_per_tensor(dev(x))
+    s_ref = oracle.scale_per_tensor(x)
+    same_bits(host(s), np.array([s_ref]))
+    same_bits(host(q), oracle.quantize(x, s_ref))
+
+
+@pytest.mark.parametrize("scale,zp,tgt", [(6 / 127, 0.0, "i8"), (0.0123, 0.0, "i8"),
+                                          (6 / 255, -128.0, "i8"), (1 / 255, 0.0, "ui8"),
+                                          (6 / 255, 3.0, "ui8"), (1e-10, 0.0, "i8"),
+                                          (1e30, 0.0, "i8"), (1.0, 0.0, "i8")])
+def test_quantize_static(ops, oracle, scale, zp, tgt):
+    x = oracle.Rng(3).normal((4099,), 0.0, 3.0)
+    x[:6] = [3.5, -2.1, 5.9, 1.234, -5.9, 0.001]       # pass.test.js:451 data
+    x[6:12] = [np.nan, np.inf, -np.inf, -0.0, 0.5, -0.5]
+    q = ops.quantize(dev(x), scale, zp, tgt)
+    same_bits(host(q), oracle.quantize(x, scale, zp, tgt == "ui8"))
+
+
+def test_quantize_static_rejects_nonpositive_scale(ops):
+    from mlfw_amd._lib import Q8Error
+    with pytest.raises(Q8Error):
+        ops.quantize(torch.zeros(4, device=DEV), 0.0)
+    with pytest.raises(Q8Error):
+        ops.quantize(torch.zeros(4, device=DEV), -1.0)
+
+
+# ------------------------------------------------------------------ dequantize
+def test_dequantize_rows_i8(ops, oracle):
+    x = edge_rows(oracle, 1024)
+    s = oracle.scales_per_token(x)
+    q = oracle.quantize_rows(x, s)
+    y = ops.dequantize(dev(q), dev(s))
+    same_bits(host(y), oracle.dequantize_rows(q, s))
+
+
+@pytest.mark.parametrize("dt,zp", [(np.int8, 0.0), (np.int8, 5.0), (np.uint8, 128.0),
+                                   (np.int32, 0.0), (np.int32, -7.0)])
+def test_dequantize_per_tensor(ops, oracle, dt, zp):
+    rng = np.random.default_rng(0)
+    if dt == np.int32:
+        q = rng.integers(-2 ** 31, 2 ** 31, size=(37, 64), dtype=np.int64).astype(np.int32)
+    else:
+        info = np.iinfo(dt)
+        q = rng.integers(info.min, info.max + 1, size=(37, 64)).astype(dt)
+    for s in (6 / 127, 0.0012345678901234, 3.0e-7 * 7.77):
+        y = ops.dequantize(dev(q), s, zp)
+        same_bits(host(y), oracle.dequantize(q, s, zp))
+
+
+def test_dequantize_scalar_path(ops, oracle):
+    q = np.random.default_rng(1).integers(-128, 128, size=(5, 13)).astype(np.int8)
+    s = oracle.Rng(9).uniform((5,), 0.001, 0.1).astype(np.float64)
+    y = ops.dequantize(dev(q), dev(s))
+    same_bits(host(y), oracle.dequantize_rows(q, s))
+
+
+# ------------------------------------------------------------------ weights
+@pytest.mark.parametrize("shape,axis", [((64, 128), 0), ((128, 64), 1), ((4096, 4096), 1),
+                                        ((10, 128), 0), ((97, 130), 1), ((3, 0), 0)])
+def test_pack_weight_per_channel(ops, oracle, shape, axis):
+    W = oracle.Rng(7).normal(shape, 0.0, 0.02)
+    if W.size > 20:
+        W.reshape(-1)[5] = np.nan
+        W.reshape(-1)[11] = 0.3
+    if shape == (10, 128):
+        W[2, :] = 0.25                         # constant channel: +-0.5 expansion
+        W[3, :] = 0.0
+        W[4, 7] = np.inf
+    Wq, s = ops.pack_weight(dev(W), axis=axis)
+    s_ref = oracle.scales_per_channel(W, axis)
+    q_ref = oracle.weight_quantize_per_channel(W, axis, s_ref)
+    same_bits(host(s), s_ref)
+    same_bits(host(Wq), q_ref if axis == 0 else q_ref.T.copy())
+
+
+def test_pack_weight_per_tensor(ops, oracle):
+    W = oracle.Rng(8).normal((96, 200), 0.0, 1.0)
+    Wq, s = ops.pack_weight(dev(W), axis=0, granularity="per_tensor")
+    s_ref = oracle.scale_const_array(W)
+    same_bits(host(s), np.array([s_ref]))
+    same_bits(host(Wq), oracle.weight_quantize_per_tensor(W, s_ref, -127, 127))
+
+
+# ------------------------------------------------------------------ matmul
+def rand_i8(rng, shape):
+    return rng.integers(-128, 128, size=shape).astype(np.int8)
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 64, 128), (17, 33, 48), (256, 256, 784),
+                                   (64, 10, 128), (300, 260, 1040), (128, 128, 4096),
+                                   (20, 30, 7)])
+def test_quantized_dot_small(ops, oracle, M, N, K):
+    rng = np.random.default_rng(M * 7 + N)
+    A, B = rand_i8(rng, (M, K)), rand_i8(rng, (N, K))
+    acc = ops.quantized_dot(dev(A), dev(B))
+    same_bits(host(acc), oracle.quantized_dot(A, B, b_layout=1))
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 4096), (2048, 4096, 4096), (768, 1280, 11008),
+                                   (4096, 4096, 4096), (4001, 3100, 2048)])
+def test_quantized_dot_large_exact(ops, M, N, K):
+    """Large shapes: integer products and sums are exact in f64 (|acc| < 2^53),
+    so an f64 matmul of the same int8 values is an exact closed-form check."""
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    A = torch.randint(-128, 128, (M, K), dtype=torch.int8, device=DEV, generator=g)
+    B = torch.randint(-128, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    acc = ops.quantized_dot(A, B)
+    ref = (A.double() @ B.double().t().contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(acc.double(), ref)
+
+
+def test_quantized_dot_wraps_like_int32(ops, oracle):
+    # |acc| up to K * 128 * 128 = 2^31 at K = 2^17: the JS accumulator is exact
+    # and the Int32Array store wraps; the GPU's int32 accumulation wraps the same.
+    K = 1 << 17
+    A = np.full((2, K), -128, np.int8)
+    B = np.full((2, K), -128, np.int8)
+    B[1, :] = 127
+    acc = ops.quantized_dot(dev(A), dev(B))
+    same_bits(host(acc), oracle.quantized_dot(A, B, b_layout=1))
+
+
+@pytest.mark.parametrize("act", [None, "relu", "silu"])
+@pytest.mark.parametrize("M,N,K", [(64, 96, 256), (300, 130, 512), (4, 200, 4096)])
+def test_qlinear_rowcol_epilogue(ops, oracle, M, N, K, act):
+    rng = oracle.Rng(M + N)
+    x = rng.normal((M, K))
+    W = rng.normal((N, K), 0.0, 0.02)
+    bias = rng.uniform((N,), -0.1, 0.1)
+    sx = oracle.scales_per_token(x)
+    xq = oracle.quantize_rows(x, sx)
+    sw = oracle.scales_per_channel(W, 0)
+    Wq = oracle.weight_quantize_per_channel(W, 0, sw)
+    y = ops.qlinear(dev(xq), dev(sx), dev(Wq), dev(sw), bias=dev(bias), act=act)
+    acc = oracle.quantized_dot(xq, Wq, b_layout=1)
+    ref = oracle.epilogue(acc, "rowcol", sx, sw, bias=bias, act=act or "none")
+    same_bits(host(y), ref)
+
+
+def test_qlinear_pertensor_scales(ops, oracle):
+    rng = oracle.Rng(44)
+    x = rng.normal((40, 128))
+    W = rng.normal((64, 128), 0.0, 0.02)
+    sx = np.array([oracle.scale_per_tensor(x)])
+    xq = oracle.quantize(x, sx[0])
+    sw = oracle.scales_per_channel(W, 0)
+    Wq = oracle.weight_quantize_per_channel(W, 0, sw)
+    y = ops.qlinear(dev(xq), dev(sx), dev(Wq), dev(sw))
+    acc = oracle.quantized_dot(xq, Wq, b_layout=1)
+    same_bits(host(y), oracle.epilogue(acc, "rowcol", sx[0], sw))
+
+
+def test_qlinear_pt_epilogue(ops, oracle):
+    rng = np.random.default_rng(3)
+    A, B = rand_i8(rng, (48, 256)), rand_i8(rng, (72, 256))
+    s_out = (5 / 127) * (6 / 127)
+    y = ops.qlinear_pt(dev(A), dev(B), s_out)
+    acc = oracle.quantized_dot(A, B, b_layout=1)
+    same_bits(host(y), oracle.epilogue(acc, "pt", s_out=s_out))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1000, 4096), (77, 8192 + 512)])
+def test_gemv(ops, oracle, M, N, K):
+    rng = oracle.Rng(M * 31 + N)
+    x = rng.normal((M, K))
+    W = rng.normal((N, K), 0.0, 0.02)
+    sx = oracle.scales_per_token(x)
+    xq = oracle.quantize_rows(x, sx)
+    sw = oracle.scales_per_channel(W, 0)
+    Wq = oracle.weight_quantize_per_channel(W, 0, sw)
+    y = ops.qlinear(dev(xq), dev(sx), dev(Wq), dev(sw))
+    acc = oracle.quantized_dot(xq, Wq, b_layout=1)
+    same_bits(host(y), oracle.epilogue(acc, "rowcol", sx, sw))
+    acc_gpu = ops.quantized_dot(dev(xq), dev(Wq))
+    same_bits(host(acc_gpu), acc)
+
+
+# ------------------------------------------------------------------ fused / inputs
+@pytest.mark.parametrize("M,K", [(4, 11008), (3, 1000), (2, 64)])
+def test_silu_mul_quantize(ops, oracle, M, K):
+    rng = oracle.Rng(K)
+    g = rng.normal((M, K), 0.0, 3.0)
+    u = rng.normal((M, K))
+    g.reshape(-1)[:4] = [0.0, -0.0, 88.0, -104.0]
+    h_out = torch.empty((M, K), dtype=torch.float32, device=DEV)
+    q, s = ops.silu_mul_quantize(dev(g), dev(u), h_out)
+    h = oracle.silu_mul(g, u)
+    same_bits(host(h_out), h)
+    s_ref = oracle.scales_per_token(h)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(h, s_ref))
+
+
+def test_fill_uniform_matches_oracle(ops, oracle):
+    r = oracle.Rng(11)
+    ref = r.uniform((10001,), -0.1, 0.1)
+    t = torch.empty(10001, dtype=torch.float32, device=DEV)
+    ops.fill_uniform(t, 11, 0, -0.1, 0.1)
+    same_bits(host(t), ref)
+
+
+def test_fill_normal_matches_oracle(ops, oracle):
+    """mulberry32 draws are integer-exact; Box-Muller uses log/cos/sin, which
+    the device libm and glibc may round differently in the last f64 bit.
+    After the f32 rounding nearly every value is identical; the rest differ
+    by one f32 ulp."""
+    r = oracle.Rng(5)
+    _ = r.normal((1001,))                 # consume 1002 draws: offset test
+    ref = r.normal((200001,), 0.0, 0.02)
+    t = torch.empty(200001, dtype=torch.float32, device=DEV)
+    ops.fill_normal(t, 5, 1002, 0.0, 0.02)
+    got = host(t)
+    diff = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert diff.max() <= 1
+    assert (diff != 0).mean() < 1e-3
