@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark of the int8 quantized-inference path on one MI355X.
+
+Headline (value): config C3, the 4096^3 int8 qmatmul.  One step = dynamic
+per-token quantize of A [4096,4096] fp32 + the int8 GEMM with the fused
+per-row x per-column dequant epilogue (fp32 out); B is a prepacked int8
+weight.  value = 2*4096^3 int ops / step time, in TOPS.
+
+roofline: the GEMM kernel alone, timed with HIP events recorded on the
+stream it runs on, inside the timed region; peak = MI355X dense int8 MFMA
+(5.0 POP/s).  secondary: the HBM-bound kernels of C5 (per-token quantize and
+dequantize of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}) and the
+C4 projection set, each timed the same way, with input buffers rotated
+through > 1 GiB so the 256 MB Infinity Cache cannot serve them.
+cpu_baseline: the reference's generated single-thread CPU kernels, mirrored
+in JavaScript (oracle/q8ref.js), timed on Node on one host core over a row
+slice of the same GEMM.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import shutil
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "int8 qmatmul TOPS @4096³ (% MFMA peak); quant/dequant GB/s (% HBM peak)"
+PEAK_INT8_TOPS = 5000.0        # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+GEMM_OPS = 2 * 4096 ** 3
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def ev():
+    import torch
+    return torch.cuda.Event(enable_timing=True)
+
+
+def kernel_avg_ms(fn, n, pairs=None):
+    """Average duration of fn(i) over n launches, each bracketed by events."""
+    import torch
+    starts = [ev() for _ in range(n)]
+    ends = [ev() for _ in range(n)]
+    for i in range(n):
+        starts[i].record()
+        fn(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    t = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return sum(t) / n, t[len(t) // 2]
+
+
+def load_traffic():
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
+# ---------------------------------------------------------------- headline
+def bench_c3(steps, warmup):
+    import torch
+    from mlfw_amd import configs as C
+    from mlfw_amd import ops as O
+
+    inp = C.c3_inputs("cuda")
+    Bq, sB = C.c3_prepare(inp["B"])
+    A = inp["A"]
+    out = torch.empty((4096, 4096), dtype=torch.float32, device="cuda")
+    Aq = torch.empty((4096, 4096), dtype=torch.int8, device="cuda")
+    sA = torch.empty(4096, dtype=torch.float64, device="cuda")
+    for _ in range(warmup):
+        C.c3_step(A, Bq, sB, out=out, bufs=(Aq, sA))
+    torch.cuda.synchronize()
+
+    e_q = [ev() for _ in range(steps)]
+    e_g = [ev() for _ in range(steps)]
+    e_e = [ev() for _ in range(steps)]
+    t_begin, t_end = ev(), ev()
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_begin.record()
+    for i in range(steps):
+        e_q[i].record()
+        O.quantize_per_token(A, Aq, sA)
+        e_g[i].record()
+        O.qlinear(Aq, sA, Bq, sB, out=out)
+        e_e[i].record()
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    step_ms = t_begin.elapsed_time(t_end) / steps
+    gemm_ms = sorted(a.elapsed_time(b) for a, b in zip(e_g, e_e))
+    quant_ms = sorted(a.elapsed_time(b) for a, b in zip(e_q, e_g))
+    gemm_avg = sum(gemm_ms) / steps
+    return {
+        "step_ms": step_ms,
+        "wall_ms_per_step": 1e3 * wall / steps,
+        "gemm_avg_ms": gemm_avg,
+        "gemm_median_ms": gemm_ms[steps // 2],
+        "quant_avg_ms": sum(quant_ms) / steps,
+    }
+
+
+# ---------------------------------------------------------------- secondary
+def rotation_copies(nbytes, total=1 << 30):
+    return max(2, math.ceil(total / max(1, nbytes)))
+
+
+def bench_c5_quant(reps=20):
+    import torch
+    from mlfw_amd import configs as C
+    from mlfw_amd import ops as O
+    X0 = C.c5_inputs("cuda")["X"]
+    M, K = X0.shape
+    n_in = 4                                   # 4 x 256 MiB inputs
+    Xs = [X0] + [X0.clone() for _ in range(n_in - 1)]
+    qs = [torch.empty((M, K), dtype=torch.int8, device="cuda") for _ in range(n_in)]
+    ss = [torch.empty(M, dtype=torch.float64, device="cuda") for _ in range(n_in)]
+    ys = [torch.empty((M, K), dtype=torch.float32, device="cuda") for _ in range(2)]
+    for i in range(n_in):
+        O.quantize_per_token(Xs[i], qs[i], ss[i])
+    torch.cuda.synchronize()
+    nbytes = M * K * 4 + M * K + M * 8
+    qa, qm = kernel_avg_ms(lambda i: O.quantize_per_token(Xs[i % n_in], qs[i % n_in], ss[i % n_in]), reps)
+    da, dm = kernel_avg_ms(lambda i: O.dequantize(qs[i % n_in], ss[i % n_in], out=ys[i % 2]), reps)
+    del Xs
+    res = {}
+    for name, avg, med in (("quantize_per_token_16384x4096", qa, qm),
+                           ("dequantize_per_token_16384x4096", da, dm)):
+        gbs = nbytes / (avg * 1e-3) / 1e9
+        res[name] = {"avg_us": 1e3 * avg, "median_us": 1e3 * med, "bytes": nbytes,
+                     "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
+    return res
+
+
+def bench_c5_gemv(reps=30):
+    import torch
+    from mlfw_amd import configs as C
+    from mlfw_amd import ops as O
+    inp = C.c5_inputs("cuda", with_quant_tensor=False)
+    K = 4096
+    res = {}
+    for N, W in inp["W"].items():
+        Wq0, sW = O.pack_weight(W, axis=0)
+        R = rotation_copies(N * K)
+        Wqs = [Wq0] + [Wq0.clone() for _ in range(R - 1)]
+        for M, x in inp["x"].items():
+            xq, sx = O.quantize_per_token(x)
+            out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            O.qlinear(xq, sx, Wqs[0], sW, out=out)
+            torch.cuda.synchronize()
+            ga, gm = kernel_avg_ms(lambda i: O.qlinear(xq, sx, Wqs[i % R], sW, out=out), reps)
+            qa, _ = kernel_avg_ms(lambda i: O.quantize_per_token(x, xq, sx), 10)
+            kb = N * K + 8 * N + M * K + 8 * M + 4 * M * N      # kernel's own traffic
+            sb = N * K + 8 * N + 4 * M * K + 4 * M * N          # step bytes (fp32 x in)
+            res[f"gemv_M{M}_N{N}"] = {
+                "gemv_avg_us": 1e3 * ga, "gemv_median_us": 1e3 * gm,
+                "gemv_GB/s": kb / (ga * 1e-3) / 1e9,
+                "gemv_frac_hbm": kb / (ga * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                "quantize_x_avg_us": 1e3 * qa,
+                "step_GB/s": sb / ((ga + qa) * 1e-3) / 1e9,
+            }
+        del Wqs
+    return res
+
+
+def bench_c4(reps=3):
+    import torch
+    from mlfw_amd import configs as C
+    inp = C.c4_inputs("cuda")
+    P = C.c4_prepare(inp["W"])
+    del inp["W"]
+    X = inp["X"]
+    C.c4_step(X, P)
+    torch.cuda.synchronize()
+    a, m = kernel_avg_ms(lambda i: C.c4_step(X, P), reps)
+    return {"c4_projection_set": {"avg_ms": a, "ops": C.C4_OPS,
+                                  "TOPS": C.C4_OPS / (a * 1e-3) / 1e12,
+                                  "frac_mfma": C.C4_OPS / (a * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(rows=64):
+    """Reference CPU path (mirrored generated JS, one core) on `rows` rows of
+    the 4096^3 GEMM: quantized_dot triple loop + fused per-channel epilogue."""
+    node = shutil.which("node")
+    js = os.path.join(ROOT, "oracle", "q8ref.js")
+    if node and os.path.exists(js):
+        p = {"kind": "qdot", "M": rows, "N": 4096, "K": 4096, "reps": 3, "seed": 2}
+        r = subprocess.run([node, js, "bench", json.dumps(p)], capture_output=True, text=True,
+                           timeout=600, check=True)
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+        tops = res["ops"] / res["seconds"] / 1e12
+        return {"value": tops, "unit": "TOPS", "cores": 1, "kind": "port",
+                "sample": (f"{rows} of 4096 rows of the 4096^3 qmatmul (quantized_dot + "
+                           f"per-channel epilogue), median of 3 after 1 warm-up, JS kernels "
+                           f"mirroring mlfw's CPU codegen on Node {res.get('node')}"),
+                "seconds_per_sample": res["seconds"]}
+    from oracle import q8ref
+    import numpy as np
+    rng = np.random.default_rng(2)
+    A = rng.integers(-127, 128, (rows, 4096)).astype(np.int8)
+    B = rng.integers(-127, 128, (4096, 4096)).astype(np.int8)
+    t0 = time.perf_counter()
+    acc = q8ref.quantized_dot(A, B, b_layout=1)
+    q8ref.epilogue(acc, "rowcol", 1e-3, np.full(4096, 1e-3))
+    dt = time.perf_counter() - t0
+    return {"value": 2 * rows * 4096 * 4096 / dt / 1e12, "unit": "TOPS", "cores": 1,
+            "kind": "port", "sample": f"{rows} rows of the 4096^3 qmatmul, C restatement -O2",
+            "seconds_per_sample": dt}
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the int8 path has no multi-GPU code, see DESIGN.md for how it would shard",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    from mlfw_amd import _lib
+    _lib.call("q8_init", 0)
+
+    log(f"[bench] C3 4096^3: warmup {args.warmup}, steps {args.steps}")
+    r = bench_c3(args.steps, args.warmup)
+    tops = GEMM_OPS / (r["step_ms"] * 1e-3) / 1e12
+    gemm_tops = GEMM_OPS / (r["gemm_avg_ms"] * 1e-3) / 1e12
+    log(f"[bench] step {r['step_ms']:.4f} ms -> {tops:.1f} TOPS; gemm {r['gemm_avg_ms'] * 1e3:.1f} us "
+        f"-> {gemm_tops:.1f} TOPS")
+
+    traffic = load_traffic().get("gemm_4096", {})
+    tb = traffic.get("hbm_bytes_per_launch")
+    roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                "frac": gemm_tops / PEAK_INT8_TOPS, "traffic": tb,
+                "kernel": "k_gemm_i8<256,256,2,2>", "avg_us": r["gemm_avg_ms"] * 1e3,
+                "algorithmic_ops_per_launch": GEMM_OPS}
+
+    secondary = {}
+    if not args.no_secondary:
+        for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", bench_c4)):
+            log(f"[bench] secondary {name}")
+            try:
+                secondary.update(fn())
+            except Exception as exc:          # reported, never hidden
+                secondary[name] = {"error": repr(exc)}
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (JS mirror of the reference CPU kernels, 1 core)")
+        try:
+            cpu = cpu_baseline()
+        except Exception as exc:
+            cpu = {"error": repr(exc)}
+
+    line = {
+        "metric": METRIC,
+        "value": tops,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["step_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded mulberry32 + Box-Muller on the device, config seed 2)",
+        "config": {"workload": "C3: int8 qmatmul M=N=K=4096, A fp32 N(0,1) per-token dynamic "
+                               "int8, B N(0,0.02) per-column int8 (prepacked), int32 acc, "
+                               "fp32 out = fround(acc*fround(sA[m]*sB[n]))",
+                   "M": 4096, "N": 4096, "K": 4096, "step": "quantize_per_token(A) + gemm",
+                   "quantize_avg_us": r["quant_avg_ms"] * 1e3,
+                   "wall_ms_per_step": r["wall_ms_per_step"]},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -109,6 +109,13 @@ int q8_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
 int q8_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset,
                     double a, double b, void* stream);
 
+/* Outlier injection of the C5 quantize workload: with a second mulberry32
+ * stream (seed, counter form as above, draw i for element i), every element
+ * whose draw u satisfies u < p is replaced by fround(x * factor).  The
+ * reference has no such generator; it defines the synthetic input only. */
+int q8_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor,
+                      void* stream);
+
 /* ---------------------------------------------------------------- quantize */
 
 /* The compiled `quantize` op with a static scale: the CUDA kernel CUDACodegen

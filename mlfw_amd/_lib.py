@@ -57,6 +57,7 @@ SIGNATURES = {
     "q8_stream_sync": [_vp],
     "q8_fill_normal": [_vp, _i64, C.c_uint32, C.c_uint64, _dbl, _dbl, _vp],
     "q8_fill_uniform": [_vp, _i64, C.c_uint32, C.c_uint64, _dbl, _dbl, _vp],
+    "q8_apply_outliers": [_vp, _i64, C.c_uint32, _dbl, _dbl, _vp],
     "q8_quantize_static": [_vp, _i64, _dbl, _dbl, _int, _vp, _vp],
     "q8_quantize_rows": [_vp, _i64, _i64, _int, _vp, _vp, _vp],
     "q8_dequantize": [_vp, _int, _i64, _i64, _vp, _int, _dbl, _vp, _vp],

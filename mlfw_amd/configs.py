@@ -1,0 +1,164 @@
+"""The five synthetic workloads of the int8 path, built and run on the device.
+
+Inputs follow the reference's seeded generators (mulberry32 +
+Box-Muller / uniform, src/util/random.ts:5-14, src/nn/init.ts:31-52): each
+config seeds one stream and draws its tensors from it in the order listed,
+so the i-th tensor starts at the draw count the previous ones consumed.
+The device generator is the counter form of the same stream.
+
+C1 qlinear 32x128 -> 64 (seed 0): X N(0,1) [32,128], W N(0,0.02) [64,128],
+   bias U(-0.1,0.1) [64].  X per-tensor dynamic (= calibration on X),
+   W per-output-channel; y = fround(fround(acc*fround(sX*sW[n])) + b[n]).
+C2 MLP 784 -> 256 -> 128 -> 10, batch 256 (seed 1): x U(0,1) [256,784],
+   W_l N(0, 1/sqrt(fan_in)) [out,in], per-output-channel; each layer's input
+   is quantized per tensor (dynamic); ReLU after layers 1 and 2; fp32 logits.
+C3 4096^3 (seed 2): A N(0,1) [M,K] per-token; B N(0,0.02) [K,N] per-column;
+   y = fround(acc * fround(sA[m] * sB[n])).
+C4 decoder projections, 2048 tokens, hidden 4096 (seed 3): X [2048,4096];
+   Wqkv [12288,4096], Wo [4096,4096], Wg, Wu [11008,4096], Wd [4096,11008],
+   all N(0,0.02) per-output-channel.  Chain (per-token int8 between
+   projections, bias 0): qkv = X Wqkv^T; o = V Wo^T with V = qkv[:, 8192:];
+   g = o Wg^T, u = o Wu^T; h = fround(silu(g) * u); d = h Wd^T.
+C5 decode shapes (seed 4): GEMV weights W_N N(0,0.02) [N,4096] for
+   N = 4096, 11008, then activations x_M N(0,1) [M,4096] for M = 1, 4, 16;
+   and the quantize/dequantize tensor X N(0,1) [16384,4096] with 1 % of the
+   elements (second stream seeded 4 ^ 0x9e3779b9, draw < 0.01) scaled by 50.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import ops
+
+SEEDS = {"C1": 0, "C2": 1, "C3": 2, "C4": 3, "C5": 4}
+C5_OUTLIER_SEED = (4 ^ 0x9E3779B9) & 0xFFFFFFFF
+C4_SHAPES = {"qkv": (12288, 4096), "o": (4096, 4096), "gate": (11008, 4096),
+             "up": (11008, 4096), "down": (4096, 11008)}
+C5_GEMV_N = (4096, 11008)
+C5_GEMV_M = (1, 4, 16)
+C5_QUANT_SHAPE = (16384, 4096)
+
+
+class DeviceStream:
+    """A seeded mulberry32 stream consumed in order, filling device tensors."""
+
+    def __init__(self, seed: int, device="cuda"):
+        self.seed = seed
+        self.offset = 0
+        self.device = device
+
+    def normal(self, shape, mean=0.0, std=1.0) -> torch.Tensor:
+        t = torch.empty(shape, dtype=torch.float32, device=self.device)
+        self.offset += ops.fill_normal(t, self.seed, self.offset, mean, std)
+        return t
+
+    def uniform(self, shape, a=0.0, b=1.0) -> torch.Tensor:
+        t = torch.empty(shape, dtype=torch.float32, device=self.device)
+        self.offset += ops.fill_uniform(t, self.seed, self.offset, a, b)
+        return t
+
+
+# ------------------------------------------------------------------ C1
+def c1_inputs(device="cuda"):
+    s = DeviceStream(SEEDS["C1"], device)
+    return {"X": s.normal((32, 128)), "W": s.normal((64, 128), 0.0, 0.02),
+            "bias": s.uniform((64,), -0.1, 0.1)}
+
+
+def c1_run(X, W, bias):
+    Wq, sW = ops.pack_weight(W, axis=0)
+    Xq, sX = ops.quantize_per_tensor(X)
+    return ops.qlinear(Xq, sX, Wq, sW, bias=bias)
+
+
+# ------------------------------------------------------------------ C2
+C2_DIMS = (784, 256, 128, 10)
+
+
+def c2_inputs(device="cuda"):
+    s = DeviceStream(SEEDS["C2"], device)
+    x = s.uniform((256, 784), 0.0, 1.0)
+    Ws = [s.normal((C2_DIMS[i + 1], C2_DIMS[i]), 0.0, 1.0 / math.sqrt(C2_DIMS[i]))
+          for i in range(3)]
+    return {"x": x, "W": Ws}
+
+
+def c2_prepare(Ws):
+    return [ops.pack_weight(W, axis=0) for W in Ws]
+
+
+def c2_run(x, packed):
+    h = x
+    for i, (Wq, sW) in enumerate(packed):
+        hq, sh = ops.quantize_per_tensor(h)
+        h = ops.qlinear(hq, sh, Wq, sW, act="relu" if i < 2 else None)
+    return h
+
+
+# ------------------------------------------------------------------ C3
+def c3_inputs(device="cuda", M=4096, N=4096, K=4096):
+    s = DeviceStream(SEEDS["C3"], device)
+    return {"A": s.normal((M, K)), "B": s.normal((K, N), 0.0, 0.02)}
+
+
+def c3_prepare(B):
+    return ops.pack_weight(B, axis=1)          # [K,N] per column -> [N,K]
+
+
+def c3_step(A, Bq, sB, out=None, bufs=None):
+    Aq, sA = ops.quantize_per_token(A, *(bufs or (None, None)))
+    return ops.qlinear(Aq, sA, Bq, sB, out=out)
+
+
+# ------------------------------------------------------------------ C4
+def c4_inputs(device="cuda", tokens=2048):
+    s = DeviceStream(SEEDS["C4"], device)
+    X = s.normal((tokens, 4096))
+    W = {k: s.normal(shape, 0.0, 0.02) for k, shape in C4_SHAPES.items()}
+    return {"X": X, "W": W}
+
+
+def c4_prepare(W):
+    return {k: ops.pack_weight(w, axis=0) for k, w in W.items()}
+
+
+def c4_step(X, P):
+    xq, sx = ops.quantize_per_token(X)
+    qkv = ops.qlinear(xq, sx, *P["qkv"])
+    v = qkv[:, 8192:].contiguous()
+    vq, sv = ops.quantize_per_token(v)
+    o = ops.qlinear(vq, sv, *P["o"])
+    oq, so = ops.quantize_per_token(o)
+    g = ops.qlinear(oq, so, *P["gate"])
+    u = ops.qlinear(oq, so, *P["up"])
+    hq, sh = ops.silu_mul_quantize(g, u)
+    d = ops.qlinear(hq, sh, *P["down"])
+    return {"qkv": qkv, "o": o, "gate": g, "up": u, "down": d}
+
+
+C4_OPS = sum(2 * 2048 * n * k for n, k in C4_SHAPES.values())
+
+
+# ------------------------------------------------------------------ C5
+def c5_inputs(device="cuda", with_quant_tensor=True):
+    s = DeviceStream(SEEDS["C5"], device)
+    W = {n: s.normal((n, 4096), 0.0, 0.02) for n in C5_GEMV_N}
+    x = {m: s.normal((m, 4096)) for m in C5_GEMV_M}
+    out = {"W": W, "x": x}
+    if with_quant_tensor:
+        X = s.normal(C5_QUANT_SHAPE)
+        ops.apply_outliers(X, C5_OUTLIER_SEED, 0.01, 50.0)
+        out["X"] = X
+    return out
+
+
+def c5_gemv(x, Wq, sW, out=None):
+    xq, sx = ops.quantize_per_token(x)
+    return ops.qlinear(xq, sx, Wq, sW, out=out)
+
+
+def c5_quant_dequant(X):
+    q, s = ops.quantize_per_token(X)
+    return q, s, ops.dequantize(q, s)

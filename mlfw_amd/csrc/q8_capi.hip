@@ -182,6 +182,15 @@ int q8_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset, doubl
                   "q8_fill_uniform launch");
 }
 
+int q8_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor, void* stream) {
+  Q8_REQUIRE(n >= 0, "q8_apply_outliers: n < 0");
+  Q8_REQUIRE(n == 0 || x, "q8_apply_outliers: x is NULL");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_apply_outliers(x, n, seed, p, factor, as_stream(stream)),
+                  "q8_apply_outliers launch");
+}
+
 int q8_quantize_static(const float* x, int64_t n, double scale, double zero_point, int target,
                        void* q, void* stream) {
   Q8_REQUIRE(n >= 0, "q8_quantize_static: n < 0");

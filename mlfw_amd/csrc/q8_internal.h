@@ -25,6 +25,8 @@ hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t off
                               double mean, double std, hipStream_t st);
 hipError_t launch_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset,
                                double a, double b, hipStream_t st);
+hipError_t launch_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor,
+                                 hipStream_t st);
 hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, int is_u8,
                                void* q, hipStream_t st);
 hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, double* scales,

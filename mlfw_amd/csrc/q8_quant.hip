@@ -75,6 +75,20 @@ hipError_t launch_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t of
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(NT) void k_apply_outliers(float* __restrict__ x, int64_t n,
+                                                       uint32_t seed, double p, double factor) {
+  for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT)
+    if (mb32(seed, (uint64_t)i) < p) x[i] = (float)((double)x[i] * factor);
+}
+
+hipError_t launch_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor,
+                                 hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_apply_outliers, dim3(grid_for(n, NT, 65536)), dim3(NT), 0, st,
+                     x, n, seed, p, factor);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ int pack4(int b0, int b1, int b2, int b3) {
   return (b0 & 0xff) | ((b1 & 0xff) << 8) | ((b2 & 0xff) << 16) | ((b3 & 0xff) << 24);

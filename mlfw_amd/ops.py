@@ -65,6 +65,12 @@ def fill_uniform(t: torch.Tensor, seed: int, offset: int = 0, a: float = 0.0,
     return t.numel()
 
 
+def apply_outliers(t: torch.Tensor, seed: int, p: float = 0.01, factor: float = 50.0) -> None:
+    """Scale the elements a second mulberry32 stream marks (draw < p) by factor."""
+    _need(t, torch.float32, "apply_outliers")
+    L.call("q8_apply_outliers", _ptr(t), t.numel(), seed & 0xFFFFFFFF, p, factor, _stream())
+
+
 # ---------------------------------------------------------------- quantize
 def quantize(x: torch.Tensor, scale: float, zero_point: float = 0.0,
              target_dtype: str = "i8") -> torch.Tensor:

@@ -1,0 +1,106 @@
+"""CPU oracle of the five workloads (TEST INFRASTRUCTURE ONLY).
+
+Each function draws the config's inputs from the oracle's mulberry32
+stream in the documented order (mlfw_amd/configs.py describes the
+workloads) and computes the expected outputs with the C restatement.  The
+large GEMMs take a `rows` subset: every row's quantization scale and output
+depend on that row alone (per-token activations, per-channel weights), so
+the expected value of a row subset is exact for those rows.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import q8ref as o
+
+C4_SHAPES = {"qkv": (12288, 4096), "o": (4096, 4096), "gate": (11008, 4096),
+             "up": (11008, 4096), "down": (4096, 11008)}
+C5_OUTLIER_SEED = (4 ^ 0x9E3779B9) & 0xFFFFFFFF
+
+
+def pack_pc(W, axis=0):
+    """Per-channel weight path of QuantizationPass -> ([N,K] int8, scales)."""
+    s = o.scales_per_channel(W, axis)
+    q = o.weight_quantize_per_channel(W, axis, s)
+    return (q if axis == 0 else np.ascontiguousarray(q.T)), s
+
+
+def qlinear_rows(x, Wq, sW, bias=None, act="none", per_tensor=False):
+    """Dynamic activation quantize + quantized_dot + per-channel epilogue."""
+    if per_tensor:
+        s = o.scale_per_tensor(x)
+        xq = o.quantize(x, s)
+        sx = s
+    else:
+        sx = o.scales_per_token(x)
+        xq = o.quantize_rows(x, sx)
+    acc = o.quantized_dot(xq, Wq, b_layout=1)
+    return o.epilogue(acc, "rowcol", sx, sW, bias=bias, act=act)
+
+
+def c1():
+    r = o.Rng(0)
+    X = r.normal((32, 128))
+    W = r.normal((64, 128), 0.0, 0.02)
+    b = r.uniform((64,), -0.1, 0.1)
+    Wq, sW = pack_pc(W, 0)
+    y = qlinear_rows(X, Wq, sW, bias=b, per_tensor=True)
+    return {"X": X, "W": W, "bias": b}, y
+
+
+C2_DIMS = (784, 256, 128, 10)
+
+
+def c2():
+    r = o.Rng(1)
+    x = r.uniform((256, 784), 0.0, 1.0)
+    Ws = [r.normal((C2_DIMS[i + 1], C2_DIMS[i]), 0.0, 1.0 / math.sqrt(C2_DIMS[i])) for i in range(3)]
+    h = x
+    for i, W in enumerate(Ws):
+        Wq, sW = pack_pc(W, 0)
+        h = qlinear_rows(h, Wq, sW, act="relu" if i < 2 else "none", per_tensor=True)
+    return {"x": x, "W": Ws}, h
+
+
+def c3_inputs(M=4096, N=4096, K=4096):
+    r = o.Rng(2)
+    return {"A": r.normal((M, K)), "B": r.normal((K, N), 0.0, 0.02)}
+
+
+def c3_expected_rows(inp, rows):
+    Bq, sB = pack_pc(inp["B"], 1)
+    return qlinear_rows(np.ascontiguousarray(inp["A"][rows]), Bq, sB)
+
+
+def c4_inputs(tokens=2048):
+    r = o.Rng(3)
+    X = r.normal((tokens, 4096))
+    W = {k: r.normal(shape, 0.0, 0.02) for k, shape in C4_SHAPES.items()}
+    return {"X": X, "W": W}
+
+
+def c4_expected_rows(inp, rows, packed=None):
+    P = packed or {k: pack_pc(w, 0) for k, w in inp["W"].items()}
+    X = np.ascontiguousarray(inp["X"][rows])
+    qkv = qlinear_rows(X, *P["qkv"])
+    v = np.ascontiguousarray(qkv[:, 8192:])
+    ob = qlinear_rows(v, *P["o"])
+    g = qlinear_rows(ob, *P["gate"])
+    u = qlinear_rows(ob, *P["up"])
+    h = o.silu_mul(g, u)
+    d = qlinear_rows(h, *P["down"])
+    return {"qkv": qkv, "o": ob, "gate": g, "up": u, "down": d}
+
+
+def c5_inputs(with_quant_tensor=True):
+    r = o.Rng(4)
+    W = {n: r.normal((n, 4096), 0.0, 0.02) for n in (4096, 11008)}
+    x = {m: r.normal((m, 4096)) for m in (1, 4, 16)}
+    out = {"W": W, "x": x}
+    if with_quant_tensor:
+        X = r.normal((16384, 4096))
+        o.apply_outliers(X, C5_OUTLIER_SEED, 0.01, 50.0)
+        out["X"] = X
+    return out

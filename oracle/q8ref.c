@@ -73,6 +73,13 @@ void q8r_fill_uniform(q8r_rng* r, float* out, int64_t n, double a, double b) {
   for (int64_t i = 0; i < n; i++) out[i] = (float)(a + q8r_rng_next(r) * range);
 }
 
+void q8r_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor) {
+  q8r_rng r;
+  q8r_rng_seed(&r, seed);
+  for (int64_t i = 0; i < n; i++)
+    if (q8r_rng_next(&r) < p) x[i] = (float)((double)x[i] * factor);
+}
+
 /* ------------------------------------------------------------------ */
 /* scales                                                              */
 /* ------------------------------------------------------------------ */

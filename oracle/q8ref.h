@@ -32,6 +32,10 @@ double   q8r_rng_next(q8r_rng* r);
 void     q8r_fill_normal(q8r_rng* r, float* out, int64_t n, double mean, double std);
 void     q8r_fill_uniform(q8r_rng* r, float* out, int64_t n, double a, double b);
 
+/* C5 outliers: a second stream seeded `seed`; element i uses draw i and
+ * becomes fround(x * factor) when that draw is below p. */
+void     q8r_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor);
+
 /* ---- scale derivation: src/compiler/ir/graph/quantization_types.ts ---- */
 /* fromRange(min,max,PER_TENSOR_SYMMETRIC) :248-254; numBits = 8 -> bound 127 */
 double   q8r_scale_sym_from_range(double mn, double mx, int num_bits);

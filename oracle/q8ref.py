@@ -54,6 +54,7 @@ def lib():
         "q8r_rng_next": (_dbl, [C.POINTER(_Rng)]),
         "q8r_fill_normal": (None, [C.POINTER(_Rng), _f32p, _i64, _dbl, _dbl]),
         "q8r_fill_uniform": (None, [C.POINTER(_Rng), _f32p, _i64, _dbl, _dbl]),
+        "q8r_apply_outliers": (None, [_f32p, _i64, C.c_uint32, _dbl, _dbl]),
         "q8r_scale_sym_from_range": (_dbl, [_dbl, _dbl, _int]),
         "q8r_params_asym_from_range": (None, [_dbl, _dbl, _int, _int, C.POINTER(_dbl), C.POINTER(_dbl)]),
         "q8r_observe_minmax": (None, [_f32p, _i64, C.POINTER(_dbl), C.POINTER(_dbl)]),
@@ -108,6 +109,10 @@ class Rng:
     def state(self) -> int:
         return int(self._s.a)
 
+    def skip(self, n: int) -> None:
+        """Advance by n draws (the state moves by n * 0x6D2B79F5)."""
+        self._s.a = (self._s.a + n * 0x6D2B79F5) & 0xFFFFFFFF
+
     def next(self) -> float:
         return lib().q8r_rng_next(C.byref(self._s))
 
@@ -122,6 +127,12 @@ class Rng:
         out = np.empty(shape, np.float32)
         lib().q8r_fill_uniform(C.byref(self._s), out.reshape(-1), out.size, a, b)
         return out
+
+
+def apply_outliers(x: np.ndarray, seed: int, p: float = 0.01, factor: float = 50.0) -> None:
+    """In place: C5 outlier protocol (second mulberry32 stream)."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().q8r_apply_outliers(x.reshape(-1), x.size, seed & 0xFFFFFFFF, p, factor)
 
 
 # ---------------------------------------------------------------- scales
