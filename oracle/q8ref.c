@@ -263,6 +263,12 @@ void q8r_weight_quantize_per_tensor(const float* w, int64_t n, double s, int lo,
   for (int64_t i = 0; i < n; i++) q[i] = (int8_t)q8r_weight_quantize_value(w[i], s, 0.0, lo, hi);
 }
 
+void q8r_weight_quantize_per_group(const float* w, int64_t n, int64_t group,
+                                   const double* scales, int lo, int hi, int8_t* q) {
+  for (int64_t i = 0; i < n; i++)
+    q[i] = (int8_t)q8r_weight_quantize_value(w[i], scales[i / group], 0.0, lo, hi);
+}
+
 /* ------------------------------------------------------------------ */
 /* D1: compiled dequantize                                             */
 /* ------------------------------------------------------------------ */

@@ -87,6 +87,10 @@ void     q8r_weight_quantize_per_channel(const float* w, int64_t rows, int64_t c
                                          const double* scales, int8_t* q);
 void     q8r_weight_quantize_per_tensor(const float* w, int64_t n, double s, int lo, int hi,
                                         int8_t* q);
+/* quantizeArrayPerGroup (:143-153): element i uses the scale of group
+ * floor(i / group); zero points are 0 (fromConstantArrayPerGroup). */
+void     q8r_weight_quantize_per_group(const float* w, int64_t n, int64_t group,
+                                       const double* scales, int lo, int hi, int8_t* q);
 
 /* ---- D1: compiled `dequantize`, quant_math.ts:29-34 ----
  * y = fround(q * s); zp != 0: y = fround(fround(q - zp) * s). */

@@ -72,6 +72,7 @@ def lib():
         "q8r_clamp_range": (None, [_int, _int, _int, C.POINTER(_int), C.POINTER(_int)]),
         "q8r_weight_quantize_per_channel": (None, [_f32p, _i64, _i64, _int, _f64p, _i8p]),
         "q8r_weight_quantize_per_tensor": (None, [_f32p, _i64, _dbl, _int, _int, _i8p]),
+        "q8r_weight_quantize_per_group": (None, [_f32p, _i64, _i64, _f64p, _int, _int, _i8p]),
         "q8r_dequantize_value": (C.c_float, [_dbl, _dbl, _dbl]),
         "q8r_dequantize_i8": (None, [_i8p, _i64, _dbl, _dbl, _f32p]),
         "q8r_dequantize_u8": (None, [_u8p, _i64, _dbl, _dbl, _f32p]),
@@ -237,6 +238,14 @@ def weight_quantize_per_tensor(w, scale, lo=-127, hi=127) -> np.ndarray:
     w = _c(w, np.float32)
     q = np.empty(w.shape, np.int8)
     lib().q8r_weight_quantize_per_tensor(w.reshape(-1), w.size, scale, lo, hi, q.reshape(-1))
+    return q
+
+
+def weight_quantize_per_group(w, group, scales, lo=-7, hi=7) -> np.ndarray:
+    """quantizeArrayPerGroup (quantization_types.ts:143-153)."""
+    w = _c(w, np.float32).reshape(-1)
+    q = np.empty(w.size, np.int8)
+    lib().q8r_weight_quantize_per_group(w, w.size, group, _c(scales, np.float64), lo, hi, q)
     return q
 
 

@@ -1,0 +1,109 @@
+"""CPU checks of the C ABI (include/q8hip.h <-> mlfw_amd/libq8hip.so).
+
+No kernel is launched here: the library is loaded, every entry point the
+header declares must be exported, and calls that fail host-side validation
+must return Q8_ERR_INVALID with a message before anything reaches a device.
+"""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "q8hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(q8_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mlfw_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libq8hip.so is not built: run `python -m mlfw_amd.build`")
+    return _lib
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("q8_init", "q8_last_error", "q8_quantize_rows", "q8_quantize_static",
+                 "q8_dequantize", "q8_pack_weight", "q8_gemm", "q8_gemv"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared_functions()
+    raw = C.CDLL(lib.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), f"{n} declared in q8hip.h but not exported"
+    assert sorted(lib.exported_symbols()) == names, "ctypes binding and header disagree"
+
+
+def test_version_and_clean_error(lib):
+    L = lib.load()
+    assert L.q8_version() == 1
+    assert L.q8_last_error() in (b"",)
+
+
+def test_device_count_does_not_fail_without_gpu(lib):
+    n = C.c_int(-1)
+    assert lib.load().q8_device_count(C.byref(n)) == lib.Q8_OK
+    assert n.value >= 0
+
+
+def expect_invalid(lib, name, *args, match=""):
+    rc = getattr(lib.load(), name)(*args)
+    assert rc == lib.Q8_ERR_INVALID, (name, rc)
+    msg = lib.load().q8_last_error().decode()
+    assert name in msg or match in msg, msg
+
+
+def test_validation_happens_before_any_launch(lib):
+    vp, nil = C.c_void_p, None
+    fake = vp(0x1000)
+    expect_invalid(lib, "q8_quantize_static", fake, 10, 0.0, 0.0, lib.Q8_I8, fake, nil)
+    expect_invalid(lib, "q8_quantize_static", fake, 10, -1.0, 0.0, lib.Q8_I8, fake, nil)
+    expect_invalid(lib, "q8_quantize_static", fake, 10, 0.1, 0.0, lib.Q8_I32, fake, nil)
+    expect_invalid(lib, "q8_quantize_static", fake, -1, 0.1, 0.0, lib.Q8_I8, fake, nil)
+    expect_invalid(lib, "q8_quantize_rows", fake, 4, 8, 7, fake, fake, nil)
+    expect_invalid(lib, "q8_quantize_rows", fake, -4, 8, lib.Q8_PER_TOKEN, fake, fake, nil)
+    expect_invalid(lib, "q8_quantize_rows", nil, 4, 8, lib.Q8_PER_TOKEN, fake, fake, nil)
+    expect_invalid(lib, "q8_dequantize", fake, lib.Q8_F32, 4, 8, fake, lib.Q8_PER_TENSOR, 0.0,
+                   fake, nil)
+    expect_invalid(lib, "q8_dequantize", fake, lib.Q8_I8, 4, 8, fake, 9, 0.0, fake, nil)
+    expect_invalid(lib, "q8_pack_weight", fake, 4, 8, 2, lib.Q8_PER_CHANNEL, fake, fake, nil)
+    expect_invalid(lib, "q8_pack_weight", fake, 4, 8, 0, lib.Q8_PER_TOKEN, fake, fake, nil)
+    g = lib.load().q8_gemm
+    # bad out_kind, act, epi, mismatched scale modes, null operands
+    assert g(fake, fake, 4, 4, 16, 0, 0, fake, 0, fake, 0, 0, 1.0, nil, 0, 7, fake, nil) == 1
+    assert g(fake, fake, 4, 4, 16, 0, 0, fake, 0, fake, 0, 0, 1.0, nil, 5, lib.Q8_F32, fake, nil) == 1
+    assert g(fake, fake, 4, 4, 16, 0, 0, fake, 0, fake, 0, 9, 1.0, nil, 0, lib.Q8_F32, fake, nil) == 1
+    assert g(nil, fake, 4, 4, 16, 0, 0, fake, 0, fake, 0, 1, 0.0, nil, 0, lib.Q8_F32, fake, nil) == 1
+    assert g(fake, fake, 4, 4, 16, 0, 0, nil, 1, fake, 2, 1, 0.0, nil, 0, lib.Q8_F32, fake, nil) == 1
+    assert g(fake, fake, 4, 4, 16, 0, 0, fake, 2, fake, 2, 1, 0.0, nil, 0, lib.Q8_F32, fake, nil) == 1
+    # int32 output takes no bias / activation
+    assert g(fake, fake, 4, 4, 16, 0, 0, nil, 0, nil, 0, 0, 0.0, fake, 0, lib.Q8_I32, fake, nil) == 1
+    assert g(fake, fake, -1, 4, 16, 0, 0, nil, 0, nil, 0, 0, 0.0, nil, 0, lib.Q8_I32, fake, nil) == 1
+    # q8_gemv only takes M <= 16
+    gv = lib.load().q8_gemv
+    assert gv(fake, fake, 17, 4, 16, fake, 0, fake, 0, 1, 0.0, nil, 0, lib.Q8_F32, fake, nil) == 1
+
+
+def test_nonzero_zero_points_are_unsupported_not_wrong(lib):
+    fake = C.c_void_p(0x1000)
+    rc = lib.load().q8_gemm(fake, fake, 4, 4, 16, 3, 0, None, 0, None, 0, 0, 0.0, None, 0,
+                            lib.Q8_I32, fake, None)
+    assert rc == lib.Q8_ERR_UNSUPPORTED
+
+
+def test_python_ops_refuse_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    from mlfw_amd import ops
+    with pytest.raises(ValueError):
+        ops.quantize_per_token(torch.zeros(2, 4))
+    with pytest.raises(TypeError):
+        ops.quantize_per_token(torch.zeros(2, 4, dtype=torch.float64))
