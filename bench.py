@@ -4,17 +4,29 @@
 Headline (value): config C3, the 4096^3 int8 qmatmul.  One step = dynamic
 per-token quantize of A [4096,4096] fp32 + the int8 GEMM with the fused
 per-row x per-column dequant epilogue (fp32 out); B is a prepacked int8
-weight.  value = 2*4096^3 int ops / step time, in TOPS.
+weight.  value = 2*4096^3 int ops / step time, in TOPS (10^12 int ops/s).
 
-roofline: the GEMM kernel alone, timed with HIP events recorded on the
-stream it runs on, inside the timed region; peak = MI355X dense int8 MFMA
-(5.0 POP/s).  secondary: the HBM-bound kernels of C5 (per-token quantize and
-dequantize of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}) and the
-C4 projection set, each timed the same way, with input buffers rotated
-through > 1 GiB so the 256 MB Infinity Cache cannot serve them.
+The step's two launches are prepared once (mlfw_amd.ops.prepare: arguments
+validated and converted up front), so the host enqueues faster than the
+GPU executes and the HIP events recorded between the launches, on the
+stream they run on, time the kernels themselves.
+
+roofline: the GEMM kernel, average of those per-launch event intervals
+inside the timed region; peak = MI355X dense int8 MFMA, 5.0 POP/s.
+`traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
+WRITE_SIZE runs (profiles/traffic.json, scaled by a copy-kernel
+calibration), or null when that file is absent.
+
+secondary: the HBM-bound kernels of C5 (per-token quantize and dequantize
+of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}) and the C4
+projection set.  Each is captured R times in a HIP graph (rotating input
+buffers so the 256 MB Infinity Cache cannot serve repeats) and the graph
+is replayed between two events: per-launch host overhead would otherwise
+dominate kernels of a few microseconds.
+
 cpu_baseline: the reference's generated single-thread CPU kernels, mirrored
-in JavaScript (oracle/q8ref.js), timed on Node on one host core over a row
-slice of the same GEMM.
+in JavaScript (oracle/q8ref.js), timed under Node on one host core over a
+row slice of the same GEMM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -36,6 +48,7 @@ METRIC = "int8 qmatmul TOPS @4096³ (% MFMA peak); quant/dequant GB/s (% HBM pea
 PEAK_INT8_TOPS = 5000.0        # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 GEMM_OPS = 2 * 4096 ** 3
+GEMM_KERNEL = "k_qgemm<256, 256, 8>"   # tile 256x256, fp32 out, row x column scales
 
 
 def log(*a):
@@ -45,20 +58,6 @@ def log(*a):
 def ev():
     import torch
     return torch.cuda.Event(enable_timing=True)
-
-
-def kernel_avg_ms(fn, n, pairs=None):
-    """Average duration of fn(i) over n launches, each bracketed by events."""
-    import torch
-    starts = [ev() for _ in range(n)]
-    ends = [ev() for _ in range(n)]
-    for i in range(n):
-        starts[i].record()
-        fn(i)
-        ends[i].record()
-    torch.cuda.synchronize()
-    t = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return sum(t) / n, t[len(t) // 2]
 
 
 def load_traffic():
@@ -82,8 +81,11 @@ def bench_c3(steps, warmup):
     out = torch.empty((4096, 4096), dtype=torch.float32, device="cuda")
     Aq = torch.empty((4096, 4096), dtype=torch.int8, device="cuda")
     sA = torch.empty(4096, dtype=torch.float64, device="cuda")
+    quant = O.prepare(O.quantize_per_token, A, Aq, sA)
+    gemm = O.prepare(O.qlinear, Aq, sA, Bq, sB, out=out)
     for _ in range(warmup):
-        C.c3_step(A, Bq, sB, out=out, bufs=(Aq, sA))
+        quant()
+        gemm()
     torch.cuda.synchronize()
 
     e_q = [ev() for _ in range(steps)]
@@ -95,9 +97,9 @@ def bench_c3(steps, warmup):
     t_begin.record()
     for i in range(steps):
         e_q[i].record()
-        O.quantize_per_token(A, Aq, sA)
+        quant()
         e_g[i].record()
-        O.qlinear(Aq, sA, Bq, sB, out=out)
+        gemm()
         e_e[i].record()
     t_end.record()
     torch.cuda.synchronize()
@@ -105,49 +107,74 @@ def bench_c3(steps, warmup):
     step_ms = t_begin.elapsed_time(t_end) / steps
     gemm_ms = sorted(a.elapsed_time(b) for a, b in zip(e_g, e_e))
     quant_ms = sorted(a.elapsed_time(b) for a, b in zip(e_q, e_g))
-    gemm_avg = sum(gemm_ms) / steps
     return {
         "step_ms": step_ms,
         "wall_ms_per_step": 1e3 * wall / steps,
-        "gemm_avg_ms": gemm_avg,
+        "gemm_avg_ms": sum(gemm_ms) / steps,
         "gemm_median_ms": gemm_ms[steps // 2],
         "quant_avg_ms": sum(quant_ms) / steps,
     }
 
 
 # ---------------------------------------------------------------- secondary
-def rotation_copies(nbytes, total=1 << 30):
-    return max(2, math.ceil(total / max(1, nbytes)))
+def graph_time_us(body, copies, replays=5):
+    """Average microseconds per launch of body(i), i < copies, captured in one
+    HIP graph and replayed `replays` times between two events.  Falls back
+    to eager launches if capture is not possible."""
+    import torch
+    try:
+        for i in range(copies):        # warm up outside the capture
+            body(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(copies):
+                body(i)
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record()
+        for _ in range(replays):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return 1e3 * a.elapsed_time(b) / (replays * copies), "graph"
+    except Exception as exc:            # eager fallback, reported
+        log(f"[bench] graph capture failed ({exc!r}); timing eager launches")
+        a, b = ev(), ev()
+        a.record()
+        for _ in range(replays):
+            for i in range(copies):
+                body(i)
+        b.record()
+        torch.cuda.synchronize()
+        return 1e3 * a.elapsed_time(b) / (replays * copies), "eager"
 
 
-def bench_c5_quant(reps=20):
+def bench_c5_quant():
     import torch
     from mlfw_amd import configs as C
     from mlfw_amd import ops as O
     X0 = C.c5_inputs("cuda")["X"]
     M, K = X0.shape
-    n_in = 4                                   # 4 x 256 MiB inputs
+    n_in = 5                                   # 5 x 256 MiB fp32 inputs: > 4 x the MALL
     Xs = [X0] + [X0.clone() for _ in range(n_in - 1)]
     qs = [torch.empty((M, K), dtype=torch.int8, device="cuda") for _ in range(n_in)]
     ss = [torch.empty(M, dtype=torch.float64, device="cuda") for _ in range(n_in)]
-    ys = [torch.empty((M, K), dtype=torch.float32, device="cuda") for _ in range(2)]
-    for i in range(n_in):
-        O.quantize_per_token(Xs[i], qs[i], ss[i])
-    torch.cuda.synchronize()
+    ys = [torch.empty((M, K), dtype=torch.float32, device="cuda") for _ in range(n_in)]
     nbytes = M * K * 4 + M * K + M * 8
-    qa, qm = kernel_avg_ms(lambda i: O.quantize_per_token(Xs[i % n_in], qs[i % n_in], ss[i % n_in]), reps)
-    da, dm = kernel_avg_ms(lambda i: O.dequantize(qs[i % n_in], ss[i % n_in], out=ys[i % 2]), reps)
-    del Xs
+    q_us, q_how = graph_time_us(lambda i: O.quantize_per_token(Xs[i], qs[i], ss[i]), n_in)
+    d_us, d_how = graph_time_us(lambda i: O.dequantize(qs[i], ss[i], out=ys[i]), n_in)
     res = {}
-    for name, avg, med in (("quantize_per_token_16384x4096", qa, qm),
-                           ("dequantize_per_token_16384x4096", da, dm)):
-        gbs = nbytes / (avg * 1e-3) / 1e9
-        res[name] = {"avg_us": 1e3 * avg, "median_us": 1e3 * med, "bytes": nbytes,
-                     "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
+    for name, us, how in (("quantize_per_token_16384x4096", q_us, q_how),
+                          ("dequantize_per_token_16384x4096", d_us, d_how)):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"avg_us": us, "bytes": nbytes, "GB/s": gbs,
+                     "frac_hbm": gbs / PEAK_HBM_GBS, "timing": how}
     return res
 
 
-def bench_c5_gemv(reps=30):
+def bench_c5_gemv():
     import torch
     from mlfw_amd import configs as C
     from mlfw_amd import ops as O
@@ -156,45 +183,42 @@ def bench_c5_gemv(reps=30):
     res = {}
     for N, W in inp["W"].items():
         Wq0, sW = O.pack_weight(W, axis=0)
-        R = rotation_copies(N * K)
+        R = max(8, math.ceil((1 << 30) / (N * K)))          # > 1 GiB of distinct weights
         Wqs = [Wq0] + [Wq0.clone() for _ in range(R - 1)]
         for M, x in inp["x"].items():
             xq, sx = O.quantize_per_token(x)
-            out = torch.empty((M, N), dtype=torch.float32, device="cuda")
-            O.qlinear(xq, sx, Wqs[0], sW, out=out)
-            torch.cuda.synchronize()
-            ga, gm = kernel_avg_ms(lambda i: O.qlinear(xq, sx, Wqs[i % R], sW, out=out), reps)
-            qa, _ = kernel_avg_ms(lambda i: O.quantize_per_token(x, xq, sx), 10)
-            kb = N * K + 8 * N + M * K + 8 * M + 4 * M * N      # kernel's own traffic
+            outs = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(R)]
+            g_us, how = graph_time_us(lambda i: O.qlinear(xq, sx, Wqs[i], sW, out=outs[i]), R)
+            q_us, _ = graph_time_us(lambda i: O.quantize_per_token(x, xq, sx), 8)
+            kb = N * K + 8 * N + M * K + 8 * M + 4 * M * N      # the GEMV kernel's own bytes
             sb = N * K + 8 * N + 4 * M * K + 4 * M * N          # step bytes (fp32 x in)
             res[f"gemv_M{M}_N{N}"] = {
-                "gemv_avg_us": 1e3 * ga, "gemv_median_us": 1e3 * gm,
-                "gemv_GB/s": kb / (ga * 1e-3) / 1e9,
-                "gemv_frac_hbm": kb / (ga * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                "quantize_x_avg_us": 1e3 * qa,
-                "step_GB/s": sb / ((ga + qa) * 1e-3) / 1e9,
+                "gemv_avg_us": g_us, "gemv_GB/s": kb / (g_us * 1e-6) / 1e9,
+                "gemv_frac_hbm": kb / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+                "quantize_x_avg_us": q_us,
+                "step_GB/s": sb / ((g_us + q_us) * 1e-6) / 1e9, "timing": how,
             }
         del Wqs
     return res
 
 
-def bench_c4(reps=3):
+def bench_c4():
     import torch
     from mlfw_amd import configs as C
     inp = C.c4_inputs("cuda")
     P = C.c4_prepare(inp["W"])
     del inp["W"]
     X = inp["X"]
-    C.c4_step(X, P)
-    torch.cuda.synchronize()
-    a, m = kernel_avg_ms(lambda i: C.c4_step(X, P), reps)
-    return {"c4_projection_set": {"avg_ms": a, "ops": C.C4_OPS,
-                                  "TOPS": C.C4_OPS / (a * 1e-3) / 1e12,
-                                  "frac_mfma": C.C4_OPS / (a * 1e-3) / 1e12 / PEAK_INT8_TOPS}}
+    us, how = graph_time_us(lambda i: C.c4_step(X, P), 1, replays=5)
+    ms = us / 1e3
+    return {"c4_projection_set": {"avg_ms": ms, "ops": C.C4_OPS,
+                                  "TOPS": C.C4_OPS / (ms * 1e-3) / 1e12,
+                                  "frac_mfma": C.C4_OPS / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+                                  "timing": how}}
 
 
 # ---------------------------------------------------------------- CPU baseline
-def cpu_baseline(rows=64):
+def cpu_baseline(rows=256):
     """Reference CPU path (mirrored generated JS, one core) on `rows` rows of
     the 4096^3 GEMM: quantized_dot triple loop + fused per-channel epilogue."""
     node = shutil.which("node")
@@ -235,7 +259,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the int8 path has no multi-GPU code, see DESIGN.md for how it would shard",
+              "the int8 path has no multi-GPU code (DESIGN.md describes how it would shard)",
               file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
@@ -254,13 +278,13 @@ def main():
     tops = GEMM_OPS / (r["step_ms"] * 1e-3) / 1e12
     gemm_tops = GEMM_OPS / (r["gemm_avg_ms"] * 1e-3) / 1e12
     log(f"[bench] step {r['step_ms']:.4f} ms -> {tops:.1f} TOPS; gemm {r['gemm_avg_ms'] * 1e3:.1f} us "
-        f"-> {gemm_tops:.1f} TOPS")
+        f"-> {gemm_tops:.1f} TOPS; host {r['wall_ms_per_step']:.4f} ms/step")
 
     traffic = load_traffic().get("gemm_4096", {})
-    tb = traffic.get("hbm_bytes_per_launch")
     roofline = {"bound": "mfma", "achieved": gemm_tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
-                "frac": gemm_tops / PEAK_INT8_TOPS, "traffic": tb,
-                "kernel": "k_gemm_i8<256,256,2,2>", "avg_us": r["gemm_avg_ms"] * 1e3,
+                "frac": gemm_tops / PEAK_INT8_TOPS,
+                "traffic": traffic.get("hbm_bytes_per_launch"),
+                "kernel": GEMM_KERNEL, "avg_us": r["gemm_avg_ms"] * 1e3,
                 "algorithmic_ops_per_launch": GEMM_OPS}
 
     secondary = {}

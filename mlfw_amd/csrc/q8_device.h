@@ -96,7 +96,7 @@ __device__ __forceinline__ float relu_js(float v) {
 
 // SiLU decomposed (decomposition_pass.ts:197-203, 224-230), each op rounded:
 // fround(x * fround(1 / fround(1 + fround(exp(-x))))), exp evaluated in f64.
-__device__ __noinline__ float silu_js(float x) {
+__device__ __forceinline__ float silu_js(float x) {
   float e = (float)exp(-(double)x);
   float d = (float)(1.0 + (double)e);
   float r = (float)(1.0 / (double)d);

@@ -1,170 +1,426 @@
 // q8_gemm.hip -- int8 x int8 -> int32 matmul with the dequant epilogue fused,
 // for gfx950 (CDNA4).
 //
-// GEMM (M > 16): C[M,N] = A[M,K] . B[N,K]^T, both operands K-contiguous.
-//   * v_mfma_i32_32x32x32_i8: a wave64 multiplies a 32x32 int8 A block by a
-//     32x32 int8 B block into 16 int32 accumulators per lane.  Each lane
-//     feeds 16 consecutive K bytes of one row of A and of one row of B
-//     (row = lane % 32, K half = lane / 32), so A and B fragments are plain
+// GEMM (M > 16): C[M,N] = A[M,K] . B[N,K]^T, both operands K-contiguous
+// (A = activations [M,K], B = the nn.Linear weight [N,K]).
+//   * Tiles of BM x BN outputs per workgroup of 4 waves (2 x 2); each wave
+//     owns a (BM/2) x (BN/2) sub-tile as a grid of 32x32 blocks computed
+//     with v_mfma_i32_32x32x32_i8 (16 int32 accumulators per lane per block,
+//     kept in AGPRs).  A lane feeds 16 K-bytes of one row of A and the same
+//     16 K-bytes of one row of B per instruction, so fragments are single
 //     128-bit LDS reads.
-//   * A workgroup owns a BM x BN output tile and walks K in BK = 128 byte
-//     steps.  Each step's A and B tiles are staged in LDS (row-major, 128 B
-//     per row) with the 16-byte chunk index XOR-swizzled by (row & 7): the
-//     32 lanes that read one column of chunks hit 8 different 16-byte bank
-//     groups, so the ds_read_b128 fragment loads are conflict-free.
-//   * Global -> LDS is double-buffered: step t+1 is loaded into registers
-//     while the MFMAs of step t run out of the other LDS buffer; one
-//     barrier per K step.
+//   * K is walked in BK = 128-byte stages.  Global -> LDS copies use the
+//     buffer_load_dwordx4 ... lds form (no VGPR staging): each instruction
+//     moves 8 tile rows x 128 B, lane l landing at LDS byte 16*l of the
+//     wave's destination.  Out-of-range rows and the K tail are fetched
+//     through offsets past the buffer resource's num_records, which the
+//     hardware returns as zero -- edge tiles need no separate code.
+//   * LDS layout: tile row r occupies 128 B; its logical 16-byte K chunk c
+//     is stored at chunk position c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7.
+//     The 32 lanes that read one K chunk of 32 consecutive rows then hit
+//     distinct 16-byte bank groups within every 8-row and every 16-row
+//     group, so fragment reads are conflict-free on a 32- or 64-bank LDS.
+//     The swizzle is applied on the global side (each lane fetches the
+//     chunk its LDS slot must hold), so the DMA writes stay linear.
+//   * Two LDS stages: while the MFMAs of stage t run, the copies of stage
+//     t+1 are in flight; one s_waitcnt + barrier per stage, placed before
+//     the stage's last 32-byte K sub-step so that sub-step's MFMAs (registers
+//     only) overlap the refill of the consumed stage and the first fragment
+//     reads of the next one.  Fragments are double-buffered in registers
+//     across the four K sub-steps.
+//   * Workgroup -> tile order undoes the round-robin dispatch over the 8
+//     XCDs (consecutive workgroup ids land on different XCDs), then walks
+//     groups of 4 tile rows column by column, so the tiles resident on one
+//     XCD share rows of A and columns of B in that XCD's L2.
 //   * The epilogue converts the int32 accumulators with the reference's
-//     f64 arithmetic (fround(acc * fround(sA[m] * sB[n])) or
-//     fround(acc * s_out)), adds the bias and applies ReLU / SiLU before the
-//     only store of the output.
-// GEMV (M <= 16): HBM-bound on B.  A workgroup of 4 waves owns 4*R rows of
-//   B; the int8 activations are staged once per workgroup in LDS; each lane
-//   streams 16-byte slices of R weight rows and accumulates with
-//   v_dot4_i32_i8; a wave reduction finishes every (token, row) pair.
+//     arithmetic (fround(acc * fround(sA[m] * sB[n])) or fround(acc * s_out),
+//     f64 where the reference is f64), adds the bias and applies ReLU /
+//     SiLU before the only store of the output.
+// GEMV (M <= 16): HBM-bound on B, packed int8 dot products, no MFMA.
+#include <type_traits>
+
 #include "q8_device.h"
 #include "q8_internal.h"
 
 namespace q8 {
 
 // ------------------------------------------------------------------ epilogue
+// y = fround(acc * sv) for an f32 scale sv.  When acc is exactly an f32
+// (|acc| <= 2^24) the f32 multiply rounds the exact product once, which is
+// what Math.fround((+acc) * sv) does in f64 (a binary32 product of two
+// binary32 values is exact in binary64); otherwise the f64 form is used.
+__device__ __forceinline__ float mul_acc_f32scale(int acc, float sv) {
+  if ((unsigned)(acc + (1 << 24)) <= (2u << 24)) return (float)acc * sv;
+  return (float)((double)acc * (double)sv);
+}
+
+__device__ __forceinline__ float epi_finish(float y, int64_t n, const GemmEpi& e) {
+  if (e.bias) y = y + e.bias[n];   // binary32 add == Math.fround(f64 add) for f32 operands
+  if (e.act == 1) y = relu_js(y);
+  else if (e.act == 2) y = silu_js(y);
+  return y;
+}
+
 __device__ __forceinline__ float epi_value(int acc, int64_t m, int64_t n, const GemmEpi& e) {
   float y;
   if (e.mode == 0) {
     y = (float)((double)acc * e.s_out);
   } else {
     const float sv = (float)(e.sA[m * e.sA_stride] * e.sB[n * e.sB_stride]);
-    y = (float)((double)acc * (double)sv);
+    y = mul_acc_f32scale(acc, sv);
   }
-  if (e.bias) y = (float)((double)y + (double)e.bias[n]);
-  if (e.act == 1) y = relu_js(y);
-  else if (e.act == 2) y = silu_js(y);
-  return y;
-}
-
-// Stores one 32x32 accumulator block of this lane: element r is row
-// row0 + (r / 4) * 8 + (r % 4) of column `col`.  Kept out of line so the
-// caller's loops over blocks unroll and index the accumulators statically.
-__device__ __noinline__ void store_acc_block(v16i a, int64_t row0, int64_t col, int M, int N,
-                                             const GemmEpi& e, void* out) {
-  if (col >= N) return;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = row0 + (r >> 2) * 8 + (r & 3);
-    if (row < M) {
-      if (e.out_i32) static_cast<int32_t*>(out)[row * N + col] = a[r];
-      else static_cast<float*>(out)[row * N + col] = epi_value(a[r], row, col, e);
-    }
-  }
+  return epi_finish(y, n, e);
 }
 
 // ------------------------------------------------------------------ MFMA GEMM
-constexpr int BK = 128;
+constexpr int BK = 128;                 // K bytes per LDS stage
+constexpr int GEMM_THREADS = 256;       // 4 waves, 2 x 2
+constexpr uint32_t OOB = 0x80000000u;   // voffset past every buffer's num_records
 
-template <int BM, int BN, int WAVES_M, int WAVES_N>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1)
-void k_gemm_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
-               GemmEpi e, void* __restrict__ out) {
-  constexpr int NT = 64 * WAVES_M * WAVES_N;
-  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_CH = BM * (BK / 16) / NT;   // 16-byte chunks per thread per step
-  constexpr int B_CH = BN * (BK / 16) / NT;
-  static_assert(A_CH * NT == BM * (BK / 16) && B_CH * NT == BN * (BK / 16), "tile / threads");
-  constexpr int TILE_BYTES = (BM + BN) * BK;
-  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+template <int BM, int BN>
+struct GemmCfg {
+  static constexpr int WM = BM / 2, WN = BN / 2;      // per-wave sub-tile
+  static constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 blocks per wave
+  static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int LDS = 2 * STAGE;                 // two K stages
+  static constexpr int LDS_TOTAL = LDS + 8 * (BM + BN);  // + the tile's f64 scales
+  static constexpr int A_LOADS = BM / 32;              // 8-row copies per wave per stage
+  static constexpr int B_LOADS = BN / 32;
+  static_assert(TM >= 1 && TN >= 1 && BM % 64 == 0 && BN % 64 == 0, "tile shape");
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 
-  v16i acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-  v4i ra[A_CH], rb[B_CH];
-  const int KT = (K + BK - 1) / BK;
-
-  auto gload = [&](int kt) {
-    const int kb = kt * BK;
-#pragma unroll
-    for (int c = 0; c < A_CH; ++c) {
-      const int ch = tid + c * NT, row = ch >> 3, col = ch & 7;
-      const int gm = m0 + row, gk = kb + col * 16;
-      v4i v = {0, 0, 0, 0};
-      if (gm < M && gk < K) v = *reinterpret_cast<const v4i*>(A + (int64_t)gm * K + gk);
-      ra[c] = v;
-    }
-#pragma unroll
-    for (int c = 0; c < B_CH; ++c) {
-      const int ch = tid + c * NT, row = ch >> 3, col = ch & 7;
-      const int gn = n0 + row, gk = kb + col * 16;
-      v4i v = {0, 0, 0, 0};
-      if (gn < N && gk < K) v = *reinterpret_cast<const v4i*>(B + (int64_t)gn * K + gk);
-      rb[c] = v;
-    }
-  };
-  auto lstore = [&](int buf) {
-    int8_t* la = lds + buf * TILE_BYTES;
-    int8_t* lb = la + BM * BK;
-#pragma unroll
-    for (int c = 0; c < A_CH; ++c) {
-      const int ch = tid + c * NT, row = ch >> 3, col = ch & 7;
-      *reinterpret_cast<v4i*>(la + row * BK + ((col ^ (row & 7)) << 4)) = ra[c];
-    }
-#pragma unroll
-    for (int c = 0; c < B_CH; ++c) {
-      const int ch = tid + c * NT, row = ch >> 3, col = ch & 7;
-      *reinterpret_cast<v4i*>(lb + row * BK + ((col ^ (row & 7)) << 4)) = rb[c];
-    }
-  };
-
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  const int r32 = lane & 31, khalf = lane >> 5;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-    const int8_t* la = lds + cur * TILE_BYTES;
-    const int8_t* lb = la + BM * BK;
-#pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      const int chunk = kk * 2 + khalf;
-      const int sw = ((chunk ^ (r32 & 7)) << 4);
-      v4i af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(la + (wm + i * 32 + r32) * BK + sw);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const v4i*>(lb + (wn + j * 32 + r32) * BK + sw);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < KT) lstore(cur ^ 1);
-    __syncthreads();
-  }
-
-  // 32x32 accumulator layout: lane l, element r holds
-  //   row = (r / 4) * 8 + (l / 32) * 4 + (r % 4), col = l % 32.
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-      store_acc_block(acc[i][j], m0 + wm + i * 32 + khalf * 4, n0 + wn + j * 32 + r32, M, N, e, out);
+// Buffer resource (V#) of a raw byte range: base, stride 0, num_records
+// bytes, gfx9 data-format word.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const int8_t* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(base), (short)0, (int)bytes,
+                                           0x00020000);
 }
 
-constexpr int gemm_lds_bytes(int bm, int bn) { return 2 * (bm + bn) * BK; }
+// 16 bytes per lane from buffer offset voff to LDS dst + 16 * lane.
+__device__ __forceinline__ void copy16_to_lds(__amdgpu_buffer_rsrc_t r, int8_t* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
+// End of a stage: this wave's LDS copies have landed and its fragment reads
+// have returned, then all waves meet.  Written as one asm statement because
+// the compiler's wait-count pass would otherwise relax an explicit
+// lgkmcnt(0) whose results it sees as not yet needed; the next stage's
+// copies overwrite the buffer those reads came from.
+__device__ __forceinline__ void stage_sync() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// As stage_sync, but up to N of this wave's most recent copies (the next
+// stage) may still be in flight.
+template <int N>
+__device__ __forceinline__ void stage_sync_keep() {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "vmcnt immediate");
+  if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroup id -> (tile row, tile col).  Dispatch places consecutive ids on
+// consecutive XCDs (id % 8); the remap gives each XCD a contiguous run of
+// the grouped tile order below.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int G = tiles_m * tiles_n;
+  const int xcd = bid & 7, k = bid >> 3;
+  const int per = G >> 3, rem = G & 7;
+  const int id = xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
+  constexpr int GROUP = 4;
+  const int group = id / (GROUP * tiles_n);
+  const int first = group * GROUP;
+  const int gm = min(tiles_m - first, GROUP);
+  const int in = id - group * GROUP * tiles_n;
+  tm = first + in % gm;
+  tn = in / gm;
+}
+
+// Compile-time epilogue variant of the MFMA kernel:
+//   bit 4 int32 output (raw accumulators), else fp32 output with
+//   bit 3 MODE (0: fround(acc * s_out), 1: fround(acc * fround(sA[m] * sB[n]))),
+//   bit 2 bias, bits 0-1 activation (0 none, 1 ReLU, 2 SiLU).
+template <int EPI>
+struct Epi {
+  static constexpr bool OUT_I32 = (EPI & 16) != 0;
+  static constexpr int MODE = (EPI >> 3) & 1;
+  static constexpr bool BIAS = (EPI & 4) != 0;
+  static constexpr int ACT = EPI & 3;
+};
+
+inline int epi_code(const GemmEpi& e) {
+  if (e.out_i32) return 16;
+  return (e.mode << 3) | (e.bias ? 4 : 0) | e.act;
+}
+
+// Epilogue of one output quad: 4 consecutive columns of one row.
+template <int EPI>
+__device__ __forceinline__ void store_quad(v4i a, int row, int col, int M, int N, bool vec_ok,
+                                           const GemmEpi& e, double sa, const double* sb,
+                                           void* out) {
+  using P = Epi<EPI>;
+  if (row >= M) return;
+  const int64_t idx = (int64_t)row * N + col;
+  if constexpr (P::OUT_I32) {
+    if (vec_ok && col + 3 < N) {
+      *reinterpret_cast<v4i*>(static_cast<int32_t*>(out) + idx) = a;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col + c < N) static_cast<int32_t*>(out)[idx + c] = a[c];
+    }
+    return;
+  } else {
+    float y[4];
+    if constexpr (P::MODE == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) y[c] = (float)((double)a[c] * e.s_out);
+    } else {
+      float sv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sv[c] = (float)(sa * sb[c]);
+      // binary32 multiply when every accumulator of the quad is exactly a
+      // binary32 value (|acc| <= 2^24), the f64 form otherwise
+      bool exact = true;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) exact &= (unsigned)(a[c] + (1 << 24)) <= (2u << 24);
+      if (exact) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = (float)a[c] * sv[c];
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = (float)((double)a[c] * (double)sv[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (P::BIAS) y[c] = y[c] + e.bias[col + c < N ? col + c : 0];
+      if constexpr (P::ACT == 1) y[c] = relu_js(y[c]);
+      if constexpr (P::ACT == 2) y[c] = silu_js(y[c]);
+    }
+    float* o = static_cast<float*>(out);
+    if (vec_ok && col + 3 < N) {
+      *reinterpret_cast<float4*>(o + idx) = make_float4(y[0], y[1], y[2], y[3]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col + c < N) o[idx + c] = y[c];
+    }
+  }
+}
+
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(GEMM_THREADS, 1)
+void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
+             int tiles_m, int tiles_n, GemmEpi e, void* __restrict__ out) {
+  using C = GemmCfg<BM, BN>;
+  constexpr bool OUT_I32 = Epi<EPI>::OUT_I32;
+  constexpr int MODE = Epi<EPI>::MODE;
+  extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const int8_t* Ab = A + (int64_t)m0 * K;
+  const int8_t* Bb = B + (int64_t)n0 * K;
+
+  // The tile's epilogue scales: loaded now, stored to LDS behind the two
+  // stages once the prologue copies are issued.
+  double* s_rows = reinterpret_cast<double*>(lds + C::LDS);
+  double* s_cols = s_rows + BM;
+  constexpr int NSC = (BM + BN + GEMM_THREADS - 1) / GEMM_THREADS;
+  double scv[NSC];
+#pragma unroll
+  for (int u = 0; u < NSC; ++u) {
+    const int t = tid + u * GEMM_THREADS;
+    double v = 0.0;
+    if (!OUT_I32 && MODE == 1) {
+      if (t < BM) { if (t < rows_a) v = e.sA[(int64_t)(m0 + t) * e.sA_stride]; }
+      else if (t < BM + BN && t - BM < rows_b) v = e.sB[(int64_t)(n0 + t - BM) * e.sB_stride];
+    }
+    scv[u] = v;
+  }
+
+  // Copy plan: wave w fills tile rows [w*BM/4, (w+1)*BM/4) of A and the
+  // same share of B, 8 rows per instruction.  Lane l lands in row
+  // 8j + l/8 at chunk position l%8 and so fetches logical chunk
+  // (l%8) ^ swz(row).
+  uint32_t offa[C::A_LOADS], offb[C::B_LOADS];
+  int kca[C::A_LOADS], kcb[C::B_LOADS];
+#pragma unroll
+  for (int j = 0; j < C::A_LOADS; ++j) {
+    const int row = wave * (BM / 4) + 8 * j + (lane >> 3);
+    kca[j] = 16 * ((lane & 7) ^ swz(row));
+    offa[j] = row < rows_a ? (uint32_t)(row * K + kca[j]) : OOB;
+  }
+#pragma unroll
+  for (int j = 0; j < C::B_LOADS; ++j) {
+    const int row = wave * (BN / 4) + 8 * j + (lane >> 3);
+    kcb[j] = 16 * ((lane & 7) ^ swz(row));
+    offb[j] = row < rows_b ? (uint32_t)(row * K + kcb[j]) : OOB;
+  }
+  const uint32_t bytes_a = (uint32_t)rows_a * (uint32_t)K;
+  const uint32_t bytes_b = (uint32_t)rows_b * (uint32_t)K;
+  const int KT = (K + BK - 1) / BK;
+
+  // Copies of K stage kt into `stage`.  kt >= KT copies nothing: with
+  // num_records 0 every lane is out of range and writes zeros into a stage
+  // that is no longer read, which keeps the loop body branch-free.
+  auto issue = [&](int kt, int8_t* stage) {
+    const bool live = kt < KT;
+    const int kb = live ? kt * BK : 0;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab + kb, live ? bytes_a - (uint32_t)kb : 0u);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
+    int8_t* sa = stage + wave * (BM / 4) * BK;
+    int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
+    const bool tail = kb + BK > K;
+#pragma unroll
+    for (int j = 0; j < C::A_LOADS; ++j)
+      copy16_to_lds(ra, sa + j * 8 * BK, (tail && kb + kca[j] >= K) ? OOB : offa[j]);
+#pragma unroll
+    for (int j = 0; j < C::B_LOADS; ++j)
+      copy16_to_lds(rb, sb + j * 8 * BK, (tail && kb + kcb[j] >= K) ? OOB : offb[j]);
+  };
+
+  // Fragment addresses: byte offset of the fragment row within a stage and
+  // the lane's swizzle (logical chunk 2*kk + kh sits at position
+  // (2*kk) ^ (kh ^ swz(row))).
+  const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
+  const int r32 = lane & 31, kh = lane >> 5;
+  int fa_off[C::TM], fa_sw[C::TM], fb_off[C::TN], fb_sw[C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) {
+    const int row = wm + 32 * i + r32;
+    fa_off[i] = row * BK;
+    fa_sw[i] = kh ^ swz(row);
+  }
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) {
+    const int row = wn + 32 * j + r32;
+    fb_off[j] = C::A_BYTES + row * BK;
+    fb_sw[j] = kh ^ swz(row);
+  }
+  auto read_frags = [&](const int8_t* st, int kk, v4i* fa, v4i* fb) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+      fa[i] = *reinterpret_cast<const v4i*>(st + fa_off[i] + 16 * ((2 * kk) ^ fa_sw[i]));
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+      fb[j] = *reinterpret_cast<const v4i*>(st + fb_off[j] + 16 * ((2 * kk) ^ fb_sw[j]));
+  };
+
+  v16i acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  auto mfma_all = [&](const v4i* fa, const v4i* fb) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  };
+
+  // Pipeline: stages kt and kt+1 are in LDS or in flight while the MFMAs
+  // of stage kt run.  The barrier of stage kt sits before its last
+  // sub-step: those MFMAs only need registers, so they overlap the refill
+  // of the stage just consumed and the first fragment reads of stage kt+1.
+  int8_t* const s0 = lds;
+  int8_t* const s1 = lds + C::STAGE;
+  issue(0, s0);
+  issue(1, s1);
+  if (!OUT_I32 && MODE == 1) {
+#pragma unroll
+    for (int u = 0; u < NSC; ++u)
+      if (tid + u * GEMM_THREADS < BM + BN) s_rows[tid + u * GEMM_THREADS] = scv[u];
+  }
+  stage_sync_keep<C::A_LOADS + C::B_LOADS>();   // stage 0 landed; stage 1 may be in flight
+  v4i fa0[C::TM], fb0[C::TN], fa1[C::TM], fb1[C::TN];
+  read_frags(s0, 0, fa0, fb0);
+  for (int kt = 0; kt < KT; ++kt) {
+    int8_t* cur = (kt & 1) ? s1 : s0;
+    int8_t* nxt = (kt & 1) ? s0 : s1;
+    read_frags(cur, 1, fa1, fb1);
+    mfma_all(fa0, fb0);
+    read_frags(cur, 2, fa0, fb0);
+    mfma_all(fa1, fb1);
+    read_frags(cur, 3, fa1, fb1);
+    mfma_all(fa0, fb0);
+    stage_sync();                        // reads of `cur` returned; stage kt+1 landed
+    issue(kt + 2, cur);                  // refill the stage just consumed
+    read_frags(nxt, 0, fa0, fb0);        // first fragments of stage kt+1
+    mfma_all(fa1, fb1);
+    // Order of the last sub-step: refill copies and next-stage reads slot
+    // between its MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+    for (int x = 0; x < C::TM + C::TN; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x020, C::A_LOADS + C::B_LOADS, 0);   // VMEM read
+    __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - 1 - (C::TM + C::TN), 0);
+  }
+  // The last iterations issued zero-filling copies for stages past KT into
+  // the stage buffers the epilogue reuses: drain them first.
+  stage_sync();
+
+  // Epilogue through LDS (free after the last barrier): each wave moves one
+  // 32-row strip of its sub-tile at a time into its own LDS region (row
+  // pitch WN + 8 words), then reads it back as 4-column quads, so every
+  // lane applies the scales to 4 adjacent outputs and stores 16 bytes.
+  constexpr int PITCH = C::WN + 8;                    // int32 words per strip row
+  constexpr int LPR = C::WN / 4;                      // lanes per strip row
+  constexpr int RPI = 64 / LPR;                       // strip rows per read
+  static_assert(4 * 32 * PITCH * 4 <= C::LDS, "epilogue strips fit in the stage buffers");
+  int32_t* strip = reinterpret_cast<int32_t*>(lds) + wave * 32 * PITCH;
+  const int qcol = 4 * (lane % LPR), qrow = lane / LPR;
+  const int col = n0 + wn + qcol;
+  const bool vec_ok = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
+  double sb[4] = {0.0, 0.0, 0.0, 0.0};
+  if (!OUT_I32 && MODE == 1) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sb[c] = s_cols[wn + qcol + c];
+  }
+  // One strip per 32-row block row i; the strip index is a template
+  // argument so the accumulators stay statically indexed (registers).
+  auto strip_out = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    // accumulator element r of lane l: strip row (r/4)*8 + (l/32)*4 + r%4,
+    // strip column 32*j + l%32
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        strip[((r >> 2) * 8 + kh * 4 + (r & 3)) * PITCH + 32 * j + r32] = acc[i][j][r];
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int sr = it * RPI + qrow;
+      const v4i q = *reinterpret_cast<const v4i*>(strip + sr * PITCH + qcol);
+      const int trow = wm + 32 * i + sr;
+      store_quad<EPI>(q, m0 + trow, col, M, N, vec_ok, e,
+                                (!OUT_I32 && MODE == 1) ? s_rows[trow] : 0.0, sb, out);
+    }
+  };
+  strip_out(std::integral_constant<int, 0>{});
+  if constexpr (C::TM > 1) strip_out(std::integral_constant<int, 1>{});
+  if constexpr (C::TM > 2) strip_out(std::integral_constant<int, 2>{});
+  if constexpr (C::TM > 3) strip_out(std::integral_constant<int, 3>{});
+  static_assert(C::TM <= 4, "strip_out calls cover TM <= 4");
+}
+
+template <int BM, int BN>
+constexpr int qgemm_lds() { return GemmCfg<BM, BN>::LDS_TOTAL; }
 
 // Generic fallback for K % 16 != 0 or unaligned operands: one thread per
 // output, byte loads, exact int32 (wrapping) accumulation.
@@ -181,12 +437,36 @@ __global__ __launch_bounds__(256) void k_gemm_i8_generic(const int8_t* __restric
   else static_cast<float*>(out)[idx] = epi_value(acc, m, n, e);
 }
 
-hipError_t setup_kernel_attributes();
+#define Q8_EPI_CODES(X) \
+  X(16) X(0) X(1) X(2) X(4) X(5) X(6) X(8) X(9) X(10) X(12) X(13) X(14)
+
+template <int BM, int BN>
+static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int N, int K,
+                                    const GemmEpi& e, void* out, hipStream_t st) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const dim3 grid((unsigned)(tm * tn)), block(GEMM_THREADS);
+  constexpr int lds = qgemm_lds<BM, BN>();
+  switch (epi_code(e)) {
+#define Q8_LAUNCH_EPI(code)                                                                  \
+  case code:                                                                                 \
+    hipLaunchKernelGGL((k_qgemm<BM, BN, code>), grid, block, lds, st, A, B, M, N, K, tm, tn, \
+                       e, out);                                                              \
+    break;
+    Q8_EPI_CODES(Q8_LAUNCH_EPI)
+#undef Q8_LAUNCH_EPI
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  const bool vec = (K % 16 == 0) && ((reinterpret_cast<uintptr_t>(A) & 15) == 0) &&
+  // The MFMA kernel needs 16-byte K chunks and 32-bit buffer offsets within
+  // a 256-row tile (offsets up to 256 * K, plus the OOB marker 2^31).
+  const bool vec = (K % 16 == 0) && K > 0 && (256 * K < (int64_t)OOB) &&
+                   ((reinterpret_cast<uintptr_t>(A) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(B) & 15) == 0);
   if (!vec) {
     const int64_t n = M * N;
@@ -194,22 +474,13 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();
   }
-  const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
-  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (tiles256 >= 192) {
-    dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256));
-    k_gemm_i8<256, 256, 2, 2><<<grid, dim3(256), gemm_lds_bytes(256, 256), st>>>(
-        A, B, (int)M, (int)N, (int)K, e, out);
-  } else if (tiles128 >= 192) {
-    dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128));
-    k_gemm_i8<128, 128, 2, 2><<<grid, dim3(256), gemm_lds_bytes(128, 128), st>>>(
-        A, B, (int)M, (int)N, (int)K, e, out);
-  } else {
-    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-    k_gemm_i8<64, 64, 2, 2><<<grid, dim3(256), gemm_lds_bytes(64, 64), st>>>(
-        A, B, (int)M, (int)N, (int)K, e, out);
-  }
-  return hipGetLastError();
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (t256 >= 192)
+    return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  if (t128 >= 192)
+    return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  return launch_qgemm_tile<64, 64>(A, B, (int)M, (int)N, (int)K, e, out, st);
 }
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
@@ -302,15 +573,22 @@ hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
   return hipGetLastError();
 }
 
+
 hipError_t setup_kernel_attributes() {
   hipError_t err;
 #define Q8_SET_LDS(kern, bytes)                                                              \
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),                             \
                             hipFuncAttributeMaxDynamicSharedMemorySize, (bytes));            \
   if (err != hipSuccess) return err;
-  Q8_SET_LDS((k_gemm_i8<256, 256, 2, 2>), gemm_lds_bytes(256, 256));
-  Q8_SET_LDS((k_gemm_i8<128, 128, 2, 2>), gemm_lds_bytes(128, 128));
-  Q8_SET_LDS((k_gemm_i8<64, 64, 2, 2>), gemm_lds_bytes(64, 64));
+#define Q8_SET_256(code) Q8_SET_LDS((k_qgemm<256, 256, code>), (qgemm_lds<256, 256>()));
+#define Q8_SET_128(code) Q8_SET_LDS((k_qgemm<128, 128, code>), (qgemm_lds<128, 128>()));
+#define Q8_SET_64(code) Q8_SET_LDS((k_qgemm<64, 64, code>), (qgemm_lds<64, 64>()));
+  Q8_EPI_CODES(Q8_SET_256)
+  Q8_EPI_CODES(Q8_SET_128)
+  Q8_EPI_CODES(Q8_SET_64)
+#undef Q8_SET_256
+#undef Q8_SET_128
+#undef Q8_SET_64
   Q8_SET_LDS(k_gemv_i8<1>, 1 * GEMV_KC);
   Q8_SET_LDS(k_gemv_i8<2>, 2 * GEMV_KC);
   Q8_SET_LDS(k_gemv_i8<4>, 4 * GEMV_KC);

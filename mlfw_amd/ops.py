@@ -21,6 +21,64 @@ def _stream() -> C.c_void_p:
     return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+class Launch:
+    """One C-ABI call with its arguments validated and converted once.
+
+    Calling it enqueues the op again on the stream captured at preparation
+    time, with the same tensors (their storage must stay alive and keep its
+    shape).  This is the host-side analogue of the reference runtime's
+    prepared plans (src/runtime/runtime.ts:290-329): a serving or benchmark
+    loop pays one foreign call per op instead of re-validating arguments.
+    """
+
+    __slots__ = ("name", "_fn", "_args", "_keep", "outputs")
+
+    def __init__(self, name: str, args: tuple, keep: tuple = ()):
+        self.name = name
+        self._fn = getattr(L.load(), name)
+        self._args = args
+        self._keep = keep          # temporaries the raw pointers refer to
+        self.outputs = None        # what the op returned (keeps the tensors alive)
+
+    def __call__(self) -> None:
+        rc = self._fn(*self._args)
+        if rc != L.Q8_OK:
+            L.check(rc)
+
+
+_capture: list | None = None
+
+
+def _call(name: str, *args, keep: tuple = ()) -> None:
+    """Run one C-ABI entry point now, or record it while prepare() is active.
+    `keep` lists temporaries a recorded launch must hold on to."""
+    if _capture is not None:
+        _capture.append(Launch(name, args, keep))
+    else:
+        L.call(name, *args)
+
+
+def prepare(op, *args, **kwargs) -> Launch:
+    """Validate `op(*args, **kwargs)` once and return its launch unrun.
+
+    `op` is one of this module's single-launch ops (quantize_per_token,
+    quantize_per_tensor, quantize, dequantize, quantized_dot, qlinear,
+    qlinear_pt, silu_mul_quantize).  The returned Launch re-enqueues exactly
+    that call; Launch.outputs holds what the op returned."""
+    global _capture
+    prev, _capture = _capture, []
+    try:
+        result = op(*args, **kwargs)
+        recorded = _capture
+    finally:
+        _capture = prev
+    if len(recorded) != 1:
+        raise ValueError(f"prepare: {getattr(op, '__name__', op)} issued {len(recorded)} "
+                         "launches; only single-launch ops can be prepared")
+    recorded[0].outputs = result
+    return recorded[0]
+
+
 def _ptr(t) -> C.c_void_p:
     return C.c_void_p(0 if t is None else t.data_ptr())
 
@@ -53,7 +111,7 @@ def fill_normal(t: torch.Tensor, seed: int, offset: int = 0, mean: float = 0.0,
                 std: float = 1.0) -> int:
     """normal_ (src/nn/init.ts:40-52) on the device; returns draws consumed."""
     _need(t, torch.float32, "fill_normal")
-    L.call("q8_fill_normal", _ptr(t), t.numel(), seed & 0xFFFFFFFF, offset, mean, std, _stream())
+    _call("q8_fill_normal", _ptr(t), t.numel(), seed & 0xFFFFFFFF, offset, mean, std, _stream())
     return 2 * ((t.numel() + 1) // 2)
 
 
@@ -61,14 +119,14 @@ def fill_uniform(t: torch.Tensor, seed: int, offset: int = 0, a: float = 0.0,
                  b: float = 1.0) -> int:
     """uniform_ (src/nn/init.ts:31-37) on the device; returns draws consumed."""
     _need(t, torch.float32, "fill_uniform")
-    L.call("q8_fill_uniform", _ptr(t), t.numel(), seed & 0xFFFFFFFF, offset, a, b, _stream())
+    _call("q8_fill_uniform", _ptr(t), t.numel(), seed & 0xFFFFFFFF, offset, a, b, _stream())
     return t.numel()
 
 
 def apply_outliers(t: torch.Tensor, seed: int, p: float = 0.01, factor: float = 50.0) -> None:
     """Scale the elements a second mulberry32 stream marks (draw < p) by factor."""
     _need(t, torch.float32, "apply_outliers")
-    L.call("q8_apply_outliers", _ptr(t), t.numel(), seed & 0xFFFFFFFF, p, factor, _stream())
+    _call("q8_apply_outliers", _ptr(t), t.numel(), seed & 0xFFFFFFFF, p, factor, _stream())
 
 
 # ---------------------------------------------------------------- quantize
@@ -81,7 +139,7 @@ def quantize(x: torch.Tensor, scale: float, zero_point: float = 0.0,
         raise ValueError(f"quantize target_dtype must be i8 or ui8, got {target_dtype}")
     q = torch.empty(x.shape, dtype=torch.int8 if target_dtype == "i8" else torch.uint8,
                     device=x.device)
-    L.call("q8_quantize_static", _ptr(x), x.numel(), float(scale), float(zero_point),
+    _call("q8_quantize_static", _ptr(x), x.numel(), float(scale), float(zero_point),
            L.Q8_I8 if target_dtype == "i8" else L.Q8_U8, _ptr(q), _stream())
     return q
 
@@ -95,7 +153,7 @@ def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
     M, K = _rows(x)
     q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
     scales = torch.empty(M, dtype=torch.float64, device=x.device) if scales is None else scales
-    L.call("q8_quantize_rows", _ptr(x), M, K, L.Q8_PER_TOKEN, _ptr(q), _ptr(scales), _stream())
+    _call("q8_quantize_rows", _ptr(x), M, K, L.Q8_PER_TOKEN, _ptr(q), _ptr(scales), _stream())
     return q, scales
 
 
@@ -106,7 +164,7 @@ def quantize_per_tensor(x: torch.Tensor, q: torch.Tensor | None = None,
     _need(x, torch.float32, "quantize_per_tensor")
     q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
     scales = torch.empty(1, dtype=torch.float64, device=x.device) if scales is None else scales
-    L.call("q8_quantize_rows", _ptr(x), 1, x.numel(), L.Q8_PER_TENSOR, _ptr(q), _ptr(scales),
+    _call("q8_quantize_rows", _ptr(x), 1, x.numel(), L.Q8_PER_TENSOR, _ptr(q), _ptr(scales),
            _stream())
     return q, scales
 
@@ -134,8 +192,8 @@ def dequantize(q: torch.Tensor, scale, zero_point: float = 0.0,
         gran = L.Q8_PER_TENSOR
         s = torch.tensor([float(scale)], dtype=torch.float64, device=q.device)
     y = torch.empty(q.shape, dtype=torch.float32, device=q.device) if out is None else out
-    L.call("q8_dequantize", _ptr(q), _SRC[q.dtype], M, K, _ptr(s), gran, float(zero_point),
-           _ptr(y), _stream())
+    _call("q8_dequantize", _ptr(q), _SRC[q.dtype], M, K, _ptr(s), gran, float(zero_point),
+          _ptr(y), _stream(), keep=(s,))
     return y
 
 
@@ -153,7 +211,7 @@ def pack_weight(W: torch.Tensor, axis: int = 0, granularity: str = "per_channel"
     per_tensor = granularity == "per_tensor"
     Wq = torch.empty((N, K), dtype=torch.int8, device=W.device)
     scales = torch.empty(1 if per_tensor else N, dtype=torch.float64, device=W.device)
-    L.call("q8_pack_weight", _ptr(W), rows, cols, axis,
+    _call("q8_pack_weight", _ptr(W), rows, cols, axis,
            L.Q8_PER_TENSOR if per_tensor else L.Q8_PER_CHANNEL, _ptr(Wq), _ptr(scales), _stream())
     return Wq, scales
 
@@ -177,7 +235,7 @@ def quantized_dot(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = N
     rhs_contracting=[1]: int32 acc[m,n] = sum_k A[m,k] * B[n,k]."""
     M, N, K = _mk(A, B)
     out = torch.empty((M, N), dtype=torch.int32, device=A.device) if out is None else out
-    L.call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT, 0.0,
+    _call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT, 0.0,
            None, L.Q8_ACT_NONE, L.Q8_I32, _ptr(out), _stream())
     return out
 
@@ -198,7 +256,7 @@ def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor
         if bias.numel() != N:
             raise ValueError("qlinear: bias must have N elements")
     out = torch.empty((M, N), dtype=torch.float32, device=A.device) if out is None else out
-    L.call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0,
+    _call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0,
            _ptr(sA), L.Q8_PER_TOKEN if sA.numel() == M and M != 1 else L.Q8_PER_TENSOR,
            _ptr(sB), L.Q8_PER_CHANNEL if sB.numel() == N and N != 1 else L.Q8_PER_TENSOR,
            L.Q8_EPI_ROWCOL, 0.0, _ptr(bias), _ACT[act], L.Q8_F32, _ptr(out), _stream())
@@ -212,7 +270,7 @@ def qlinear_pt(A: torch.Tensor, B: torch.Tensor, s_out: float,
     s_out = lhs_scale * rhs_scale in f64."""
     M, N, K = _mk(A, B)
     out = torch.empty((M, N), dtype=torch.float32, device=A.device) if out is None else out
-    L.call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT,
+    _call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT,
            float(s_out), _ptr(bias), _ACT[act], L.Q8_F32, _ptr(out), _stream())
     return out
 
@@ -229,6 +287,6 @@ def silu_mul_quantize(g: torch.Tensor, u: torch.Tensor, h_out: torch.Tensor | No
     scales = torch.empty(M, dtype=torch.float64, device=g.device)
     if h_out is not None:
         _need(h_out, torch.float32, "h_out")
-    L.call("q8_silu_mul_quantize_rows", _ptr(g), _ptr(u), M, K, _ptr(h_out), _ptr(q),
+    _call("q8_silu_mul_quantize_rows", _ptr(g), _ptr(u), M, K, _ptr(h_out), _ptr(q),
            _ptr(scales), _stream())
     return q, scales

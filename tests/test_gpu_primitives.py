@@ -210,7 +210,9 @@ def test_quantized_dot_small(ops, oracle, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 4096), (2048, 4096, 4096), (768, 1280, 11008),
-                                   (4096, 4096, 4096), (4001, 3100, 2048)])
+                                   (4096, 4096, 4096), (4001, 3100, 2048), (4001, 3099, 2064),
+                                   (1000, 1001, 4112), (513, 4095, 272), (2048, 12288, 4096),
+                                   (100, 3000, 16), (3000, 100, 32)])
 def test_quantized_dot_large_exact(ops, M, N, K):
     """Large shapes: integer products and sums are exact in f64 (|acc| < 2^53),
     so an f64 matmul of the same int8 values is an exact closed-form check."""
@@ -235,7 +237,8 @@ def test_quantized_dot_wraps_like_int32(ops, oracle):
 
 
 @pytest.mark.parametrize("act", [None, "relu", "silu"])
-@pytest.mark.parametrize("M,N,K", [(64, 96, 256), (300, 130, 512), (4, 200, 4096)])
+@pytest.mark.parametrize("M,N,K", [(64, 96, 256), (300, 130, 512), (4, 200, 4096),
+                                   (257, 131, 144), (1030, 2050, 1024), (33, 4099, 784)])
 def test_qlinear_rowcol_epilogue(ops, oracle, M, N, K, act):
     rng = oracle.Rng(M + N)
     x = rng.normal((M, K))
@@ -262,6 +265,22 @@ def test_qlinear_pertensor_scales(ops, oracle):
     y = ops.qlinear(dev(xq), dev(sx), dev(Wq), dev(sw))
     acc = oracle.quantized_dot(xq, Wq, b_layout=1)
     same_bits(host(y), oracle.epilogue(acc, "rowcol", sx[0], sw))
+
+
+@pytest.mark.parametrize("M,N,K", [(2000, 3000, 1024), (4096, 4096, 4096), (515, 517, 528)])
+def test_qlinear_large_rowcol_exact(ops, oracle, M, N, K):
+    """Full-size epilogue check: accumulators from an exact f64 matmul of the
+    same int8 values, then the oracle epilogue on every element."""
+    g = torch.Generator(device=DEV).manual_seed(M * 3 + N)
+    A = torch.randint(-128, 128, (M, K), dtype=torch.int8, device=DEV, generator=g)
+    B = torch.randint(-128, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    sA = torch.rand(M, dtype=torch.float64, device=DEV, generator=g) * 1e-2 + 1e-4
+    sB = torch.rand(N, dtype=torch.float64, device=DEV, generator=g) * 1e-3 + 1e-5
+    bias = torch.rand(N, dtype=torch.float32, device=DEV, generator=g) - 0.5
+    y = ops.qlinear(A, sA, B, sB, bias=bias)
+    acc = (A.double() @ B.double().t().contiguous()).to(torch.int32)
+    ref = oracle.epilogue(host(acc), "rowcol", host(sA), host(sB), bias=host(bias))
+    same_bits(host(y), ref)
 
 
 def test_qlinear_pt_epilogue(ops, oracle):
