@@ -1,0 +1,431 @@
+/*
+ * q8hip_napi.c -- Node N-API addon over the C ABI of libq8hip.so
+ * (include/q8hip.h).  This is the thin native layer the reference's
+ * TypeScript runtime would load in place of its koffi bindings to libcuda
+ * (src/runtime/node/cuda/ffi.ts:53-97): the JS side (hip_backend.js)
+ * registers a runtime backend, an external-codegen entry and a dispatcher
+ * library on top of it.
+ *
+ * Conventions:
+ *   - device buffers are napi externals wrapping {device pointer, bytes};
+ *     they are released by free() or, as a backstop, by the garbage
+ *     collector (the reference's terac runtime module keeps the same
+ *     explicit-release-plus-finalizer rule,
+ *     src/backend/terac/runtime_module.ts:22,37,89-94);
+ *   - host memory stays owned by JS: upload()/download() copy between a
+ *     typed array (or ArrayBuffer) and a device buffer and block;
+ *   - ops enqueue on the null stream and return immediately; sync() waits;
+ *   - a non-zero status from the C ABI becomes a thrown Error whose message
+ *     is q8_last_error() (the reference maps driver codes to JS errors the
+ *     same way, src/runtime/node/cuda/ffi.ts:102-104).
+ */
+#define NAPI_VERSION 8
+#include <node_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "q8hip.h"
+
+typedef struct {
+  void* ptr;
+  size_t bytes;
+} DevBuf;
+
+#define NAPI_CALL(env, call)                                      \
+  do {                                                            \
+    if ((call) != napi_ok) {                                      \
+      napi_throw_error((env), NULL, "q8hip: N-API call failed");  \
+      return NULL;                                                \
+    }                                                             \
+  } while (0)
+
+static napi_value throw_q8(napi_env env, int rc) {
+  char code[16];
+  snprintf(code, sizeof(code), "Q8_ERR_%d", rc);
+  const char* msg = q8_last_error();
+  napi_throw_error(env, code, (msg && msg[0]) ? msg : "q8hip: operation failed");
+  return NULL;
+}
+
+#define Q8_CHECK(env, expr)              \
+  do {                                   \
+    int rc_ = (expr);                    \
+    if (rc_ != Q8_OK) return throw_q8((env), rc_); \
+  } while (0)
+
+static napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+static int get_args(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, NULL, NULL) != napi_ok) return 0;
+  if (argc < want) {
+    napi_throw_type_error(env, NULL, "q8hip: too few arguments");
+    return 0;
+  }
+  return 1;
+}
+
+static int arg_i64(napi_env env, napi_value v, int64_t* out) {
+  if (napi_get_value_int64(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, NULL, "q8hip: expected a number");
+    return 0;
+  }
+  return 1;
+}
+
+static int arg_f64(napi_env env, napi_value v, double* out) {
+  if (napi_get_value_double(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, NULL, "q8hip: expected a number");
+    return 0;
+  }
+  return 1;
+}
+
+/* A device buffer argument; null / undefined give NULL when allowed. */
+static int arg_buf(napi_env env, napi_value v, int nullable, void** out) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok) return 0;
+  if (t == napi_null || t == napi_undefined) {
+    if (nullable) {
+      *out = NULL;
+      return 1;
+    }
+    napi_throw_type_error(env, NULL, "q8hip: device buffer required");
+    return 0;
+  }
+  if (t != napi_external) {
+    napi_throw_type_error(env, NULL, "q8hip: expected a device buffer from alloc()");
+    return 0;
+  }
+  DevBuf* b = NULL;
+  if (napi_get_value_external(env, v, (void**)&b) != napi_ok || b == NULL) return 0;
+  if (b->ptr == NULL && b->bytes != 0) {
+    napi_throw_error(env, NULL, "q8hip: device buffer was freed");
+    return 0;
+  }
+  *out = b->ptr;
+  return 1;
+}
+
+static int arg_devbuf(napi_env env, napi_value v, DevBuf** out) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) {
+    napi_throw_type_error(env, NULL, "q8hip: expected a device buffer from alloc()");
+    return 0;
+  }
+  return napi_get_value_external(env, v, (void**)out) == napi_ok && *out != NULL;
+}
+
+/* Host bytes of a typed array, DataView or ArrayBuffer. */
+static int arg_host(napi_env env, napi_value v, void** data, size_t* bytes) {
+  bool is;
+  if (napi_is_typedarray(env, v, &is) == napi_ok && is) {
+    napi_typedarray_type tt;
+    size_t len, off;
+    napi_value ab;
+    if (napi_get_typedarray_info(env, v, &tt, &len, data, &ab, &off) != napi_ok) return 0;
+    static const size_t esz[] = {1, 1, 1, 2, 2, 4, 4, 4, 8, 8, 8};
+    *bytes = len * (tt < (int)(sizeof(esz) / sizeof(esz[0])) ? esz[tt] : 1);
+    return 1;
+  }
+  if (napi_is_arraybuffer(env, v, &is) == napi_ok && is)
+    return napi_get_arraybuffer_info(env, v, data, bytes) == napi_ok;
+  napi_throw_type_error(env, NULL, "q8hip: expected a typed array or ArrayBuffer");
+  return 0;
+}
+
+/* ---------------------------------------------------------------- runtime */
+
+static napi_value js_version(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value r;
+  NAPI_CALL(env, napi_create_int32(env, q8_version(), &r));
+  return r;
+}
+
+static napi_value js_last_error(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value r;
+  NAPI_CALL(env, napi_create_string_utf8(env, q8_last_error(), NAPI_AUTO_LENGTH, &r));
+  return r;
+}
+
+static napi_value js_device_count(napi_env env, napi_callback_info info) {
+  (void)info;
+  int n = 0;
+  Q8_CHECK(env, q8_device_count(&n));
+  napi_value r;
+  NAPI_CALL(env, napi_create_int32(env, n, &r));
+  return r;
+}
+
+static napi_value js_init(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  int64_t dev;
+  if (!get_args(env, info, 1, argv) || !arg_i64(env, argv[0], &dev)) return NULL;
+  Q8_CHECK(env, q8_init((int)dev));
+  return undefined(env);
+}
+
+static void finalize_buf(napi_env env, void* data, void* hint) {
+  (void)env;
+  (void)hint;
+  DevBuf* b = (DevBuf*)data;
+  if (b->ptr) q8_free(b->ptr);
+  free(b);
+}
+
+static napi_value js_alloc(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  int64_t bytes;
+  if (!get_args(env, info, 1, argv) || !arg_i64(env, argv[0], &bytes)) return NULL;
+  if (bytes < 0) {
+    napi_throw_range_error(env, NULL, "q8hip.alloc: negative size");
+    return NULL;
+  }
+  DevBuf* b = (DevBuf*)calloc(1, sizeof(DevBuf));
+  if (!b) {
+    napi_throw_error(env, NULL, "q8hip.alloc: out of host memory");
+    return NULL;
+  }
+  int rc = q8_alloc(&b->ptr, (size_t)bytes);
+  if (rc != Q8_OK) {
+    free(b);
+    return throw_q8(env, rc);
+  }
+  b->bytes = (size_t)bytes;
+  napi_value ext;
+  if (napi_create_external(env, b, finalize_buf, NULL, &ext) != napi_ok) {
+    q8_free(b->ptr);
+    free(b);
+    napi_throw_error(env, NULL, "q8hip.alloc: napi_create_external failed");
+    return NULL;
+  }
+  return ext;
+}
+
+static napi_value js_free(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  DevBuf* b;
+  if (!get_args(env, info, 1, argv) || !arg_devbuf(env, argv[0], &b)) return NULL;
+  void* p = b->ptr;
+  b->ptr = NULL;
+  b->bytes = 0;
+  Q8_CHECK(env, q8_free(p));
+  return undefined(env);
+}
+
+static napi_value js_bytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  DevBuf* b;
+  if (!get_args(env, info, 1, argv) || !arg_devbuf(env, argv[0], &b)) return NULL;
+  napi_value r;
+  NAPI_CALL(env, napi_create_double(env, (double)b->bytes, &r));
+  return r;
+}
+
+/* upload(dev, hostArray): host -> device, blocking; sizes must fit. */
+static napi_value js_upload(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  DevBuf* b;
+  void* host;
+  size_t n;
+  if (!get_args(env, info, 2, argv) || !arg_devbuf(env, argv[0], &b) ||
+      !arg_host(env, argv[1], &host, &n))
+    return NULL;
+  if (n > b->bytes) {
+    napi_throw_range_error(env, NULL, "q8hip.upload: host array larger than the device buffer");
+    return NULL;
+  }
+  Q8_CHECK(env, q8_h2d(b->ptr, host, n, NULL));
+  return undefined(env);
+}
+
+/* download(hostArray, dev): device -> host, blocking; copies hostArray's size. */
+static napi_value js_download(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  DevBuf* b;
+  void* host;
+  size_t n;
+  if (!get_args(env, info, 2, argv) || !arg_host(env, argv[0], &host, &n) ||
+      !arg_devbuf(env, argv[1], &b))
+    return NULL;
+  if (n > b->bytes) {
+    napi_throw_range_error(env, NULL, "q8hip.download: host array larger than the device buffer");
+    return NULL;
+  }
+  Q8_CHECK(env, q8_d2h(host, b->ptr, n, NULL));
+  return undefined(env);
+}
+
+static napi_value js_sync(napi_env env, napi_callback_info info) {
+  (void)info;
+  Q8_CHECK(env, q8_stream_sync(NULL));
+  return undefined(env);
+}
+
+/* ---------------------------------------------------------------- ops */
+
+/* fillNormal(t, n, seed, offset, mean, std) / fillUniform(t, n, seed, offset, a, b) */
+static napi_value fill(napi_env env, napi_callback_info info, int normal) {
+  napi_value argv[6];
+  void* t;
+  int64_t n, seed, offset;
+  double a, b;
+  if (!get_args(env, info, 6, argv) || !arg_buf(env, argv[0], 0, &t) || !arg_i64(env, argv[1], &n) ||
+      !arg_i64(env, argv[2], &seed) || !arg_i64(env, argv[3], &offset) || !arg_f64(env, argv[4], &a) ||
+      !arg_f64(env, argv[5], &b))
+    return NULL;
+  if (normal)
+    Q8_CHECK(env, q8_fill_normal((float*)t, n, (uint32_t)seed, (uint64_t)offset, a, b, NULL));
+  else
+    Q8_CHECK(env, q8_fill_uniform((float*)t, n, (uint32_t)seed, (uint64_t)offset, a, b, NULL));
+  return undefined(env);
+}
+static napi_value js_fill_normal(napi_env env, napi_callback_info info) { return fill(env, info, 1); }
+static napi_value js_fill_uniform(napi_env env, napi_callback_info info) { return fill(env, info, 0); }
+
+/* quantizeStatic(x, n, scale, zeroPoint, target, q) */
+static napi_value js_quantize_static(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  void *x, *q;
+  int64_t n, target;
+  double s, zp;
+  if (!get_args(env, info, 6, argv) || !arg_buf(env, argv[0], 1, &x) || !arg_i64(env, argv[1], &n) ||
+      !arg_f64(env, argv[2], &s) || !arg_f64(env, argv[3], &zp) || !arg_i64(env, argv[4], &target) ||
+      !arg_buf(env, argv[5], 1, &q))
+    return NULL;
+  Q8_CHECK(env, q8_quantize_static((const float*)x, n, s, zp, (int)target, q, NULL));
+  return undefined(env);
+}
+
+/* quantizeRows(x, M, K, mode, q, scales) */
+static napi_value js_quantize_rows(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  void *x, *q, *sc;
+  int64_t M, K, mode;
+  if (!get_args(env, info, 6, argv) || !arg_buf(env, argv[0], 1, &x) || !arg_i64(env, argv[1], &M) ||
+      !arg_i64(env, argv[2], &K) || !arg_i64(env, argv[3], &mode) || !arg_buf(env, argv[4], 1, &q) ||
+      !arg_buf(env, argv[5], 1, &sc))
+    return NULL;
+  Q8_CHECK(env, q8_quantize_rows((const float*)x, M, K, (int)mode, (int8_t*)q, (double*)sc, NULL));
+  return undefined(env);
+}
+
+/* dequantize(q, src, M, K, scales, granularity, zeroPoint, y) */
+static napi_value js_dequantize(napi_env env, napi_callback_info info) {
+  napi_value argv[8];
+  void *q, *sc, *y;
+  int64_t src, M, K, gran;
+  double zp;
+  if (!get_args(env, info, 8, argv) || !arg_buf(env, argv[0], 1, &q) || !arg_i64(env, argv[1], &src) ||
+      !arg_i64(env, argv[2], &M) || !arg_i64(env, argv[3], &K) || !arg_buf(env, argv[4], 1, &sc) ||
+      !arg_i64(env, argv[5], &gran) || !arg_f64(env, argv[6], &zp) || !arg_buf(env, argv[7], 1, &y))
+    return NULL;
+  Q8_CHECK(env, q8_dequantize(q, (int)src, M, K, (const double*)sc, (int)gran, zp, (float*)y, NULL));
+  return undefined(env);
+}
+
+/* packWeight(W, rows, cols, axis, granularity, Wq, scales) */
+static napi_value js_pack_weight(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  void *w, *wq, *sc;
+  int64_t rows, cols, axis, gran;
+  if (!get_args(env, info, 7, argv) || !arg_buf(env, argv[0], 1, &w) || !arg_i64(env, argv[1], &rows) ||
+      !arg_i64(env, argv[2], &cols) || !arg_i64(env, argv[3], &axis) || !arg_i64(env, argv[4], &gran) ||
+      !arg_buf(env, argv[5], 1, &wq) || !arg_buf(env, argv[6], 1, &sc))
+    return NULL;
+  Q8_CHECK(env, q8_pack_weight((const float*)w, rows, cols, (int)axis, (int)gran, (int8_t*)wq,
+                               (double*)sc, NULL));
+  return undefined(env);
+}
+
+/* gemm(A, B, M, N, K, zpA, zpB, sA, sAmode, sB, sBmode, epi, sOut, bias, act, outKind, out) */
+static napi_value js_gemm(napi_env env, napi_callback_info info) {
+  napi_value argv[17];
+  void *A, *B, *sA, *sB, *bias, *out;
+  int64_t M, N, K, zpA, zpB, sAm, sBm, epi, act, ok;
+  double sOut;
+  if (!get_args(env, info, 17, argv) || !arg_buf(env, argv[0], 1, &A) || !arg_buf(env, argv[1], 1, &B) ||
+      !arg_i64(env, argv[2], &M) || !arg_i64(env, argv[3], &N) || !arg_i64(env, argv[4], &K) ||
+      !arg_i64(env, argv[5], &zpA) || !arg_i64(env, argv[6], &zpB) || !arg_buf(env, argv[7], 1, &sA) ||
+      !arg_i64(env, argv[8], &sAm) || !arg_buf(env, argv[9], 1, &sB) || !arg_i64(env, argv[10], &sBm) ||
+      !arg_i64(env, argv[11], &epi) || !arg_f64(env, argv[12], &sOut) ||
+      !arg_buf(env, argv[13], 1, &bias) || !arg_i64(env, argv[14], &act) ||
+      !arg_i64(env, argv[15], &ok) || !arg_buf(env, argv[16], 1, &out))
+    return NULL;
+  Q8_CHECK(env, q8_gemm((const int8_t*)A, (const int8_t*)B, M, N, K, (int32_t)zpA, (int32_t)zpB,
+                        (const double*)sA, (int)sAm, (const double*)sB, (int)sBm, (int)epi, sOut,
+                        (const float*)bias, (int)act, (int)ok, out, NULL));
+  return undefined(env);
+}
+
+/* siluMulQuantizeRows(g, u, M, K, h, q, scales) */
+static napi_value js_silu_mul_quantize_rows(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  void *g, *u, *h, *q, *sc;
+  int64_t M, K;
+  if (!get_args(env, info, 7, argv) || !arg_buf(env, argv[0], 1, &g) || !arg_buf(env, argv[1], 1, &u) ||
+      !arg_i64(env, argv[2], &M) || !arg_i64(env, argv[3], &K) || !arg_buf(env, argv[4], 1, &h) ||
+      !arg_buf(env, argv[5], 1, &q) || !arg_buf(env, argv[6], 1, &sc))
+    return NULL;
+  Q8_CHECK(env, q8_silu_mul_quantize_rows((const float*)g, (const float*)u, M, K, (float*)h,
+                                          (int8_t*)q, (double*)sc, NULL));
+  return undefined(env);
+}
+
+/* ---------------------------------------------------------------- module */
+
+static napi_value init_module(napi_env env, napi_value exports) {
+  const struct {
+    const char* name;
+    napi_callback fn;
+  } fns[] = {
+      {"version", js_version},
+      {"lastError", js_last_error},
+      {"deviceCount", js_device_count},
+      {"init", js_init},
+      {"alloc", js_alloc},
+      {"free", js_free},
+      {"bytes", js_bytes},
+      {"upload", js_upload},
+      {"download", js_download},
+      {"sync", js_sync},
+      {"fillNormal", js_fill_normal},
+      {"fillUniform", js_fill_uniform},
+      {"quantizeStatic", js_quantize_static},
+      {"quantizeRows", js_quantize_rows},
+      {"dequantize", js_dequantize},
+      {"packWeight", js_pack_weight},
+      {"gemm", js_gemm},
+      {"siluMulQuantizeRows", js_silu_mul_quantize_rows},
+  };
+  for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); ++i) {
+    napi_value f;
+    NAPI_CALL(env, napi_create_function(env, fns[i].name, NAPI_AUTO_LENGTH, fns[i].fn, NULL, &f));
+    NAPI_CALL(env, napi_set_named_property(env, exports, fns[i].name, f));
+  }
+  const struct {
+    const char* name;
+    int value;
+  } consts[] = {
+      {"Q8_I8", Q8_I8}, {"Q8_U8", Q8_U8}, {"Q8_I32", Q8_I32}, {"Q8_F32", Q8_F32},
+      {"Q8_PER_TENSOR", Q8_PER_TENSOR}, {"Q8_PER_TOKEN", Q8_PER_TOKEN},
+      {"Q8_PER_CHANNEL", Q8_PER_CHANNEL}, {"Q8_EPI_PT", Q8_EPI_PT}, {"Q8_EPI_ROWCOL", Q8_EPI_ROWCOL},
+      {"Q8_ACT_NONE", Q8_ACT_NONE}, {"Q8_ACT_RELU", Q8_ACT_RELU}, {"Q8_ACT_SILU", Q8_ACT_SILU},
+  };
+  for (size_t i = 0; i < sizeof(consts) / sizeof(consts[0]); ++i) {
+    napi_value v;
+    NAPI_CALL(env, napi_create_int32(env, consts[i].value, &v));
+    NAPI_CALL(env, napi_set_named_property(env, exports, consts[i].name, v));
+  }
+  return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, init_module)

@@ -1,0 +1,261 @@
+'use strict';
+/*
+ * Node-side tests of mlfw_amd/node (run by tests/test_node_host.py).
+ *   node hip_backend_test.js cpu          registration, TIR matching, errors (no GPU)
+ *   node hip_backend_test.js gpu <dir>    C1 through the 'hip' runtime backend and the
+ *                                          eager library; writes outputs into <dir>
+ * Mock registries and TIR nodes follow the reference's shapes
+ * (src/runtime/backend_registry.ts:14-32, src/backend/codegen_registry.ts:17-36,
+ * src/compiler/pipeline/external_codegen.ts:11-35, src/dispatcher/library.ts:30-72,
+ * node field names as read by src/backend/cpu/codegen.ts:428-552).
+ */
+const fs = require('fs');
+const path = require('path');
+const assert = require('assert');
+
+const ROOT = path.join(__dirname, '..', '..');
+const hip = require(path.join(ROOT, 'mlfw_amd', 'node', 'hip_backend.js'));
+
+let failures = 0;
+function test(name, fn) {
+  try { fn(); console.log(`ok   ${name}`); } catch (e) { failures++; console.log(`FAIL ${name}\n     ${e.stack}`); }
+}
+
+// ---------------------------------------------------------------- mocks
+function makeRegistries() {
+  const backends = new Map(), codegens = new Map(), providers = new Map(), ops = [], impls = new Map();
+  class Library {
+    constructor(ns, kind) { this.ns = ns; this.kind = kind; }
+    def(schema) { ops.push(`${this.ns}::${schema}`); return this; }
+    impl(name, key, fn) { impls.set(`${this.ns}::${name}`, { key, fn }); return this; }
+  }
+  return {
+    backends, codegens, providers, ops, impls,
+    registerBackend: (k, b) => backends.set(k, b),
+    registerExternalCodegen: (n, e) => codegens.set(n, e),
+    registerExternalCodegenProvider: (p) => providers.set(p.name, p),
+    FuncAttr: { EXTERNAL_CODEGEN: 'external_codegen' },
+    Library, DispatchKey: { CPU: 0, GPU: 1 },
+    tensors: { data: (t) => t.data, shape: (t) => t.shape, make: (data, shape) => ({ data, shape }) },
+  };
+}
+
+const V = (name) => ({ type: 'VariableNode', name });
+const F = (value) => ({ type: 'FloatImmNode', value });
+const I = (value) => ({ type: 'IntImmNode', value });
+const buf = (name, shape, dtype) => ({ name, shape, dtype });
+const load = (b, idx) => ({ type: 'BufferLoadNode', buffer: b, indices: idx });
+const ext = (externName, args) => ({ type: 'CallExternNode', externName, args });
+const math = (op, a, b) => ({ type: 'MathOpNode', op, a, b });
+const cast = (expr, toDtype) => ({ type: 'CastNode', expr, toDtype });
+function primFunc(name, params, blocks) {
+  const attrs = {};
+  const bufferMap = new Map(params.map((b, i) => [`v${i}`, b]));
+  let body = blocks.length === 1 ? blocks[0] : { type: 'SeqNode', stmts: blocks };
+  body = { type: 'ForNode', body };
+  return { name, params, bufferMap, body, attrs, setAttr(k, v) { attrs[k] = v; return this; } };
+}
+function quantizePF(scale, zp, tgt) {
+  const x = buf('x', [32, 128], 'f32'), q = buf('q', [32, 128], tgt);
+  let e = math('/', load(x, [V('i'), V('j')]), F(scale));
+  if (zp !== 0) e = math('+', e, F(zp));
+  const value = cast(ext('min', [ext('max', [ext('round', [e]), F(tgt === 'ui8' ? 0 : -128)]), F(tgt === 'ui8' ? 255 : 127)]), tgt);
+  const block = { type: 'BlockNode', name: 'quantize_block_0', reads: [{ buffer: x }], writes: [{ buffer: q }],
+                  body: { type: 'BufferStoreNode', buffer: q, indices: [V('i'), V('j')], value } };
+  return primFunc('quant', [x, q], [block]);
+}
+function dequantizePF(scale, zp, src) {
+  const q = buf('q', [32, 128], src), y = buf('y', [32, 128], 'f32');
+  let e = cast(load(q, [V('i'), V('j')]), 'f32');
+  if (zp !== 0) e = math('-', e, F(zp));
+  const block = { type: 'BlockNode', name: 'dequantize_block', reads: [{ buffer: q }], writes: [{ buffer: y }],
+                  body: { type: 'BufferStoreNode', buffer: y, indices: [V('i'), V('j')], value: math('*', e, F(scale)) } };
+  return primFunc('deq', [q, y], [block]);
+}
+function qdotPF(M, N, K, layout, zpA, zpB) {
+  const a = buf('a', [M, K], 'i8'), b = buf('b', layout === 'KN' ? [K, N] : [N, K], 'i8'), c = buf('c', [M, N], 'i32');
+  const m = V('m'), n = V('n'), k = V('k');
+  let la = cast(load(a, [m, k]), 'i32'), lb = cast(load(b, layout === 'KN' ? [k, n] : [n, k]), 'i32');
+  if (zpA) la = math('-', la, I(zpA));
+  if (zpB) lb = math('-', lb, I(zpB));
+  const init = { type: 'BlockNode', name: 'qmatmul_init', reads: [], writes: [{ buffer: c }],
+                 body: { type: 'BufferStoreNode', buffer: c, indices: [m, n], value: I(0) } };
+  const acc = { type: 'BlockNode', name: 'qmatmul_acc_1', reads: [{ buffer: a }, { buffer: b }], writes: [{ buffer: c }],
+                body: { type: 'BufferStoreNode', buffer: c, indices: [m, n],
+                        value: math('+', load(c, [m, n]), math('*', la, lb)) } };
+  return primFunc('qdot', [a, b, c], [init, acc]);
+}
+
+// ---------------------------------------------------------------- CPU tests
+function cpuTests() {
+  test('registerHip plugs into all three registries', () => {
+    const r = makeRegistries();
+    const res = hip.registerHip(r);
+    assert.strictEqual(res.kind, 'hip');
+    const be = r.backends.get('hip');
+    for (const k of ['instantiate', 'runSync', 'runAsync', 'isAsync']) assert.strictEqual(typeof be[k], 'function', k);
+    assert.strictEqual(be.isAsync(), false);
+    const cg = r.codegens.get('hip_int8');
+    assert.strictEqual(cg.runtimeKind, 'hip');
+    const out = cg.compile({ params: [] }, hip.hipTarget(), { op: 'quantize', outputIndices: [1] });
+    assert.strictEqual(out.source, '');
+    assert.deepStrictEqual(out.metadata.outputIndices, [1]);
+    assert.strictEqual(out.metadata.kind, 'hip');
+    assert.ok(r.ops.some((s) => s.startsWith('q8::quantize_per_token(')));
+    assert.strictEqual(r.impls.get('q8::qlinear').key, 1);
+  });
+
+  test('provider is enabled only for the hip target with quantization on', () => {
+    const p = hip.createHipProvider();
+    assert.strictEqual(p.enabled({ quantization: { enabled: true } }, hip.hipTarget()), true);
+    assert.strictEqual(p.enabled({ quantization: { enabled: false } }, hip.hipTarget()), false);
+    assert.strictEqual(p.enabled({ quantization: { enabled: true } }, { kind: 'cuda' }), false);
+  });
+
+  test('detects quantize with its static scale, zero point and target dtype', () => {
+    const d = hip.detectInt8Kernel(quantizePF(6 / 127, 0, 'i8'));
+    assert.deepStrictEqual(d, { op: 'quantize', n: 4096, scale: 6 / 127, zeroPoint: 0, targetDtype: 'i8',
+                                inIdx: 0, outIdx: 1, outputIndices: [1] });
+    const u = hip.detectInt8Kernel(quantizePF(1 / 255, 3, 'ui8'));
+    assert.strictEqual(u.zeroPoint, 3);
+    assert.strictEqual(u.targetDtype, 'ui8');
+  });
+
+  test('detects dequantize from i8, ui8 and i32', () => {
+    for (const src of ['i8', 'ui8', 'i32']) {
+      const d = hip.detectInt8Kernel(dequantizePF(0.02, src === 'ui8' ? 128 : 0, src));
+      assert.strictEqual(d.op, 'dequantize');
+      assert.strictEqual(d.srcDtype, src);
+      assert.strictEqual(d.scale, 0.02);
+    }
+  });
+
+  test('detects quantized_dot layout from the reduction index, also when square', () => {
+    for (const [M, N, K] of [[32, 64, 128], [64, 64, 64]]) {
+      for (const layout of ['NK', 'KN']) {
+        const d = hip.detectInt8Kernel(qdotPF(M, N, K, layout, 0, 0));
+        assert.ok(d, `${layout} ${M}x${N}x${K}`);
+        assert.strictEqual(d.rhsLayout, layout);
+        assert.deepStrictEqual([d.M, d.N, d.K, d.aIdx, d.bIdx, d.outIdx], [M, N, K, 0, 1, 2]);
+      }
+    }
+    const z = hip.detectInt8Kernel(qdotPF(8, 8, 16, 'NK', 3, -2));
+    assert.deepStrictEqual([z.zpA, z.zpB], [3, -2]);
+  });
+
+  test('annotate tags only the int8 PrimFuncs', () => {
+    const p = hip.createHipProvider('external_codegen');
+    const funcs = [quantizePF(0.1, 0, 'i8'), qdotPF(4, 4, 16, 'NK', 0, 0),
+                   primFunc('other', [buf('a', [4], 'f32')], [{ type: 'BlockNode', name: 'add_block', reads: [], writes: [], body: null }])];
+    p.annotate(funcs);
+    assert.strictEqual(funcs[0].attrs.external_codegen.name, 'hip_int8');
+    assert.strictEqual(funcs[1].attrs.external_codegen.info.op, 'quantized_dot');
+    assert.strictEqual(funcs[2].attrs.external_codegen, undefined);
+  });
+
+  test('runtime backend validates descriptors before touching a device', () => {
+    const be = hip.createHipRuntimeBackend();
+    assert.throws(() => be.instantiate({ metadata: { kind: 'cuda' } }), /not hip/);
+    assert.throws(() => be.instantiate({ metadata: { kind: 'hip' } }), /no q8 descriptor/);
+    const inst = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'quantize', n: 4, scale: 1, zeroPoint: 0,
+                                                                 targetDtype: 'i8', inIdx: 0, outIdx: 1 } } });
+    assert.throws(() => be.runSync(inst, [new Float64Array(4), new Int8Array(4)], null), /Float32Array/);
+    assert.throws(() => be.runSync(inst, [new Float32Array(4), new Int8Array(4)], [7]), /dynamic shapes/);
+  });
+
+  test('the addon loads and reports errors as coded exceptions', () => {
+    const a = require(path.join(ROOT, 'mlfw_amd', 'node', 'index.js'));
+    assert.strictEqual(a.version(), 1);
+    assert.ok(a.deviceCount() >= 0);
+    assert.throws(() => a.quantizeStatic(null, 10, 0.0, 0, a.Q8_I8, null), (e) => e.code === 'Q8_ERR_1');
+    assert.throws(() => a.gemm(null, null, 4, 4, 16, 0, 0, null, 0, null, 0, 9, 0, null, 0, a.Q8_F32, null),
+                  (e) => e.code === 'Q8_ERR_1' && /bad epi/.test(e.message));
+    assert.throws(() => a.upload({}, new Float32Array(1)), TypeError);
+  });
+}
+
+// ---------------------------------------------------------------- GPU tests
+function readArr(dir, name, T) {
+  const b = fs.readFileSync(path.join(dir, name));
+  return new T(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
+}
+function writeArr(dir, name, a) {
+  fs.writeFileSync(path.join(dir, name), Buffer.from(a.buffer, a.byteOffset, a.byteLength));
+}
+
+function gpuTests(dir) {
+  const a = require(path.join(ROOT, 'mlfw_amd', 'node', 'index.js'));
+  a.init(0);
+  const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json')));
+  const X = readArr(dir, 'X.bin', Float32Array), Xq = readArr(dir, 'Xq.bin', Int8Array);
+  const Wq = readArr(dir, 'Wq.bin', Int8Array), sW = readArr(dir, 'sW.bin', Float64Array);
+  const bias = readArr(dir, 'bias.bin', Float32Array);
+  const { M, N, K, sX } = meta;
+  const r = makeRegistries();
+  hip.registerHip(r);
+  const be = r.backends.get('hip');
+  const cg = r.codegens.get('hip_int8');
+
+  test('runtime backend: compiled quantize (static scale) on the GPU', () => {
+    const kern = cg.compile({}, hip.hipTarget(), { op: 'quantize', n: M * K, scale: sX, zeroPoint: 0,
+                                                   targetDtype: 'i8', inIdx: 0, outIdx: 1, outputIndices: [1] });
+    const inst = be.instantiate(kern);
+    const q = new Int8Array(M * K);
+    be.runSync(inst, [X, q], null);
+    writeArr(dir, 'out_quantize.bin', q);
+  });
+
+  test('runtime backend: quantized_dot [N,K] and [K,N] weights on the GPU', () => {
+    for (const layout of ['NK', 'KN']) {
+      let B = Wq;
+      if (layout === 'KN') { B = new Int8Array(K * N); for (let n = 0; n < N; n++) for (let k = 0; k < K; k++) B[k * N + n] = Wq[n * K + k]; }
+      const kern = cg.compile({}, hip.hipTarget(), { op: 'quantized_dot', M, N, K, rhsLayout: layout, zpA: 0, zpB: 0,
+                                                     aIdx: 0, bIdx: 1, outIdx: 2, outputIndices: [2] });
+      const acc = new Int32Array(M * N);
+      be.runSync(be.instantiate(kern), [Xq, B, acc], null);
+      writeArr(dir, `out_qdot_${layout}.bin`, acc);
+    }
+  });
+
+  test('runtime backend: dequantize of int32 accumulators (per-tensor epilogue E-pt)', () => {
+    const acc = readArr(dir, 'out_qdot_NK.bin', Int32Array);
+    const kern = cg.compile({}, hip.hipTarget(), { op: 'dequantize', n: M * N, scale: meta.sOut, zeroPoint: 0,
+                                                   srcDtype: 'i32', inIdx: 0, outIdx: 1, outputIndices: [1] });
+    const y = new Float32Array(M * N);
+    be.runSync(be.instantiate(kern), [acc, y], null);
+    writeArr(dir, 'out_dequant_i32.bin', y);
+  });
+
+  test('runtime backend: fused qlinear (C1: per-tensor dynamic quantize + GEMM + per-channel epilogue + bias)', () => {
+    const y = new Float32Array(M * N);
+    const inst = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'qlinear', M, N, K, xIdx: 0, wqIdx: 1, wsIdx: 2,
+                                                                  biasIdx: 3, outIdx: 4, granularity: 'per_tensor', act: 'none' } } });
+    be.runSync(inst, [X, Wq, sW, bias, y], null);
+    writeArr(dir, 'out_c1.bin', y);
+  });
+
+  test('eager library: q8::quantize_per_token and q8::dequantize_per_token', () => {
+    const qpt = r.impls.get('q8::quantize_per_token').fn;
+    const dpt = r.impls.get('q8::dequantize_per_token').fn;
+    const [q, s] = qpt({ data: X, shape: [M, K] });
+    writeArr(dir, 'out_qpt_q.bin', q.data);
+    writeArr(dir, 'out_qpt_s.bin', s.data);
+    const y = dpt(q, s);
+    assert.deepStrictEqual(y.shape, [M, K]);
+    writeArr(dir, 'out_dpt.bin', y.data);
+  });
+
+  test('async path resolves to the same result', () => {
+    const kern = cg.compile({}, hip.hipTarget(), { op: 'quantize', n: M * K, scale: sX, zeroPoint: 0,
+                                                   targetDtype: 'i8', inIdx: 0, outIdx: 1, outputIndices: [1] });
+    const q = new Int8Array(M * K);
+    return be.runAsync(be.instantiate(kern), [X, q], null);
+  });
+}
+
+const mode = process.argv[2];
+if (mode === 'cpu') cpuTests();
+else if (mode === 'gpu') gpuTests(process.argv[3]);
+else { console.error('usage: hip_backend_test.js cpu | gpu <dir>'); process.exit(2); }
+if (failures) { console.log(`${failures} failed`); process.exit(1); }
+console.log('all passed');

@@ -1,0 +1,83 @@
+"""The Node host side (mlfw_amd/node: N-API addon + hip_backend.js).
+
+CPU: registration into mock registries shaped like the reference's, TIR
+matching of QuantizationPass's lowered ops, argument errors (no device).
+GPU: C1 through the 'hip' runtime backend and the eager library, every
+output compared bit for bit with the oracle.
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SCRIPT = os.path.join(ROOT, "tests", "node", "hip_backend_test.js")
+ADDON = os.path.join(ROOT, "mlfw_amd", "node", "q8hip.node")
+NODE = shutil.which("node")
+
+needs_node = pytest.mark.skipif(NODE is None, reason="node is not installed")
+
+
+def run_node(*args, timeout=120):
+    r = subprocess.run([NODE, SCRIPT, *args], capture_output=True, text=True, timeout=timeout)
+    print(r.stdout)
+    print(r.stderr)
+    return r
+
+
+@needs_node
+def test_node_host_cpu():
+    if not os.path.exists(ADDON):
+        pytest.fail("q8hip.node is not built: run `python -m mlfw_amd.build`")
+    r = run_node("cpu")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all passed" in r.stdout
+
+
+def same_bits(a, b, what):
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype, (what, a.shape, b.shape, a.dtype, b.dtype)
+    bad = np.nonzero(a.view(np.uint8).reshape(-1, a.itemsize) != b.view(np.uint8).reshape(-1, b.itemsize))[0]
+    assert bad.size == 0, f"{what}: {np.unique(bad).size} elements differ"
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_host_gpu_c1(tmp_path, oracle):
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from oracle import configs as OC
+    inp, y_ref = OC.c1()
+    X, W, bias = inp["X"], inp["W"], inp["bias"]
+    M, K = X.shape
+    N = W.shape[0]
+    Wq, sW = OC.pack_pc(W, 0)
+    sX = oracle.scale_per_tensor(X)
+    Xq = oracle.quantize(X, sX)
+    s_out = sX * float(sW[0])
+    for name, arr in (("X", X), ("Xq", Xq), ("Wq", Wq), ("sW", sW), ("bias", bias)):
+        np.ascontiguousarray(arr).tofile(tmp_path / f"{name}.bin")
+    (tmp_path / "meta.json").write_text(json.dumps({"M": M, "N": N, "K": K, "sX": sX, "sOut": s_out}))
+    r = run_node("gpu", str(tmp_path))
+    assert r.returncode == 0, r.stdout + r.stderr
+
+    def out(name, dt, shape):
+        return np.fromfile(tmp_path / f"{name}.bin", dtype=dt).reshape(shape)
+
+    same_bits(out("out_quantize", np.int8, (M, K)), Xq, "compiled quantize")
+    acc = oracle.quantized_dot(Xq, Wq, b_layout=1)
+    same_bits(out("out_qdot_NK", np.int32, (M, N)), acc, "quantized_dot [N,K]")
+    same_bits(out("out_qdot_KN", np.int32, (M, N)), acc, "quantized_dot [K,N]")
+    same_bits(out("out_dequant_i32", np.float32, (M, N)), oracle.dequantize(acc, s_out), "E-pt")
+    same_bits(out("out_c1", np.float32, (M, N)), y_ref, "C1 fused qlinear")
+    s_tok = oracle.scales_per_token(X)
+    q_tok = oracle.quantize_rows(X, s_tok)
+    same_bits(out("out_qpt_q", np.int8, (M, K)), q_tok, "eager quantize_per_token codes")
+    same_bits(out("out_qpt_s", np.float64, (M,)), s_tok, "eager quantize_per_token scales")
+    same_bits(out("out_dpt", np.float32, (M, K)), oracle.dequantize_rows(q_tok, s_tok),
+              "eager dequantize_per_token")
