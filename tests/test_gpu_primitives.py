@@ -292,8 +292,9 @@ def test_qlinear_pt_epilogue(ops, oracle):
     same_bits(host(y), oracle.epilogue(acc, "pt", s_out=s_out))
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
-@pytest.mark.parametrize("N,K", [(4096, 4096), (1000, 4096), (77, 8192 + 512)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 13, 15, 16])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1000, 4096), (77, 8192 + 512), (11008, 4096),
+                                 (5, 16), (33, 16400)])
 def test_gemv(ops, oracle, M, N, K):
     rng = oracle.Rng(M * 31 + N)
     x = rng.normal((M, K))
