@@ -256,6 +256,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy three times: the known-size "
+                         "reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -286,6 +289,19 @@ def main():
                 "traffic": traffic.get("hbm_bytes_per_launch"),
                 "kernel": GEMM_KERNEL, "avg_us": r["gemm_avg_ms"] * 1e3,
                 "algorithmic_ops_per_launch": GEMM_OPS}
+
+    if args.copy_calibration:
+        # a plain elementwise copy of known size: 16384 rows of 16 KiB read from
+        # every other 16 KiB of a 512 MiB buffer (a strided view, so torch runs
+        # its direct-copy kernel rather than a DMA blit) and written densely
+        big = torch.ones((16384, 8192), dtype=torch.float32, device="cuda")
+        src = big[:, :4096]
+        dst = torch.empty((16384, 4096), dtype=torch.float32, device="cuda")
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 3 x {dst.numel() * 4} B read + {dst.numel() * 4} B written")
+        del big, src, dst
 
     secondary = {}
     if not args.no_secondary:
