@@ -67,6 +67,19 @@ extern "C" {
 #define Q8_ACT_RELU 1      /* Math.max(v, 0): NaN stays NaN, -0 -> +0 */
 #define Q8_ACT_SILU 2      /* v * (1 / (1 + exp(-v))), every step rounded to f32 */
 
+/* calibration modes (CalibrationResult._mode, calibration.ts:192,246-268) */
+#define Q8_CALIB_MINMAX     0
+#define Q8_CALIB_PERCENTILE 1   /* 99.9th percentile of the histogram, symmetric */
+#define Q8_CALIB_ENTROPY    2   /* KL-divergence threshold, symmetric */
+
+/* QuantizationScheme (src/compiler/ir/graph/quantization_types.ts:4-8) */
+#define Q8_SCHEME_PER_TENSOR_SYMMETRIC  0
+#define Q8_SCHEME_PER_TENSOR_ASYMMETRIC 1
+#define Q8_SCHEME_PER_CHANNEL           2
+
+#define Q8_OBS_MAX_BINS 8192    /* largest histogram an observer may keep */
+#define Q8_OBS_SUMMARY  9       /* doubles written by q8_observer_read */
+
 /* ---------------------------------------------------------------- runtime */
 
 /* Library version (Q8HIP_VERSION). */
@@ -211,6 +224,55 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
  * NULL (the fp32 h is then not written). */
 int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K,
                               float* h_out, int8_t* q, double* scales, void* stream);
+
+/* ------------------------------------------------------------ calibration */
+
+/* An observer is a device buffer of q8_observer_state_bytes(num_bins) bytes
+ * holding a ValueObserver (min / max / count) and, when enabled, its
+ * HistogramCollector (src/compiler/analysis/calibration.ts:11-126).  The
+ * caller allocates it (q8_alloc) and owns it; calls on one observer are
+ * ordered by the stream they are made on. */
+int q8_observer_state_bytes(int num_bins, size_t* bytes);
+
+/* new ValueObserver() (calibration.ts:17-22), plus enableHistogram(num_bins)
+ * (:36-38) when histogram != 0.  1 <= num_bins <= Q8_OBS_MAX_BINS. */
+int q8_observer_reset(void* state, int num_bins, int histogram, void* stream);
+
+/* ValueObserver.update(x) (calibration.ts:24-34) with HistogramCollector.update
+ * (:58-80, _initRange :82-92, _expandAndRebucket :94-126) for n fp32 values
+ * in device memory.  NaN values count but are not binned, as in the
+ * reference.  Enqueued only: no host synchronisation. */
+int q8_observer_update(void* state, const float* x, int64_t n, void* stream);
+
+/* Synchronously reads an observer back.  summary[Q8_OBS_SUMMARY] =
+ * {min, max, count, histogram, initialized, range_min, range_max,
+ *  total_count, num_bins}; bins (may be NULL) receives num_bins counts.
+ * min is -0.0 or +0.0 when the smallest values seen are zeros of both signs
+ * (the reference keeps whichever came first). */
+int q8_observer_read(const void* state, double* summary, double* bins, void* stream);
+
+/* HistogramCollector.computePercentileThreshold(percentile)
+ * (calibration.ts:130-141) on a read-back observer (summary and bins as
+ * written by q8_observer_read).  Host only. */
+int q8_hist_percentile(const double* summary, const double* bins, double percentile,
+                       double* threshold);
+
+/* HistogramCollector.computeEntropyThreshold(num_quant_bins)
+ * (calibration.ts:143-187): the threshold whose num_quant_bins-level
+ * requantisation of the histogram has the least KL divergence.  Host only. */
+int q8_hist_entropy(const double* summary, const double* bins, int num_quant_bins,
+                    double* threshold);
+
+/* CalibrationResult.getQuantParams (calibration.ts:246-268) on a read-back
+ * observer: mode Q8_CALIB_*, scheme Q8_SCHEME_*, unsigned_ = dtype ui8.
+ * Percentile (0.999) / entropy (255 levels, 256 for ui8) thresholds apply
+ * unless the scheme is per-tensor asymmetric; the range then goes through
+ * QuantizationParams.fromRange (quantization_types.ts:248-263), whose
+ * zero-point form serves every scheme but the symmetric one.
+ * *has_params = 0 (and Q8_OK) when the observer saw no values (getRange ->
+ * null).  Host only; bins may be NULL for Q8_CALIB_MINMAX. */
+int q8_calib_params(const double* summary, const double* bins, int mode, int scheme,
+                    int unsigned_, double* scale, double* zero_point, int* has_params);
 
 #ifdef __cplusplus
 }

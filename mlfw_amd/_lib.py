@@ -28,6 +28,10 @@ Q8_I8, Q8_U8, Q8_I32, Q8_F32 = 0, 1, 2, 3
 Q8_PER_TENSOR, Q8_PER_TOKEN, Q8_PER_CHANNEL = 0, 1, 2
 Q8_EPI_PT, Q8_EPI_ROWCOL = 0, 1
 Q8_ACT_NONE, Q8_ACT_RELU, Q8_ACT_SILU = 0, 1, 2
+Q8_CALIB_MINMAX, Q8_CALIB_PERCENTILE, Q8_CALIB_ENTROPY = 0, 1, 2
+Q8_SCHEME_PER_TENSOR_SYMMETRIC, Q8_SCHEME_PER_TENSOR_ASYMMETRIC, Q8_SCHEME_PER_CHANNEL = 0, 1, 2
+Q8_OBS_MAX_BINS = 8192
+Q8_OBS_SUMMARY = 9
 
 
 class Q8Error(RuntimeError):
@@ -67,6 +71,13 @@ SIGNATURES = {
     "q8_gemv": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                 _int, _vp, _vp],
     "q8_silu_mul_quantize_rows": [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp],
+    "q8_observer_state_bytes": [_int, _vp],
+    "q8_observer_reset": [_vp, _int, _int, _vp],
+    "q8_observer_update": [_vp, _vp, _i64, _vp],
+    "q8_observer_read": [_vp, _vp, _vp, _vp],
+    "q8_hist_percentile": [_vp, _vp, _dbl, _vp],
+    "q8_hist_entropy": [_vp, _vp, _int, _vp],
+    "q8_calib_params": [_vp, _vp, _int, _int, _int, _vp, _vp, _vp],
 }
 
 _lib = None

@@ -22,7 +22,7 @@ NODE_ADDON = os.path.join(NODE_DIR, "q8hip.node")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip"]
+SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip"]
 
 # IEEE arithmetic everywhere (the kernels reproduce the reference's f64 /
 # f32 rounding bit for bit), no packed-FP32 instructions, gfx950 only.

@@ -7,10 +7,12 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "../../include/q8hip.h"
 #include "q8_internal.h"
@@ -90,6 +92,89 @@ bool mul_ok(int64_t a, int64_t b) { return a >= 0 && b >= 0 && (b == 0 || a <= I
   } while (0)
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- calibration scale selection (host side of the observer) ----
+
+// JS Math.max / Math.min on doubles (NaN wins; max(-0,+0) = +0).
+double js_max(double a, double b) {
+  if (std::isnan(a) || std::isnan(b)) return NAN;
+  if (a == b) return std::signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+double js_min(double a, double b) {
+  if (std::isnan(a) || std::isnan(b)) return NAN;
+  if (a == b) return std::signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+// `v || 1e-10` for a number.
+double or_tiny(double v) { return (v == 0.0 || std::isnan(v)) ? 1e-10 : v; }
+// Math.round: floor(y + 0.5) computed without the double-rounding of y + 0.5.
+double js_round(double y) {
+  if (!std::isfinite(y)) return y;
+  const double f = std::floor(y);
+  const double r = (y - f >= 0.5) ? f + 1.0 : f;
+  return (r == 0.0 && std::signbit(y)) ? -0.0 : r;
+}
+
+// QuantizationParams.fromRange, 8 bits (quantization_types.ts:248-263).
+void params_from_range(double mn, double mx, bool symmetric, bool is_u8, double* scale,
+                       double* zp) {
+  if (symmetric) {
+    *scale = or_tiny(js_max(std::fabs(mn), std::fabs(mx)) / 127.0);
+    *zp = 0.0;
+    return;
+  }
+  const double cmin = is_u8 ? 0.0 : -128.0, cmax = is_u8 ? 255.0 : 127.0;
+  const double s = or_tiny(mx - mn) / (cmax - cmin);
+  *scale = s;
+  *zp = js_max(cmin, js_min(cmax, js_round(cmin - mn / s)));
+}
+
+// computePercentileThreshold (calibration.ts:128-139).
+double hist_percentile(const double* bins, int nb, double lo, double hi, double total, double p) {
+  const double target = total * p, w = (hi - lo) / nb;
+  double cum = 0.0;
+  for (int i = 0; i < nb; ++i) {
+    cum += bins[i];
+    if (cum >= target) return lo + (i + 1) * w;
+  }
+  return hi;
+}
+
+// computeEntropyThreshold (calibration.ts:141-187): the threshold bin count
+// t in [nq, nb] whose nq-level requantisation of bins[0..t) has the least
+// KL divergence from the normalised histogram.  Every sum is formed left to
+// right, in the reference's order, so the chosen t matches it exactly.
+double hist_entropy(const double* bins, int nb, double lo, double hi, double total, int nq) {
+  if (total == 0.0) return hi;
+  std::vector<double> ref(nb), q(nb);
+  for (int i = 0; i < nb; ++i) ref[i] = bins[i] / total;
+  int best_t = nb;
+  double best_kl = INFINITY;
+  for (int t = nq; t <= nb; ++t) {
+    const double qw = (double)t / nq;
+    for (int j = 0; j < t; ++j) q[j] = 0.0;
+    for (int i = 0; i < nq; ++i) {
+      const int start = (int)std::floor(i * qw);
+      const double e = std::floor((i + 1) * qw);
+      const int end = e < t ? (int)e : t;
+      double sum = 0.0;
+      for (int j = start; j < end; ++j) sum += ref[j];
+      if (end > start) {
+        const double avg = sum / (end - start);
+        for (int j = start; j < end; ++j) q[j] = avg;
+      }
+    }
+    double kl = 0.0;
+    for (int i = 0; i < t; ++i)
+      if (ref[i] > 0.0 && q[i] > 0.0) kl += ref[i] * std::log(ref[i] / q[i]);
+    if (kl < best_kl) {
+      best_kl = kl;
+      best_t = t;
+    }
+  }
+  return lo + best_t * ((hi - lo) / nb);
+}
 
 }  // namespace
 
@@ -329,6 +414,134 @@ int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_silu_mul_quant_rows(g, u, M, K, h_out, q, scales, as_stream(stream)),
                   "q8_silu_mul_quantize_rows launch");
+}
+
+int q8_observer_state_bytes(int num_bins, size_t* bytes) {
+  Q8_REQUIRE(num_bins >= 1 && num_bins <= Q8_OBS_MAX_BINS,
+             "q8_observer_state_bytes: num_bins must be in [1, %d] (got %d)", Q8_OBS_MAX_BINS,
+             num_bins);
+  Q8_REQUIRE(bytes != nullptr, "q8_observer_state_bytes: bytes is NULL");
+  *bytes = q8::obs_state_bytes(num_bins);
+  return Q8_OK;
+}
+
+int q8_observer_reset(void* state, int num_bins, int histogram, void* stream) {
+  Q8_REQUIRE(state != nullptr, "q8_observer_reset: state is NULL");
+  Q8_REQUIRE((reinterpret_cast<uintptr_t>(state) & 7) == 0, "q8_observer_reset: state must be 8-byte aligned");
+  Q8_REQUIRE(num_bins >= 1 && num_bins <= Q8_OBS_MAX_BINS,
+             "q8_observer_reset: num_bins must be in [1, %d] (got %d)", Q8_OBS_MAX_BINS, num_bins);
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_obs_reset(static_cast<q8::ObsState*>(state), num_bins,
+                                       histogram ? 1 : 0, as_stream(stream)),
+                  "q8_observer_reset launch");
+}
+
+int q8_observer_update(void* state, const float* x, int64_t n, void* stream) {
+  Q8_REQUIRE(state != nullptr, "q8_observer_update: state is NULL");
+  Q8_REQUIRE((reinterpret_cast<uintptr_t>(state) & 7) == 0, "q8_observer_update: state must be 8-byte aligned");
+  Q8_REQUIRE(n >= 0, "q8_observer_update: n must be >= 0");
+  Q8_REQUIRE(n == 0 || x != nullptr, "q8_observer_update: x is NULL");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_obs_update(static_cast<q8::ObsState*>(state), x, n, as_stream(stream)),
+                  "q8_observer_update launch");
+}
+
+int q8_observer_read(const void* state, double* summary, double* bins, void* stream) {
+  Q8_REQUIRE(state != nullptr && summary != nullptr, "q8_observer_read: NULL pointer");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  q8::ObsState h;
+  hipStream_t s = as_stream(stream);
+  hipError_t e = hipMemcpyAsync(&h, state, sizeof(h), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "q8_observer_read");
+  if (h.num_bins < 1 || h.num_bins > Q8_OBS_MAX_BINS)
+    return fail(Q8_ERR_INVALID, "q8_observer_read: state was not set up by q8_observer_reset");
+  const bool any = h.min_key != 0x7fffffff;
+  auto key_to_double = [](int k) {
+    const int bits = k < 0 ? (k ^ 0x7fffffff) : k;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return (double)f;
+  };
+  summary[0] = any ? key_to_double(h.min_key) : INFINITY;
+  summary[1] = any ? key_to_double(h.max_key) : -INFINITY;
+  summary[2] = (double)h.count;
+  summary[3] = h.has_hist;
+  summary[4] = h.initialized;
+  summary[5] = h.range_min;
+  summary[6] = h.range_max;
+  summary[7] = (double)h.total_count;
+  summary[8] = h.num_bins;
+  if (bins) {
+    std::vector<unsigned long long> b(h.num_bins);
+    const char* src = static_cast<const char*>(state) + q8::Q8_OBS_HEADER;
+    e = hipMemcpyAsync(b.data(), src, b.size() * 8, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "q8_observer_read bins");
+    for (int i = 0; i < h.num_bins; ++i) bins[i] = (double)b[i];
+  }
+  g_err[0] = '\0';
+  return Q8_OK;
+}
+
+static int hist_args(const char* who, const double* summary, const double* bins) {
+  Q8_REQUIRE(summary && bins, "%s: NULL pointer", who);
+  const double nb = summary[8];
+  Q8_REQUIRE(nb >= 1 && nb <= Q8_OBS_MAX_BINS && nb == (int)nb,
+             "%s: summary does not come from q8_observer_read", who);
+  return Q8_OK;
+}
+
+int q8_hist_percentile(const double* summary, const double* bins, double percentile,
+                       double* threshold) {
+  int rc = hist_args("q8_hist_percentile", summary, bins);
+  if (rc != Q8_OK) return rc;
+  Q8_REQUIRE(threshold != nullptr, "q8_hist_percentile: threshold is NULL");
+  *threshold = hist_percentile(bins, (int)summary[8], summary[5], summary[6], summary[7], percentile);
+  return Q8_OK;
+}
+
+int q8_hist_entropy(const double* summary, const double* bins, int num_quant_bins,
+                    double* threshold) {
+  int rc = hist_args("q8_hist_entropy", summary, bins);
+  if (rc != Q8_OK) return rc;
+  Q8_REQUIRE(threshold != nullptr, "q8_hist_entropy: threshold is NULL");
+  Q8_REQUIRE(num_quant_bins >= 1, "q8_hist_entropy: num_quant_bins must be >= 1");
+  *threshold = hist_entropy(bins, (int)summary[8], summary[5], summary[6], summary[7], num_quant_bins);
+  return Q8_OK;
+}
+
+int q8_calib_params(const double* summary, const double* bins, int mode, int scheme,
+                    int unsigned_, double* scale, double* zero_point, int* has_params) {
+  Q8_REQUIRE(summary && scale && zero_point && has_params, "q8_calib_params: NULL pointer");
+  Q8_REQUIRE(mode == Q8_CALIB_MINMAX || mode == Q8_CALIB_PERCENTILE || mode == Q8_CALIB_ENTROPY,
+             "q8_calib_params: bad mode %d", mode);
+  Q8_REQUIRE(scheme == Q8_SCHEME_PER_TENSOR_SYMMETRIC || scheme == Q8_SCHEME_PER_TENSOR_ASYMMETRIC ||
+                 scheme == Q8_SCHEME_PER_CHANNEL,
+             "q8_calib_params: bad scheme %d", scheme);
+  *has_params = 0;
+  if (summary[2] == 0.0) return Q8_OK;                      // getRange -> null
+  const bool hist = summary[3] != 0.0 && mode != Q8_CALIB_MINMAX &&
+                    scheme != Q8_SCHEME_PER_TENSOR_ASYMMETRIC;
+  double lo = summary[0], hi = summary[1];
+  if (hist) {
+    int rc = hist_args("q8_calib_params", summary, bins);
+    if (rc != Q8_OK) return rc;
+    const int nb = (int)summary[8];
+    const double t = mode == Q8_CALIB_PERCENTILE
+                         ? hist_percentile(bins, nb, summary[5], summary[6], summary[7], 0.999)
+                         : hist_entropy(bins, nb, summary[5], summary[6], summary[7],
+                                        unsigned_ ? 256 : 255);
+    lo = -t;
+    hi = t;
+  }
+  params_from_range(lo, hi, scheme == Q8_SCHEME_PER_TENSOR_SYMMETRIC, unsigned_ != 0, scale,
+                    zero_point);
+  *has_params = 1;
+  return Q8_OK;
 }
 
 }  // extern "C"

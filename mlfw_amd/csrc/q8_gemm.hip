@@ -119,10 +119,11 @@ __device__ __forceinline__ void stage_sync() {
 // stage) may still be in flight.
 template <int N>
 __device__ __forceinline__ void stage_sync_keep() {
-  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "vmcnt immediate");
-  if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(N == 4 || N == 6 || N == 8 || N == 12 || N == 16, "vmcnt immediate");
   if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -475,13 +476,27 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();
   }
-  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (t256 >= 192)
-    return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
-  if (t128 >= 192)
-    return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
-  return launch_qgemm_tile<64, 64>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  // Tile choice: every tile of one launch runs concurrently when the grid
+  // fits the 256 CUs (one workgroup per CU), so the cost is
+  //   rounds = ceil(tiles / 256), times the time of one tile,
+  // where a tile's time is its area times a per-shape factor: smaller tiles
+  // move more bytes through LDS per MAC (measured ratios, C3/C4 shapes).
+  struct Cand { int bm, bn; double cost_per_area; };
+  const Cand cands[] = {{256, 256, 1.00}, {256, 128, 1.15}, {128, 128, 1.40}, {64, 64, 2.50}};
+  int best = 0;
+  double best_cost = 1e300;
+  for (int c = 0; c < 4; ++c) {
+    const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
+    const int64_t rounds = (tiles + 255) / 256;
+    const double cost = (double)rounds * cands[c].bm * cands[c].bn * cands[c].cost_per_area;
+    if (cost < best_cost * 0.999) { best_cost = cost; best = c; }
+  }
+  switch (best) {
+    case 0: return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
+    case 1: return launch_qgemm_tile<256, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
+    case 2: return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
+    default: return launch_qgemm_tile<64, 64>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  }
 }
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
@@ -627,12 +642,15 @@ hipError_t setup_kernel_attributes() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, (bytes));            \
   if (err != hipSuccess) return err;
 #define Q8_SET_256(code) Q8_SET_LDS((k_qgemm<256, 256, code>), (qgemm_lds<256, 256>()));
+#define Q8_SET_256x128(code) Q8_SET_LDS((k_qgemm<256, 128, code>), (qgemm_lds<256, 128>()));
 #define Q8_SET_128(code) Q8_SET_LDS((k_qgemm<128, 128, code>), (qgemm_lds<128, 128>()));
 #define Q8_SET_64(code) Q8_SET_LDS((k_qgemm<64, 64, code>), (qgemm_lds<64, 64>()));
   Q8_EPI_CODES(Q8_SET_256)
+  Q8_EPI_CODES(Q8_SET_256x128)
   Q8_EPI_CODES(Q8_SET_128)
   Q8_EPI_CODES(Q8_SET_64)
 #undef Q8_SET_256
+#undef Q8_SET_256x128
 #undef Q8_SET_128
 #undef Q8_SET_64
 #undef Q8_SET_LDS

@@ -45,6 +45,30 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
 
+// Calibration observer state in device memory: this header, then
+// num_bins 64-bit bin counts, then num_bins words of re-bucketing scratch.
+constexpr size_t Q8_OBS_HEADER = 128;
+struct ObsState {
+  int min_key, max_key;              // observer min / max as order keys
+  int bmin_key, bmax_key;            // the current batch
+  int has_hist, num_bins, initialized, mode;
+  unsigned long long count;          // ValueObserver.count
+  unsigned long long total_count;    // HistogramCollector.totalCount
+  double range_min, range_max;       // HistogramCollector range
+  double act_min, act_scale;         // range the current batch is binned with
+};
+static_assert(sizeof(ObsState) <= Q8_OBS_HEADER, "observer header");
+__host__ __device__ inline unsigned long long* obs_bins(ObsState* st) {
+  return reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(st) + Q8_OBS_HEADER);
+}
+__host__ __device__ inline unsigned long long* obs_scratch(ObsState* st) {
+  return obs_bins(st) + st->num_bins;
+}
+inline size_t obs_state_bytes(int num_bins) { return Q8_OBS_HEADER + 16 * (size_t)num_bins; }
+
+hipError_t launch_obs_reset(ObsState* st, int num_bins, int has_hist, hipStream_t s);
+hipError_t launch_obs_update(ObsState* st, const float* x, int64_t n, hipStream_t s);
+
 // One-time per-device kernel attribute set-up (dynamic LDS limits).
 hipError_t setup_kernel_attributes();
 

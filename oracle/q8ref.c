@@ -17,6 +17,7 @@
 
 #include <math.h>
 #include <stddef.h>
+#include <stdlib.h>
 
 /* ------------------------------------------------------------------ */
 /* rounding primitives                                                 */
@@ -358,4 +359,171 @@ void q8r_epilogue(const int32_t* acc, int64_t M, int64_t N, int mode,
       else if (act == 2) v = q8r_silu(v);
       y[m * N + n] = v;
     }
+}
+
+/* ------------------------------------------------------------------ */
+/* calibration observers (src/compiler/analysis/calibration.ts)        */
+/* ------------------------------------------------------------------ */
+
+void q8r_observer_init(q8r_observer* o, double* bins, int num_bins, int has_hist) {
+  o->min = INFINITY;
+  o->max = -INFINITY;
+  o->count = 0.0;
+  o->has_hist = has_hist;
+  o->num_bins = num_bins;
+  o->initialized = 0;
+  o->range_min = 0.0;
+  o->range_max = 0.0;
+  o->total_count = 0.0;
+  o->bins = bins;
+  if (bins)
+    for (int i = 0; i < num_bins; i++) bins[i] = 0.0;
+}
+
+/* Math.min(numBins - 1, Math.floor((v - lo) * scale)); NaN maps to -1 (a
+ * typed-array store at a NaN index is dropped). */
+static int64_t bin_of(double v, double lo, double scale, int num_bins) {
+  double f = floor((v - lo) * scale);
+  if (f != f) return -1;
+  return f < (double)(num_bins - 1) ? (int64_t)f : num_bins - 1;
+}
+
+/* HistogramCollector.update (:58-80), _initRange (:82-92),
+ * _expandAndRebucket (:94-126) */
+static void hist_update(q8r_observer* o, const float* x, int64_t n) {
+  if (!o->initialized) {
+    double mn = INFINITY, mx = -INFINITY;
+    for (int64_t i = 0; i < n; i++) {
+      double v = x[i];
+      if (v < mn) mn = v;
+      if (v > mx) mx = v;
+    }
+    if (mn == mx) mx = mn + 1.0;
+    o->range_min = mn;
+    o->range_max = mx;
+    o->initialized = 1;
+  }
+  double range = o->range_max - o->range_min;
+  if (range <= 0.0) return;                       /* a NaN range continues, as in JS */
+  int outside = 0;
+  for (int64_t i = 0; i < n; i++) {
+    double v = x[i];
+    if (v < o->range_min || v > o->range_max) { outside = 1; break; }
+  }
+  if (outside) {
+    double new_min = o->range_min, new_max = o->range_max;
+    for (int64_t i = 0; i < n; i++) {
+      double v = x[i];
+      if (v < new_min) new_min = v;
+      if (v > new_max) new_max = v;
+    }
+    double old_min = o->range_min, old_range = o->range_max - o->range_min;
+    double* old = (double*)malloc(sizeof(double) * (size_t)o->num_bins);
+    for (int i = 0; i < o->num_bins; i++) old[i] = o->bins[i];
+    o->range_min = new_min;
+    o->range_max = new_max;
+    double new_scale = o->num_bins / (new_max - new_min);
+    for (int i = 0; i < o->num_bins; i++) o->bins[i] = 0.0;
+    if (old_range > 0.0) {
+      double w = old_range / o->num_bins;
+      for (int i = 0; i < o->num_bins; i++) {
+        if (old[i] == 0.0) continue;
+        double center = old_min + (i + 0.5) * w;
+        int64_t b = bin_of(center, new_min, new_scale, o->num_bins);
+        if (b >= 0) o->bins[b] += old[i];
+      }
+    }
+    free(old);
+    for (int64_t i = 0; i < n; i++) {
+      int64_t b = bin_of(x[i], new_min, new_scale, o->num_bins);
+      if (b >= 0) o->bins[b] += 1.0;
+    }
+    o->total_count += (double)n;
+    return;
+  }
+  double scale = o->num_bins / range;
+  for (int64_t i = 0; i < n; i++) {
+    int64_t b = bin_of(x[i], o->range_min, scale, o->num_bins);
+    if (b >= 0) o->bins[b] += 1.0;
+  }
+  o->total_count += (double)n;
+}
+
+/* ValueObserver.update (:24-34) */
+void q8r_observer_update(q8r_observer* o, const float* x, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    double v = x[i];
+    if (v < o->min) o->min = v;
+    if (v > o->max) o->max = v;
+  }
+  o->count += (double)n;
+  if (o->has_hist) hist_update(o, x, n);
+}
+
+/* computePercentileThreshold (:128-139) */
+double q8r_hist_percentile(const q8r_observer* o, double percentile) {
+  double target = o->total_count * percentile;
+  double cum = 0.0;
+  double w = (o->range_max - o->range_min) / o->num_bins;
+  for (int i = 0; i < o->num_bins; i++) {
+    cum += o->bins[i];
+    if (cum >= target) return o->range_min + (i + 1) * w;
+  }
+  return o->range_max;
+}
+
+/* computeEntropyThreshold (:141-187) */
+double q8r_hist_entropy(const q8r_observer* o, int nq) {
+  if (o->total_count == 0.0) return o->range_max;
+  int nb = o->num_bins;
+  double* ref = (double*)malloc(sizeof(double) * (size_t)nb);
+  double* q = (double*)malloc(sizeof(double) * (size_t)nb);
+  for (int i = 0; i < nb; i++) ref[i] = o->bins[i] / o->total_count;
+  int best_t = nb;
+  double best_kl = INFINITY;
+  for (int t = nq; t <= nb; t++) {
+    double qw = (double)t / nq;
+    for (int j = 0; j < t; j++) q[j] = 0.0;
+    for (int i = 0; i < nq; i++) {
+      int start = (int)floor(i * qw);
+      double e = floor((i + 1) * qw);
+      int end = e < t ? (int)e : t;
+      double sum = 0.0;
+      for (int j = start; j < end; j++) sum += ref[j];
+      int cnt = end - start;
+      if (cnt > 0) {
+        double avg = sum / cnt;
+        for (int j = start; j < end; j++) q[j] = avg;
+      }
+    }
+    double kl = 0.0;
+    for (int i = 0; i < t; i++)
+      if (ref[i] > 0.0 && q[i] > 0.0) kl += ref[i] * log(ref[i] / q[i]);
+    if (kl < best_kl) { best_kl = kl; best_t = t; }
+  }
+  free(ref);
+  free(q);
+  double w = (o->range_max - o->range_min) / nb;
+  return o->range_min + best_t * w;
+}
+
+int q8r_calib_params(const q8r_observer* o, int mode, int scheme, int is_ui8,
+                     double* scale, double* zero_point) {
+  if (o->count == 0.0) return 0;                  /* getRange -> null */
+  int asymmetric = scheme == 1;                   /* PER_TENSOR_ASYMMETRIC (:253) */
+  double lo = o->min, hi = o->max;
+  if (!asymmetric && o->has_hist && mode == 1) {
+    double t = q8r_hist_percentile(o, 0.999);
+    lo = -t; hi = t;
+  } else if (!asymmetric && o->has_hist && mode == 2) {
+    double t = q8r_hist_entropy(o, is_ui8 ? 256 : 255);
+    lo = -t; hi = t;
+  }
+  if (scheme != 0) {                              /* fromRange, non-symmetric branch */
+    q8r_params_asym_from_range(lo, hi, is_ui8, 8, scale, zero_point);
+  } else {
+    *scale = q8r_scale_sym_from_range(lo, hi, 8);
+    *zero_point = 0.0;
+  }
+  return 1;
 }

@@ -122,6 +122,28 @@ float    q8r_mul(float a, float b);
 /* h = fround(silu(g) * u) elementwise */
 void     q8r_silu_mul(const float* g, const float* u, int64_t n, float* h);
 
+/* ---- calibration observers: src/compiler/analysis/calibration.ts ----
+ * ValueObserver (:11-39) with an optional HistogramCollector (:41-189).
+ * bins are integer counts held in doubles, exactly as the reference's
+ * Float64Array. */
+typedef struct {
+  double min, max, count;           /* ValueObserver */
+  int has_hist, num_bins, initialized;
+  double range_min, range_max, total_count;
+  double* bins;                      /* num_bins entries, caller-owned */
+} q8r_observer;
+void     q8r_observer_init(q8r_observer* o, double* bins, int num_bins, int has_hist);
+void     q8r_observer_update(q8r_observer* o, const float* x, int64_t n);
+double   q8r_hist_percentile(const q8r_observer* o, double percentile);
+double   q8r_hist_entropy(const q8r_observer* o, int num_quant_bins);
+/* CalibrationResult.getQuantParams (:246-268).  mode 0 minmax, 1 percentile,
+ * 2 entropy; scheme 0 per_tensor_symmetric, 1 per_tensor_asymmetric,
+ * 2 per_channel (fromRange treats every scheme but the symmetric one with the
+ * zero-point formula); returns 0 when the observer saw no data (the
+ * reference returns null). */
+int      q8r_calib_params(const q8r_observer* o, int mode, int scheme, int is_ui8,
+                          double* scale, double* zero_point);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,10 +33,17 @@ class _Rng(C.Structure):
     _fields_ = [("a", C.c_uint32)]
 
 
+class _Observer(C.Structure):
+    _fields_ = [("min", C.c_double), ("max", C.c_double), ("count", C.c_double),
+                ("has_hist", C.c_int), ("num_bins", C.c_int), ("initialized", C.c_int),
+                ("range_min", C.c_double), ("range_max", C.c_double),
+                ("total_count", C.c_double), ("bins", C.POINTER(C.c_double))]
+
+
 def build(force: bool = False) -> str:
-    if force or not os.path.exists(LIB_PATH):
-        subprocess.run(["make", "-s"] + (["-B"] if force else []) + ["-C", HERE],
-                       check=True, stdout=subprocess.DEVNULL)
+    # make rebuilds only when q8ref.c / q8ref.h are newer than the library
+    subprocess.run(["make", "-s"] + (["-B"] if force else []) + ["-C", HERE],
+                   check=True, stdout=subprocess.DEVNULL)
     return LIB_PATH
 
 
@@ -85,6 +92,12 @@ def lib():
         "q8r_silu": (C.c_float, [C.c_float]),
         "q8r_mul": (C.c_float, [C.c_float, C.c_float]),
         "q8r_silu_mul": (None, [_f32p, _f32p, _i64, _f32p]),
+        "q8r_observer_init": (None, [C.POINTER(_Observer), C.POINTER(C.c_double), _int, _int]),
+        "q8r_observer_update": (None, [C.POINTER(_Observer), _f32p, _i64]),
+        "q8r_hist_percentile": (_dbl, [C.POINTER(_Observer), _dbl]),
+        "q8r_hist_entropy": (_dbl, [C.POINTER(_Observer), _int]),
+        "q8r_calib_params": (_int, [C.POINTER(_Observer), _int, _int, _int, C.POINTER(_dbl),
+                                    C.POINTER(_dbl)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -314,3 +327,43 @@ def silu_mul(g, u) -> np.ndarray:
     h = np.empty(g.shape, np.float32)
     lib().q8r_silu_mul(g.reshape(-1), u.reshape(-1), g.size, h.reshape(-1))
     return h
+
+
+# ---------------------------------------------------------------- calibration
+CALIB_MODES = {"minmax": 0, "percentile": 1, "entropy": 2}
+SCHEMES = {"per_tensor_symmetric": 0, "per_tensor_asymmetric": 1, "per_channel": 2}
+
+
+class Observer:
+    """ValueObserver + HistogramCollector (src/compiler/analysis/calibration.ts:11-189)."""
+
+    def __init__(self, num_bins: int = 2048, histogram: bool = True):
+        self._bins = np.zeros(num_bins, np.float64)
+        self._o = _Observer()
+        lib().q8r_observer_init(C.byref(self._o), self._bins.ctypes.data_as(C.POINTER(C.c_double)),
+                                num_bins, int(histogram))
+
+    def update(self, x) -> None:
+        x = _c(x, np.float32).reshape(-1)
+        lib().q8r_observer_update(C.byref(self._o), x, x.size)
+
+    @property
+    def state(self) -> dict:
+        o = self._o
+        return {"min": o.min, "max": o.max, "count": o.count, "initialized": o.initialized,
+                "range_min": o.range_min, "range_max": o.range_max,
+                "total_count": o.total_count, "bins": self._bins.copy()}
+
+    def percentile(self, p: float = 0.999) -> float:
+        return lib().q8r_hist_percentile(C.byref(self._o), p)
+
+    def entropy(self, num_quant_bins: int = 255) -> float:
+        return lib().q8r_hist_entropy(C.byref(self._o), num_quant_bins)
+
+    def params(self, mode: str = "minmax", scheme: str = "per_tensor_symmetric",
+               unsigned: bool = False):
+        """getQuantParams (calibration.ts:246-268) -> (scale, zero_point) or None."""
+        s, z = _dbl(), _dbl()
+        ok = lib().q8r_calib_params(C.byref(self._o), CALIB_MODES[mode], SCHEMES[scheme],
+                                    int(unsigned), C.byref(s), C.byref(z))
+        return (s.value, z.value) if ok else None
