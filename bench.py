@@ -8,11 +8,12 @@ weight.  value = 2*4096^3 int ops / step time, in TOPS (10^12 int ops/s).
 
 The step's two launches are prepared once (mlfw_amd.ops.prepare: arguments
 validated and converted up front), so the host enqueues faster than the
-GPU executes and the HIP events recorded between the launches, on the
-stream they run on, time the kernels themselves.
+GPU executes; the timed region is K steps back to back between two HIP
+events on the stream the kernels run on.
 
-roofline: the GEMM kernel, average of those per-launch event intervals
-inside the timed region; peak = MI355X dense int8 MFMA, 5.0 POP/s.
+roofline: the GEMM kernel's average duration over a second pass of the same
+K steps with an event pair around each kernel (events between launches
+would slow the timed pass itself); peak = MI355X dense int8 MFMA, 5.0 POP/s.
 `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
 WRITE_SIZE runs (profiles/traffic.json, scaled by a copy-kernel
 calibration), or null when that file is absent.
@@ -88,31 +89,41 @@ def bench_c3(steps, warmup):
         gemm()
     torch.cuda.synchronize()
 
-    e_q = [ev() for _ in range(steps)]
-    e_g = [ev() for _ in range(steps)]
-    e_e = [ev() for _ in range(steps)]
+    # (1) the timed steps: quantize + GEMM back to back, nothing in between
     t_begin, t_end = ev(), ev()
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_begin.record()
-    for i in range(steps):
-        e_q[i].record()
+    for _ in range(steps):
         quant()
-        e_g[i].record()
         gemm()
-        e_e[i].record()
     t_end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     step_ms = t_begin.elapsed_time(t_end) / steps
-    gemm_ms = sorted(a.elapsed_time(b) for a, b in zip(e_g, e_e))
-    quant_ms = sorted(a.elapsed_time(b) for a, b in zip(e_q, e_g))
+
+    # (2) per-kernel durations for the roofline: the same step sequence
+    # again, with an event pair around each kernel, on the stream both run
+    # on (the events add a little time to each interval, so the rate derived
+    # from it errs low)
+    e_q = [(ev(), ev()) for _ in range(steps)]
+    e_g = [(ev(), ev()) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        e_q[i][0].record()
+        quant()
+        e_q[i][1].record()
+        e_g[i][0].record()
+        gemm()
+        e_g[i][1].record()
+    torch.cuda.synchronize()
+    quant_ms = sum(a.elapsed_time(b) for a, b in e_q) / steps
+    gemm_ms = sum(a.elapsed_time(b) for a, b in e_g) / steps
     return {
         "step_ms": step_ms,
         "wall_ms_per_step": 1e3 * wall / steps,
-        "gemm_avg_ms": sum(gemm_ms) / steps,
-        "gemm_median_ms": gemm_ms[steps // 2],
-        "quant_avg_ms": sum(quant_ms) / steps,
+        "gemm_avg_ms": gemm_ms,
+        "quant_avg_ms": quant_ms,
     }
 
 

@@ -60,6 +60,7 @@ int init_device(int dev) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   e = q8::setup_kernel_attributes();
+  (void)q8::cu_count();
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&g_dev[dev].work), 256);
   if (cur != dev) (void)hipSetDevice(cur);
   if (e != hipSuccess) return hip_fail(e, "device set-up");

@@ -161,62 +161,6 @@ inline int epi_code(const GemmEpi& e) {
   return (e.mode << 3) | (e.bias ? 4 : 0) | e.act;
 }
 
-// Epilogue of one output quad: 4 consecutive columns of one row.
-template <int EPI>
-__device__ __forceinline__ void store_quad(v4i a, int row, int col, int M, int N, bool vec_ok,
-                                           const GemmEpi& e, double sa, const double* sb,
-                                           void* out) {
-  using P = Epi<EPI>;
-  if (row >= M) return;
-  const int64_t idx = (int64_t)row * N + col;
-  if constexpr (P::OUT_I32) {
-    if (vec_ok && col + 3 < N) {
-      *reinterpret_cast<v4i*>(static_cast<int32_t*>(out) + idx) = a;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (col + c < N) static_cast<int32_t*>(out)[idx + c] = a[c];
-    }
-    return;
-  } else {
-    float y[4];
-    if constexpr (P::MODE == 0) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) y[c] = (float)((double)a[c] * e.s_out);
-    } else {
-      float sv[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) sv[c] = (float)(sa * sb[c]);
-      // binary32 multiply when every accumulator of the quad is exactly a
-      // binary32 value (|acc| <= 2^24), the f64 form otherwise
-      bool exact = true;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) exact &= (unsigned)(a[c] + (1 << 24)) <= (2u << 24);
-      if (exact) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] = (float)a[c] * sv[c];
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] = (float)((double)a[c] * (double)sv[c]);
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if constexpr (P::BIAS) y[c] = y[c] + e.bias[col + c < N ? col + c : 0];
-      if constexpr (P::ACT == 1) y[c] = relu_js(y[c]);
-      if constexpr (P::ACT == 2) y[c] = silu_js(y[c]);
-    }
-    float* o = static_cast<float*>(out);
-    if (vec_ok && col + 3 < N) {
-      *reinterpret_cast<float4*>(o + idx) = make_float4(y[0], y[1], y[2], y[3]);
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (col + c < N) o[idx + c] = y[c];
-    }
-  }
-}
-
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(GEMM_THREADS, 1)
 void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
@@ -377,41 +321,107 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   // the stage buffers the epilogue reuses: drain them first.
   stage_sync();
 
-  // Epilogue through LDS (free after the last barrier): each wave moves one
-  // 32-row strip of its sub-tile at a time into its own LDS region (row
-  // pitch WN + 8 words), then reads it back as 4-column quads, so every
-  // lane applies the scales to 4 adjacent outputs and stores 16 bytes.
-  constexpr int PITCH = C::WN + 8;                    // int32 words per strip row
+  // Epilogue, one 32-row strip of the wave's sub-tile at a time:
+  //  1. the scales, bias and activation are applied in the accumulator
+  //     layout (lane l holds column 32j + l%32 and rows (r/4)*8 + (l/32)*4
+  //     + r%4 of each 32x32 block), with one exactness test per strip;
+  //  2. the 32 x WN results go through this wave's own LDS region (row
+  //     pitch WN + 8 words; the stage buffers are free after the last
+  //     barrier) and come back as 4-column quads, so every lane stores 16
+  //     bytes.  Stores are non-temporal: the kernel never reads them back.
+  using P = Epi<EPI>;
+  constexpr int PITCH = C::WN + 8;                    // 32-bit words per strip row
   constexpr int LPR = C::WN / 4;                      // lanes per strip row
   constexpr int RPI = 64 / LPR;                       // strip rows per read
+  constexpr int NQ = 32 / RPI;                        // quads per lane per strip
   static_assert(4 * 32 * PITCH * 4 <= C::LDS, "epilogue strips fit in the stage buffers");
   int32_t* strip = reinterpret_cast<int32_t*>(lds) + wave * 32 * PITCH;
   const int qcol = 4 * (lane % LPR), qrow = lane / LPR;
-  const int col = n0 + wn + qcol;
-  const bool vec_ok = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
-  double sb[4] = {0.0, 0.0, 0.0, 0.0};
-  if (!OUT_I32 && MODE == 1) {
+  const int gcol = n0 + wn + qcol;
+  const bool interior = m0 + BM <= M && n0 + BN <= N && (N % 4 == 0) &&
+                        (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  double sbj[C::TN];
+  float bj[C::TN];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) sb[c] = s_cols[wn + qcol + c];
+  for (int j = 0; j < C::TN; ++j) {
+    const int lc = wn + 32 * j + r32;
+    sbj[j] = (!OUT_I32 && MODE == 1) ? s_cols[lc] : 0.0;
+    if constexpr (P::BIAS) bj[j] = e.bias[n0 + lc < N ? n0 + lc : N - 1];
+    else bj[j] = 0.0f;
   }
-  // One strip per 32-row block row i; the strip index is a template
-  // argument so the accumulators stay statically indexed (registers).
   auto strip_out = [&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    // accumulator element r of lane l: strip row (r/4)*8 + (l/32)*4 + r%4,
-    // strip column 32*j + l%32
+    auto slot = [&](int j, int r) -> int32_t& {
+      return strip[((r >> 2) * 8 + kh * 4 + (r & 3)) * PITCH + 32 * j + r32];
+    };
+    if constexpr (OUT_I32) {
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j)
+      for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        strip[((r >> 2) * 8 + kh * 4 + (r & 3)) * PITCH + 32 * j + r32] = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) slot(j, r) = acc[i][j][r];
+    } else {
+      double sar[16];
+      if constexpr (MODE == 1) {
 #pragma unroll
-    for (int it = 0; it < 32 / RPI; ++it) {
-      const int sr = it * RPI + qrow;
-      const v4i q = *reinterpret_cast<const v4i*>(strip + sr * PITCH + qcol);
-      const int trow = wm + 32 * i + sr;
-      store_quad<EPI>(q, m0 + trow, col, M, N, vec_ok, e,
-                                (!OUT_I32 && MODE == 1) ? s_rows[trow] : 0.0, sb, out);
+        for (int r = 0; r < 16; ++r) sar[r] = s_rows[wm + 32 * i + (r >> 2) * 8 + kh * 4 + (r & 3)];
+      }
+      // binary32 multiply when every accumulator of the strip is exactly a
+      // binary32 value (|acc| <= 2^24), the f64 form otherwise
+      bool exact = true;
+      if constexpr (MODE == 1) {
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) exact &= (unsigned)(acc[i][j][r] + (1 << 24)) <= (2u << 24);
+      }
+      const bool fast = __all(exact);
+      auto finish = [&](float y, int j) {
+        if constexpr (P::BIAS) y = y + bj[j];
+        if constexpr (P::ACT == 1) y = relu_js(y);
+        if constexpr (P::ACT == 2) y = silu_js(y);
+        return y;
+      };
+      if (MODE == 0 || fast) {
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float y;
+            if constexpr (MODE == 0) y = (float)((double)acc[i][j][r] * e.s_out);
+            else y = (float)acc[i][j][r] * (float)(sar[r] * sbj[j]);
+            slot(j, r) = __float_as_int(finish(y, j));
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float y = mul_acc_f32scale(acc[i][j][r], (float)(sar[r] * sbj[j]));
+            slot(j, r) = __float_as_int(finish(y, j));
+          }
+      }
+    }
+    v4i q[NQ];
+#pragma unroll
+    for (int it = 0; it < NQ; ++it)
+      q[it] = *reinterpret_cast<const v4i*>(strip + (it * RPI + qrow) * PITCH + qcol);
+    int32_t* o = static_cast<int32_t*>(out);
+    if (interior) {
+#pragma unroll
+      for (int it = 0; it < NQ; ++it) {
+        const int64_t row = m0 + wm + 32 * i + it * RPI + qrow;
+        __builtin_nontemporal_store(q[it], reinterpret_cast<v4i*>(o + row * N + gcol));
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < NQ; ++it) {
+        const int row = m0 + wm + 32 * i + it * RPI + qrow;
+        if (row < M) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (gcol + c < N) o[(int64_t)row * N + gcol + c] = q[it][c];
+        }
+      }
     }
   };
   strip_out(std::integral_constant<int, 0>{});

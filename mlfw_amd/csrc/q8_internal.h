@@ -72,4 +72,7 @@ hipError_t launch_obs_update(ObsState* st, const float* x, int64_t n, hipStream_
 // One-time per-device kernel attribute set-up (dynamic LDS limits).
 hipError_t setup_kernel_attributes();
 
+// Compute units of the current device (cached per device).
+int cu_count();
+
 }  // namespace q8

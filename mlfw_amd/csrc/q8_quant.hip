@@ -8,6 +8,8 @@
 // is 16-byte aligned; a scalar grid-stride form handles everything else.
 // Per-row absmax reductions run in registers: a row of up to 12 KiB floats
 // stays in VGPRs (VPT float4 per thread) so the row is read from HBM once.
+#include <atomic>
+
 #include "q8_device.h"
 #include "q8_internal.h"
 
@@ -51,6 +53,21 @@ __global__ __launch_bounds__(NT) void k_fill_uniform(float* __restrict__ out, in
   for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * NT)
     out[i] = (float)(a + mb32(seed, offset + i) * range);
+}
+
+// Compute units of the current device, cached per device (the first call
+// is made by device set-up, so launches inside a graph capture only read).
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 static int grid_for(int64_t work, int64_t per_block, int cap) {
@@ -171,46 +188,53 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // quantize, so such rows are read once; longer rows re-read the tail.
 // Loads and stores are non-temporal: the stream is touched once, and
 // keeping it out of the caches measured ~5-10% faster than plain accesses.
-template <int VPT>
+template <int VPT, bool FULL>
 __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t M,
                                                    int64_t K, int8_t* __restrict__ q,
                                                    double* __restrict__ scales) {
   __shared__ int red[NT / 64];
   const int tid = threadIdx.x;
-  const int64_t K4 = K >> 2;
+  const int64_t K4 = K >> 2;       // FULL: K4 == VPT * NT, no bounds to test
   for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
     const v4f* xr = reinterpret_cast<const v4f*>(x + row * K);
     int* qr = reinterpret_cast<int*>(q + row * K);
     float4 v[VPT];
     int key = -1;
+    // Every load is issued unconditionally (a lane past the row end reloads
+    // the last group and ignores it) so that all VPT loads are in flight
+    // together; a conditional load would be waited for one at a time.
+    const int last = (int)K4 - 1;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int64_t i = tid + (int64_t)j * NT;
-      if (i < K4) {
-        const v4f t = __builtin_nontemporal_load(xr + i);
-        v[j] = make_float4(t.x, t.y, t.z, t.w);
-        int k = key4(v[j]);
+      const int i = tid + j * NT;
+      const v4f t = __builtin_nontemporal_load(xr + (FULL ? i : min(i, last)));
+      v[j] = make_float4(t.x, t.y, t.z, t.w);
+      const int k = key4(v[j]);
+      key = (FULL || i <= last) && k > key ? k : key;
+    }
+    if constexpr (!FULL) {
+      for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
+        const v4f t = xr[i];
+        int k = key4(make_float4(t.x, t.y, t.z, t.w));
         key = key > k ? key : k;
       }
     }
-    for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
-      const v4f t = xr[i];
-      int k = key4(make_float4(t.x, t.y, t.z, t.w));
-      key = key > k ? key : k;
-    }
     key = block_max_i32(key, red);
-    const double s = K == 0 ? 6.0 / 127.0 : scale_from_key(key);
+    const double s = scale_from_key(key);
     if (tid == 0) scales[row] = s;
     const bool fast = fast_scale_ok(s);
     const float r32 = (float)(1.0 / s);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int64_t i = tid + (int64_t)j * NT;
-      if (i < K4) __builtin_nontemporal_store(quant4_sym(v[j], fast, r32, s), qr + i);
+      const int i = tid + j * NT;
+      if (FULL || i < K4) __builtin_nontemporal_store(quant4_sym(v[j], fast, r32, s), qr + i);
     }
-    for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
-      const v4f t = xr[i];
-      __builtin_nontemporal_store(quant4_sym(make_float4(t.x, t.y, t.z, t.w), fast, r32, s), qr + i);
+    if constexpr (!FULL) {
+      for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
+        const v4f t = xr[i];
+        __builtin_nontemporal_store(quant4_sym(make_float4(t.x, t.y, t.z, t.w), fast, r32, s),
+                                    qr + i);
+      }
     }
   }
 }
@@ -249,16 +273,31 @@ hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, do
     return hipGetLastError();
   }
   const int64_t K4 = K / 4;
-  if (K4 <= 1 * NT)
-    hipLaunchKernelGGL(k_quant_rows<1>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
-  else if (K4 <= 2 * NT)
-    hipLaunchKernelGGL(k_quant_rows<2>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
-  else if (K4 <= 4 * NT)
-    hipLaunchKernelGGL(k_quant_rows<4>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
-  else if (K4 <= 8 * NT)
-    hipLaunchKernelGGL(k_quant_rows<8>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
-  else
-    hipLaunchKernelGGL(k_quant_rows<12>, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+  if (K4 == 0) {        // rows of zero length: only the scales are written
+    hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+    return hipGetLastError();
+  }
+  // Row workers: one workgroup per row, except that up to two rows per
+  // workgroup go to a single resident round (8 workgroups per CU at this
+  // block size) when the rows would fill at most two rounds (measured
+  // faster for [4096,4096]; one row per workgroup is faster for more rows).
+  const int64_t slots = 8 * (int64_t)cu_count();
+  const int workers = (int)(M <= 2 * slots ? (M < slots ? M : slots) : (M < 1048576 ? M : 1048576));
+#define Q8_QROWS(V)                                                                          \
+  do {                                                                                       \
+    if (K4 == (V) * NT)                                                                      \
+      hipLaunchKernelGGL((k_quant_rows<V, true>), dim3(workers), dim3(NT), 0, st, x, M, K, q, \
+                         scales);                                                            \
+    else                                                                                     \
+      hipLaunchKernelGGL((k_quant_rows<V, false>), dim3(workers), dim3(NT), 0, st, x, M, K,  \
+                         q, scales);                                                         \
+  } while (0)
+  if (K4 <= 1 * NT) Q8_QROWS(1);
+  else if (K4 <= 2 * NT) Q8_QROWS(2);
+  else if (K4 <= 4 * NT) Q8_QROWS(4);
+  else if (K4 <= 8 * NT) Q8_QROWS(8);
+  else Q8_QROWS(12);
+#undef Q8_QROWS
   return hipGetLastError();
 }
 
@@ -610,22 +649,31 @@ __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows(const float* __restr
     const float4* ur = reinterpret_cast<const float4*>(u + row * K);
     float4 v[VPT];
     int key = -1;
+    // loads issued unconditionally (a lane past the row end reloads the
+    // last group), so they are all in flight together
+    float4 a[VPT], b[VPT];
+    const int last = (int)K4 - 1;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int i = min(tid + j * NT, last);
+      a[j] = gr[i];
+      b[j] = ur[i];
+    }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t i = tid + (int64_t)j * NT;
+      v[j] = make_float4((float)((double)silu_js(a[j].x) * (double)b[j].x),
+                         (float)((double)silu_js(a[j].y) * (double)b[j].y),
+                         (float)((double)silu_js(a[j].z) * (double)b[j].z),
+                         (float)((double)silu_js(a[j].w) * (double)b[j].w));
       if (i < K4) {
-        float4 a = gr[i], b = ur[i];
-        v[j] = make_float4((float)((double)silu_js(a.x) * (double)b.x),
-                           (float)((double)silu_js(a.y) * (double)b.y),
-                           (float)((double)silu_js(a.z) * (double)b.z),
-                           (float)((double)silu_js(a.w) * (double)b.w));
         if (h) reinterpret_cast<float4*>(h + row * K)[i] = v[j];
-        int k = key4(v[j]);
+        const int k = key4(v[j]);
         key = key > k ? key : k;
       }
     }
     key = block_max_i32(key, red);
-    const double s = K == 0 ? 6.0 / 127.0 : scale_from_key(key);
+    const double s = scale_from_key(key);
     if (tid == 0) scales[row] = s;
     const bool fast = fast_scale_ok(s);
     const float r32 = (float)(1.0 / s);
@@ -678,12 +726,17 @@ hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M,
     return hipGetLastError();
   }
   const int64_t K4 = K / 4;
+  if (K4 == 0) {
+    hipLaunchKernelGGL(k_silu_mul_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    return hipGetLastError();
+  }
+  const int workers = (int)(M < 8 * cu_count() ? M : 8 * cu_count());
   if (K4 <= 4 * NT)
-    hipLaunchKernelGGL(k_silu_mul_quant_rows<4>, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    hipLaunchKernelGGL(k_silu_mul_quant_rows<4>, dim3(workers), dim3(NT), 0, st, g, u, M, K, h, q, scales);
   else if (K4 <= 8 * NT)
-    hipLaunchKernelGGL(k_silu_mul_quant_rows<8>, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    hipLaunchKernelGGL(k_silu_mul_quant_rows<8>, dim3(workers), dim3(NT), 0, st, g, u, M, K, h, q, scales);
   else
-    hipLaunchKernelGGL(k_silu_mul_quant_rows<12>, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    hipLaunchKernelGGL(k_silu_mul_quant_rows<12>, dim3(workers), dim3(NT), 0, st, g, u, M, K, h, q, scales);
   return hipGetLastError();
 }
 
