@@ -11,9 +11,9 @@ validated and converted up front), so the host enqueues faster than the
 GPU executes; the timed region is K steps back to back between two HIP
 events on the stream the kernels run on.
 
-roofline: the GEMM kernel's average duration over a second pass of the same
-K steps with an event pair around each kernel (events between launches
-would slow the timed pass itself); peak = MI355X dense int8 MFMA, 5.0 POP/s.
+roofline: the GEMM kernel's average duration over K further launches of
+the GEMM alone, back to back between two events on the same stream;
+peak = MI355X dense int8 MFMA, 5.0 POP/s.
 `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
 WRITE_SIZE runs (profiles/traffic.json, scaled by a copy-kernel
 calibration), or null when that file is absent.
@@ -102,23 +102,21 @@ def bench_c3(steps, warmup):
     wall = time.perf_counter() - wall0
     step_ms = t_begin.elapsed_time(t_end) / steps
 
-    # (2) per-kernel durations for the roofline: the same step sequence
-    # again, with an event pair around each kernel, on the stream both run
-    # on (the events add a little time to each interval, so the rate derived
-    # from it errs low)
-    e_q = [(ev(), ev()) for _ in range(steps)]
-    e_g = [(ev(), ev()) for _ in range(steps)]
-    torch.cuda.synchronize()
-    for i in range(steps):
-        e_q[i][0].record()
-        quant()
-        e_q[i][1].record()
-        e_g[i][0].record()
-        gemm()
-        e_g[i][1].record()
-    torch.cuda.synchronize()
-    quant_ms = sum(a.elapsed_time(b) for a, b in e_q) / steps
-    gemm_ms = sum(a.elapsed_time(b) for a, b in e_g) / steps
+    # (2) per-kernel durations for the roofline: K launches of one kernel
+    # back to back between two events on the stream both kernels run on
+    # (an event pair around every launch would add the dispatch gap to each
+    # interval)
+    def back_to_back(fn):
+        a, b = ev(), ev()
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps
+    gemm_ms = back_to_back(gemm)
+    quant_ms = back_to_back(quant)
     return {
         "step_ms": step_ms,
         "wall_ms_per_step": 1e3 * wall / steps,

@@ -9,25 +9,27 @@
 //     kept in AGPRs).  A lane feeds 16 K-bytes of one row of A and the same
 //     16 K-bytes of one row of B per instruction, so fragments are single
 //     128-bit LDS reads.
-//   * K is walked in BK = 128-byte stages.  Global -> LDS copies use the
-//     buffer_load_dwordx4 ... lds form (no VGPR staging): each instruction
-//     moves 8 tile rows x 128 B, lane l landing at LDS byte 16*l of the
-//     wave's destination.  Out-of-range rows and the K tail are fetched
-//     through offsets past the buffer resource's num_records, which the
-//     hardware returns as zero -- edge tiles need no separate code.
-//   * LDS layout: tile row r occupies 128 B; its logical 16-byte K chunk c
-//     is stored at chunk position c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7.
-//     The 32 lanes that read one K chunk of 32 consecutive rows then hit
-//     distinct 16-byte bank groups within every 8-row and every 16-row
-//     group, so fragment reads are conflict-free on a 32- or 64-bank LDS.
-//     The swizzle is applied on the global side (each lane fetches the
-//     chunk its LDS slot must hold), so the DMA writes stay linear.
-//   * Two LDS stages: while the MFMAs of stage t run, the copies of stage
-//     t+1 are in flight; one s_waitcnt + barrier per stage, placed before
-//     the stage's last 32-byte K sub-step so that sub-step's MFMAs (registers
-//     only) overlap the refill of the consumed stage and the first fragment
-//     reads of the next one.  Fragments are double-buffered in registers
-//     across the four K sub-steps.
+//   * K is walked in BK = 64-byte stages held in a ring of four LDS
+//     buffers.  Global -> LDS copies use the buffer_load_dwordx4 ... lds
+//     form (no VGPR staging): each instruction moves 16 tile rows x 64 B,
+//     lane l landing at LDS byte 16*l of the wave's destination.
+//     Out-of-range rows and the K tail are fetched through offsets past
+//     the buffer resource's num_records, which the hardware returns as
+//     zero -- edge tiles need no separate code.
+//   * LDS layout: tile row r occupies 64 B; its logical 16-byte K chunk c
+//     is stored at chunk position c ^ swz(r), swz(r) = ((r>>1) ^ (r>>3)) & 3.
+//     The lanes that read one K chunk of 32 consecutive rows then hit
+//     distinct 16-byte bank groups within every 8-row group (32 banks)
+//     and every 16-row group (64 banks), so fragment reads are
+//     conflict-free.  The swizzle is applied on the global side (each lane
+//     fetches the chunk its LDS slot must hold), so the DMA writes stay
+//     linear.
+//   * Pipeline: one barrier per stage, between its two 32-byte K sub-steps;
+//     a stage's refill is spread over the following two sub-steps, so each
+//     sub-step issues a quarter of a stage's copies between its MFMAs (a
+//     burst of copies backs up the address unit and stalls MFMA issue) and
+//     copies run more than two stages ahead of their use.  Fragments are
+//     double-buffered in registers: every sub-step reads the next one's.
 //   * Workgroup -> tile order undoes the round-robin dispatch over the 8
 //     XCDs (consecutive workgroup ids land on different XCDs), then walks
 //     groups of 4 tile rows column by column, so the tiles resident on one
@@ -74,7 +76,8 @@ __device__ __forceinline__ float epi_value(int acc, int64_t m, int64_t n, const 
 }
 
 // ------------------------------------------------------------------ MFMA GEMM
-constexpr int BK = 128;                 // K bytes per LDS stage
+constexpr int BK = 64;                  // K bytes per LDS stage
+constexpr int NBUF = 4;                 // LDS stages in the ring
 constexpr int GEMM_THREADS = 256;       // 4 waves, 2 x 2
 constexpr uint32_t OOB = 0x80000000u;   // voffset past every buffer's num_records
 
@@ -84,14 +87,14 @@ struct GemmCfg {
   static constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 blocks per wave
   static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int LDS = 2 * STAGE;                 // two K stages
+  static constexpr int LDS = NBUF * STAGE;              // the stage ring
   static constexpr int LDS_TOTAL = LDS + 8 * (BM + BN);  // + the tile's f64 scales
-  static constexpr int A_LOADS = BM / 32;              // 8-row copies per wave per stage
-  static constexpr int B_LOADS = BN / 32;
+  static constexpr int A_LOADS = BM / 64;              // 16-row copies per wave per stage
+  static constexpr int B_LOADS = BN / 64;
   static_assert(TM >= 1 && TN >= 1 && BM % 64 == 0 && BN % 64 == 0, "tile shape");
 };
 
-__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 // Buffer resource (V#) of a raw byte range: base, stride 0, num_records
 // bytes, gfx9 data-format word.
@@ -115,16 +118,51 @@ __device__ __forceinline__ void stage_sync() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// As stage_sync, but up to N of this wave's most recent copies (the next
-// stage) may still be in flight.
+// As stage_sync, but up to N of this wave's most recent copies (later
+// stages) may still be in flight: vector-memory loads complete in issue
+// order, so vmcnt(N) means every older copy has landed.
 template <int N>
 __device__ __forceinline__ void stage_sync_keep() {
-  static_assert(N == 4 || N == 6 || N == 8 || N == 12 || N == 16, "vmcnt immediate");
-  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Instruction order of one sub-step (compiler schedule groups): NF
+// fragment reads paired with the first MFMAs, then NC copies spread evenly
+// over the remaining MFMAs.  Keeps the LDS reads one sub-step ahead of
+// their use and never lets a burst of copies back up the address unit
+// while the MFMAs wait behind them.
+template <int NF, int NM, int NC>
+__device__ __forceinline__ void sched_substep() {
+  constexpr int G1 = NF < NM ? NF : NM;
+#pragma unroll
+  for (int x = 0; x < G1; ++x) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+  }
+  if constexpr (NF > G1) __builtin_amdgcn_sched_group_barrier(0x100, NF - G1, 0);
+  constexpr int R = NM - G1;
+  if constexpr (NC == 0) {
+    if constexpr (R > 0) __builtin_amdgcn_sched_group_barrier(0x008, R, 0);
+  } else if constexpr (R == 0) {
+    __builtin_amdgcn_sched_group_barrier(0x020, NC, 0);
+  } else if constexpr (NC <= R) {
+    constexpr int PER = R / NC;
+#pragma unroll
+    for (int x = 0; x < NC; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (copy)
+    }
+    if constexpr (R - PER * NC > 0) __builtin_amdgcn_sched_group_barrier(0x008, R - PER * NC, 0);
+  } else {
+    constexpr int PER = NC / R;
+#pragma unroll
+    for (int x = 0; x < R; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);
+    }
+    if constexpr (NC - PER * R > 0) __builtin_amdgcn_sched_group_barrier(0x020, NC - PER * R, 0);
+  }
 }
 
 // Workgroup id -> (tile row, tile col).  Dispatch places consecutive ids on
@@ -195,49 +233,55 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   }
 
   // Copy plan: wave w fills tile rows [w*BM/4, (w+1)*BM/4) of A and the
-  // same share of B, 8 rows per instruction.  Lane l lands in row
-  // 8j + l/8 at chunk position l%8 and so fetches logical chunk
-  // (l%8) ^ swz(row).
+  // same share of B, 16 rows per instruction.  Lane l lands in row
+  // 16j + l/4 at chunk position l%4 and so fetches logical chunk
+  // (l%4) ^ swz(row).
   uint32_t offa[C::A_LOADS], offb[C::B_LOADS];
   int kca[C::A_LOADS], kcb[C::B_LOADS];
 #pragma unroll
   for (int j = 0; j < C::A_LOADS; ++j) {
-    const int row = wave * (BM / 4) + 8 * j + (lane >> 3);
-    kca[j] = 16 * ((lane & 7) ^ swz(row));
+    const int row = wave * (BM / 4) + 16 * j + (lane >> 2);
+    kca[j] = 16 * ((lane & 3) ^ swz(row));
     offa[j] = row < rows_a ? (uint32_t)(row * K + kca[j]) : OOB;
   }
 #pragma unroll
   for (int j = 0; j < C::B_LOADS; ++j) {
-    const int row = wave * (BN / 4) + 8 * j + (lane >> 3);
-    kcb[j] = 16 * ((lane & 7) ^ swz(row));
+    const int row = wave * (BN / 4) + 16 * j + (lane >> 2);
+    kcb[j] = 16 * ((lane & 3) ^ swz(row));
     offb[j] = row < rows_b ? (uint32_t)(row * K + kcb[j]) : OOB;
   }
   const uint32_t bytes_a = (uint32_t)rows_a * (uint32_t)K;
   const uint32_t bytes_b = (uint32_t)rows_b * (uint32_t)K;
   const int KT = (K + BK - 1) / BK;
 
-  // Copies of K stage kt into `stage`.  kt >= KT copies nothing: with
-  // num_records 0 every lane is out of range and writes zeros into a stage
-  // that is no longer read, which keeps the loop body branch-free.
-  auto issue = [&](int kt, int8_t* stage) {
+  // Copies of the A (resp. B) half of K stage kt into `stage`.  kt >= KT
+  // copies nothing: with num_records 0 every lane is out of range and
+  // writes zeros into a stage that is no longer read, which keeps the loop
+  // body branch-free.
+  auto issue_a = [&](int kt, int8_t* stage) {
     const bool live = kt < KT;
     const int kb = live ? kt * BK : 0;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab + kb, live ? bytes_a - (uint32_t)kb : 0u);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
     int8_t* sa = stage + wave * (BM / 4) * BK;
-    int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
     const bool tail = kb + BK > K;
 #pragma unroll
     for (int j = 0; j < C::A_LOADS; ++j)
-      copy16_to_lds(ra, sa + j * 8 * BK, (tail && kb + kca[j] >= K) ? OOB : offa[j]);
+      copy16_to_lds(ra, sa + j * 16 * BK, (tail && kb + kca[j] >= K) ? OOB : offa[j]);
+  };
+  auto issue_b = [&](int kt, int8_t* stage) {
+    const bool live = kt < KT;
+    const int kb = live ? kt * BK : 0;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
+    int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
+    const bool tail = kb + BK > K;
 #pragma unroll
     for (int j = 0; j < C::B_LOADS; ++j)
-      copy16_to_lds(rb, sb + j * 8 * BK, (tail && kb + kcb[j] >= K) ? OOB : offb[j]);
+      copy16_to_lds(rb, sb + j * 16 * BK, (tail && kb + kcb[j] >= K) ? OOB : offb[j]);
   };
 
   // Fragment addresses: byte offset of the fragment row within a stage and
-  // the lane's swizzle (logical chunk 2*kk + kh sits at position
-  // (2*kk) ^ (kh ^ swz(row))).
+  // the lane's swizzle (sub-step kk reads logical chunk 2*kk + kh, which
+  // sits at position (2*kk) ^ (kh ^ swz(row))).
   const int wm = (wave >> 1) * C::WM, wn = (wave & 1) * C::WN;
   const int r32 = lane & 31, kh = lane >> 5;
   int fa_off[C::TM], fa_sw[C::TM], fb_off[C::TN], fb_sw[C::TN];
@@ -277,45 +321,48 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
   };
 
-  // Pipeline: stages kt and kt+1 are in LDS or in flight while the MFMAs
-  // of stage kt run.  The barrier of stage kt sits before its last
-  // sub-step: those MFMAs only need registers, so they overlap the refill
-  // of the stage just consumed and the first fragment reads of stage kt+1.
-  int8_t* const s0 = lds;
-  int8_t* const s1 = lds + C::STAGE;
-  issue(0, s0);
-  issue(1, s1);
+  // Pipeline over a ring of NBUF = 4 stages (stage kt in buffer kt % 4).
+  // A stage is two 32-byte K sub-steps.  Barrier B_kt sits between the two
+  // sub-steps of stage kt: after it every wave has finished reading buffer
+  // kt % 4 and stage kt+1 has landed.  The refill of that buffer with
+  // stage kt+4 is spread over the next two sub-steps (A half after B_kt,
+  // B half in the first sub-step of stage kt+1) so that each sub-step
+  // issues only a quarter of a stage's copies between its MFMAs, and every
+  // copy is issued more than two stages ahead of its use.  Each sub-step
+  // also reads the next sub-step's fragments into the other register set.
+  int8_t* const ring = lds;
+  auto buf = [&](int kt) { return ring + (kt & (NBUF - 1)) * C::STAGE; };
+  constexpr int NV = C::A_LOADS + C::B_LOADS;    // copies per stage
+  issue_a(0, buf(0));
+  issue_b(0, buf(0));
+  issue_a(1, buf(1));
+  issue_b(1, buf(1));
+  issue_a(2, buf(2));
+  issue_b(2, buf(2));
+  issue_a(3, buf(3));
   if (!OUT_I32 && MODE == 1) {
 #pragma unroll
     for (int u = 0; u < NSC; ++u)
       if (tid + u * GEMM_THREADS < BM + BN) s_rows[tid + u * GEMM_THREADS] = scv[u];
   }
-  stage_sync_keep<C::A_LOADS + C::B_LOADS>();   // stage 0 landed; stage 1 may be in flight
+  stage_sync_keep<2 * NV + C::A_LOADS>();       // stage 0 landed
   v4i fa0[C::TM], fb0[C::TN], fa1[C::TM], fb1[C::TN];
-  read_frags(s0, 0, fa0, fb0);
+  read_frags(buf(0), 0, fa0, fb0);
   for (int kt = 0; kt < KT; ++kt) {
-    int8_t* cur = (kt & 1) ? s1 : s0;
-    int8_t* nxt = (kt & 1) ? s0 : s1;
+    int8_t* cur = buf(kt);
+    // sub-step 0 of stage kt; B half of stage kt+3 into the buffer freed by B_{kt-1}
     read_frags(cur, 1, fa1, fb1);
+    issue_b(kt + 3, buf(kt + 3));
     mfma_all(fa0, fb0);
-    read_frags(cur, 2, fa0, fb0);
+    sched_substep<C::TM + C::TN, C::TM * C::TN, C::B_LOADS>();
+    // B_kt: reads of `cur` returned everywhere; stage kt+1 landed (stages
+    // kt+2 and kt+3 may still be in flight)
+    stage_sync_keep<2 * NV>();
+    // sub-step 1 of stage kt; A half of stage kt+4 into `cur`
+    read_frags(buf(kt + 1), 0, fa0, fb0);
+    issue_a(kt + 4, cur);
     mfma_all(fa1, fb1);
-    read_frags(cur, 3, fa1, fb1);
-    mfma_all(fa0, fb0);
-    stage_sync();                        // reads of `cur` returned; stage kt+1 landed
-    issue(kt + 2, cur);                  // refill the stage just consumed
-    read_frags(nxt, 0, fa0, fb0);        // first fragments of stage kt+1
-    mfma_all(fa1, fb1);
-    // Order of the last sub-step: refill copies and next-stage reads slot
-    // between its MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-    for (int x = 0; x < C::TM + C::TN; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
-    }
-    __builtin_amdgcn_sched_group_barrier(0x020, C::A_LOADS + C::B_LOADS, 0);   // VMEM read
-    __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - 1 - (C::TM + C::TN), 0);
+    sched_substep<C::TM + C::TN, C::TM * C::TN, C::A_LOADS>();
   }
   // The last iterations issued zero-filling copies for stages past KT into
   // the stage buffers the epilogue reuses: drain them first.
