@@ -38,8 +38,10 @@
 //     arithmetic (fround(acc * fround(sA[m] * sB[n])) or fround(acc * s_out),
 //     f64 where the reference is f64), adds the bias and applies ReLU /
 //     SiLU before the only store of the output.
-// GEMV (M <= 16): HBM-bound on B, packed int8 dot products (v_dot4_i32_i8),
-// no MFMA; see the kernel's own comment.
+// GEMV (M <= 16): HBM-bound on B.  M <= 4: packed int8 dot products
+// (v_dot4_i32_i8), no MFMA; 4 < M <= 16: one 16x16x64 MFMA per 16 weight
+// rows x 64 K-bytes (dot4 would make it VALU-bound); see the kernels' own
+// comments.
 #include <type_traits>
 
 #include "q8_device.h"
@@ -589,14 +591,17 @@ __device__ __forceinline__ int wave_butterfly_sum(int (&a)[V], int lane) {
   return a[0];
 }
 
-// One workgroup (4 waves) per group of GV_ROWS weight rows.  K is cut into
-// 16-byte chunks spread over all 256 lanes (CPT chunks per lane), so every
-// load instruction of a wave reads 1 KiB of one weight row and a lane's
-// activation chunks for all MT tokens stay in registers for the whole
-// group.  Partial dot products (v_dot4_i32_i8) are reduced across the wave
-// by a butterfly and across the 4 waves through a small LDS array; lanes of
-// wave 0 apply the epilogue.  All weight loads of a group are issued before
-// the first dot product.
+// ---- dot4 GEMV, M <= 4 tokens.  One workgroup (4 waves) per group of
+// GV_ROWS = 4 weight rows.  K is cut into 16-byte chunks spread over all
+// 256 lanes (CPT chunks per lane), so every load instruction of a wave
+// reads 1 KiB of one weight row, and a lane's activation chunks for all MT
+// tokens stay in registers for the group.  Small groups and many
+// workgroups keep the load ramp short and the reduction tail of each
+// workgroup small (measured against 16-row groups, which re-read the
+// activations 4x less but ran slower at every M <= 4).  All weight loads
+// of a group are issued before the first dot product.  Partial dot products
+// (v_dot4_i32_i8) are reduced across the wave by a butterfly and across the
+// 4 waves through a small LDS array; lanes of wave 0 apply the epilogue.
 constexpr int GV_ROWS = 4;
 
 template <int MT, int CPT>
@@ -604,22 +609,12 @@ __global__ __launch_bounds__(256)
 void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
                GemmEpi e, void* __restrict__ out) {
   constexpr int V = GV_ROWS * MT;
+  static_assert(V <= 64, "butterfly width");
   __shared__ int red[4][V];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int C = K >> 4;                                // 16-byte chunks per row
   const int n0 = blockIdx.x * GV_ROWS;
 
-  v4i xa[CPT][MT];
-#pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const int ch = tid + 256 * c;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      v4i v = {0, 0, 0, 0};
-      if (ch < C && m < M) v = *reinterpret_cast<const v4i*>(A + (int64_t)m * K + 16 * ch);
-      xa[c][m] = v;
-    }
-  }
   v4i w[GV_ROWS][CPT];
 #pragma unroll
   for (int r = 0; r < GV_ROWS; ++r)
@@ -631,6 +626,17 @@ void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M
         v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(B + (int64_t)(n0 + r) * K) + ch);
       w[r][c] = v;
     }
+  v4i xa[CPT][MT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int ch = tid + 256 * c;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      v4i v = {0, 0, 0, 0};
+      if (ch < C && m < M) v = *reinterpret_cast<const v4i*>(A + (int64_t)m * K + 16 * ch);
+      xa[c][m] = v;
+    }
+  }
   int acc[V];
 #pragma unroll
   for (int r = 0; r < GV_ROWS; ++r)
@@ -651,13 +657,88 @@ void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M
   if ((lane & ((1 << SHIFT) - 1)) == 0) red[wave][lane >> SHIFT] = total;
   __syncthreads();
   if (tid < V) {
-    const int r = tid / MT, m = tid % MT, n = n0 + r;
+    // lanes of one token write consecutive outputs: tid -> (token, row)
+    const int m = tid / GV_ROWS, r = tid % GV_ROWS, n = n0 + r, i = r * MT + m;
     if (m < M && n < N) {
       // int32 wrap-around sum, as the reference's Int32Array store
-      const int s = (int)((uint32_t)red[0][tid] + (uint32_t)red[1][tid] + (uint32_t)red[2][tid] +
-                          (uint32_t)red[3][tid]);
+      const int s = (int)((uint32_t)red[0][i] + (uint32_t)red[1][i] + (uint32_t)red[2][i] +
+                          (uint32_t)red[3][i]);
       if (e.out_i32) static_cast<int32_t*>(out)[(int64_t)m * N + n] = s;
       else static_cast<float*>(out)[(int64_t)m * N + n] = epi_value(s, m, n, e);
+    }
+  }
+}
+
+// ---- MFMA GEMV, 4 < M <= 16 tokens.  At 16 tokens a v_dot4 kernel spends
+// 64 VALU instructions per 16 weight bytes per lane and stops being
+// HBM-bound; one v_mfma_i32_16x16x64_i8 does the same work for 16 weight
+// rows x 64 K-bytes x all 16 tokens.  Weights are the A operand (lane l:
+// row l%16, K bytes 16*(l/16) of each 64-byte block), the tokens the B
+// operand in the same lane layout (rows >= M zero), so both operands
+// pair the same K bytes.  The workgroup's 4 waves split K into quarters of
+// KB blocks; each wave keeps its activation fragments in registers for
+// all the weight-row blocks it visits (grid-stride over blocks of 16 rows),
+// and the 4 partial 16x16 results meet in LDS (double-buffered: one
+// barrier per block).  Output element (row n0 + 4*(l/16) + r, token l%16)
+// is accumulator r of lane l.  At most 168 VGPRs (3 waves per SIMD), so
+// 3 workgroups per CU are resident and the C5 shapes run in one round.
+template <int KB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
+                 GemmEpi e, void* __restrict__ out) {
+  __shared__ int red[2][4][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int nblk = (N + 15) >> 4;
+  const int passes = (K + 256 * KB - 1) / (256 * KB);  // K bytes per pass: 4 waves x KB x 64
+  // Buffer loads: offsets past num_records return zeros.  Activation
+  // chunks past K are masked explicitly (zeros); weight chunks past K then
+  // only ever meet zero activations, so they need no mask.
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
+  v4i xf[KB];
+  auto load_x = [&](int pass) {
+    const int kw = pass * 256 * KB + wave * 64 * KB + 16 * g;
+    const uint32_t xrow = r16 < M ? (uint32_t)(r16 * K) : OOB;
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const int k = kw + 64 * j;
+      const uint32_t off = k < K ? xrow + (uint32_t)k : OOB;   // OOB + k stays past num_records
+      xf[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+    }
+  };
+  if (passes == 1) load_x(0);
+  int rb = 0;
+  for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x, rb ^= 1) {
+    const int n0 = blk * 16;
+    const int rows = N - n0 < 16 ? N - n0 : 16;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(B + (int64_t)n0 * K, (uint32_t)rows * (uint32_t)K);
+    v4i acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};     // two chains of dependent MFMAs
+    for (int pass = 0; pass < passes; ++pass) {
+      if (passes > 1) load_x(pass);
+      const uint32_t wo = (uint32_t)(r16 * K + pass * 256 * KB + wave * 64 * KB + 16 * g);
+      v4i w[KB];
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 64 * j, 0, 0));
+      // all KB weight loads in flight before the first MFMA waits on one
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < KB; j += 2) {
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], xf[j], acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j + 1], xf[j + 1], acc2, 0, 0, 0);
+      }
+    }
+    acc += acc2;   // int32 wrap-around sums: exact in any order
+    // token-major: red[.][t * 16 + i] holds (token t, row i) of this block
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[rb][wave][r16 * 16 + 4 * g + r] = acc[r];
+    __syncthreads();
+    const int t = tid >> 4, i = tid & 15, n = n0 + i;
+    if (t < M && n < N) {
+      const int s = (int)((uint32_t)red[rb][0][tid] + (uint32_t)red[rb][1][tid] +
+                          (uint32_t)red[rb][2][tid] + (uint32_t)red[rb][3][tid]);
+      if (e.out_i32) static_cast<int32_t*>(out)[(int64_t)t * N + n] = s;
+      else static_cast<float*>(out)[(int64_t)t * N + n] = epi_value(s, t, n, e);
     }
   }
 }
@@ -666,30 +747,47 @@ template <int MT>
 static hipError_t launch_gemv_mt(const int8_t* A, const int8_t* B, int M, int N, int K,
                                  const GemmEpi& e, void* out, hipStream_t st) {
   const dim3 grid((unsigned)((N + GV_ROWS - 1) / GV_ROWS)), block(256);
-  const int cpt = (K / 16 + 255) / 256;
+  const int cpt = (K / 16 + 255) / 256;               // <= 2 (K <= 8192)
   if (cpt <= 1)
     hipLaunchKernelGGL((k_gemv_i8<MT, 1>), grid, block, 0, st, A, B, M, N, K, e, out);
-  else if (cpt <= 2)
-    hipLaunchKernelGGL((k_gemv_i8<MT, 2>), grid, block, 0, st, A, B, M, N, K, e, out);
   else
-    hipLaunchKernelGGL((k_gemv_i8<MT, 4>), grid, block, 0, st, A, B, M, N, K, e, out);
+    hipLaunchKernelGGL((k_gemv_i8<MT, 2>), grid, block, 0, st, A, B, M, N, K, e, out);
+  return hipGetLastError();
+}
+
+static hipError_t launch_gemv_mfma(const int8_t* A, const int8_t* B, int M, int N, int K,
+                                   const GemmEpi& e, void* out, hipStream_t st) {
+  // every workgroup resident at once (3 per CU): weight loads of all row
+  // blocks are in flight together
+  const int nblk = (N + 15) / 16;
+  const int cap = 3 * cu_count();
+  const dim3 grid((unsigned)(nblk < cap ? nblk : cap)), block(256);
+  if (K <= 1024)
+    hipLaunchKernelGGL((k_gemv_mfma<4>), grid, block, 0, st, A, B, M, N, K, e, out);
+  else if (K <= 2048)
+    hipLaunchKernelGGL((k_gemv_mfma<8>), grid, block, 0, st, A, B, M, N, K, e, out);
+  else
+    hipLaunchKernelGGL((k_gemv_mfma<16>), grid, block, 0, st, A, B, M, N, K, e, out);
   return hipGetLastError();
 }
 
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  // 16-byte chunks, aligned rows, and K <= 4 * 256 * 16 for the register-resident activations;
-  // everything else goes to the GEMM kernels (which handle any M)
-  const bool vec = (K % 16 == 0) && K > 0 && K <= 16384 &&
+  // 16-byte chunks and aligned rows, else the GEMM kernels (which handle
+  // any M).  The dot4 kernel keeps 16 weight rows of K <= 2 * 256 * 16
+  // bytes in registers; the MFMA kernel walks any K in passes.
+  const bool vec = (K % 16 == 0) && K > 0 && K < (int64_t)1 << 30 &&
                    ((reinterpret_cast<uintptr_t>(A) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(B) & 15) == 0);
   if (!vec) return launch_gemm(A, B, M, N, K, e, out, st);
+  if (M > 4 || K > 8192) {
+    if (16 * K >= (int64_t)OOB) return launch_gemm(A, B, M, N, K, e, out, st);
+    return launch_gemv_mfma(A, B, (int)M, (int)N, (int)K, e, out, st);
+  }
   if (M <= 1) return launch_gemv_mt<1>(A, B, (int)M, (int)N, (int)K, e, out, st);
   if (M <= 2) return launch_gemv_mt<2>(A, B, (int)M, (int)N, (int)K, e, out, st);
-  if (M <= 4) return launch_gemv_mt<4>(A, B, (int)M, (int)N, (int)K, e, out, st);
-  if (M <= 8) return launch_gemv_mt<8>(A, B, (int)M, (int)N, (int)K, e, out, st);
-  return launch_gemv_mt<16>(A, B, (int)M, (int)N, (int)K, e, out, st);
+  return launch_gemv_mt<4>(A, B, (int)M, (int)N, (int)K, e, out, st);
 }
 
 hipError_t setup_kernel_attributes() {
