@@ -215,6 +215,37 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int epi, double s_out, const float* bias, int act,
             int out_kind, void* out, void* stream);
 
+/* ---------------------------------------------------------------- conv */
+
+/* quantized_conv (src/compiler/ir/graph/ops/quantization.ts:156-190), as
+ * lowered by rules/quantization.ts:44-62 through buildConvNest
+ * (src/compiler/passes/lowering/lowering_registry.ts:335-449), with the
+ * per-tensor `dequantize` QuantizationPass appends to it fused
+ * (quantization_pass.ts:286-360; output_scale = input_scale * kernel_scale).
+ * Layouts are the op's default input_layout "NCHW" / kernel_layout "OIHW"
+ * and their 1-D / 3-D forms (spatial_dims 1..3):
+ *   x: int8 [N, C, S_0..S_{d-1}], w: int8 [O, C/groups, K_0..K_{d-1}],
+ *   out: [N, O, P_0..P_{d-1}] with
+ *   P_i = floor((S_i + pad_lo_i + pad_hi_i - ((K_i - 1) * dilation_i + 1)) / strides_i) + 1
+ *   (inferConvResultTypes, src/compiler/ir/graph/ops/linalg.ts:222-248).
+ * acc[n,o,p] = sum over ic < C/groups and kernel positions k of
+ *   (x[n, g*C/groups + ic, p*stride + k*dilation - pad_lo] - zp_x) * (w[o, ic, k] - zp_w),
+ *   g = o / (O/groups); a tap in the padding adds 0; int32 wrap-around.
+ * out_kind Q8_I32: out = acc; Q8_F32: out = fround(acc * s_out).
+ * zp_x / zp_w must be 0 in this build (Q8_ERR_UNSUPPORTED otherwise).
+ * workspace: device memory of at least q8_quantized_conv_workspace bytes
+ * (may be 0: then NULL is accepted); calls that share a workspace must be
+ * ordered (same stream). */
+int q8_quantized_conv_workspace(int spatial_dims, const int64_t* x_shape, const int64_t* w_shape,
+                                const int64_t* strides, const int64_t* pad_lo,
+                                const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                                size_t* bytes);
+int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const int64_t* x_shape,
+                      const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
+                      const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                      int32_t zp_x, int32_t zp_w, int out_kind, double s_out, void* workspace,
+                      size_t workspace_bytes, void* out, void* stream);
+
 /* ---------------------------------------------------------------- fused */
 
 /* h = fround(silu(g) * u) for the gated MLP (SiLU decomposition

@@ -22,7 +22,7 @@ NODE_ADDON = os.path.join(NODE_DIR, "q8hip.node")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip"]
+SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip", "q8_conv.hip"]
 
 # IEEE arithmetic everywhere (the kernels reproduce the reference's f64 /
 # f32 rounding bit for bit), no packed-FP32 instructions, gfx950 only.
@@ -42,9 +42,28 @@ HIP_FLAGS = [
 
 
 def build_hip(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    """Compile every source to an object in parallel (they share no device
+    code), then link the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+
+    def compile_one(src):
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        cmd = [HIPCC, *compile_flags, "-I", os.path.join(ROOT, "include"), "-c", "-o", obj,
+               os.path.join(CSRC, src)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        return obj
+
+    workers = min(len(SOURCES), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objs = list(pool.map(compile_one, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

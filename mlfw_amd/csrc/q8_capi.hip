@@ -406,6 +406,112 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, c
   return launched(q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream)), "q8_gemv launch");
 }
 
+static int conv_geom(const char* who, int d, const int64_t* xs, const int64_t* ws,
+                     const int64_t* strides, const int64_t* pad_lo, const int64_t* pad_hi,
+                     const int64_t* dilation, int64_t groups, q8::ConvGeom* G) {
+  Q8_REQUIRE(d >= 1 && d <= 3, "%s: spatial_dims must be 1, 2 or 3 (got %d)", who, d);
+  Q8_REQUIRE(xs && ws && strides && pad_lo && pad_hi && dilation, "%s: NULL shape array", who);
+  constexpr int64_t LIM = (1LL << 31) - 1;
+  Q8_REQUIRE(xs[0] >= 0 && xs[1] >= 1 && ws[0] >= 1 && ws[1] >= 1 && xs[0] <= LIM &&
+                 xs[1] <= LIM && ws[0] <= LIM && ws[1] <= LIM,
+             "%s: bad channel or batch sizes", who);
+  Q8_REQUIRE(groups >= 1 && xs[1] % groups == 0 && ws[0] % groups == 0 && ws[1] * groups == xs[1],
+             "%s: groups=%lld must divide C=%lld and O=%lld with kernel I = C / groups (I=%lld)", who,
+             (long long)groups, (long long)xs[1], (long long)ws[0], (long long)ws[1]);
+  G->d = d;
+  G->N = xs[0];
+  G->C = xs[1];
+  G->O = ws[0];
+  G->groups = groups;
+  G->Cg = (int)ws[1];
+  G->Og = (int)(ws[0] / groups);
+  int64_t Sn = 1, Kn = 1, Pn = 1;
+  for (int i = 0; i < 3; ++i) {
+    if (i >= d) {
+      G->S[i] = G->K[i] = G->P[i] = 1;
+      G->st[i] = 1;
+      G->lo[i] = 0;
+      G->dl[i] = 1;
+      continue;
+    }
+    const int64_t S = xs[2 + i], K = ws[2 + i];
+    Q8_REQUIRE(S >= 1 && S <= LIM && K >= 1 && K <= LIM, "%s: bad spatial size in dim %d", who, i);
+    Q8_REQUIRE(strides[i] >= 1 && strides[i] <= LIM && dilation[i] >= 1 && dilation[i] <= LIM,
+               "%s: stride and dilation must be >= 1 (dim %d)", who, i);
+    Q8_REQUIRE(pad_lo[i] >= 0 && pad_hi[i] >= 0 && pad_lo[i] <= LIM && pad_hi[i] <= LIM,
+               "%s: padding must be >= 0 (dim %d)", who, i);
+    const int64_t eff = (K - 1) * dilation[i] + 1;
+    const int64_t span = S + pad_lo[i] + pad_hi[i] - eff;
+    Q8_REQUIRE(span >= 0, "%s: kernel extent %lld exceeds the padded input %lld in dim %d", who,
+               (long long)eff, (long long)(S + pad_lo[i] + pad_hi[i]), i);
+    const int64_t P = span / strides[i] + 1;
+    G->S[i] = (int)S;
+    G->K[i] = (int)K;
+    G->P[i] = (int)P;
+    G->st[i] = strides[i];
+    G->lo[i] = pad_lo[i];
+    G->dl[i] = dilation[i];
+    Q8_REQUIRE(mul_ok(Sn, S) && mul_ok(Kn, K) && mul_ok(Pn, P), "%s: size overflow", who);
+    Sn *= S;
+    Kn *= K;
+    Pn *= P;
+  }
+  Q8_REQUIRE(Kn <= LIM && mul_ok(Kn, G->Cg) && Kn * G->Cg <= LIM - 16, "%s: contraction too long", who);
+  Q8_REQUIRE(mul_ok(G->N * G->C, Sn) && mul_ok(G->N * G->O, Pn) && G->N * G->O * Pn < (1LL << 39) &&
+                 mul_ok(Pn, Kn * G->Cg + 16) && Pn * (Kn * G->Cg + 16) < (1LL << 39),
+             "%s: tensor too large", who);
+  G->Sn = Sn;
+  G->Pn = Pn;
+  G->Kn = (int)Kn;
+  G->Kc = (int)(Kn * G->Cg);
+  G->Kc16 = (G->Kc + 15) & ~15;
+  return Q8_OK;
+}
+
+int q8_quantized_conv_workspace(int spatial_dims, const int64_t* x_shape, const int64_t* w_shape,
+                                const int64_t* strides, const int64_t* pad_lo,
+                                const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                                size_t* bytes) {
+  Q8_REQUIRE(bytes != nullptr, "q8_quantized_conv_workspace: bytes is NULL");
+  q8::ConvGeom G;
+  int rc = conv_geom("q8_quantized_conv_workspace", spatial_dims, x_shape, w_shape, strides,
+                     pad_lo, pad_hi, dilation, groups, &G);
+  if (rc != Q8_OK) return rc;
+  *bytes = q8::conv_workspace_bytes(G);
+  g_err[0] = '\0';
+  return Q8_OK;
+}
+
+int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const int64_t* x_shape,
+                      const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
+                      const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                      int32_t zp_x, int32_t zp_w, int out_kind, double s_out, void* workspace,
+                      size_t workspace_bytes, void* out, void* stream) {
+  q8::ConvGeom G;
+  int rc = conv_geom("q8_quantized_conv", spatial_dims, x_shape, w_shape, strides, pad_lo, pad_hi,
+                     dilation, groups, &G);
+  if (rc != Q8_OK) return rc;
+  Q8_REQUIRE(out_kind == Q8_F32 || out_kind == Q8_I32,
+             "q8_quantized_conv: out_kind must be Q8_F32 or Q8_I32");
+  const bool empty = G.N * G.O * G.Pn == 0;
+  Q8_REQUIRE(empty || (x && w && out), "q8_quantized_conv: NULL pointer");
+  const size_t need = q8::conv_workspace_bytes(G);
+  Q8_REQUIRE(empty || workspace_bytes >= need,
+             "q8_quantized_conv: workspace of %zu bytes is smaller than the %zu bytes required "
+             "(q8_quantized_conv_workspace)", workspace_bytes, need);
+  Q8_REQUIRE(empty || need == 0 || workspace, "q8_quantized_conv: workspace is NULL");
+  if (zp_x != 0 || zp_w != 0)
+    return fail(Q8_ERR_UNSUPPORTED, "q8_quantized_conv: non-zero zero points are not supported by this build");
+  q8::GemmEpi e{};
+  e.mode = 0;
+  e.s_out = s_out;
+  e.out_i32 = out_kind == Q8_I32;
+  rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_conv(x, w, G, e, workspace, out, as_stream(stream)),
+                  "q8_quantized_conv launch");
+}
+
 int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K, float* h_out,
                               int8_t* q, double* scales, void* stream) {
   Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_silu_mul_quantize_rows: bad shape");

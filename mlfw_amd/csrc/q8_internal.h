@@ -45,6 +45,23 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
 
+// Geometry of a quantized_conv (NC(spatial) input, OI(spatial) kernel);
+// unused trailing spatial dimensions have size 1.  Validated by the C ABI:
+// every int field and Cg * prod(K) below 2^31.
+struct ConvGeom {
+  int d;                         // spatial rank, 1..3
+  int64_t N, C, O, groups;
+  int Cg, Og;                    // input / output channels per group
+  int S[3], K[3], P[3];          // input, kernel, output spatial sizes
+  int64_t st[3], lo[3], dl[3];   // stride, leading padding, dilation
+  int64_t Sn, Pn;                // prod(S), prod(P)
+  int Kn, Kc, Kc16;              // prod(K), Cg * prod(K), Kc rounded up to 16
+};
+bool conv_uses_gemm(const ConvGeom& G);
+size_t conv_workspace_bytes(const ConvGeom& G);
+hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, const GemmEpi& e,
+                       void* workspace, void* out, hipStream_t st);
+
 // Calibration observer state in device memory: this header, then
 // num_bins 64-bit bin counts, then num_bins words of re-bucketing scratch.
 constexpr size_t Q8_OBS_HEADER = 128;

@@ -275,6 +275,60 @@ def qlinear_pt(A: torch.Tensor, B: torch.Tensor, s_out: float,
     return out
 
 
+def _i64_array(vals):
+    arr = (C.c_int64 * max(1, len(vals)))(*[int(v) for v in vals])
+    return arr
+
+
+def conv_out_shape(x_shape, w_shape, strides, padding, dilation=None):
+    """[N, O, P_0..] of quantized_conv (inferConvResultTypes,
+    src/compiler/ir/graph/ops/linalg.ts:222-248); padding is [[lo, hi], ...]."""
+    d = len(strides)
+    dilation = list(dilation) if dilation is not None else [1] * d
+    out = [int(x_shape[0]), int(w_shape[0])]
+    for i in range(d):
+        eff = (int(w_shape[2 + i]) - 1) * dilation[i] + 1
+        out.append((int(x_shape[2 + i]) + padding[i][0] + padding[i][1] - eff) // strides[i] + 1)
+    return out
+
+
+def quantized_conv(x: torch.Tensor, w: torch.Tensor, strides, padding, dilation=None,
+                   groups: int = 1, s_out: float | None = None, out: torch.Tensor | None = None,
+                   workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """quantized_conv (src/compiler/ir/graph/ops/quantization.ts:156-190):
+    int8 x [N, C, S..] (NCHW and its 1-D / 3-D forms) and w [O, C/groups, K..]
+    (OIHW), padding as [[lo, hi], ...] per spatial dim.  s_out None: the
+    int32 accumulator; otherwise the fused per-tensor dequantize
+    fround(acc * s_out) as fp32 (the `dequantize` QuantizationPass appends,
+    output_scale = input_scale * kernel_scale)."""
+    _need(x, torch.int8, "quantized_conv x")
+    _need(w, torch.int8, "quantized_conv w")
+    d = len(strides)
+    if x.dim() != 2 + d or w.dim() != 2 + d or len(padding) != d:
+        raise ValueError(f"quantized_conv: {d} spatial dims need {2 + d}-D x and w and {d} padding pairs")
+    dilation = list(dilation) if dilation is not None else [1] * d
+    xs, ws = _i64_array(x.shape), _i64_array(w.shape)
+    st, dl = _i64_array(strides), _i64_array(dilation)
+    lo, hi = _i64_array([p[0] for p in padding]), _i64_array([p[1] for p in padding])
+    need = C.c_size_t(0)
+    L.call("q8_quantized_conv_workspace", d, xs, ws, st, lo, hi, dl, groups, C.byref(need))
+    shape = conv_out_shape(x.shape, w.shape, strides, padding, dilation)
+    dtype = torch.int32 if s_out is None else torch.float32
+    if out is None:
+        out = torch.empty(shape, dtype=dtype, device=x.device)
+    else:
+        _need(out, dtype, "quantized_conv out")
+        if list(out.shape) != shape:
+            raise ValueError(f"quantized_conv: out must have shape {shape}")
+    if need.value and (workspace is None or workspace.numel() < need.value):
+        workspace = torch.empty(need.value, dtype=torch.int8, device=x.device)
+    _call("q8_quantized_conv", _ptr(x), _ptr(w), d, xs, ws, st, lo, hi, dl, groups, 0, 0,
+          L.Q8_I32 if s_out is None else L.Q8_F32, 0.0 if s_out is None else float(s_out),
+          _ptr(workspace if need.value else None), need.value, _ptr(out), _stream(),
+          keep=(xs, ws, st, lo, hi, dl, workspace))
+    return out
+
+
 def silu_mul_quantize(g: torch.Tensor, u: torch.Tensor, h_out: torch.Tensor | None = None):
     """h = fround(silu(g) * u), then per-token int8 quantize of h.
     Returns (int8 codes, f64 scales[M])."""

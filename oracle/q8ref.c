@@ -316,6 +316,62 @@ void q8r_quantized_dot(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
     }
 }
 
+/* quantized_conv: the loop nest buildConvNest emits
+ * (lowering_registry.ts:335-449) -- zero-init the output, then for every
+ * (n, oc, output position, ic, kernel position) add the guarded product
+ * (x - zpx) * (w - zpw) (rules/quantization.ts:44-62), 0 for a tap in the
+ * padding.  The JS accumulation is exact (|sum| < 2^53), the store is
+ * ToInt32. */
+void q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* x_shape,
+                        const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
+                        const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                        int32_t zpx, int32_t zpw, int32_t* out) {
+  const int64_t N = x_shape[0], C = x_shape[1], O = w_shape[0], Cg = w_shape[1];
+  const int64_t Og = O / groups;
+  int64_t S[3] = {1, 1, 1}, K[3] = {1, 1, 1}, P[3] = {1, 1, 1};
+  int64_t st[3] = {1, 1, 1}, lo[3] = {0, 0, 0}, dl[3] = {1, 1, 1};
+  for (int i = 0; i < d; i++) {
+    S[i] = x_shape[2 + i];
+    K[i] = w_shape[2 + i];
+    st[i] = strides[i];
+    lo[i] = pad_lo[i];
+    dl[i] = dilation[i];
+    P[i] = (S[i] + pad_lo[i] + pad_hi[i] - ((K[i] - 1) * dilation[i] + 1)) / strides[i] + 1;
+  }
+  const int64_t Sn = S[0] * S[1] * S[2], Kn = K[0] * K[1] * K[2], Pn = P[0] * P[1] * P[2];
+  for (int64_t n = 0; n < N; n++)
+    for (int64_t o = 0; o < O; o++) {
+      const int64_t g = o / Og;
+      for (int64_t p0 = 0; p0 < P[0]; p0++)
+        for (int64_t p1 = 0; p1 < P[1]; p1++)
+          for (int64_t p2 = 0; p2 < P[2]; p2++) {
+            int64_t acc = 0;
+            for (int64_t ic = 0; ic < Cg; ic++) {
+              const int8_t* xc = x + (n * C + g * Cg + ic) * Sn;
+              const int8_t* wc = w + (o * Cg + ic) * Kn;
+              for (int64_t k0 = 0; k0 < K[0]; k0++) {
+                const int64_t s0 = p0 * st[0] + k0 * dl[0] - lo[0];
+                if (s0 < 0 || s0 >= S[0]) continue;
+                for (int64_t k1 = 0; k1 < K[1]; k1++) {
+                  const int64_t s1 = p1 * st[1] + k1 * dl[1] - lo[1];
+                  if (s1 < 0 || s1 >= S[1]) continue;
+                  for (int64_t k2 = 0; k2 < K[2]; k2++) {
+                    const int64_t s2 = p2 * st[2] + k2 * dl[2] - lo[2];
+                    if (s2 < 0 || s2 >= S[2]) continue;
+                    const int64_t a = (int64_t)xc[(s0 * S[1] + s1) * S[2] + s2] - zpx;
+                    const int64_t b = (int64_t)wc[(k0 * K[1] + k1) * K[2] + k2] - zpw;
+                    acc += a * b;
+                  }
+                }
+              }
+            }
+            out[((n * O + o) * P[0] + p0) * P[1] * P[2] + p1 * P[2] + p2] =
+                (int32_t)(uint32_t)(uint64_t)acc;
+          }
+    }
+  (void)Pn;
+}
+
 /* ------------------------------------------------------------------ */
 /* epilogues and elementwise                                           */
 /* ------------------------------------------------------------------ */

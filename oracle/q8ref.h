@@ -107,6 +107,24 @@ void     q8r_dequantize_rows_i8(const int8_t* q, int64_t M, int64_t K, const dou
 void     q8r_quantized_dot(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                            int b_layout, int32_t zpA, int32_t zpB, int32_t* acc);
 
+/* ---- quantized_conv, src/compiler/ir/graph/ops/quantization.ts:156-190,
+ * lowering rules/quantization.ts:44-62 through buildConvNest
+ * (src/compiler/passes/lowering/lowering_registry.ts:335-449) ----
+ * Layouts NC(spatial) / OI(spatial) (input_layout "NCHW", kernel_layout
+ * "OIHW" and their 1-D / 3-D forms), spatial_dims d in 1..3:
+ *   x [N, C, S_0..S_{d-1}], w [O, C/groups, K_0..K_{d-1}],
+ *   out [N, O, P_0..P_{d-1}],
+ *   P_i = floor((S_i + lo_i + hi_i - ((K_i - 1) * dil_i + 1)) / stride_i) + 1
+ *   (inferConvResultTypes, src/compiler/ir/graph/ops/linalg.ts:222-248).
+ * out[n,o,p] = sum over ic, k of (x[n, g*Cg + ic, p*stride + k*dil - lo] - zpx)
+ *              * (w[o, ic, k] - zpw), g = o / (O / groups), where a tap whose
+ * input coordinate falls outside [0, S_i) adds 0 (the guardFill of the
+ * IfThenElse, not (0 - zpx) * (w - zpw)); exact, stored ToInt32. */
+void     q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* x_shape,
+                            const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
+                            const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                            int32_t zpx, int32_t zpw, int32_t* out);
+
 /* ---- epilogues (quantization_pass.ts:335-355 E-pt, :431-456 E-pc) ----
  * mode 0 (E-pt):      y = fround(acc * s_out)            s_out = sA*sB in f64
  * mode 1 (E-pc/rowcol): y = fround(acc * fround(sA[m] * sB[n]))

@@ -24,6 +24,7 @@ _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _i64 = C.c_int64
 _dbl = C.c_double
 _int = C.c_int
@@ -86,6 +87,8 @@ def lib():
         "q8r_dequantize_i32": (None, [_i32p, _i64, _dbl, _dbl, _f32p]),
         "q8r_dequantize_rows_i8": (None, [_i8p, _i64, _i64, _f64p, _f32p]),
         "q8r_quantized_dot": (None, [_i8p, _i8p, _i64, _i64, _i64, _int, C.c_int32, C.c_int32, _i32p]),
+        "q8r_quantized_conv": (None, [_i8p, _i8p, _int, _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
+                                      _i64, C.c_int32, C.c_int32, _i32p]),
         "q8r_epilogue": (None, [_i32p, _i64, _i64, _int, _f64p, _i64, _f64p, _i64, _dbl,
                                 C.c_void_p, _int, _f32p]),
         "q8r_relu": (C.c_float, [C.c_float]),
@@ -294,6 +297,32 @@ def quantized_dot(A, B, b_layout=1, zpA=0, zpB=0) -> np.ndarray:
     acc = np.empty((M, N), np.int32)
     lib().q8r_quantized_dot(A.reshape(-1), B.reshape(-1), M, N, K, b_layout, zpA, zpB, acc.reshape(-1))
     return acc
+
+
+def conv_out_shape(x_shape, w_shape, strides, padding, dilation):
+    """inferConvResultTypes (src/compiler/ir/graph/ops/linalg.ts:222-248):
+    [N, O, P_0..]; padding is a list of [lo, hi] pairs."""
+    out = [int(x_shape[0]), int(w_shape[0])]
+    for i in range(len(strides)):
+        eff = (int(w_shape[2 + i]) - 1) * dilation[i] + 1
+        out.append((int(x_shape[2 + i]) + padding[i][0] + padding[i][1] - eff) // strides[i] + 1)
+    return out
+
+
+def quantized_conv(x, w, strides, padding, dilation=None, groups=1, zpx=0, zpw=0) -> np.ndarray:
+    """quantized_conv with NC(spatial) input / OI(spatial) kernel, int32 out
+    (ops/quantization.ts:156-190, buildConvNest lowering_registry.ts:335-449)."""
+    x = _c(x, np.int8)
+    w = _c(w, np.int8)
+    d = len(strides)
+    dilation = list(dilation) if dilation is not None else [1] * d
+    shp = conv_out_shape(x.shape, w.shape, strides, padding, dilation)
+    out = np.empty(shp, np.int32)
+    a64 = lambda v: _c(list(v), np.int64)  # noqa: E731
+    lib().q8r_quantized_conv(x.reshape(-1), w.reshape(-1), d, a64(x.shape), a64(w.shape), a64(strides),
+                             a64([p[0] for p in padding]), a64([p[1] for p in padding]),
+                             a64(dilation), groups, zpx, zpw, out.reshape(-1))
+    return out
 
 
 ACT = {"none": 0, "relu": 1, "silu": 2}

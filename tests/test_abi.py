@@ -107,3 +107,43 @@ def test_python_ops_refuse_cpu_tensors():
         ops.quantize_per_token(torch.zeros(2, 4))
     with pytest.raises(TypeError):
         ops.quantize_per_token(torch.zeros(2, 4, dtype=torch.float64))
+
+
+def _conv_args(x_shape, w_shape, strides, lo, hi, dil):
+    a = lambda v: (C.c_int64 * len(v))(*v)  # noqa: E731
+    return a(x_shape), a(w_shape), a(strides), a(lo), a(hi), a(dil)
+
+
+def test_conv_workspace_query_and_validation(lib):
+    L = lib.load()
+    need = C.c_size_t(123)
+    # the reference's own conv test shape (pass.test.js:255-274): 27-long contraction -> direct kernel
+    xs, ws, st, lo, hi, dl = _conv_args([1, 3, 8, 8], [16, 3, 3, 3], [1, 1], [0, 0], [0, 0], [1, 1])
+    assert L.q8_quantized_conv_workspace(2, xs, ws, st, lo, hi, dl, 1, C.byref(need)) == lib.Q8_OK
+    assert need.value == 0
+    # 64 x 3 x 3 contraction -> im2col matrix of 36 positions x 576 bytes
+    xs, ws, st, lo, hi, dl = _conv_args([2, 64, 8, 8], [32, 64, 3, 3], [1, 1], [0, 0], [0, 0], [1, 1])
+    assert L.q8_quantized_conv_workspace(2, xs, ws, st, lo, hi, dl, 1, C.byref(need)) == lib.Q8_OK
+    assert need.value >= 36 * 576
+    fake = C.c_void_p(0x1000)
+    bad = [
+        ([1, 4, 8, 8], [8, 3, 3, 3], 1),      # kernel I != C / groups
+        ([1, 4, 8, 8], [6, 2, 3, 3], 4),      # groups does not divide O
+        ([1, 4, 2, 2], [8, 4, 3, 3], 1),      # kernel larger than the input
+    ]
+    for x_shape, w_shape, groups in bad:
+        args = _conv_args(x_shape, w_shape, [1, 1], [0, 0], [0, 0], [1, 1])
+        expect_invalid(lib, "q8_quantized_conv_workspace", 2, *args, groups, C.byref(need))
+        expect_invalid(lib, "q8_quantized_conv", fake, fake, 2, *args, groups, 0, 0, lib.Q8_I32,
+                       0.0, fake, 1 << 20, fake, None)
+    args = _conv_args([1, 4, 8, 8], [8, 4, 3, 3], [0, 1], [0, 0], [0, 0], [1, 1])   # stride 0
+    expect_invalid(lib, "q8_quantized_conv_workspace", 2, *args, 1, C.byref(need))
+    args = _conv_args([1, 4, 8, 8], [8, 4, 3, 3], [1, 1], [-1, 0], [0, 0], [1, 1])  # negative pad
+    expect_invalid(lib, "q8_quantized_conv_workspace", 2, *args, 1, C.byref(need))
+    args = _conv_args([1, 64, 8, 8], [8, 64, 3, 3], [1, 1], [0, 0], [0, 0], [1, 1])
+    expect_invalid(lib, "q8_quantized_conv", fake, fake, 2, *args, 1, 0, 0, lib.Q8_I32, 0.0,
+                   fake, 16, fake, None, match="workspace")                          # workspace too small
+    expect_invalid(lib, "q8_quantized_conv", fake, fake, 4, *args, 1, 0, 0, lib.Q8_I32, 0.0,
+                   fake, 1 << 20, fake, None)                                        # rank 4
+    rc = L.q8_quantized_conv(fake, fake, 2, *args, 1, 2, 0, lib.Q8_I32, 0.0, fake, 1 << 20, fake, None)
+    assert rc == lib.Q8_ERR_UNSUPPORTED

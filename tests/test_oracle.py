@@ -222,6 +222,78 @@ def test_quantized_dot_int32_wrap(oracle):
     assert acc[0, 1] == -128 * 127 * K
 
 
+def _conv_windows(x, w, strides, padding, dilation, groups, zpx=0, zpw=0):
+    """Independent formulation of the convolution: pad the input with zpx
+    (so padded taps contribute (zpx - zpx) * (w - zpw) = 0), take strided
+    windows per kernel position and contract with numpy in int64."""
+    import itertools
+    N, C = x.shape[:2]
+    O, Cg = w.shape[:2]
+    d = len(strides)
+    pad = [(0, 0), (0, 0)] + [tuple(p) for p in padding]
+    xp = np.pad(x.astype(np.int64) - zpx, pad)            # padding = 0 after the shift
+    wz = w.astype(np.int64) - zpw
+    out_sp = [(xp.shape[2 + i] - ((w.shape[2 + i] - 1) * dilation[i] + 1)) // strides[i] + 1
+              for i in range(d)]
+    out = np.zeros([N, O] + out_sp, np.int64)
+    Og = O // groups
+    for kk in itertools.product(*[range(w.shape[2 + i]) for i in range(d)]):
+        sl = tuple(slice(kk[i] * dilation[i], kk[i] * dilation[i] + (out_sp[i] - 1) * strides[i] + 1,
+                         strides[i]) for i in range(d))
+        for g in range(groups):
+            xs = xp[(slice(None), slice(g * Cg, (g + 1) * Cg)) + sl]
+            ws = wz[(slice(g * Og, (g + 1) * Og), slice(None)) + tuple(kk)]
+            out[:, g * Og:(g + 1) * Og] += np.einsum("nc...,oc->no...", xs, ws)
+    return out.astype(np.int32)
+
+
+CONV_CASES = [
+    # x shape, w shape, strides, padding, dilation, groups
+    ((1, 3, 8, 8), (16, 3, 3, 3), [1, 1], [[0, 0], [0, 0]], [1, 1], 1),   # pass.test.js:255-274
+    ((1, 3, 8, 8), (16, 3, 3, 3), [2, 2], [[1, 1], [1, 1]], [1, 1], 1),   # pass.test.js:308-320
+    ((2, 4, 9, 7), (6, 2, 3, 2), [2, 1], [[1, 2], [0, 1]], [2, 1], 2),
+    ((1, 6, 10), (6, 1, 3), [1], [[1, 1]], [2], 6),                       # depthwise 1-D
+    ((1, 2, 5, 6, 4), (3, 2, 2, 3, 2), [1, 2, 1], [[1, 0], [0, 1], [1, 1]], [1, 1, 2], 1),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_quantized_conv_matches_window_formulation(oracle, case):
+    xs, ws, st, pd, dl, g = case
+    rng = np.random.default_rng(len(xs) * 7 + g)
+    x = rng.integers(-128, 128, xs).astype(np.int8)
+    w = rng.integers(-128, 128, ws).astype(np.int8)
+    same_bits(oracle.quantized_conv(x, w, st, pd, dl, g), _conv_windows(x, w, st, pd, dl, g))
+    # zero points: a padded tap adds 0, not (0 - zpx) * (w - zpw)
+    same_bits(oracle.quantized_conv(x, w, st, pd, dl, g, zpx=3, zpw=-2),
+              _conv_windows(x, w, st, pd, dl, g, zpx=3, zpw=-2))
+
+
+def test_quantized_conv_counts_valid_taps(oracle):
+    """(x - zpx) = (w - zpw) = 1 everywhere: every output is the number of
+    taps whose input coordinate is inside the image, a closed form."""
+    x = np.full((1, 2, 5, 4), 4, np.int8)
+    w = np.full((3, 2, 3, 2), -1, np.int8)
+    out = oracle.quantized_conv(x, w, [1, 1], [[1, 1], [0, 1]], [1, 1], 1, zpx=3, zpw=-2)
+    for oh in range(out.shape[2]):
+        for ow in range(out.shape[3]):
+            rows = sum(1 for kh in range(3) if 0 <= oh + kh - 1 < 5)
+            cols = sum(1 for kw in range(2) if 0 <= ow + kw < 4)
+            assert (out[0, :, oh, ow] == 2 * rows * cols).all()
+
+
+def test_quantized_conv_1x1_is_a_matmul(oracle):
+    """A 1x1 stride-1 conv is quantized_dot of the [C, H*W] image with the
+    [O, C] weight (the brute-forced M1 above)."""
+    rng = np.random.default_rng(5)
+    x = rng.integers(-128, 128, (1, 40, 3, 5)).astype(np.int8)
+    w = rng.integers(-128, 128, (24, 40, 1, 1)).astype(np.int8)
+    out = oracle.quantized_conv(x, w, [1, 1], [[0, 0], [0, 0]], [1, 1], 1)
+    mat = oracle.quantized_dot(np.ascontiguousarray(w.reshape(24, 40)),
+                               np.ascontiguousarray(x.reshape(40, 15).T), b_layout=1)
+    same_bits(out.reshape(24, 15), mat)
+
+
 def test_scales_per_token_closed_form(oracle):
     rng = np.random.default_rng(1)
     x = rng.standard_normal((6, 33)).astype(np.float32)
