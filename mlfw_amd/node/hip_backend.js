@@ -11,7 +11,7 @@
  *      src/backend/codegen_registry.ts:17-36) and its provider
  *      (registerExternalCodegenProvider, src/compiler/pipeline/external_codegen.ts:11-35):
  *      annotate() tags the PrimFuncs that QuantizationPass's ops lower to
- *      (`quantize`, `dequantize`, `quantized_dot`; block names from
+ *      (`quantize`, `dequantize`, `quantized_dot`, `quantized_conv`; block names from
  *      src/compiler/passes/lowering/rules/quantization.ts and
  *      lowering_registry.ts:313,329,574) and compile() returns a descriptor
  *      instead of source, the pattern of the cuBLAS entry
@@ -123,10 +123,83 @@ function findLoad(node, buffer) {
     const n = stack.pop();
     if (!n) continue;
     if (n.type === 'BufferLoadNode' && n.buffer.name === buffer.name) return n;
-    for (const k of ['a', 'b', 'expr', 'value']) if (n[k]) stack.push(n[k]);
+    for (const k of ['a', 'b', 'expr', 'value', 'condition', 'thenBody', 'elseBody']) if (n[k]) stack.push(n[k]);
     if (n.args) for (const a of n.args) stack.push(a);
   }
   return null;
+}
+
+// An index expression as sum(coef * var) + const, or null when it is not
+// linear (floor division, modulo, loads).  mathOp folds x*1 and x+0
+// (src/compiler/ir/tensor/nodes.ts:394-430), so the forms vary.
+function linearize(e) {
+  if (!e) return null;
+  if (e.type === 'IntImmNode') return { coef: new Map(), c: e.value };
+  if (e.type === 'VariableNode') return { coef: new Map([[e.name, 1]]), c: 0 };
+  if (e.type !== 'MathOpNode') return null;
+  const a = linearize(e.a), b = linearize(e.b);
+  if (!a || !b) return null;
+  if (e.op === '+' || e.op === '-') {
+    const sg = e.op === '+' ? 1 : -1;
+    const coef = new Map(a.coef);
+    for (const [v, k] of b.coef) coef.set(v, (coef.get(v) || 0) + sg * k);
+    return { coef, c: a.c + sg * b.c };
+  }
+  if (e.op === '*') {
+    if (a.coef.size === 0) return { coef: new Map([...b.coef].map(([v, k]) => [v, k * a.c])), c: a.c * b.c };
+    if (b.coef.size === 0) return { coef: new Map([...a.coef].map(([v, k]) => [v, k * b.c])), c: a.c * b.c };
+  }
+  return null;
+}
+
+// qconv_acc of buildConvNest (src/compiler/passes/lowering/lowering_registry.ts:
+// 335-449): out[n, oc, o..] += guard(in[n, c(oc, ic), o*stride + k*dil - lo], ker[oc, ic, k..]).
+// Strides, dilation and leading padding are the coefficients and constant
+// of each input spatial index; the trailing padding only fixes the output
+// size, so the smallest one that gives the output's shape is used.
+function detectConv(blocks, primFunc) {
+  const init = blocks.find((b) => b.name.startsWith('qconv_init'));
+  const acc = blocks.find((b) => b.name.startsWith('qconv_acc'));
+  if (!init || !acc || acc.reads.length !== 2 || acc.writes.length !== 1) return null;
+  const X = acc.reads[0].buffer, W = acc.reads[1].buffer, Y = acc.writes[0].buffer;
+  if ((X.dtype !== 'i8') || W.dtype !== 'i8' || Y.dtype !== 'i32') return null;
+  const r = X.shape.length, d = r - 2;
+  if (d < 1 || d > 3 || W.shape.length !== r || Y.shape.length !== r) return null;
+  if (![...X.shape, ...W.shape, ...Y.shape].every((v) => typeof v === 'number')) return null;
+  if (X.shape[1] % W.shape[1] !== 0) return null;
+  const groups = X.shape[1] / W.shape[1];
+  if (W.shape[0] % groups !== 0 || Y.shape[0] !== X.shape[0] || Y.shape[1] !== W.shape[0]) return null;
+  const store = findStore(acc.body);
+  if (!store || store.indices.length !== r) return null;
+  const xl = findLoad(store.value, X), wl = findLoad(store.value, W);
+  if (!xl || !wl) return null;
+  const outVar = (i) => (store.indices[i].type === 'VariableNode' ? store.indices[i].name : null);
+  const kerVar = (i) => (wl.indices[i].type === 'VariableNode' ? wl.indices[i].name : null);
+  const strides = [], padLo = [], padHi = [], dilation = [];
+  for (let s = 0; s < d; s++) {
+    const S = X.shape[2 + s], K = W.shape[2 + s], P = Y.shape[2 + s];
+    const lin = linearize(xl.indices[2 + s]);
+    if (!lin) return null;
+    const ov = outVar(2 + s), kv = kerVar(2 + s);
+    for (const v of lin.coef.keys()) if (v !== ov && v !== kv) return null;
+    // a dimension of extent 1 may have its variable folded away
+    const st = ov ? (lin.coef.get(ov) || 0) : 0, dl = kv ? (lin.coef.get(kv) || 0) : 0;
+    const stride = P === 1 && st === 0 ? 1 : st, dil = K === 1 && dl === 0 ? 1 : dl;
+    if (stride < 1 || dil < 1 || lin.c > 0) return null;
+    const lo = 0 - lin.c, eff = (K - 1) * dil + 1;   // 0 - 0 is +0
+    const hi = Math.max(0, (P - 1) * stride + eff - S - lo);
+    if (Math.floor((S + lo + hi - eff) / stride) + 1 !== P) return null;
+    strides.push(stride); padLo.push(lo); padHi.push(hi); dilation.push(dil);
+  }
+  const product = isMath(store.value, '+') ? store.value.b : null;
+  const inner = product && product.type === 'IfThenElseNode' ? product.thenBody : product;
+  const zpX = inner && isMath(inner, '*') ? zeroPointOf(inner, X) : 0;
+  const zpW = inner && isMath(inner, '*') ? zeroPointOf(inner, W) : 0;
+  const xIdx = paramIndex(primFunc, X), wIdx = paramIndex(primFunc, W), outIdx = paramIndex(primFunc, Y);
+  if (xIdx < 0 || wIdx < 0 || outIdx < 0) return null;
+  return { op: 'quantized_conv', d, xShape: X.shape.slice(), wShape: W.shape.slice(),
+           outShape: Y.shape.slice(), strides, padLo, padHi, dilation, groups, zpX, zpW,
+           xIdx, wIdx, outIdx, outputIndices: [outIdx] };
 }
 
 // acc += ((a|0) [- zpA]) * ((b|0) [- zpB])  (rules/quantization.ts:33-39)
@@ -163,6 +236,9 @@ function detectInt8Kernel(primFunc) {
     if (!m || outBuf.dtype !== 'f32' || ['i8', 'ui8', 'i32'].indexOf(inBuf.dtype) < 0) return null;
     return { op: 'dequantize', n, scale: m.scale, zeroPoint: m.zeroPoint, srcDtype: inBuf.dtype,
              inIdx, outIdx, outputIndices: [outIdx] };
+  }
+  if (blocks.length === 2 && blocks.some((b) => b.name.startsWith('qconv_acc'))) {
+    return detectConv(blocks, primFunc);
   }
   if (blocks.length === 2) {
     const init = blocks.find((b) => b.name.startsWith('qmatmul_init'));
@@ -271,6 +347,23 @@ function runDescriptor(d, args, dev) {
     A.upload(db, d.rhsLayout === 'KN' ? transposeI8(b, d.K, d.N) : b);
     A.gemm(da, db, d.M, d.N, d.K, d.zpA, d.zpB, null, A.Q8_PER_TENSOR, null, A.Q8_PER_TENSOR,
            A.Q8_EPI_PT, 0, null, A.Q8_ACT_NONE, A.Q8_I32, dout);
+    A.download(out, dout);
+    return out;
+  }
+  if (d.op === 'quantized_conv') {
+    const x = args[d.xIdx], w = args[d.wIdx], out = args[d.outIdx];
+    const nx = numel(d.xShape), nw = numel(d.wShape), ny = numel(d.outShape);
+    need(x instanceof Int8Array && x.length === nx, 'quantized_conv input');
+    need(w instanceof Int8Array && w.length === nw, 'quantized_conv kernel');
+    need(out instanceof Int32Array && out.length === ny, 'quantized_conv output');
+    const wsBytes = A.convWorkspace(d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups);
+    const dx = dev.get('x', nx), dw = dev.get('w', nw), dout = dev.get('out', 4 * ny);
+    const dws = wsBytes > 0 ? dev.get('ws', wsBytes) : null;
+    A.upload(dx, x);
+    A.upload(dw, w);
+    // non-zero zero points are refused by the C ABI (Q8_ERR_UNSUPPORTED)
+    A.quantizedConv(dx, dw, d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation,
+                    d.groups, d.zpX, d.zpW, A.Q8_I32, 0, dws, dout);
     A.download(out, dout);
     return out;
   }

@@ -140,6 +140,27 @@ static int arg_host(napi_env env, napi_value v, void** data, size_t* bytes) {
   return 0;
 }
 
+/* A JS array of at most `max` integers. */
+static int arg_i64_array(napi_env env, napi_value v, int64_t* out, uint32_t max, uint32_t* n) {
+  bool is;
+  if (napi_is_array(env, v, &is) != napi_ok || !is) {
+    napi_throw_type_error(env, NULL, "q8hip: expected an array of numbers");
+    return 0;
+  }
+  uint32_t len;
+  if (napi_get_array_length(env, v, &len) != napi_ok) return 0;
+  if (len > max) {
+    napi_throw_range_error(env, NULL, "q8hip: array too long");
+    return 0;
+  }
+  for (uint32_t i = 0; i < len; i++) {
+    napi_value e;
+    if (napi_get_element(env, v, i, &e) != napi_ok || !arg_i64(env, e, &out[i])) return 0;
+  }
+  *n = len;
+  return 1;
+}
+
 /* ---------------------------------------------------------------- runtime */
 
 static napi_value js_version(napi_env env, napi_callback_info info) {
@@ -366,6 +387,64 @@ static napi_value js_gemm(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* Shape arguments of the conv entry points: xShape, wShape, strides, padLo,
+ * padHi, dilation as JS arrays (argv[0..5]) for `d` spatial dims. */
+typedef struct {
+  int64_t xs[5], ws[5], st[3], lo[3], hi[3], dl[3];
+} ConvArgs;
+static int conv_args(napi_env env, napi_value* argv, int64_t d, ConvArgs* c) {
+  uint32_t n[6];
+  if (d < 1 || d > 3) {
+    napi_throw_range_error(env, NULL, "q8hip: spatial dims must be 1, 2 or 3");
+    return 0;
+  }
+  if (!arg_i64_array(env, argv[0], c->xs, 5, &n[0]) || !arg_i64_array(env, argv[1], c->ws, 5, &n[1]) ||
+      !arg_i64_array(env, argv[2], c->st, 3, &n[2]) || !arg_i64_array(env, argv[3], c->lo, 3, &n[3]) ||
+      !arg_i64_array(env, argv[4], c->hi, 3, &n[4]) || !arg_i64_array(env, argv[5], c->dl, 3, &n[5]))
+    return 0;
+  if (n[0] != 2 + d || n[1] != 2 + d || n[2] != d || n[3] != d || n[4] != d || n[5] != d) {
+    napi_throw_range_error(env, NULL, "q8hip: conv shape arrays do not match the spatial rank");
+    return 0;
+  }
+  return 1;
+}
+
+/* convWorkspace(d, xShape, wShape, strides, padLo, padHi, dilation, groups) -> bytes */
+static napi_value js_conv_workspace(napi_env env, napi_callback_info info) {
+  napi_value argv[8], r;
+  int64_t d, groups;
+  ConvArgs c;
+  size_t bytes = 0;
+  if (!get_args(env, info, 8, argv) || !arg_i64(env, argv[0], &d) || !conv_args(env, argv + 1, d, &c) ||
+      !arg_i64(env, argv[7], &groups))
+    return NULL;
+  Q8_CHECK(env, q8_quantized_conv_workspace((int)d, c.xs, c.ws, c.st, c.lo, c.hi, c.dl, groups, &bytes));
+  napi_create_double(env, (double)bytes, &r);
+  return r;
+}
+
+/* quantizedConv(x, w, d, xShape, wShape, strides, padLo, padHi, dilation, groups,
+ *               zpX, zpW, outKind, sOut, workspace, out) */
+static napi_value js_quantized_conv(napi_env env, napi_callback_info info) {
+  napi_value argv[16];
+  void *x, *w, *ws, *out;
+  int64_t d, groups, zpx, zpw, ok;
+  double sOut;
+  ConvArgs c;
+  DevBuf* wsb = NULL;
+  if (!get_args(env, info, 16, argv) || !arg_buf(env, argv[0], 1, &x) || !arg_buf(env, argv[1], 1, &w) ||
+      !arg_i64(env, argv[2], &d) || !conv_args(env, argv + 3, d, &c) || !arg_i64(env, argv[9], &groups) ||
+      !arg_i64(env, argv[10], &zpx) || !arg_i64(env, argv[11], &zpw) || !arg_i64(env, argv[12], &ok) ||
+      !arg_f64(env, argv[13], &sOut) || !arg_buf(env, argv[14], 1, &ws) || !arg_buf(env, argv[15], 1, &out))
+    return NULL;
+  size_t ws_bytes = 0;
+  if (ws != NULL && arg_devbuf(env, argv[14], &wsb)) ws_bytes = wsb->bytes;
+  Q8_CHECK(env, q8_quantized_conv((const int8_t*)x, (const int8_t*)w, (int)d, c.xs, c.ws, c.st, c.lo,
+                                  c.hi, c.dl, groups, (int32_t)zpx, (int32_t)zpw, (int)ok, sOut, ws,
+                                  ws_bytes, out, NULL));
+  return undefined(env);
+}
+
 /* siluMulQuantizeRows(g, u, M, K, h, q, scales) */
 static napi_value js_silu_mul_quantize_rows(napi_env env, napi_callback_info info) {
   napi_value argv[7];
@@ -405,6 +484,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"packWeight", js_pack_weight},
       {"gemm", js_gemm},
       {"siluMulQuantizeRows", js_silu_mul_quantize_rows},
+      {"convWorkspace", js_conv_workspace},
+      {"quantizedConv", js_quantized_conv},
   };
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); ++i) {
     napi_value f;

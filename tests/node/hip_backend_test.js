@@ -86,8 +86,72 @@ function qdotPF(M, N, K, layout, zpA, zpB) {
   return primFunc('qdot', [a, b, c], [init, acc]);
 }
 
+// mathOp's constant folding (src/compiler/ir/tensor/nodes.ts:394-430)
+function mop(op, a, b) {
+  if (a.type === 'IntImmNode' && b.type === 'IntImmNode') {
+    if (op === '+') return I(a.value + b.value);
+    if (op === '*') return I(a.value * b.value);
+  }
+  if (b.type === 'IntImmNode' && ((op === '+' && b.value === 0) || (op === '*' && b.value === 1))) return a;
+  if (a.type === 'IntImmNode' && ((op === '+' && a.value === 0) || (op === '*' && a.value === 1))) return b;
+  return math(op, a, b);
+}
+// qconv_init / qconv_acc as buildConvNest emits them
+// (src/compiler/passes/lowering/lowering_registry.ts:335-449), NCHW / OIHW.
+function qconvPF(xs, ws, strides, padding, dilation, groups) {
+  const d = strides.length;
+  const os = [xs[0], ws[0]];
+  for (let s = 0; s < d; s++) {
+    const eff = (ws[2 + s] - 1) * dilation[s] + 1;
+    os.push(Math.floor((xs[2 + s] + padding[s][0] + padding[s][1] - eff) / strides[s]) + 1);
+  }
+  const x = buf('x', xs, 'i8'), w = buf('w', ws, 'i8'), y = buf('y', os, 'i32');
+  const n = V('qcv0'), oc = V('qcv1'), ic = V(`qcv${2 + d}`);
+  const so = [], sk = [];
+  for (let s = 0; s < d; s++) { so.push(V(`qcv${2 + s}`)); sk.push(V(`qcv${3 + d + s}`)); }
+  const Cg = ws[1], Og = ws[0] / groups;
+  const inIdx = [n, groups > 1 ? math('+', math('*', math('//', oc, I(Og)), I(Cg)), ic) : ic];
+  const kerIdx = [oc, ic];
+  let bounds = null;
+  for (let s = 0; s < d; s++) {
+    const e = mop('+', mop('*', so[s], I(strides[s])), mop('+', mop('*', sk[s], I(dilation[s])), I(-padding[s][0])));
+    inIdx.push(e);
+    kerIdx.push(sk[s]);
+    if (padding[s][0] || padding[s][1]) {
+      const ok = math('*', { type: 'CompareNode', op: 'ge', a: e, b: I(0) }, { type: 'CompareNode', op: 'lt', a: e, b: I(xs[2 + s]) });
+      bounds = bounds ? math('*', bounds, ok) : ok;
+    }
+  }
+  const outIdx = [n, oc, ...so];
+  const prod = math('*', cast(load(x, inIdx), 'i32'), cast(load(w, kerIdx), 'i32'));
+  const guarded = bounds ? { type: 'IfThenElseNode', condition: bounds, thenBody: prod, elseBody: I(0) } : prod;
+  const init = { type: 'BlockNode', name: 'qconv_init', reads: [], writes: [{ buffer: y }],
+                 body: { type: 'BufferStoreNode', buffer: y, indices: outIdx, value: I(0) } };
+  const acc = { type: 'BlockNode', name: 'qconv_acc_2', reads: [{ buffer: x }, { buffer: w }], writes: [{ buffer: y }],
+                body: { type: 'BufferStoreNode', buffer: y, indices: outIdx, value: math('+', load(y, outIdx), guarded) } };
+  return primFunc('qconv', [x, w, y], [init, acc]);
+}
+const CONV_CASE = { xs: [2, 4, 9, 7], ws: [6, 2, 3, 2], strides: [2, 1], padding: [[1, 2], [0, 1]],
+                    dilation: [2, 1], groups: 2 };
+
 // ---------------------------------------------------------------- CPU tests
 function cpuTests() {
+  test('detects quantized_conv geometry from the index expressions', () => {
+    const c = CONV_CASE;
+    const d = hip.detectInt8Kernel(qconvPF(c.xs, c.ws, c.strides, c.padding, c.dilation, c.groups));
+    assert.ok(d);
+    assert.strictEqual(d.op, 'quantized_conv');
+    assert.deepStrictEqual([d.strides, d.padLo, d.dilation, d.groups], [[2, 1], [1, 0], [2, 1], 2]);
+    assert.deepStrictEqual(d.outShape, [2, 6, 4, 7]);
+    // the trailing padding is the smallest that yields the output size
+    assert.deepStrictEqual(d.padHi, [1, 1]);
+    // stride 1, dilation 1 and no padding fold to bare variables (x*1, +0)
+    const e = hip.detectInt8Kernel(qconvPF([1, 3, 8, 8], [16, 3, 3, 3], [1, 1], [[0, 0], [0, 0]], [1, 1], 1));
+    assert.deepStrictEqual([e.strides, e.padLo, e.padHi, e.dilation, e.groups], [[1, 1], [0, 0], [0, 0], [1, 1], 1]);
+    const f = hip.detectInt8Kernel(qconvPF([1, 2, 10], [4, 2, 3], [3], [[2, 2]], [1], 1));
+    assert.deepStrictEqual([f.d, f.strides, f.padLo, f.outShape], [1, [3], [2], [1, 4, 4]]);
+  });
+
   test('registerHip plugs into all three registries', () => {
     const r = makeRegistries();
     const res = hip.registerHip(r);
@@ -243,6 +307,17 @@ function gpuTests(dir) {
     const y = dpt(q, s);
     assert.deepStrictEqual(y.shape, [M, K]);
     writeArr(dir, 'out_dpt.bin', y.data);
+  });
+
+  test('runtime backend: quantized_conv PrimFunc on the GPU', () => {
+    const c = CONV_CASE;
+    const xc = readArr(dir, 'conv_x.bin', Int8Array), wc = readArr(dir, 'conv_w.bin', Int8Array);
+    const pf = qconvPF(c.xs, c.ws, c.strides, c.padding, c.dilation, c.groups);
+    const info = hip.detectInt8Kernel(pf);
+    const kern = cg.compile(pf, hip.hipTarget(), info);
+    const y = new Int32Array(info.outShape.reduce((a, b) => a * b, 1));
+    be.runSync(be.instantiate(kern), [xc, wc, y], null);
+    writeArr(dir, 'out_conv.bin', y);
   });
 
   test('async path resolves to the same result', () => {

@@ -2,8 +2,9 @@
 
 CPU: registration into mock registries shaped like the reference's, TIR
 matching of QuantizationPass's lowered ops, argument errors (no device).
-GPU: C1 through the 'hip' runtime backend and the eager library, every
-output compared bit for bit with the oracle.
+GPU: C1 and a grouped, strided, dilated, padded quantized_conv through the
+'hip' runtime backend and the eager library, every output compared bit for
+bit with the oracle.
 """
 import json
 import os
@@ -63,6 +64,12 @@ def test_node_host_gpu_c1(tmp_path, oracle):
     for name, arr in (("X", X), ("Xq", Xq), ("Wq", Wq), ("sW", sW), ("bias", bias)):
         np.ascontiguousarray(arr).tofile(tmp_path / f"{name}.bin")
     (tmp_path / "meta.json").write_text(json.dumps({"M": M, "N": N, "K": K, "sX": sX, "sOut": s_out}))
+    # CONV_CASE of hip_backend_test.js
+    crng = np.random.default_rng(11)
+    xc = crng.integers(-128, 128, (2, 4, 9, 7)).astype(np.int8)
+    wc = crng.integers(-128, 128, (6, 2, 3, 2)).astype(np.int8)
+    xc.tofile(tmp_path / "conv_x.bin")
+    wc.tofile(tmp_path / "conv_w.bin")
     r = run_node("gpu", str(tmp_path))
     assert r.returncode == 0, r.stdout + r.stderr
 
@@ -81,3 +88,5 @@ def test_node_host_gpu_c1(tmp_path, oracle):
     same_bits(out("out_qpt_s", np.float64, (M,)), s_tok, "eager quantize_per_token scales")
     same_bits(out("out_dpt", np.float32, (M, K)), oracle.dequantize_rows(q_tok, s_tok),
               "eager dequantize_per_token")
+    conv_ref = oracle.quantized_conv(xc, wc, [2, 1], [[1, 2], [0, 1]], [2, 1], 2)
+    same_bits(out("out_conv", np.int32, conv_ref.shape), conv_ref, "quantized_conv PrimFunc")
