@@ -226,6 +226,39 @@ def bench_c4():
                                   "timing": how}}
 
 
+# ---------------------------------------------------------------- ceilings
+def ceilings():
+    """Practical ceilings measured on this box (mlfw_amd/libq8ceiling.so):
+    the C3 GEMM's MFMA work alone with random int8 operands (the clock the
+    part holds under that load), and the streaming-read time of one kernel
+    at the byte counts of the HBM-bound workloads (launch and ramp
+    included).  Reported beside the roofline fractions, which stay against
+    the datasheet peaks."""
+    import ctypes as C
+    from mlfw_amd import build as B
+    lib = C.CDLL(B.CEILING_LIB)
+    lib.q8c_mfma.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    lib.q8c_read.argtypes = [C.c_size_t, C.c_int, C.c_int, C.POINTER(C.c_double)]
+    us, mhz = C.c_double(), C.c_double()
+    out = {}
+    if lib.q8c_mfma(2048, 10, C.byref(us), C.byref(mhz)) == 0:
+        tops = GEMM_OPS / (us.value * 1e-6) / 1e12
+        out["mfma_random_int8_4096cube"] = {
+            "what": "256 workgroups x 4 waves x 2048 v_mfma_i32_32x32x32_i8 (the C3 GEMM's MFMA "
+                    "count), random operands, no loads or stores",
+            "avg_us": us.value, "TOPS": tops, "frac_of_peak": tops / PEAK_INT8_TOPS,
+            "shader_clock_mhz": mhz.value}
+    for name, nbytes in (("gemv_N4096", 4096 * 4096 + 8 * 4096 + 4 * 4096),
+                         ("gemv_N11008", 11008 * 4096 + 8 * 11008 + 4 * 4096),
+                         ("quantize_16384x4096", 335675392)):
+        bufs = max(5, math.ceil((1 << 30) / nbytes))
+        if lib.q8c_read(nbytes, bufs, 5, C.byref(us)) == 0:
+            gbs = nbytes / (us.value * 1e-6) / 1e9
+            out[f"read_{name}"] = {"bytes": nbytes, "avg_us": us.value, "GB/s": gbs,
+                                   "frac_of_peak": gbs / PEAK_HBM_GBS}
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(rows=256):
     """Reference CPU path (mirrored generated JS, one core) on `rows` rows of
@@ -265,6 +298,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the MFMA / streaming-read ceiling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy three times: the known-size "
                          "reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -322,6 +357,20 @@ def main():
                 secondary[name] = {"error": repr(exc)}
             torch.cuda.empty_cache()
 
+    ceil = None
+    if not args.no_ceilings:
+        log("[bench] ceilings (random-operand MFMA, single-kernel streaming reads)")
+        try:
+            ceil = ceilings()
+            m = ceil.get("mfma_random_int8_4096cube")
+            if m:
+                roofline["practical_ceiling"] = {
+                    "achieved": m["TOPS"], "unit": "TOPS", "frac_of_peak": m["frac_of_peak"],
+                    "shader_clock_mhz": m["shader_clock_mhz"],
+                    "gemm_frac_of_ceiling": gemm_tops / m["TOPS"]}
+        except Exception as exc:
+            ceil = {"error": repr(exc)}
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline (JS mirror of the reference CPU kernels, 1 core)")
@@ -351,6 +400,7 @@ def main():
                    "wall_ms_per_step": r["wall_ms_per_step"]},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "ceilings": ceil,
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)

@@ -21,6 +21,9 @@ NODE_DIR = os.path.join(HERE, "node")
 NODE_ADDON = os.path.join(NODE_DIR, "q8hip.node")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# measurement kernels of bench.py, kept out of the product library
+CEILING_LIB = os.path.join(HERE, "libq8ceiling.so")
+CEILING_SRC = "q8_ceiling.hip"
 
 SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip", "q8_conv.hip"]
 
@@ -71,6 +74,18 @@ def build_hip(verbose: bool = False) -> str:
     return LIB
 
 
+def build_ceiling(verbose: bool = False) -> str:
+    """libq8ceiling.so: the MFMA and streaming-read ceiling kernels bench.py
+    reports beside its roofline fractions (no C ABI of the int8 path)."""
+    tmp = CEILING_LIB + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-o", tmp, os.path.join(CSRC, CEILING_SRC)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, CEILING_LIB)
+    return CEILING_LIB
+
+
 def build_node_addon(verbose: bool = False) -> str | None:
     inc = "/usr/include/node"
     src = os.path.join(NODE_DIR, "q8hip_napi.c")
@@ -88,6 +103,7 @@ def build_node_addon(verbose: bool = False) -> str | None:
 
 def build_all(verbose: bool = False) -> None:
     build_hip(verbose)
+    build_ceiling(verbose)
     build_node_addon(verbose)
 
 
