@@ -215,6 +215,23 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int epi, double s_out, const float* bias, int act,
             int out_kind, void* out, void* stream);
 
+/* q8_gemm's fp32 result, requantized in the epilogue with the next layer's
+ * static scale and stored as int8: QuantizationPass's calibrated chain
+ * dequantize -> [add bias] -> [relu] -> quantize(s_next)
+ * (quantization_pass.ts:286-360, :390-459, with the `quantize` of the
+ * following dot) evaluated without the fp32 tensor ever reaching memory:
+ *   out[m,n] = (Math.min(Math.max(Math.round(Math.fround(y / s_next)), -128), 127) | 0),
+ *   y = act(bias + epilogue(acc)) exactly as q8_gemm's Q8_F32 output
+ * (the compiled quantize, quant_math.ts:16-27, symmetric int8).  s_next is
+ * a static (calibrated) scale: a dynamic per-token or per-tensor requant
+ * needs the whole row's / tensor's absmax before any element is rounded,
+ * which q8_quantize_rows provides as a separate pass.  Routes M <= 16 to
+ * the GEMV kernels. */
+int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                    const double* sA, int sA_mode, const double* sB, int sB_mode,
+                    int epi, double s_out, const float* bias, int act,
+                    double s_next, int8_t* out, void* stream);
+
 /* ---------------------------------------------------------------- conv */
 
 /* quantized_conv (src/compiler/ir/graph/ops/quantization.ts:156-190), as

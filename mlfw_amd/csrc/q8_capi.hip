@@ -367,6 +367,10 @@ static int gemm_common(const char* who, const int8_t* A, const int8_t* B, int64_
   e->mode = epi == Q8_EPI_ROWCOL ? 1 : 0;
   e->act = act;
   e->out_i32 = out_kind == Q8_I32;
+  e->out_q8 = 0;
+  e->s_q = 0.0;
+  e->rq32 = 0.0f;
+  e->q_fast = 0;
   if (out_kind == Q8_F32 && epi == Q8_EPI_ROWCOL) {
     Q8_REQUIRE(sA && sB, "%s: ROWCOL epilogue needs sA and sB", who);
     Q8_REQUIRE(sA_mode == Q8_PER_TENSOR || sA_mode == Q8_PER_TOKEN, "%s: bad sA_mode %d", who, sA_mode);
@@ -404,6 +408,28 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, c
   rc = ensure_current(nullptr);
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream)), "q8_gemv launch");
+}
+
+int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                    const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
+                    double s_out, const float* bias, int act, double s_next, int8_t* out,
+                    void* stream) {
+  q8::GemmEpi e;
+  int rc = gemm_common("q8_gemm_requant", A, B, M, N, K, 0, 0, sA, sA_mode, sB, sB_mode, epi,
+                       s_out, bias, act, Q8_F32, out, &e);
+  if (rc != Q8_OK) return rc;
+  // the `quantize` op's verifier (ops/quantization.ts:44-47): scale > 0
+  Q8_REQUIRE(s_next > 0.0 && std::isfinite(s_next),
+             "q8_gemm_requant: s_next must be a finite scale > 0 (got %g)", s_next);
+  e.out_q8 = 1;
+  e.s_q = s_next;
+  e.rq32 = (float)(1.0 / s_next);
+  e.q_fast = (s_next >= 0x1p-100 && s_next <= 0x1p100) ? 1 : 0;
+  rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  hipError_t err = (M <= 16) ? q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream))
+                             : q8::launch_gemm(A, B, M, N, K, e, out, as_stream(stream));
+  return launched(err, "q8_gemm_requant launch");
 }
 
 static int conv_geom(const char* who, int d, const int64_t* xs, const int64_t* ws,

@@ -77,6 +77,20 @@ __device__ __forceinline__ float epi_value(int acc, int64_t m, int64_t n, const 
   return epi_finish(y, n, e);
 }
 
+// The compiled `quantize` (quant_math.ts:16-27) of an epilogue value with the
+// next layer's static scale: q = (min(max(Math.round(fround(y / s)), -128), 127) | 0).
+__device__ __forceinline__ int requant(float y, const GemmEpi& e) {
+  return e.q_fast ? quant_sym_fast(y, e.rq32, e.s_q) : quant_exact(y, e.s_q, 0.0, -128, 127);
+}
+
+// Final store of one output element of the GEMV / generic kernels.
+__device__ __forceinline__ void store_out(void* out, int64_t idx, int acc, int64_t m, int64_t n,
+                                          const GemmEpi& e) {
+  if (e.out_i32) static_cast<int32_t*>(out)[idx] = acc;
+  else if (e.out_q8) static_cast<int8_t*>(out)[idx] = (int8_t)requant(epi_value(acc, m, n, e), e);
+  else static_cast<float*>(out)[idx] = epi_value(acc, m, n, e);
+}
+
 // ------------------------------------------------------------------ MFMA GEMM
 constexpr int BK = 64;                  // K bytes per LDS stage
 constexpr int NBUF = 4;                 // LDS stages in the ring
@@ -187,10 +201,13 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // Compile-time epilogue variant of the MFMA kernel:
 //   bit 4 int32 output (raw accumulators), else fp32 output with
 //   bit 3 MODE (0: fround(acc * s_out), 1: fround(acc * fround(sA[m] * sB[n]))),
-//   bit 2 bias, bits 0-1 activation (0 none, 1 ReLU, 2 SiLU).
+//   bit 2 bias, bits 0-1 activation (0 none, 1 ReLU, 2 SiLU);
+//   bit 5 int8 output: the fp32 value (MODE as above, bias and activation
+//   taken from the runtime epilogue) requantized with a static scale.
 template <int EPI>
 struct Epi {
   static constexpr bool OUT_I32 = (EPI & 16) != 0;
+  static constexpr bool OUT_Q8 = (EPI & 32) != 0;
   static constexpr int MODE = (EPI >> 3) & 1;
   static constexpr bool BIAS = (EPI & 4) != 0;
   static constexpr int ACT = EPI & 3;
@@ -198,6 +215,7 @@ struct Epi {
 
 inline int epi_code(const GemmEpi& e) {
   if (e.out_i32) return 16;
+  if (e.out_q8) return 32 | (e.mode << 3);
   return (e.mode << 3) | (e.bias ? 4 : 0) | e.act;
 }
 
@@ -396,6 +414,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const int lc = wn + 32 * j + r32;
     sbj[j] = (!OUT_I32 && MODE == 1) ? s_cols[lc] : 0.0;
     if constexpr (P::BIAS) bj[j] = e.bias[n0 + lc < N ? n0 + lc : N - 1];
+    else if constexpr (P::OUT_Q8) bj[j] = e.bias ? e.bias[n0 + lc < N ? n0 + lc : N - 1] : 0.0f;
     else bj[j] = 0.0f;
   }
   auto strip_out = [&](auto ic) {
@@ -425,6 +444,12 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
       }
       const bool fast = __all(exact);
       auto finish = [&](float y, int j) {
+        if constexpr (P::OUT_Q8) {
+          if (e.bias) y = y + bj[j];
+          if (e.act == 1) y = relu_js(y);
+          else if (e.act == 2) y = silu_js(y);
+          return __int_as_float(requant(y, e));   // the int8 code, carried in the slot
+        }
         if constexpr (P::BIAS) y = y + bj[j];
         if constexpr (P::ACT == 1) y = relu_js(y);
         if constexpr (P::ACT == 2) y = silu_js(y);
@@ -454,6 +479,28 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
 #pragma unroll
     for (int it = 0; it < NQ; ++it)
       q[it] = *reinterpret_cast<const v4i*>(strip + (it * RPI + qrow) * PITCH + qcol);
+    if constexpr (P::OUT_Q8) {
+      int8_t* o8 = static_cast<int8_t*>(out);
+      if (interior) {
+#pragma unroll
+        for (int it = 0; it < NQ; ++it) {
+          const int64_t row = m0 + wm + 32 * i + it * RPI + qrow;
+          const int packed = (q[it][0] & 0xff) | ((q[it][1] & 0xff) << 8) |
+                             ((q[it][2] & 0xff) << 16) | ((q[it][3] & 0xff) << 24);
+          __builtin_nontemporal_store(packed, reinterpret_cast<int*>(o8 + row * N + gcol));
+        }
+      } else {
+#pragma unroll
+        for (int it = 0; it < NQ; ++it) {
+          const int row = m0 + wm + 32 * i + it * RPI + qrow;
+          if (row < M) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (gcol + c < N) o8[(int64_t)row * N + gcol + c] = (int8_t)q[it][c];
+          }
+        }
+      }
+    } else {
     int32_t* o = static_cast<int32_t*>(out);
     if (interior) {
 #pragma unroll
@@ -471,6 +518,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
             if (gcol + c < N) o[(int64_t)row * N + gcol + c] = q[it][c];
         }
       }
+    }
     }
   };
   strip_out(std::integral_constant<int, 0>{});
@@ -493,13 +541,11 @@ __global__ __launch_bounds__(256) void k_gemm_i8_generic(const int8_t* __restric
   const int64_t m = idx / N, n = idx % N;
   uint32_t s = 0;
   for (int k = 0; k < K; ++k) s += (uint32_t)((int)A[m * K + k] * (int)B[n * K + k]);
-  const int acc = (int)s;
-  if (e.out_i32) static_cast<int32_t*>(out)[idx] = acc;
-  else static_cast<float*>(out)[idx] = epi_value(acc, m, n, e);
+  store_out(out, idx, (int)s, m, n, e);
 }
 
 #define Q8_EPI_CODES(X) \
-  X(16) X(0) X(1) X(2) X(4) X(5) X(6) X(8) X(9) X(10) X(12) X(13) X(14)
+  X(16) X(0) X(1) X(2) X(4) X(5) X(6) X(8) X(9) X(10) X(12) X(13) X(14) X(32) X(40)
 
 template <int BM, int BN>
 static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int N, int K,
@@ -663,8 +709,7 @@ void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M
       // int32 wrap-around sum, as the reference's Int32Array store
       const int s = (int)((uint32_t)red[0][i] + (uint32_t)red[1][i] + (uint32_t)red[2][i] +
                           (uint32_t)red[3][i]);
-      if (e.out_i32) static_cast<int32_t*>(out)[(int64_t)m * N + n] = s;
-      else static_cast<float*>(out)[(int64_t)m * N + n] = epi_value(s, m, n, e);
+      store_out(out, (int64_t)m * N + n, s, m, n, e);
     }
   }
 }
@@ -737,8 +782,7 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
     if (t < M && n < N) {
       const int s = (int)((uint32_t)red[rb][0][tid] + (uint32_t)red[rb][1][tid] +
                           (uint32_t)red[rb][2][tid] + (uint32_t)red[rb][3][tid]);
-      if (e.out_i32) static_cast<int32_t*>(out)[(int64_t)t * N + n] = s;
-      else static_cast<float*>(out)[(int64_t)t * N + n] = epi_value(s, t, n, e);
+      store_out(out, (int64_t)t * N + n, s, t, n, e);
     }
   }
 }

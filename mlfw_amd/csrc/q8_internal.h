@@ -19,6 +19,10 @@ struct GemmEpi {
   int mode;             // 0 = PT, 1 = ROWCOL
   int act;              // 0 none, 1 relu, 2 silu
   int out_i32;          // 1: write the raw int32 accumulator
+  int out_q8;           // 1: requantize the fp32 result to int8 with the static scale s_q
+  double s_q;           // next layer's quantize scale (out_q8)
+  float rq32;           // (float)(1 / s_q), for the f32 fast path of R1
+  int q_fast;           // s_q admits the fast path (normal, in [2^-100, 2^100])
 };
 
 hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,

@@ -275,6 +275,36 @@ def qlinear_pt(A: torch.Tensor, B: torch.Tensor, s_out: float,
     return out
 
 
+def qlinear_requant(A: torch.Tensor, sA: torch.Tensor | None, B: torch.Tensor,
+                    sB: torch.Tensor | None, s_next: float, bias: torch.Tensor | None = None,
+                    act: str | None = None, s_out: float | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """int8 linear whose fp32 result (the qlinear epilogue, or with s_out
+    the per-tensor one) is requantized in the epilogue with the next layer's
+    static scale s_next: the calibrated dequantize -> [bias] -> [relu] ->
+    quantize chain of QuantizationPass, returned as int8 [M, N]."""
+    M, N, K = _mk(A, B)
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.numel() != N:
+            raise ValueError("qlinear_requant: bias must have N elements")
+    out = torch.empty((M, N), dtype=torch.int8, device=A.device) if out is None else out
+    _need(out, torch.int8, "qlinear_requant out")
+    if s_out is None:
+        _need(sA, torch.float64, "sA")
+        _need(sB, torch.float64, "sB")
+        if sA.numel() not in (1, M) or sB.numel() not in (1, N):
+            raise ValueError("qlinear_requant: scale sizes must be 1 or M (sA) and 1 or N (sB)")
+        _call("q8_gemm_requant", _ptr(A), _ptr(B), M, N, K,
+               _ptr(sA), L.Q8_PER_TOKEN if sA.numel() == M and M != 1 else L.Q8_PER_TENSOR,
+               _ptr(sB), L.Q8_PER_CHANNEL if sB.numel() == N and N != 1 else L.Q8_PER_TENSOR,
+               L.Q8_EPI_ROWCOL, 0.0, _ptr(bias), _ACT[act], float(s_next), _ptr(out), _stream())
+    else:
+        _call("q8_gemm_requant", _ptr(A), _ptr(B), M, N, K, None, 0, None, 0, L.Q8_EPI_PT,
+               float(s_out), _ptr(bias), _ACT[act], float(s_next), _ptr(out), _stream())
+    return out
+
+
 def _i64_array(vals):
     arr = (C.c_int64 * max(1, len(vals)))(*[int(v) for v in vals])
     return arr

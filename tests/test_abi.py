@@ -147,3 +147,16 @@ def test_conv_workspace_query_and_validation(lib):
                    fake, 1 << 20, fake, None)                                        # rank 4
     rc = L.q8_quantized_conv(fake, fake, 2, *args, 1, 2, 0, lib.Q8_I32, 0.0, fake, 1 << 20, fake, None)
     assert rc == lib.Q8_ERR_UNSUPPORTED
+
+
+def test_requant_validation(lib):
+    fake = C.c_void_p(0x1000)
+    L = lib.load()
+    # the quantize verifier's scale > 0 (ops/quantization.ts:44-47)
+    for s_next in (0.0, -1.0, float("inf"), float("nan")):
+        rc = L.q8_gemm_requant(fake, fake, 32, 32, 64, fake, lib.Q8_PER_TOKEN, fake,
+                               lib.Q8_PER_CHANNEL, lib.Q8_EPI_ROWCOL, 0.0, None, 0, s_next, fake, None)
+        assert rc == lib.Q8_ERR_INVALID, s_next
+    rc = L.q8_gemm_requant(fake, fake, 32, 32, 64, None, lib.Q8_PER_TOKEN, fake, lib.Q8_PER_CHANNEL,
+                           lib.Q8_EPI_ROWCOL, 0.0, None, 0, 0.1, fake, None)
+    assert rc == lib.Q8_ERR_INVALID          # ROWCOL without sA
