@@ -238,7 +238,7 @@ def ceilings():
     from mlfw_amd import build as B
     lib = C.CDLL(B.CEILING_LIB)
     lib.q8c_mfma.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
-    lib.q8c_read.argtypes = [C.c_size_t, C.c_int, C.c_int, C.POINTER(C.c_double)]
+    lib.q8c_stream.argtypes = [C.c_size_t, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
     us, mhz = C.c_double(), C.c_double()
     out = {}
     if lib.q8c_mfma(2048, 10, C.byref(us), C.byref(mhz)) == 0:
@@ -248,14 +248,15 @@ def ceilings():
                     "count), random operands, no loads or stores",
             "avg_us": us.value, "TOPS": tops, "frac_of_peak": tops / PEAK_INT8_TOPS,
             "shader_clock_mhz": mhz.value}
-    for name, nbytes in (("gemv_N4096", 4096 * 4096 + 8 * 4096 + 4 * 4096),
-                         ("gemv_N11008", 11008 * 4096 + 8 * 11008 + 4 * 4096),
-                         ("quantize_16384x4096", 335675392)):
+    for kind, name, nbytes in (("read", "gemv_N4096", 4096 * 4096 + 8 * 4096 + 4 * 4096),
+                               ("read", "gemv_N11008", 11008 * 4096 + 8 * 11008 + 4 * 4096),
+                               ("read", "quantize_16384x4096", 335675392),
+                               ("write", "dequantize_out_16384x4096", 268435456)):
         bufs = max(5, math.ceil((1 << 30) / nbytes))
-        if lib.q8c_read(nbytes, bufs, 5, C.byref(us)) == 0:
+        if lib.q8c_stream(nbytes, bufs, 5, 1 if kind == "write" else 0, C.byref(us)) == 0:
             gbs = nbytes / (us.value * 1e-6) / 1e9
-            out[f"read_{name}"] = {"bytes": nbytes, "avg_us": us.value, "GB/s": gbs,
-                                   "frac_of_peak": gbs / PEAK_HBM_GBS}
+            out[f"{kind}_{name}"] = {"bytes": nbytes, "avg_us": us.value, "GB/s": gbs,
+                                     "frac_of_peak": gbs / PEAK_HBM_GBS}
     return out
 
 

@@ -9,10 +9,11 @@
 //     random int8 operands (operand entropy sets the power draw, and so the
 //     clock MI355X holds).  Reports the kernel time and the shader clock
 //     read in the kernel (s_memtime against the 100 MHz s_memrealtime).
-//   * q8c_read: a streaming read of `bytes` (16-byte non-temporal loads,
-//     1 KiB per wave instruction), the HBM floor of a single kernel of that
-//     size including launch and ramp, timed as a graph of `buffers`
-//     launches over distinct buffers (rotation defeats the 256 MB MALL).
+//   * q8c_stream: a streaming read or write of `bytes` (16-byte
+//     non-temporal accesses, 1 KiB per wave instruction), the HBM floor of a
+//     single kernel of that size including launch and ramp, timed as a graph
+//     of `buffers` launches over distinct buffers (rotation defeats the
+//     256 MB MALL).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -92,6 +93,16 @@ __global__ __launch_bounds__(256) void k_read(const v4i* __restrict__ p, int64_t
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5eed1234) out[blockIdx.x] = acc.x;
 }
 
+__global__ __launch_bounds__(256) void k_write(v4i* __restrict__ p, int64_t nchunks, int seed) {
+  constexpr int U = 4;
+  const int64_t base = (int64_t)blockIdx.x * 256 * U;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * 256 + threadIdx.x;
+    if (i < nchunks) __builtin_nontemporal_store(v4i{seed, (int)i, u, seed}, p + i);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -133,9 +144,10 @@ int q8c_mfma(int iters_per_wave, int reps, double* us, double* mhz) {
   return rc;
 }
 
-// Streaming-read floor: a graph of `buffers` launches, each reading its own
-// buffer of `bytes`, replayed `reps` times; *us = average per launch.
-int q8c_read(size_t bytes, int buffers, int reps, double* us) {
+// Streaming-read (write = 0) or streaming-write (write = 1) floor: a graph
+// of `buffers` launches, each on its own buffer of `bytes`, replayed `reps`
+// times; *us = average per launch.
+int q8c_stream(size_t bytes, int buffers, int reps, int write, double* us) {
   if (bytes < 16 || buffers < 1 || reps < 1 || !us) return 1;
   std::vector<v4i*> bufs(buffers, nullptr);
   int* out = nullptr;
@@ -152,8 +164,12 @@ int q8c_read(size_t bytes, int buffers, int reps, double* us) {
   const int64_t nch = (int64_t)(bytes / 16);
   const int grid = (int)((nch + 1023) / 1024);
   if (ok && hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-    for (int i = 0; i < buffers; ++i)
-      hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, bufs[i], nch, out);
+    for (int i = 0; i < buffers; ++i) {
+      if (write)
+        hipLaunchKernelGGL(k_write, dim3(grid), dim3(256), 0, s, bufs[i], nch, i);
+      else
+        hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, bufs[i], nch, out);
+    }
     ok = hipStreamEndCapture(s, &g) == hipSuccess &&
          hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess;
     if (ok) ok = hipGraphLaunch(ge, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess;
