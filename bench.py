@@ -19,8 +19,8 @@ WRITE_SIZE runs (profiles/traffic.json, scaled by a copy-kernel
 calibration), or null when that file is absent.
 
 secondary: the HBM-bound kernels of C5 (per-token quantize and dequantize
-of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}) and the C4
-projection set.  Each is captured R times in a HIP graph (rotating input
+of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}, and the same
+GEMVs for M <= 4 with 4-bit per-group weights) and the C4 projection set.  Each is captured R times in a HIP graph (rotating input
 buffers so the 256 MB Infinity Cache cannot serve repeats) and the graph
 is replayed between two events: per-launch host overhead would otherwise
 dominate kernels of a few microseconds.
@@ -207,7 +207,23 @@ def bench_c5_gemv():
                 "quantize_x_avg_us": q_us,
                 "step_GB/s": sb / ((g_us + q_us) * 1e-6) / 1e9, "timing": how,
             }
-        del Wqs
+        # the same weights as 4-bit per-group codes (group 128): W4A8 decode GEMV
+        g = 128
+        Wq40, sW4 = O.pack_weight_int4(W, g)
+        Wq4s = [Wq40] + [Wq40.clone() for _ in range(2 * R - 1)]      # same > 1 GiB rotation
+        for M, x in inp["x"].items():
+            if M > 4:
+                continue
+            xq, sx = O.quantize_per_token(x)
+            outs = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(2 * R)]
+            g_us, how = graph_time_us(lambda i: O.qlinear_w4(xq, sx, Wq4s[i], sW4, K, g, out=outs[i]),
+                                      2 * R)
+            kb = N * K // 2 + 8 * N * K // g + M * K + 8 * M + 4 * M * N
+            res[f"gemv_w4_M{M}_N{N}"] = {
+                "gemv_avg_us": g_us, "gemv_GB/s": kb / (g_us * 1e-6) / 1e9,
+                "gemv_frac_hbm": kb / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+                "bytes": kb, "group": g, "timing": how}
+        del Wqs, Wq4s
     return res
 
 

@@ -232,6 +232,35 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
                     int epi, double s_out, const float* bias, int act,
                     double s_next, int8_t* out, void* stream);
 
+/* ---------------------------------------------------------------- 4-bit weights */
+
+/* fromConstantArrayPerGroup (quantization_types.ts:319-340, numBits 4) +
+ * quantizeArrayPerGroup (:143-153) of a row-major fp32 [N, K] weight over
+ * its flat element order, on the device: scales[g] = absmax / 7 || 1e-10
+ * (f64) for each run of group_size elements, codes
+ * Math.max(-8, Math.min(7, Math.round(w / s))) (f64, NaN -> 0), packed two
+ * per byte (element 2j in the low nibble, two's complement) into
+ * Wq4 [N, K/2].  group_size must be even and divide K, so every group lies
+ * in one row; scales has N * K / group_size entries (row n's groups at
+ * n * K / group_size). */
+int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size,
+                        uint8_t* Wq4, double* scales, void* stream);
+
+/* Decode-time linear with 4-bit per-group weights and int8 activations
+ * (W4A8).  The reference has no op for it; it is defined as a composition
+ * that stays exact:
+ *   acc_g = sum over group g of xq[m,k] * q[n,k]              (int32)
+ *   S     = acc_0*sw[n,0] + acc_1*sw[n,1] + ...  in f64, groups in ascending order
+ *   y     = fround(S * sx[m]), then fround(y + bias[n]) and act (Q8_ACT_*)
+ * xq: int8 [M, K] (q8_quantize_rows codes); sx: f64, sx_mode Q8_PER_TOKEN
+ * ([M]) or Q8_PER_TENSOR ([1]); Wq4 / sw as written by q8_pack_weight_int4.
+ * Fast kernel for M <= 4, power-of-two group_size in [32, 2048] and
+ * K <= 8192 (half the weight bytes of int8); any other shape runs a simple
+ * exact kernel. */
+int q8_gemv_w4(const int8_t* xq, const double* sx, int sx_mode, const uint8_t* Wq4,
+               const double* sw, int64_t M, int64_t N, int64_t K, int64_t group_size,
+               const float* bias, int act, float* out, void* stream);
+
 /* ---------------------------------------------------------------- conv */
 
 /* quantized_conv (src/compiler/ir/graph/ops/quantization.ts:156-190), as

@@ -432,6 +432,40 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
   return launched(err, "q8_gemm_requant launch");
 }
 
+int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size,
+                        uint8_t* Wq4, double* scales, void* stream) {
+  Q8_REQUIRE(N >= 0 && K >= 0 && mul_ok(N, K), "q8_pack_weight_int4: bad shape [%lld,%lld]",
+             (long long)N, (long long)K);
+  Q8_REQUIRE(group_size >= 2 && group_size % 2 == 0 && K % group_size == 0,
+             "q8_pack_weight_int4: group_size (%lld) must be even and divide K (%lld)",
+             (long long)group_size, (long long)K);
+  Q8_REQUIRE(N * K == 0 || (W && Wq4 && scales), "q8_pack_weight_int4: NULL pointer");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_pack_w4(W, N, K, group_size, Wq4, scales, as_stream(stream)),
+                  "q8_pack_weight_int4 launch");
+}
+
+int q8_gemv_w4(const int8_t* xq, const double* sx, int sx_mode, const uint8_t* Wq4,
+               const double* sw, int64_t M, int64_t N, int64_t K, int64_t group_size,
+               const float* bias, int act, float* out, void* stream) {
+  Q8_REQUIRE(M >= 0 && N >= 0 && K >= 0 && mul_ok(M, N) && mul_ok(M, K) && mul_ok(N, K),
+             "q8_gemv_w4: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  Q8_REQUIRE(M * K < (1LL << 31) && N * (K / 2) < (1LL << 31) && M * N < (1LL << 39),
+             "q8_gemv_w4: tensors too large for 32-bit offsets");
+  Q8_REQUIRE(group_size >= 2 && group_size % 2 == 0 && K % group_size == 0,
+             "q8_gemv_w4: group_size (%lld) must be even and divide K (%lld)",
+             (long long)group_size, (long long)K);
+  Q8_REQUIRE(sx_mode == Q8_PER_TENSOR || sx_mode == Q8_PER_TOKEN, "q8_gemv_w4: bad sx_mode %d", sx_mode);
+  Q8_REQUIRE(act == Q8_ACT_NONE || act == Q8_ACT_RELU || act == Q8_ACT_SILU, "q8_gemv_w4: bad act %d", act);
+  Q8_REQUIRE(M * N == 0 || (xq && sx && Wq4 && sw && out), "q8_gemv_w4: NULL pointer");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_gemv_w4(xq, sx, sx_mode == Q8_PER_TOKEN ? 1 : 0, Wq4, sw, M, N, K,
+                                     group_size, bias, act, out, as_stream(stream)),
+                  "q8_gemv_w4 launch");
+}
+
 static int conv_geom(const char* who, int d, const int64_t* xs, const int64_t* ws,
                      const int64_t* strides, const int64_t* pad_lo, const int64_t* pad_hi,
                      const int64_t* dilation, int64_t groups, q8::ConvGeom* G) {

@@ -49,6 +49,13 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
 
+// 4-bit per-group weights (q8_w4.hip).
+hipError_t launch_pack_w4(const float* W, int64_t N, int64_t K, int64_t group, uint8_t* wq4,
+                          double* scales, hipStream_t st);
+hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, const uint8_t* wq4,
+                          const double* sw, int64_t M, int64_t N, int64_t K, int64_t group,
+                          const float* bias, int act, float* y, hipStream_t st);
+
 // Geometry of a quantized_conv (NC(spatial) input, OI(spatial) kernel);
 // unused trailing spatial dimensions have size 1.  Validated by the C ABI:
 // every int field and Cg * prod(K) below 2^31.

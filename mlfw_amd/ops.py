@@ -305,6 +305,38 @@ def qlinear_requant(A: torch.Tensor, sA: torch.Tensor | None, B: torch.Tensor,
     return out
 
 
+def pack_weight_int4(W: torch.Tensor, group_size: int):
+    """4-bit per-group weight packing (fromConstantArrayPerGroup +
+    quantizeArrayPerGroup, quantization_types.ts:319-340, :143-153) of an
+    fp32 [N, K] weight -> (uint8 [N, K/2] nibbles, f64 scales [N*K/group])."""
+    _need(W, torch.float32, "pack_weight_int4", ndim=2)
+    N, K = W.shape
+    wq = torch.empty((N, K // 2), dtype=torch.uint8, device=W.device)
+    s = torch.empty(N * K // max(group_size, 1), dtype=torch.float64, device=W.device)
+    _call("q8_pack_weight_int4", _ptr(W), N, K, group_size, _ptr(wq), _ptr(s), _stream())
+    return wq, s
+
+
+def qlinear_w4(xq: torch.Tensor, sx: torch.Tensor, Wq4: torch.Tensor, sw: torch.Tensor,
+               K: int, group_size: int, bias: torch.Tensor | None = None,
+               act: str | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """W4A8 linear (q8_gemv_w4): int8 [M, K] activations with f64 scales
+    ([M] per token or [1]) times 4-bit per-group weights -> fp32 [M, N]."""
+    _need(xq, torch.int8, "qlinear_w4 xq", ndim=2)
+    _need(sx, torch.float64, "qlinear_w4 sx")
+    _need(Wq4, torch.uint8, "qlinear_w4 Wq4", ndim=2)
+    _need(sw, torch.float64, "qlinear_w4 sw")
+    M, N = xq.shape[0], Wq4.shape[0]
+    if xq.shape[1] != K or Wq4.shape[1] != K // 2:
+        raise ValueError("qlinear_w4: shapes do not match K")
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+    out = torch.empty((M, N), dtype=torch.float32, device=xq.device) if out is None else out
+    _call("q8_gemv_w4", _ptr(xq), _ptr(sx), L.Q8_PER_TOKEN if sx.numel() == M and M != 1 else L.Q8_PER_TENSOR,
+          _ptr(Wq4), _ptr(sw), M, N, K, group_size, _ptr(bias), _ACT[act], _ptr(out), _stream())
+    return out
+
+
 def _i64_array(vals):
     arr = (C.c_int64 * max(1, len(vals)))(*[int(v) for v in vals])
     return arr

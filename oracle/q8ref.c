@@ -372,6 +372,33 @@ void q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* 
   (void)Pn;
 }
 
+/* W4A8 per-group GEMV as defined in q8ref.h: exact per-group integer
+ * sums, then an f64 sum over groups in ascending order. */
+void q8r_gemv_w4(const int8_t* xq, const double* sx, int64_t sx_stride, const uint8_t* wq4,
+                 const double* sw, int64_t M, int64_t N, int64_t K, int64_t group,
+                 const float* bias, int act, float* y) {
+  const int64_t G = K / group, KB = (K + 1) / 2;
+  for (int64_t m = 0; m < M; m++)
+    for (int64_t n = 0; n < N; n++) {
+      double S = 0.0;
+      for (int64_t g = 0; g < G; g++) {
+        int64_t acc = 0;
+        for (int64_t k = g * group; k < (g + 1) * group; k++) {
+          const int nib = (wq4[n * KB + k / 2] >> (4 * (k & 1))) & 0xF;
+          const int q = nib >= 8 ? nib - 16 : nib;
+          acc += (int64_t)xq[m * K + k] * q;
+        }
+        const double t = (double)acc * sw[n * G + g];
+        S = g == 0 ? t : S + t;
+      }
+      float v = q8r_fround(S * sx[m * sx_stride]);
+      if (bias) v = q8r_fround((double)v + (double)bias[n]);
+      if (act == 1) v = q8r_relu(v);
+      else if (act == 2) v = q8r_silu(v);
+      y[m * N + n] = v;
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* epilogues and elementwise                                           */
 /* ------------------------------------------------------------------ */

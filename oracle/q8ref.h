@@ -125,6 +125,20 @@ void     q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64
                             const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
                             int32_t zpx, int32_t zpw, int32_t* out);
 
+/* ---- W4A8 per-group GEMV (no reference op; composed here) ----
+ * Weights: 4-bit codes of fromConstantArrayPerGroup + quantizeArrayPerGroup
+ * (quantization_types.ts:319-340, :143-153) over the flat [N, K] array with
+ * K % group == 0, packed two per byte (element 2j in the low nibble, two's
+ * complement); sw[n * G + g], G = K / group.  Activations: int8 codes xq
+ * with scales sx[m * sx_stride].
+ *   acc_g = sum_{k in group g} xq[m,k] * q[n,k]          (exact int)
+ *   S     = (((acc_0 * sw_0) + acc_1 * sw_1) + ...)      (f64, g ascending)
+ *   y     = fround(S * sx[m]), then bias fround(y + b[n]) and act as in
+ *           q8r_epilogue. */
+void     q8r_gemv_w4(const int8_t* xq, const double* sx, int64_t sx_stride, const uint8_t* wq4,
+                     const double* sw, int64_t M, int64_t N, int64_t K, int64_t group,
+                     const float* bias, int act, float* y);
+
 /* ---- epilogues (quantization_pass.ts:335-355 E-pt, :431-456 E-pc) ----
  * mode 0 (E-pt):      y = fround(acc * s_out)            s_out = sA*sB in f64
  * mode 1 (E-pc/rowcol): y = fround(acc * fround(sA[m] * sB[n]))

@@ -89,6 +89,8 @@ def lib():
         "q8r_quantized_dot": (None, [_i8p, _i8p, _i64, _i64, _i64, _int, C.c_int32, C.c_int32, _i32p]),
         "q8r_quantized_conv": (None, [_i8p, _i8p, _int, _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
                                       _i64, C.c_int32, C.c_int32, _i32p]),
+        "q8r_gemv_w4": (None, [_i8p, _f64p, _i64, _u8p, _f64p, _i64, _i64, _i64, _i64, C.c_void_p,
+                               _int, _f32p]),
         "q8r_epilogue": (None, [_i32p, _i64, _i64, _int, _f64p, _i64, _f64p, _i64, _dbl,
                                 C.c_void_p, _int, _f32p]),
         "q8r_relu": (C.c_float, [C.c_float]),
@@ -326,6 +328,22 @@ def quantized_conv(x, w, strides, padding, dilation=None, groups=1, zpx=0, zpw=0
 
 
 ACT = {"none": 0, "relu": 1, "silu": 2}
+
+
+def gemv_w4(xq, sx, wq4, sw, K, group, bias=None, act="none") -> np.ndarray:
+    """W4A8 per-group GEMV (composition defined in q8ref.h): exact per-group
+    int sums, f64 sum over groups in ascending order, fround(S * sx[m])."""
+    xq = _c(xq, np.int8)
+    M = xq.shape[0]
+    wq4 = _c(wq4, np.uint8)
+    N = wq4.shape[0]
+    sx = np.atleast_1d(_c(sx, np.float64))
+    y = np.empty((M, N), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib().q8r_gemv_w4(xq.reshape(-1), sx, 1 if sx.size > 1 else 0, wq4.reshape(-1),
+                      _c(sw, np.float64).reshape(-1), M, N, K, group,
+                      None if b is None else b.ctypes.data_as(C.c_void_p), ACT[act], y.reshape(-1))
+    return y
 
 
 def epilogue(acc, mode, sA=None, sB=None, s_out=0.0, bias=None, act="none") -> np.ndarray:

@@ -429,3 +429,29 @@ def test_js_silu_mul_matches(oracle, tmp_path):
     got = oracle.silu_mul(g, u)
     d = np.abs(got.view(np.int32).astype(np.int64) - h.view(np.int32).astype(np.int64))
     assert d.max() <= 1 and (d != 0).mean() < 1e-3
+
+
+def test_gemv_w4_matches_independent_evaluation(oracle):
+    """The W4A8 per-group GEMV (a composition defined in oracle/q8ref.h; the
+    reference has no such op) evaluated independently: nibbles unpacked with
+    numpy, per-group int64 sums by einsum, the f64 sum over groups by a Python
+    loop in ascending order, one binary32 rounding at the end."""
+    from mlfw_amd.checkpoint import pack_int4
+    rng = np.random.default_rng(9)
+    for M, N, K, g in [(1, 5, 64, 32), (3, 7, 256, 64), (4, 3, 96, 32), (2, 4, 128, 128)]:
+        xq = rng.integers(-128, 128, (M, K)).astype(np.int8)
+        q = rng.integers(-8, 8, (N, K)).astype(np.int8)
+        G = K // g
+        sw = rng.random(N * G) * 1e-2 + 1e-6
+        sx = rng.random(M) * 1e-1 + 1e-4
+        got = oracle.gemv_w4(xq, sx, pack_int4(q), sw, K, g)
+        parts = np.einsum("mgk,ngk->mng", xq.astype(np.int64).reshape(M, G, g),
+                          q.astype(np.int64).reshape(N, G, g))
+        want = np.empty((M, N), np.float32)
+        for m in range(M):
+            for n in range(N):
+                S = float(parts[m, n, 0]) * sw[n * G]
+                for gi in range(1, G):
+                    S = S + float(parts[m, n, gi]) * sw[n * G + gi]
+                want[m, n] = np.float32(S * sx[m])
+        same_bits(got, want)
