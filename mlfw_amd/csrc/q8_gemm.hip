@@ -661,16 +661,21 @@ void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M
   const int C = K >> 4;                                // 16-byte chunks per row
   const int n0 = blockIdx.x * GV_ROWS;
 
+  // Buffer loads, every one issued unconditionally: the weight resource
+  // starts at row n0 and ends after the group's last row, the activation
+  // resource ends after token M - 1, and chunks past the row end take an
+  // offset past num_records -- all of those read zero.
+  const uint32_t rows = (uint32_t)min(GV_ROWS, N - n0);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (int64_t)n0 * K, rows * (uint32_t)K);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
   v4i w[GV_ROWS][CPT];
 #pragma unroll
   for (int r = 0; r < GV_ROWS; ++r)
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
       const int ch = tid + 256 * c;
-      v4i v = {0, 0, 0, 0};
-      if (ch < C && n0 + r < N)
-        v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(B + (int64_t)(n0 + r) * K) + ch);
-      w[r][c] = v;
+      const uint32_t off = ch < C ? (uint32_t)r * (uint32_t)K + 16u * (uint32_t)ch : OOB;
+      w[r][c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2));
     }
   v4i xa[CPT][MT];
 #pragma unroll
@@ -678,11 +683,11 @@ void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M
     const int ch = tid + 256 * c;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      v4i v = {0, 0, 0, 0};
-      if (ch < C && m < M) v = *reinterpret_cast<const v4i*>(A + (int64_t)m * K + 16 * ch);
-      xa[c][m] = v;
+      const uint32_t off = ch < C ? (uint32_t)m * (uint32_t)K + 16u * (uint32_t)ch : OOB;
+      xa[c][m] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
   int acc[V];
 #pragma unroll
   for (int r = 0; r < GV_ROWS; ++r)

@@ -209,8 +209,14 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
       const int i = tid + j * NT;
       const v4f t = __builtin_nontemporal_load(xr + (FULL ? i : min(i, last)));
       v[j] = make_float4(t.x, t.y, t.z, t.w);
+    }
+    // no arithmetic between the loads (the scheduler would otherwise start
+    // on the first group and issue the rest after waiting for it)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
       const int k = key4(v[j]);
-      key = (FULL || i <= last) && k > key ? k : key;
+      key = (FULL || tid + j * NT <= last) && k > key ? k : key;
     }
     if constexpr (!FULL) {
       for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
@@ -387,23 +393,37 @@ __global__ __launch_bounds__(NT) void k_dequant_vec(const void* __restrict__ qv,
     const double s = scales[per_row ? row : 0];
     for (int64_t g0 = blockIdx.x * (int64_t)(NT * GPT) + threadIdx.x; g0 < groups;
          g0 += (int64_t)gridDim.x * NT * GPT) {
+      // every load is issued, unconditionally (a lane past the row end
+      // reloads the last group and stores nothing), before any arithmetic
+      v4i c32[SRC == 2 ? GPT : 1];
+      int c8[GPT];
+#pragma unroll
+      for (int t = 0; t < GPT; ++t) {
+        const int64_t g = min(g0 + (int64_t)t * NT, groups - 1);
+        if constexpr (SRC == 2)
+          c32[t] = __builtin_nontemporal_load(
+              reinterpret_cast<const v4i*>(static_cast<const int32_t*>(qv) + row * K) + g);
+        else
+          c8[t] = __builtin_nontemporal_load(
+              reinterpret_cast<const int*>(static_cast<const int8_t*>(qv) + row * K) + g);
+      }
+      // an unconditional use of each value here, after all the loads: the
+      // compiler may not sink a load into the branch that stores its group
+#pragma unroll
+      for (int t = 0; t < GPT; ++t) {
+        if constexpr (SRC == 2) asm volatile("" ::"v"(c32[t]));
+        else asm volatile("" ::"v"(c8[t]));
+      }
       int w[GPT][4];
 #pragma unroll
       for (int t = 0; t < GPT; ++t) {
-        const int64_t g = g0 + (int64_t)t * NT;
-        if (g < groups) {
-          if (SRC == 2) {
-            const v4i c = __builtin_nontemporal_load(
-                reinterpret_cast<const v4i*>(static_cast<const int32_t*>(qv) + row * K) + g);
-            w[t][0] = c.x; w[t][1] = c.y; w[t][2] = c.z; w[t][3] = c.w;
-          } else {
-            const int c = __builtin_nontemporal_load(
-                reinterpret_cast<const int*>(static_cast<const int8_t*>(qv) + row * K) + g);
+        if constexpr (SRC == 2) {
+          w[t][0] = c32[t].x; w[t][1] = c32[t].y; w[t][2] = c32[t].z; w[t][3] = c32[t].w;
+        } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              int b = (c >> (8 * e)) & 0xff;
-              w[t][e] = SRC == 0 ? (int)(int8_t)b : b;
-            }
+          for (int e = 0; e < 4; ++e) {
+            const int b = (c8[t] >> (8 * e)) & 0xff;
+            w[t][e] = SRC == 0 ? (int)(int8_t)b : b;
           }
         }
       }
@@ -659,6 +679,9 @@ __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows(const float* __restr
       a[j] = gr[i];
       b[j] = ur[i];
     }
+    // keep the SiLU arithmetic below every load (it would otherwise be
+    // scheduled between them and hold later loads behind the first waits)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t i = tid + (int64_t)j * NT;

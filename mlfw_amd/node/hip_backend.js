@@ -392,6 +392,58 @@ function runDescriptor(d, args, dev) {
     A.download(out, dout);
     return out;
   }
+  if (d.op === 'qlinear_requant') {
+    // int8 linear whose output is requantized with the next layer's static
+    // scale (the calibrated chain ... mul(sv) -> add(b) -> max -> quantize):
+    // xq int8 [M,K] + f64 scale(s), wq int8 [N,K] + f64 scales [N] -> int8 [M,N]
+    const xq = args[d.xqIdx], sx = args[d.sxIdx], wq = args[d.wqIdx], ws = args[d.wsIdx];
+    const out = args[d.outIdx];
+    const bias = d.biasIdx === undefined || d.biasIdx < 0 ? null : args[d.biasIdx];
+    const perTensor = d.granularity === 'per_tensor';
+    need(xq instanceof Int8Array && xq.length === d.M * d.K, 'qlinear_requant xq');
+    need(sx instanceof Float64Array && sx.length === (perTensor ? 1 : d.M), 'qlinear_requant activation scales');
+    need(wq instanceof Int8Array && wq.length === d.N * d.K, 'qlinear_requant wq');
+    need(ws instanceof Float64Array && ws.length === d.N, 'qlinear_requant weight scales');
+    need(out instanceof Int8Array && out.length === d.M * d.N, 'qlinear_requant out');
+    need(bias === null || (bias instanceof Float32Array && bias.length === d.N), 'qlinear_requant bias');
+    need(typeof d.sNext === 'number', 'qlinear_requant needs the static scale sNext');
+    const dxq = dev.get('xq', d.M * d.K), dsx = dev.get('sx', bytesOf(sx));
+    const dwq = dev.get('wq', d.N * d.K), dws = dev.get('ws', 8 * d.N);
+    const db = bias ? dev.get('bias', 4 * d.N) : null, dout = dev.get('out', d.M * d.N);
+    A.upload(dxq, xq);
+    A.upload(dsx, sx);
+    A.upload(dwq, wq);
+    A.upload(dws, ws);
+    if (bias) A.upload(db, bias);
+    A.gemmRequant(dxq, dwq, d.M, d.N, d.K, dsx, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN,
+                  dws, A.Q8_PER_CHANNEL, A.Q8_EPI_ROWCOL, 0, db, A[ACT_CODE[d.act || 'none']], d.sNext, dout);
+    A.download(out, dout);
+    return out;
+  }
+  if (d.op === 'qlinear_w4') {
+    // decode linear with 4-bit per-group weights: x fp32 [M,K], per-token
+    // int8 quantize, then the W4A8 GEMV; wq4 uint8 [N, K/2] (two codes per
+    // byte), sw f64 [N * K / group]
+    const x = args[d.xIdx], wq = args[d.wqIdx], sw = args[d.swIdx], out = args[d.outIdx];
+    const bias = d.biasIdx === undefined || d.biasIdx < 0 ? null : args[d.biasIdx];
+    need(x instanceof Float32Array && x.length === d.M * d.K, 'qlinear_w4 x');
+    need(wq instanceof Uint8Array && wq.length === d.N * d.K / 2, 'qlinear_w4 packed weights');
+    need(d.group > 0 && d.K % d.group === 0, 'qlinear_w4 group must divide K');
+    need(sw instanceof Float64Array && sw.length === d.N * d.K / d.group, 'qlinear_w4 group scales');
+    need(out instanceof Float32Array && out.length === d.M * d.N, 'qlinear_w4 out');
+    need(bias === null || (bias instanceof Float32Array && bias.length === d.N), 'qlinear_w4 bias');
+    const dx = dev.get('x', 4 * d.M * d.K), dxq = dev.get('xq', d.M * d.K), dsx = dev.get('sx', 8 * d.M);
+    const dwq = dev.get('wq', bytesOf(wq)), dsw = dev.get('sw', bytesOf(sw));
+    const db = bias ? dev.get('bias', 4 * d.N) : null, dout = dev.get('out', 4 * d.M * d.N);
+    A.upload(dx, x);
+    A.upload(dwq, wq);
+    A.upload(dsw, sw);
+    if (bias) A.upload(db, bias);
+    A.quantizeRows(dx, d.M, d.K, A.Q8_PER_TOKEN, dxq, dsx);
+    A.gemvW4(dxq, dsx, A.Q8_PER_TOKEN, dwq, dsw, d.M, d.N, d.K, d.group, db, A[ACT_CODE[d.act || 'none']], dout);
+    A.download(out, dout);
+    return out;
+  }
   throw new Error(`hip backend: unknown op '${d.op}'`);
 }
 

@@ -387,6 +387,55 @@ static napi_value js_gemm(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* gemmRequant(A, B, M, N, K, sA, sAMode, sB, sBMode, epi, sOut, bias, act, sNext, out):
+ * the epilogue value requantized with the next layer's static scale (int8 out). */
+static napi_value js_gemm_requant(napi_env env, napi_callback_info info) {
+  napi_value argv[15];
+  void *A, *B, *sA, *sB, *bias, *out;
+  int64_t M, N, K, sAm, sBm, epi, act;
+  double sOut, sNext;
+  if (!get_args(env, info, 15, argv) || !arg_buf(env, argv[0], 1, &A) || !arg_buf(env, argv[1], 1, &B) ||
+      !arg_i64(env, argv[2], &M) || !arg_i64(env, argv[3], &N) || !arg_i64(env, argv[4], &K) ||
+      !arg_buf(env, argv[5], 1, &sA) || !arg_i64(env, argv[6], &sAm) || !arg_buf(env, argv[7], 1, &sB) ||
+      !arg_i64(env, argv[8], &sBm) || !arg_i64(env, argv[9], &epi) || !arg_f64(env, argv[10], &sOut) ||
+      !arg_buf(env, argv[11], 1, &bias) || !arg_i64(env, argv[12], &act) ||
+      !arg_f64(env, argv[13], &sNext) || !arg_buf(env, argv[14], 1, &out))
+    return NULL;
+  Q8_CHECK(env, q8_gemm_requant((const int8_t*)A, (const int8_t*)B, M, N, K, (const double*)sA, (int)sAm,
+                                (const double*)sB, (int)sBm, (int)epi, sOut, (const float*)bias, (int)act,
+                                sNext, (int8_t*)out, NULL));
+  return undefined(env);
+}
+
+/* packWeightInt4(W, N, K, groupSize, wq4, scales) */
+static napi_value js_pack_weight_int4(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  void *W, *wq, *s;
+  int64_t N, K, g;
+  if (!get_args(env, info, 6, argv) || !arg_buf(env, argv[0], 1, &W) || !arg_i64(env, argv[1], &N) ||
+      !arg_i64(env, argv[2], &K) || !arg_i64(env, argv[3], &g) || !arg_buf(env, argv[4], 1, &wq) ||
+      !arg_buf(env, argv[5], 1, &s))
+    return NULL;
+  Q8_CHECK(env, q8_pack_weight_int4((const float*)W, N, K, g, (uint8_t*)wq, (double*)s, NULL));
+  return undefined(env);
+}
+
+/* gemvW4(xq, sx, sxMode, wq4, sw, M, N, K, groupSize, bias, act, out) */
+static napi_value js_gemv_w4(napi_env env, napi_callback_info info) {
+  napi_value argv[12];
+  void *xq, *sx, *wq, *sw, *bias, *out;
+  int64_t sxm, M, N, K, g, act;
+  if (!get_args(env, info, 12, argv) || !arg_buf(env, argv[0], 1, &xq) || !arg_buf(env, argv[1], 1, &sx) ||
+      !arg_i64(env, argv[2], &sxm) || !arg_buf(env, argv[3], 1, &wq) || !arg_buf(env, argv[4], 1, &sw) ||
+      !arg_i64(env, argv[5], &M) || !arg_i64(env, argv[6], &N) || !arg_i64(env, argv[7], &K) ||
+      !arg_i64(env, argv[8], &g) || !arg_buf(env, argv[9], 1, &bias) || !arg_i64(env, argv[10], &act) ||
+      !arg_buf(env, argv[11], 1, &out))
+    return NULL;
+  Q8_CHECK(env, q8_gemv_w4((const int8_t*)xq, (const double*)sx, (int)sxm, (const uint8_t*)wq,
+                           (const double*)sw, M, N, K, g, (const float*)bias, (int)act, (float*)out, NULL));
+  return undefined(env);
+}
+
 /* Shape arguments of the conv entry points: xShape, wShape, strides, padLo,
  * padHi, dilation as JS arrays (argv[0..5]) for `d` spatial dims. */
 typedef struct {
@@ -483,6 +532,9 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"dequantize", js_dequantize},
       {"packWeight", js_pack_weight},
       {"gemm", js_gemm},
+      {"gemmRequant", js_gemm_requant},
+      {"packWeightInt4", js_pack_weight_int4},
+      {"gemvW4", js_gemv_w4},
       {"siluMulQuantizeRows", js_silu_mul_quantize_rows},
       {"convWorkspace", js_conv_workspace},
       {"quantizedConv", js_quantized_conv},

@@ -235,6 +235,24 @@ function cpuTests() {
     assert.throws(() => a.gemm(null, null, 4, 4, 16, 0, 0, null, 0, null, 0, 9, 0, null, 0, a.Q8_F32, null),
                   (e) => e.code === 'Q8_ERR_1' && /bad epi/.test(e.message));
     assert.throws(() => a.upload({}, new Float32Array(1)), TypeError);
+    for (const f of ['gemmRequant', 'packWeightInt4', 'gemvW4']) assert.strictEqual(typeof a[f], 'function', f);
+    assert.throws(() => a.gemvW4(null, null, a.Q8_PER_TOKEN, null, null, 1, 4, 96, 64, null, 0, null),
+                  (e) => e.code === 'Q8_ERR_1' && /group_size/.test(e.message));
+    assert.throws(() => a.packWeightInt4(null, 4, 96, 7, null, null), (e) => e.code === 'Q8_ERR_1');
+    assert.throws(() => a.gemmRequant(null, null, 4, 4, 16, null, 0, null, 0, 9, 0, null, 0, 0.1, null),
+                  (e) => e.code === 'Q8_ERR_1');
+  });
+
+  test('runtime backend validates the requant and W4 descriptors', () => {
+    const be = hip.createHipRuntimeBackend();
+    const rq = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'qlinear_requant', M: 2, N: 4, K: 16, xqIdx: 0,
+                                                               sxIdx: 1, wqIdx: 2, wsIdx: 3, outIdx: 4, sNext: 0.1 } } });
+    assert.throws(() => be.runSync(rq, [new Int8Array(32), new Float64Array(2), new Int8Array(64),
+                                        new Float64Array(4), new Float32Array(8)], null), /qlinear_requant out/);
+    const w4 = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'qlinear_w4', M: 1, N: 4, K: 64, group: 32,
+                                                               xIdx: 0, wqIdx: 1, swIdx: 2, outIdx: 3 } } });
+    assert.throws(() => be.runSync(w4, [new Float32Array(64), new Int8Array(128), new Float64Array(8),
+                                        new Float32Array(4)], null), /packed weights/);
   });
 }
 
@@ -318,6 +336,27 @@ function gpuTests(dir) {
     const y = new Int32Array(info.outShape.reduce((a, b) => a * b, 1));
     be.runSync(be.instantiate(kern), [xc, wc, y], null);
     writeArr(dir, 'out_conv.bin', y);
+  });
+
+  test('runtime backend: int8 linear with the fused static requant (int8 out)', () => {
+    const sx = readArr(dir, 'sx_tok.bin', Float64Array), xq = readArr(dir, 'xq_tok.bin', Int8Array);
+    const out = new Int8Array(M * N);
+    const inst = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'qlinear_requant', M, N, K, xqIdx: 0, sxIdx: 1,
+                                                                  wqIdx: 2, wsIdx: 3, biasIdx: 4, outIdx: 5,
+                                                                  act: 'relu', sNext: meta.sNext } } });
+    be.runSync(inst, [xq, sx, Wq, sW, bias, out], null);
+    writeArr(dir, 'out_requant.bin', out);
+  });
+
+  test('runtime backend: W4A8 decode linear (4-bit per-group weights)', () => {
+    const wq4 = readArr(dir, 'w4_q.bin', Uint8Array), sw4 = readArr(dir, 'w4_s.bin', Float64Array);
+    const xs = X.subarray(0, meta.w4M * K);
+    const y = new Float32Array(meta.w4M * N);
+    const inst = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'qlinear_w4', M: meta.w4M, N, K,
+                                                                  group: meta.w4Group, xIdx: 0, wqIdx: 1, swIdx: 2,
+                                                                  biasIdx: 3, outIdx: 4, act: 'silu' } } });
+    be.runSync(inst, [xs, wq4, sw4, bias, y], null);
+    writeArr(dir, 'out_w4.bin', y);
   });
 
   test('async path resolves to the same result', () => {
