@@ -199,13 +199,19 @@ def bench_c5_gemv():
             outs = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(R)]
             g_us, how = graph_time_us(lambda i: O.qlinear(xq, sx, Wqs[i], sW, out=outs[i]), R)
             q_us, _ = graph_time_us(lambda i: O.quantize_per_token(x, xq, sx), 8)
+            # the whole dynamic linear in one call (one kernel for M <= 4)
+            d_us, _ = graph_time_us(
+                lambda i: O.qlinear_dynamic(x, Wqs[i], sW, out=outs[i], xq=xq, sx=sx), R)
             kb = N * K + 8 * N + M * K + 8 * M + 4 * M * N      # the GEMV kernel's own bytes
             sb = N * K + 8 * N + 4 * M * K + 4 * M * N          # step bytes (fp32 x in)
             res[f"gemv_M{M}_N{N}"] = {
                 "gemv_avg_us": g_us, "gemv_GB/s": kb / (g_us * 1e-6) / 1e9,
                 "gemv_frac_hbm": kb / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
                 "quantize_x_avg_us": q_us,
-                "step_GB/s": sb / ((g_us + q_us) * 1e-6) / 1e9, "timing": how,
+                "step_GB/s": sb / ((g_us + q_us) * 1e-6) / 1e9,
+                "qlinear_dynamic_avg_us": d_us, "qlinear_dynamic_GB/s": sb / (d_us * 1e-6) / 1e9,
+                "qlinear_dynamic_frac_hbm": sb / (d_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+                "timing": how,
             }
         # the same weights as 4-bit per-group codes (group 128): W4A8 decode GEMV
         g = 128

@@ -215,6 +215,22 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int epi, double s_out, const float* bias, int act,
             int out_kind, void* out, void* stream);
 
+/* Dynamic int8 linear in one call: QuantizationPass's chain for a linear
+ * (quantization_pass.ts:286-459: quantize(x) -> quantized_dot ->
+ * convert -> mul(sv) [-> add bias -> max]) with the activation scale taken
+ * from x itself, per token or per tensor, as q8_quantize_rows does, on an
+ * nn.Linear weight (src/nn/functional/linear.ts:6-16, W [N,K] = Wq with
+ * f64 scales sW, Q8_PER_CHANNEL [N] or Q8_PER_TENSOR [1]):
+ *   xq, sx  = q8_quantize_rows(x, M, K, x_mode)          (written to xq, sx)
+ *   out     = q8_gemm(xq, Wq, ..., Q8_EPI_ROWCOL, bias, act, Q8_F32)
+ * bit for bit.  For one-token decode (M == 1, K <= 4096, K % 16 == 0,
+ * 16-byte aligned x and Wq) both steps run in one kernel; otherwise as
+ * two (the same kernels as the separate calls).
+ * xq: int8 [M,K]; sx: f64 [M] (per token) or [1] (per tensor). */
+int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const int8_t* Wq,
+                       const double* sW, int sW_mode, int64_t N, const float* bias, int act,
+                       float* out, int8_t* xq, double* sx, void* stream);
+
 /* q8_gemm's fp32 result, requantized in the epilogue with the next layer's
  * static scale and stored as int8: QuantizationPass's calibrated chain
  * dequantize -> [add bias] -> [relu] -> quantize(s_next)

@@ -72,6 +72,8 @@ SIGNATURES = {
                 _int, _vp, _vp],
     "q8_gemm_requant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                         _dbl, _vp, _vp],
+    "q8_qlinear_dynamic": [_vp, _i64, _i64, _int, _vp, _vp, _int, _i64, _vp, _int, _vp, _vp, _vp,
+                           _vp],
     "q8_pack_weight_int4": [_vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "q8_gemv_w4": [_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _int, _vp, _vp],
     "q8_quantized_conv_workspace": [_int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp],

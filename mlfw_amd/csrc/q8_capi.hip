@@ -410,6 +410,33 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, c
   return launched(q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream)), "q8_gemv launch");
 }
 
+int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const int8_t* Wq,
+                       const double* sW, int sW_mode, int64_t N, const float* bias, int act,
+                       float* out, int8_t* xq, double* sx, void* stream) {
+  Q8_REQUIRE(x_mode == Q8_PER_TOKEN || x_mode == Q8_PER_TENSOR,
+             "q8_qlinear_dynamic: x_mode must be Q8_PER_TOKEN or Q8_PER_TENSOR (got %d)", x_mode);
+  q8::GemmEpi e;
+  int rc = gemm_common("q8_qlinear_dynamic", xq, Wq, M, N, K, 0, 0, sx, x_mode, sW, sW_mode,
+                       Q8_EPI_ROWCOL, 0.0, bias, act, Q8_F32, out, &e);
+  if (rc != Q8_OK) return rc;
+  Q8_REQUIRE(M * K == 0 || x, "q8_qlinear_dynamic: x is NULL");
+  int* work = nullptr;
+  rc = ensure_current(&work);
+  if (rc != Q8_OK) return rc;
+  hipStream_t st = as_stream(stream);
+  if (M * N == 0 && M * K == 0) return Q8_OK;
+  if (N > 0 && q8::qlinear_fused_ok(x, Wq, M, K))
+    return launched(q8::launch_qlinear_fused(x, M, K, x_mode == Q8_PER_TENSOR ? 1 : 0, Wq, sW,
+                                             e.sB_stride, N, bias, act, out, sx, xq, st),
+                    "q8_qlinear_dynamic launch");
+  hipError_t err = x_mode == Q8_PER_TOKEN ? q8::launch_quant_rows(x, M, K, xq, sx, st)
+                                          : q8::launch_quant_tensor(x, M * K, xq, sx, work, st);
+  if (err != hipSuccess || M * N == 0) return launched(err, "q8_qlinear_dynamic quantize launch");
+  err = (M <= 16) ? q8::launch_gemv(xq, Wq, M, N, K, e, out, st)
+                  : q8::launch_gemm(xq, Wq, M, N, K, e, out, st);
+  return launched(err, "q8_qlinear_dynamic launch");
+}
+
 int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                     const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
                     double s_out, const float* bias, int act, double s_next, int8_t* out,

@@ -43,24 +43,27 @@ __device__ __forceinline__ int quant_exact(float x, double s, double zp, int lo,
 // by at most 2^-17 there; Math.round only changes value across a
 // half-integer, so when t's fraction is more than 2^-13 away from 0.5 the
 // integer is decided by t.  |t| >= 256 implies |y| > 128.5 (clamped).
-// Everything else (near-ties, NaN) takes the exact f64 path, so the result
-// is always the exact one.  Callers guarantee s is a normal double in
-// [2^-100, 2^100] (else they use quant_exact for every element).
+// Callers guarantee s is a normal double in [2^-100, 2^100] (else they use
+// quant_exact for every element).
+// quant_sym_try is that decision without branches: floor(t) clamped to
+// [-256, 256] (so |t| >= 256, infinities included, saturate through the
+// integer clamp), plus the rounding step; `bad` flags the inputs the fast
+// path cannot decide -- near-ties and NaN -- which take the exact f64 path.
+__device__ __forceinline__ int quant_sym_try(float x, float r32, bool& bad) {
+  const float t = x * r32;
+  const float fl = __builtin_floorf(t);
+  const float fr = t - fl;
+  int r = (int)__builtin_amdgcn_fmed3f(fl, -256.0f, 256.0f) + (fr > 0.5f ? 1 : 0);
+  r = r < -128 ? -128 : (r > 127 ? 127 : r);
+  bad = (__builtin_fabsf(t) < 256.0f && !(__builtin_fabsf(fr - 0.5f) > 0x1p-13f)) || t != t;
+  return r;
+}
+
 __device__ __forceinline__ int quant_sym_fast(float x, float r32, double s) {
-  float t = x * r32;
-  float at = __builtin_fabsf(t);
-  if (at < 256.0f) {
-    float fl = __builtin_floorf(t);
-    float fr = t - fl;
-    if (__builtin_fabsf(fr - 0.5f) > 0x1p-13f) {
-      int r = (int)fl + (fr > 0.5f ? 1 : 0);
-      r = r < -128 ? -128 : r;
-      return r > 127 ? 127 : r;
-    }
-  } else if (at >= 256.0f) {          // false for NaN
-    return t > 0.0f ? 127 : -128;
-  }
-  return quant_exact(x, s, 0.0, -128, 127);
+  bool bad;
+  int r = quant_sym_try(x, r32, bad);
+  if (bad) r = quant_exact(x, s, 0.0, -128, 127);
+  return r;
 }
 
 // Order key of |x| for a NaN-ignoring absmax: the bit pattern of |x| (an
@@ -77,6 +80,39 @@ __device__ __forceinline__ double scale_from_key(int key) {
   double amax = key < 0 ? __builtin_inf() : (double)__uint_as_float((unsigned)key);
   double s = amax / 127.0;
   return (s == 0.0 || s != s) ? 1e-10 : s;
+}
+
+// Four int8 codes packed little-endian into one dword.
+__device__ __forceinline__ int pack4(int b0, int b1, int b2, int b3) {
+  return (b0 & 0xff) | ((b1 & 0xff) << 8) | ((b2 & 0xff) << 16) | ((b3 & 0xff) << 24);
+}
+
+// absmax_key of four values.
+__device__ __forceinline__ int key4(float4 v) {
+  int a = absmax_key(v.x), b = absmax_key(v.y), c = absmax_key(v.z), d = absmax_key(v.w);
+  a = a > b ? a : b;
+  c = c > d ? c : d;
+  return a > c ? a : c;
+}
+
+// Symmetric int8 codes of four values (R1 with zp = 0), packed.
+// Symmetric int8 codes of four values (R1 with zp = 0), packed; one branch
+// to the exact path for the four.
+__device__ __forceinline__ int quant4_sym(float4 v, bool fast, float r32, double s) {
+  if (fast) {
+    bool b0, b1, b2, b3;
+    int c0 = quant_sym_try(v.x, r32, b0), c1 = quant_sym_try(v.y, r32, b1);
+    int c2 = quant_sym_try(v.z, r32, b2), c3 = quant_sym_try(v.w, r32, b3);
+    if (b0 | b1 | b2 | b3) {
+      if (b0) c0 = quant_exact(v.x, s, 0.0, -128, 127);
+      if (b1) c1 = quant_exact(v.y, s, 0.0, -128, 127);
+      if (b2) c2 = quant_exact(v.z, s, 0.0, -128, 127);
+      if (b3) c3 = quant_exact(v.w, s, 0.0, -128, 127);
+    }
+    return pack4(c0, c1, c2, c3);
+  }
+  return pack4(quant_exact(v.x, s, 0.0, -128, 127), quant_exact(v.y, s, 0.0, -128, 127),
+               quant_exact(v.z, s, 0.0, -128, 127), quant_exact(v.w, s, 0.0, -128, 127));
 }
 
 // Whether the f32 fast path of quant_sym_fast is valid for scale s.

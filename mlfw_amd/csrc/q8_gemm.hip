@@ -719,6 +719,168 @@ void k_gemv_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M
   }
 }
 
+// ---- Fused dynamic qlinear for one-token decode (K <= 4096): the per-token
+// (or per-tensor) int8 quantize of the fp32 activations and the dot4 GEMV
+// in one kernel.  Every workgroup reads the whole activation row (16 fp32
+// elements per lane; cached, it is the same for all workgroups), takes its
+// absmax key (wave max, then LDS across the 4 waves), derives the scale and
+// codes with the same functions as q8_quantize_rows -- so codes and scale
+// are identical to that kernel's -- and goes on as k_gemv_i8 with R weight
+// rows per workgroup.  One launch and one dependent memory round trip less
+// than quantize + GEMV.  The template also takes MT <= 4 tokens; only
+// MT = 1 is launched (the quantize repeated per workgroup grows with MT).
+// R1's exact form, symmetric int8 -- out of line: it runs only for
+// near-ties (and non-normal scales), and inlining it at each of a lane's
+// 16 x MT elements would multiply the kernel's code size.
+__device__ __noinline__ int quant_exact_sym_call(float x, double s) {
+  return quant_exact(x, s, 0.0, -128, 127);
+}
+
+// quant4_sym with the exact path out of line.
+__device__ __forceinline__ int quant4_sym_call(v4f v, bool fast, float r32, double s) {
+  if (fast) {
+    bool b0, b1, b2, b3;
+    int c0 = quant_sym_try(v.x, r32, b0), c1 = quant_sym_try(v.y, r32, b1);
+    int c2 = quant_sym_try(v.z, r32, b2), c3 = quant_sym_try(v.w, r32, b3);
+    if (b0 | b1 | b2 | b3) {
+      if (b0) c0 = quant_exact_sym_call(v.x, s);
+      if (b1) c1 = quant_exact_sym_call(v.y, s);
+      if (b2) c2 = quant_exact_sym_call(v.z, s);
+      if (b3) c3 = quant_exact_sym_call(v.w, s);
+    }
+    return pack4(c0, c1, c2, c3);
+  }
+  return pack4(quant_exact_sym_call(v.x, s), quant_exact_sym_call(v.y, s),
+               quant_exact_sym_call(v.z, s), quant_exact_sym_call(v.w, s));
+}
+
+template <int MT, int R>
+__global__ __launch_bounds__(256)
+void k_qlinear_dot4(const float* __restrict__ x, int M, int K, int per_tensor,
+                    const int8_t* __restrict__ W, const double* __restrict__ sW, int sW_stride,
+                    int N, const float* __restrict__ bias, int act, float* __restrict__ y,
+                    double* __restrict__ sx_out, int8_t* __restrict__ xq_out) {
+  constexpr int V = R * MT;
+  static_assert(V <= 64, "butterfly width");
+  __shared__ int kred[4][MT];
+  __shared__ int red[4][V];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = K >> 4;                               // 16-element chunks per row (<= 256)
+  const bool live = tid < C;                          // this lane's chunk exists
+  const int n0 = blockIdx.x * R;
+
+  // activations first (the reduction needs them first), then the weights,
+  // then the epilogue operands; every load issued before any arithmetic
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, (int)((uint32_t)M * (uint32_t)K * 4u),
+                                        0x00020000);
+  v4f xv[MT][4];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t off = (live && m < M) ? ((uint32_t)m * (uint32_t)K + 16u * (uint32_t)tid) * 4u + 16u * j : OOB;
+      xv[m][j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+    }
+  const uint32_t rows = (uint32_t)min(R, N - n0);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(W + (int64_t)n0 * K, rows * (uint32_t)K);
+  v4i w[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t off = live ? (uint32_t)r * (uint32_t)K + 16u * (uint32_t)tid : OOB;
+    w[r] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 2));
+  }
+  // output lane tid < V finishes (token tid / R, row n0 + tid % R)
+  const int om = tid / R, on = n0 + tid % R;
+  const bool out_lane = tid < V && om < M && on < N;
+  const double sw = out_lane ? sW[(int64_t)on * sW_stride] : 0.0;
+  const float bv = (out_lane && bias) ? bias[on] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+
+  // absmax keys: -1 (no value) for absent chunks and tokens
+  int key[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    int k = -1;
+    if (live && m < M) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kj = key4(make_float4(xv[m][j].x, xv[m][j].y, xv[m][j].z, xv[m][j].w));
+        k = k > kj ? k : kj;
+      }
+    }
+    key[m] = wave_max_i32(k);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) kred[wave][m] = key[m];
+  }
+  __syncthreads();
+  int kt = -1;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    int k = kred[0][m];
+#pragma unroll
+    for (int v = 1; v < 4; ++v) k = k > kred[v][m] ? k : kred[v][m];
+    key[m] = k;
+    if (m < M) kt = kt > k ? kt : k;
+  }
+  // scales and codes (q8_quantize_rows' arithmetic)
+  double s[MT];
+  v4i xa[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    s[m] = scale_from_key(per_tensor ? kt : key[m]);
+    const bool fast = fast_scale_ok(s[m]);
+    const float r32 = (float)(1.0 / s[m]);
+    int c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      c[j] = quant4_sym_call(xv[m][j], fast, r32, s[m]);
+    xa[m] = v4i{c[0], c[1], c[2], c[3]};
+    if (xq_out && blockIdx.x == 0 && live && m < M)
+      *reinterpret_cast<v4i*>(xq_out + (int64_t)m * K + 16 * tid) = xa[m];
+  }
+  if (sx_out && blockIdx.x == 0 && tid < (per_tensor ? 1 : M)) {
+    double v = s[0];
+#pragma unroll
+    for (int m = 1; m < MT; ++m)
+      if (tid == m) v = s[m];
+    sx_out[tid] = v;
+  }
+  int acc[V];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      int a = 0;
+      a = __builtin_amdgcn_sdot4(xa[m].x, w[r].x, a, false);
+      a = __builtin_amdgcn_sdot4(xa[m].y, w[r].y, a, false);
+      a = __builtin_amdgcn_sdot4(xa[m].z, w[r].z, a, false);
+      a = __builtin_amdgcn_sdot4(xa[m].w, w[r].w, a, false);
+      acc[r * MT + m] = a;
+    }
+  const int total = wave_butterfly_sum<V>(acc, lane);
+  constexpr int SHIFT = V == 64 ? 0 : V == 32 ? 1 : V == 16 ? 2 : V == 8 ? 3 : V == 4 ? 4 : 5;
+  if ((lane & ((1 << SHIFT) - 1)) == 0) red[wave][lane >> SHIFT] = total;
+  __syncthreads();
+  if (out_lane) {
+    const int i = (tid % R) * MT + om;
+    const int a = (int)((uint32_t)red[0][i] + (uint32_t)red[1][i] + (uint32_t)red[2][i] +
+                        (uint32_t)red[3][i]);
+    double sm = s[0];
+#pragma unroll
+    for (int m = 1; m < MT; ++m)
+      if (om == m) sm = s[m];
+    // E-rowcol: fround(acc * fround(sx[m] * sW[n])), then bias and activation
+    float v = mul_acc_f32scale(a, (float)(sm * sw));
+    if (bias) v = v + bv;
+    if (act == 1) v = relu_js(v);
+    else if (act == 2) v = silu_js(v);
+    y[(int64_t)om * N + on] = v;
+  }
+}
+
 // ---- MFMA GEMV, 4 < M <= 16 tokens.  At 16 tokens a v_dot4 kernel spends
 // 64 VALU instructions per 16 weight bytes per lane and stops being
 // HBM-bound; one v_mfma_i32_16x16x64_i8 does the same work for 16 weight
@@ -837,6 +999,30 @@ hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
   if (M <= 1) return launch_gemv_mt<1>(A, B, (int)M, (int)N, (int)K, e, out, st);
   if (M <= 2) return launch_gemv_mt<2>(A, B, (int)M, (int)N, (int)K, e, out, st);
   return launch_gemv_mt<4>(A, B, (int)M, (int)N, (int)K, e, out, st);
+}
+
+bool qlinear_fused_ok(const float* x, const int8_t* W, int64_t M, int64_t K) {
+  return M == 1 && K >= 16 && K <= 4096 && K % 16 == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0;
+}
+
+hipError_t launch_qlinear_fused(const float* x, int64_t M, int64_t K, int per_tensor,
+                                const int8_t* W, const double* sW, int sW_stride, int64_t N,
+                                const float* bias, int act, float* y, double* sx_out,
+                                int8_t* xq_out, hipStream_t st) {
+  if (M == 0 || N == 0) return hipSuccess;
+#define Q8_QLF(MT, R)                                                                            \
+  hipLaunchKernelGGL((k_qlinear_dot4<MT, R>), dim3((unsigned)((N + (R)-1) / (R))), dim3(256), 0, \
+                     st, x, (int)M, (int)K, per_tensor, W, sW, sW_stride, (int)N, bias, act, y,   \
+                     sx_out, xq_out)
+  // one token: 16 weight rows per workgroup (measured against 4, 8, 32 and
+  // 64: fewer, larger workgroups repeat the quantize less often but stream
+  // fewer rows at once).  With more tokens the quantize repeated in every
+  // workgroup costs more than the launch it saves, so M > 1 runs as two
+  // kernels (see qlinear_fused_ok).
+  Q8_QLF(1, 16);
+#undef Q8_QLF
+  return hipGetLastError();
 }
 
 hipError_t setup_kernel_attributes() {

@@ -52,6 +52,14 @@ hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 // 4-bit per-group weights (q8_w4.hip).
 hipError_t launch_pack_w4(const float* W, int64_t N, int64_t K, int64_t group, uint8_t* wq4,
                           double* scales, hipStream_t st);
+// Dynamic qlinear for one-token decode in one kernel (per-token or
+// per-tensor quantize of fp32 x + dot4 GEMV + E-rowcol epilogue);
+// qlinear_fused_ok says whether the shape and alignment fit it.
+bool qlinear_fused_ok(const float* x, const int8_t* W, int64_t M, int64_t K);
+hipError_t launch_qlinear_fused(const float* x, int64_t M, int64_t K, int per_tensor,
+                                const int8_t* W, const double* sW, int sW_stride, int64_t N,
+                                const float* bias, int act, float* y, double* sx_out,
+                                int8_t* xq_out, hipStream_t st);
 hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, const uint8_t* wq4,
                           const double* sw, int64_t M, int64_t N, int64_t K, int64_t group,
                           const float* bias, int act, float* y, hipStream_t st);

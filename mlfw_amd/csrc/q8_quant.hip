@@ -107,25 +107,6 @@ hipError_t launch_apply_outliers(float* x, int64_t n, uint32_t seed, double p, d
 }
 
 // ------------------------------------------------------------------ helpers
-__device__ __forceinline__ int pack4(int b0, int b1, int b2, int b3) {
-  return (b0 & 0xff) | ((b1 & 0xff) << 8) | ((b2 & 0xff) << 16) | ((b3 & 0xff) << 24);
-}
-
-__device__ __forceinline__ int key4(float4 v) {
-  int a = absmax_key(v.x), b = absmax_key(v.y), c = absmax_key(v.z), d = absmax_key(v.w);
-  a = a > b ? a : b;
-  c = c > d ? c : d;
-  return a > c ? a : c;
-}
-
-__device__ __forceinline__ int quant4_sym(float4 v, bool fast, float r32, double s) {
-  if (fast)
-    return pack4(quant_sym_fast(v.x, r32, s), quant_sym_fast(v.y, r32, s),
-                 quant_sym_fast(v.z, r32, s), quant_sym_fast(v.w, r32, s));
-  return pack4(quant_exact(v.x, s, 0.0, -128, 127), quant_exact(v.y, s, 0.0, -128, 127),
-               quant_exact(v.z, s, 0.0, -128, 127), quant_exact(v.w, s, 0.0, -128, 127));
-}
-
 // Block-wide max of an int key (256 threads = 4 waves).  `red` is LDS.
 __device__ __forceinline__ int block_max_i32(int key, int* red) {
   key = wave_max_i32(key);

@@ -385,10 +385,9 @@ function runDescriptor(d, args, dev) {
     A.upload(dwq, wq);
     A.upload(dws, ws);
     if (bias) A.upload(db, bias);
-    if (perTensor) A.quantizeRows(dx, 1, d.M * d.K, A.Q8_PER_TENSOR, dxq, dsx);
-    else A.quantizeRows(dx, d.M, d.K, A.Q8_PER_TOKEN, dxq, dsx);
-    A.gemm(dxq, dwq, d.M, d.N, d.K, 0, 0, dsx, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN,
-           dws, A.Q8_PER_CHANNEL, A.Q8_EPI_ROWCOL, 0, db, A[ACT_CODE[d.act || 'none']], A.Q8_F32, dout);
+    // quantize + GEMM + epilogue in one call (one kernel for a single token)
+    A.qlinearDynamic(dx, d.M, d.K, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN, dwq, dws, A.Q8_PER_CHANNEL,
+                     d.N, db, A[ACT_CODE[d.act || 'none']], dout, dxq, dsx);
     A.download(out, dout);
     return out;
   }

@@ -407,6 +407,23 @@ static napi_value js_gemm_requant(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* qlinearDynamic(x, M, K, xMode, wq, sW, sWMode, N, bias, act, out, xq, sx) */
+static napi_value js_qlinear_dynamic(napi_env env, napi_callback_info info) {
+  napi_value argv[13];
+  void *x, *wq, *sw, *bias, *out, *xq, *sx;
+  int64_t M, K, xm, swm, N, act;
+  if (!get_args(env, info, 13, argv) || !arg_buf(env, argv[0], 1, &x) || !arg_i64(env, argv[1], &M) ||
+      !arg_i64(env, argv[2], &K) || !arg_i64(env, argv[3], &xm) || !arg_buf(env, argv[4], 1, &wq) ||
+      !arg_buf(env, argv[5], 1, &sw) || !arg_i64(env, argv[6], &swm) || !arg_i64(env, argv[7], &N) ||
+      !arg_buf(env, argv[8], 1, &bias) || !arg_i64(env, argv[9], &act) || !arg_buf(env, argv[10], 1, &out) ||
+      !arg_buf(env, argv[11], 1, &xq) || !arg_buf(env, argv[12], 1, &sx))
+    return NULL;
+  Q8_CHECK(env, q8_qlinear_dynamic((const float*)x, M, K, (int)xm, (const int8_t*)wq, (const double*)sw,
+                                   (int)swm, N, (const float*)bias, (int)act, (float*)out, (int8_t*)xq,
+                                   (double*)sx, NULL));
+  return undefined(env);
+}
+
 /* packWeightInt4(W, N, K, groupSize, wq4, scales) */
 static napi_value js_pack_weight_int4(napi_env env, napi_callback_info info) {
   napi_value argv[6];
@@ -533,6 +550,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"packWeight", js_pack_weight},
       {"gemm", js_gemm},
       {"gemmRequant", js_gemm_requant},
+      {"qlinearDynamic", js_qlinear_dynamic},
       {"packWeightInt4", js_pack_weight_int4},
       {"gemvW4", js_gemv_w4},
       {"siluMulQuantizeRows", js_silu_mul_quantize_rows},

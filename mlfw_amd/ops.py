@@ -263,6 +263,37 @@ def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor
     return out
 
 
+def qlinear_dynamic(x: torch.Tensor, Wq: torch.Tensor, sW: torch.Tensor,
+                    bias: torch.Tensor | None = None, act: str | None = None,
+                    per_tensor: bool = False, out: torch.Tensor | None = None,
+                    xq: torch.Tensor | None = None, sx: torch.Tensor | None = None):
+    """Dynamic int8 linear in one call: quantize x (fp32 [M,K]) per token (or
+    per tensor), then the int8 GEMM with the qlinear epilogue.  Equal bit
+    for bit to quantize_per_token / quantize_per_tensor followed by qlinear;
+    decode shapes (M <= 4, K <= 4096) run as one kernel.
+    Returns (y fp32 [M,N], int8 codes [M,K], f64 scales [M] or [1])."""
+    _need(x, torch.float32, "x")
+    M, K = _rows(x)
+    _need(Wq, torch.int8, "Wq")
+    if Wq.dim() != 2 or Wq.shape[1] != K or not Wq.is_contiguous():
+        raise ValueError("qlinear_dynamic: Wq must be a contiguous [N, K] int8 tensor")
+    N = Wq.shape[0]
+    _need(sW, torch.float64, "sW")
+    if sW.numel() not in (1, N):
+        raise ValueError("qlinear_dynamic: sW must have 1 or N elements")
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.numel() != N:
+            raise ValueError("qlinear_dynamic: bias must have N elements")
+    out = torch.empty((M, N), dtype=torch.float32, device=x.device) if out is None else out
+    xq = torch.empty((M, K), dtype=torch.int8, device=x.device) if xq is None else xq
+    sx = torch.empty(1 if per_tensor else M, dtype=torch.float64, device=x.device) if sx is None else sx
+    _call("q8_qlinear_dynamic", _ptr(x), M, K, L.Q8_PER_TENSOR if per_tensor else L.Q8_PER_TOKEN,
+           _ptr(Wq), _ptr(sW), L.Q8_PER_CHANNEL if sW.numel() == N and N != 1 else L.Q8_PER_TENSOR,
+           N, _ptr(bias), _ACT[act], _ptr(out), _ptr(xq), _ptr(sx), _stream())
+    return out, xq, sx
+
+
 def qlinear_pt(A: torch.Tensor, B: torch.Tensor, s_out: float,
                bias: torch.Tensor | None = None, act: str | None = None,
                out: torch.Tensor | None = None) -> torch.Tensor:

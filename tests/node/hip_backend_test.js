@@ -235,7 +235,9 @@ function cpuTests() {
     assert.throws(() => a.gemm(null, null, 4, 4, 16, 0, 0, null, 0, null, 0, 9, 0, null, 0, a.Q8_F32, null),
                   (e) => e.code === 'Q8_ERR_1' && /bad epi/.test(e.message));
     assert.throws(() => a.upload({}, new Float32Array(1)), TypeError);
-    for (const f of ['gemmRequant', 'packWeightInt4', 'gemvW4']) assert.strictEqual(typeof a[f], 'function', f);
+    for (const f of ['gemmRequant', 'packWeightInt4', 'gemvW4', 'qlinearDynamic']) assert.strictEqual(typeof a[f], 'function', f);
+    assert.throws(() => a.qlinearDynamic(null, 1, 16, 9, null, null, 0, 4, null, 0, null, null, null),
+                  (e) => e.code === 'Q8_ERR_1' && /x_mode/.test(e.message));
     assert.throws(() => a.gemvW4(null, null, a.Q8_PER_TOKEN, null, null, 1, 4, 96, 64, null, 0, null),
                   (e) => e.code === 'Q8_ERR_1' && /group_size/.test(e.message));
     assert.throws(() => a.packWeightInt4(null, 4, 96, 7, null, null), (e) => e.code === 'Q8_ERR_1');
@@ -336,6 +338,15 @@ function gpuTests(dir) {
     const y = new Int32Array(info.outShape.reduce((a, b) => a * b, 1));
     be.runSync(be.instantiate(kern), [xc, wc, y], null);
     writeArr(dir, 'out_conv.bin', y);
+  });
+
+  test('runtime backend: one-token dynamic qlinear (quantize + GEMV in one kernel)', () => {
+    const y = new Float32Array(N);
+    const inst = be.instantiate({ metadata: { kind: 'hip', q8: { op: 'qlinear', M: 1, N, K, xIdx: 0, wqIdx: 1, wsIdx: 2,
+                                                                  biasIdx: 3, outIdx: 4, granularity: 'per_token',
+                                                                  act: 'silu' } } });
+    be.runSync(inst, [X.subarray(0, K), Wq, sW, bias, y], null);
+    writeArr(dir, 'out_qlinear1.bin', y);
   });
 
   test('runtime backend: int8 linear with the fused static requant (int8 out)', () => {

@@ -104,6 +104,8 @@ def test_node_host_gpu_c1(tmp_path, oracle):
     same_bits(out("out_conv", np.int32, conv_ref.shape), conv_ref, "quantized_conv PrimFunc")
     same_bits(out("out_requant", np.int8, (M, N)), oracle.quantize(y_rq.reshape(-1), s_next).reshape(M, N),
               "qlinear with fused static requant")
+    same_bits(out("out_qlinear1", np.float32, (1, N)),
+              OC.qlinear_rows(X[:1], Wq, sW, bias=bias, act="silu"), "one-token dynamic qlinear")
     xs = X[:w4_m]
     sxs = oracle.scales_per_token(xs)
     want_w4 = oracle.gemv_w4(oracle.quantize_rows(xs, sxs), sxs, wq4, sw4, K, w4_group, bias=bias, act="silu")
