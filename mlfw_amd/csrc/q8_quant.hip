@@ -169,6 +169,13 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // quantize, so such rows are read once; longer rows re-read the tail.
 // Loads and stores are non-temporal: the stream is touched once, and
 // keeping it out of the caches measured ~5-10% faster than plain accesses.
+// A block with several rows loads the next row while it reduces and
+// quantizes the current one (two register sets, used alternately).  Every
+// row is loaded through its own buffer resource whose size is 0 past the
+// last row, so the loads are issued unconditionally and a missing row
+// reads zeros without touching memory; the loads in flight are then the
+// same on every path and the wait before a row's reduction leaves the
+// next row's loads outstanding.
 template <int VPT, bool FULL>
 __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t M,
                                                    int64_t K, int8_t* __restrict__ q,
@@ -176,24 +183,24 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
   __shared__ int red[NT / 64];
   const int tid = threadIdx.x;
   const int64_t K4 = K >> 2;       // FULL: K4 == VPT * NT, no bounds to test
-  for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
-    const v4f* xr = reinterpret_cast<const v4f*>(x + row * K);
-    int* qr = reinterpret_cast<int*>(q + row * K);
-    float4 v[VPT];
-    int key = -1;
-    // Every load is issued unconditionally (a lane past the row end reloads
-    // the last group and ignores it) so that all VPT loads are in flight
-    // together; a conditional load would be waited for one at a time.
-    const int last = (int)K4 - 1;
+  const int last = (int)K4 - 1;
+  const int64_t G = gridDim.x;
+  auto load_row = [&](int64_t row, float4* v) {
+    const bool in = row < M;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + (in ? row : 0) * K), (short)0, in ? (int)(K * 4) : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int i = tid + j * NT;
-      const v4f t = __builtin_nontemporal_load(xr + (FULL ? i : min(i, last)));
+      const uint32_t off = (FULL || i <= last) ? 16u * (uint32_t)i : 0x80000000u;
+      const v4f t = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
       v[j] = make_float4(t.x, t.y, t.z, t.w);
     }
-    // no arithmetic between the loads (the scheduler would otherwise start
-    // on the first group and issue the rest after waiting for it)
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto process_row = [&](int64_t row, const float4* v) {
+    const v4f* xr = reinterpret_cast<const v4f*>(x + row * K);
+    int* qr = reinterpret_cast<int*>(q + row * K);
+    int key = -1;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int k = key4(v[j]);
@@ -223,6 +230,20 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
                                     qr + i);
       }
     }
+  };
+  float4 va[VPT], vb[VPT];
+  int64_t row = blockIdx.x;
+  load_row(row, va);
+  for (; row < M; row += 2 * G) {
+    load_row(row + G, vb);
+    // no arithmetic above this point of the iteration (the scheduler would
+    // otherwise start on the first loaded group and issue the rest after it)
+    __builtin_amdgcn_sched_barrier(0);
+    process_row(row, va);
+    load_row(row + 2 * G, va);
+    if (row + G >= M) break;                       // uniform
+    __builtin_amdgcn_sched_barrier(0);
+    process_row(row + G, vb);
   }
 }
 
@@ -264,12 +285,11 @@ hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, do
     hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
     return hipGetLastError();
   }
-  // Row workers: one workgroup per row, except that up to two rows per
-  // workgroup go to a single resident round (8 workgroups per CU at this
-  // block size) when the rows would fill at most two rounds (measured
-  // faster for [4096,4096]; one row per workgroup is faster for more rows).
-  const int64_t slots = 8 * (int64_t)cu_count();
-  const int workers = (int)(M <= 2 * slots ? (M < slots ? M : slots) : (M < 1048576 ? M : 1048576));
+  // Row workers: one workgroup per row (measured against resident grids of
+  // 0.5x to 4x the 8 workgroups per CU, which pipeline several rows per
+  // workgroup: equal for 2048-4096 rows, 10-20% slower for 16384); a grid
+  // capped at 2^20 workgroups walks the rest with the pipelined loop.
+  const int workers = (int)(M < 1048576 ? M : 1048576);
 #define Q8_QROWS(V)                                                                          \
   do {                                                                                       \
     if (K4 == (V) * NT)                                                                      \
