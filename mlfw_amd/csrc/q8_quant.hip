@@ -107,6 +107,21 @@ hipError_t launch_apply_outliers(float* x, int64_t n, uint32_t seed, double p, d
 }
 
 // ------------------------------------------------------------------ helpers
+// Block-wide max of an int key over TPB threads (TPB / 64 waves).  `red`
+// is LDS of TPB / 64 ints.
+template <int TPB>
+__device__ __forceinline__ int block_max_i32_n(int key, int* red) {
+  key = wave_max_i32(key);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = key;
+  __syncthreads();
+  int k = red[0];
+#pragma unroll
+  for (int w = 1; w < TPB / 64; ++w) k = k > red[w] ? k : red[w];
+  __syncthreads();   // red is reused by the next row
+  return k;
+}
+
 // Block-wide max of an int key (256 threads = 4 waves).  `red` is LDS.
 __device__ __forceinline__ int block_max_i32(int key, int* red) {
   key = wave_max_i32(key);
@@ -655,13 +670,18 @@ hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int ax
 }
 
 // ------------------------------------------------------------------ SiLU(g)*u + per-token quantize
-template <int VPT>
-__global__ __launch_bounds__(NT) void k_silu_mul_quant_rows(const float* __restrict__ g,
-                                                            const float* __restrict__ u,
-                                                            int64_t M, int64_t K,
-                                                            float* __restrict__ h,
-                                                            int8_t* __restrict__ q,
-                                                            double* __restrict__ scales) {
+// TPB threads per row: 256, or 512 for long rows, where a 256-thread
+// block would hold 8-12 float4 of g and of u per lane and run 2 waves per
+// SIMD; at 512 threads a lane holds 4-6 and the SIMD keeps more waves to
+// hide the f64 exp behind the loads of other rows.
+template <int VPT, int TPB>
+__global__ __launch_bounds__(TPB) void k_silu_mul_quant_rows(const float* __restrict__ g,
+                                                             const float* __restrict__ u,
+                                                             int64_t M, int64_t K,
+                                                             float* __restrict__ h,
+                                                             int8_t* __restrict__ q,
+                                                             double* __restrict__ scales) {
+  constexpr int NT = TPB;
   __shared__ int red[NT / 64];
   const int tid = threadIdx.x;
   const int64_t K4 = K >> 2;
@@ -696,7 +716,7 @@ __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows(const float* __restr
         key = key > k ? key : k;
       }
     }
-    key = block_max_i32(key, red);
+    key = block_max_i32_n<TPB>(key, red);
     const double s = scale_from_key(key);
     if (tid == 0) scales[row] = s;
     const bool fast = fast_scale_ok(s);
@@ -740,7 +760,7 @@ hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M,
                                       float* h, int8_t* q, double* scales, hipStream_t st) {
   if (M == 0) return hipSuccess;
   const int grid = (int)(M < 1048576 ? M : 1048576);
-  const bool vec = (K % 4 == 0) && (K / 4 <= 12 * NT) &&
+  const bool vec = (K % 4 == 0) && (K / 4 <= 6 * 512) &&
                    ((reinterpret_cast<uintptr_t>(g) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(u) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(h) & 15) == 0) &&
@@ -755,12 +775,18 @@ hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M,
     return hipGetLastError();
   }
   const int workers = (int)(M < 8 * cu_count() ? M : 8 * cu_count());
-  if (K4 <= 4 * NT)
-    hipLaunchKernelGGL(k_silu_mul_quant_rows<4>, dim3(workers), dim3(NT), 0, st, g, u, M, K, h, q, scales);
-  else if (K4 <= 8 * NT)
-    hipLaunchKernelGGL(k_silu_mul_quant_rows<8>, dim3(workers), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+  // 256 threads per row up to 4 float4 per lane, then 512 (measured at
+  // [2048, 8192] and [2048, 11008] against 256 threads x 8-12 and 1024
+  // threads x 2-3 per lane, with and without occupancy limits)
+  if (K4 <= 4 * 256)
+    hipLaunchKernelGGL((k_silu_mul_quant_rows<4, 256>), dim3(workers), dim3(256), 0, st, g, u, M, K, h,
+                       q, scales);
+  else if (K4 <= 4 * 512)
+    hipLaunchKernelGGL((k_silu_mul_quant_rows<4, 512>), dim3(workers), dim3(512), 0, st, g, u, M, K, h,
+                       q, scales);
   else
-    hipLaunchKernelGGL(k_silu_mul_quant_rows<12>, dim3(workers), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    hipLaunchKernelGGL((k_silu_mul_quant_rows<6, 512>), dim3(workers), dim3(512), 0, st, g, u, M, K, h,
+                       q, scales);
   return hipGetLastError();
 }
 
