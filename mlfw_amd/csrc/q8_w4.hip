@@ -150,18 +150,22 @@ __global__ __launch_bounds__(256) void k_gemv_w4(const int8_t* __restrict__ xq,
 
   // this lane's activation chunk for every token, loaded once and first
   // (vector loads complete in order: waiting for these does not wait for
-  // the weights); the token scales
+  // the weights)
   const __amdgpu_buffer_rsrc_t rx = w4_rsrc(xq, (uint32_t)M * (uint32_t)K);
   v4i xa[MT][2];
-  double sxv[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    sxv[m] = m < M ? sx[(int64_t)m * sx_stride] : 0.0;
     const uint32_t xm = (m < M && live_c) ? (uint32_t)m : (uint32_t)M;   // token M: past the end
     const uint32_t off = xm * (uint32_t)K + 32u * (uint32_t)c;
     xa[m][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
     xa[m][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16u, 0, 0));
   }
+  // the token scale of the output this lane finishes (the same token in
+  // both blocks), before the weights so that waiting for it does not wait
+  // for them; one value per lane, not an array indexed by token, which the
+  // compiler would keep in scratch memory
+  const int om = tid % MT;
+  const double sxm = (tid < NO && om < M) ? sx[(int64_t)om * sx_stride] : 0.0;
   // the first two blocks of weights.  Every load is issued on every path
   // (a block past the end reads zero without touching memory), so the
   // loads in flight are the same at every wait.  The bias, needed last,
@@ -250,10 +254,6 @@ __global__ __launch_bounds__(256) void k_gemv_w4(const int8_t* __restrict__ xq,
           for (int j = 0; j < 8; ++j) S = S + v[j];
         }
         for (; g < G; ++g) S = S + t[g * pitch];
-        double sxm = sxv[0];
-#pragma unroll
-        for (int j = 1; j < MT; ++j)
-          if (m == j) sxm = sxv[j];
         float v = (float)(S * sxm);
         if (bias) v = v + bv;
         if (act == 1) v = relu_js(v);

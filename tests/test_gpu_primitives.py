@@ -311,7 +311,7 @@ def test_gemv(ops, oracle, M, N, K):
 
 
 # ------------------------------------------------------------------ fused / inputs
-@pytest.mark.parametrize("M,K", [(4, 11008), (3, 1000), (2, 64)])
+@pytest.mark.parametrize("M,K", [(4, 11008), (3, 1000), (2, 64), (2, 8192), (3, 6000), (2, 12288)])
 def test_silu_mul_quantize(ops, oracle, M, K):
     rng = oracle.Rng(K)
     g = rng.normal((M, K), 0.0, 3.0)
