@@ -11,16 +11,19 @@ validated and converted up front), so the host enqueues faster than the
 GPU executes; the timed region is K steps back to back between two HIP
 events on the stream the kernels run on.
 
-roofline: the GEMM kernel's average duration over K further launches of
-the GEMM alone, back to back between two events on the same stream;
-peak = MI355X dense int8 MFMA, 5.0 POP/s.
+roofline: the GEMM kernel's average duration in the timed region, i.e.
+the step time less the quantize's (timed alone over K launches between
+two events on the same stream); peak = MI355X dense int8 MFMA, 5.0 POP/s.
+(GEMMs launched back to back on their own run ~15-20% longer: without the
+quantize between them the part holds the MFMA load and lowers its clock.)
 `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
 WRITE_SIZE runs (profiles/traffic.json, scaled by a copy-kernel
 calibration), or null when that file is absent.
 
 secondary: the HBM-bound kernels of C5 (per-token quantize and dequantize
 of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}, and the same
-GEMVs for M <= 4 with 4-bit per-group weights) and the C4 projection set.  Each is captured R times in a HIP graph (rotating input
+GEMVs for M <= 4 with 4-bit per-group weights, and the one-call dynamic
+qlinear) and the C4 projection set.  Each is captured R times in a HIP graph (rotating input
 buffers so the 256 MB Infinity Cache cannot serve repeats) and the graph
 is replayed between two events: per-launch host overhead would otherwise
 dominate kernels of a few microseconds.
@@ -102,21 +105,23 @@ def bench_c3(steps, warmup):
     wall = time.perf_counter() - wall0
     step_ms = t_begin.elapsed_time(t_end) / steps
 
-    # (2) per-kernel durations for the roofline: K launches of one kernel
-    # back to back between two events on the stream both kernels run on
-    # (an event pair around every launch would add the dispatch gap to each
-    # interval)
-    def back_to_back(fn):
-        a, b = ev(), ev()
-        torch.cuda.synchronize()
-        a.record()
-        for _ in range(steps):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / steps
-    gemm_ms = back_to_back(gemm)
-    quant_ms = back_to_back(quant)
+    # (2) the GEMM's average duration in the timed region: the step time
+    # less the quantize's, the quantize timed alone over K launches back to
+    # back between two events on the same stream (memory-bound, it runs
+    # the same alone as between GEMMs).  Event pairs around every launch
+    # would add a marker and a dispatch gap (~6 us) to each interval, and
+    # GEMMs launched back to back on their own hold the MFMA load without
+    # a break, so the part lowers its clock (~90 us instead of ~75-80 us).
+    # The GEMM's share keeps one dispatch gap per step: it errs high.
+    a, b = ev(), ev()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        quant()
+    b.record()
+    torch.cuda.synchronize()
+    quant_ms = a.elapsed_time(b) / steps
+    gemm_ms = step_ms - quant_ms
     return {
         "step_ms": step_ms,
         "wall_ms_per_step": 1e3 * wall / steps,
