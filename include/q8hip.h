@@ -215,6 +215,24 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int epi, double s_out, const float* bias, int act,
             int out_kind, void* out, void* stream);
 
+/* quantized_dot as the reference defines it (src/compiler/ir/graph/ops/
+ * quantization.ts:103-155, lowering rules/quantization.ts:23-42): operands
+ * i8 or ui8 (Q8_I8 / Q8_U8: Int8Array or Uint8Array elements, the
+ * verifier's QUANTIZED_INT_DTYPES), zero points, int32 output
+ *   out[m,n] = ToInt32( sum_k (A[m,k] - zpA) * (B[n,k] - zpB) )
+ * with B in the [N,K] layout (rhs_contracting = [1]).  The reference's
+ * QuantizationPass sets non-zero zero points for affine schemes
+ * (quantization_pass.ts:303-332, :415-425).  Runs the int8 GEMM / GEMV on
+ * operands made signed (ui8 bytes flipped by 128) and adds the exact
+ * zero-point correction from row sums; the caller passes a device
+ * workspace of q8_quantized_dot_workspace bytes (0 for i8 operands with
+ * zero zero points, where this is q8_gemm with Q8_I32 output). */
+int q8_quantized_dot_workspace(int64_t M, int64_t N, int64_t K, int a_dtype, int b_dtype,
+                               int32_t zpA, int32_t zpB, size_t* bytes);
+int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int64_t M,
+                     int64_t N, int64_t K, int32_t zpA, int32_t zpB, void* workspace,
+                     size_t workspace_bytes, int32_t* out, void* stream);
+
 /* Dynamic int8 linear in one call: QuantizationPass's chain for a linear
  * (quantization_pass.ts:286-459: quantize(x) -> quantized_dot ->
  * convert -> mul(sv) [-> add bias -> max]) with the activation scale taken
@@ -294,7 +312,8 @@ int q8_gemv_w4(const int8_t* xq, const double* sx, int sx_mode, const uint8_t* W
  *   (x[n, g*C/groups + ic, p*stride + k*dilation - pad_lo] - zp_x) * (w[o, ic, k] - zp_w),
  *   g = o / (O/groups); a tap in the padding adds 0; int32 wrap-around.
  * out_kind Q8_I32: out = acc; Q8_F32: out = fround(acc * s_out).
- * zp_x / zp_w must be 0 in this build (Q8_ERR_UNSUPPORTED otherwise).
+ * Zero points (the op's input_zero_point / kernel_zero_point) run the
+ * direct kernel, exact for any value.
  * workspace: device memory of at least q8_quantized_conv_workspace bytes
  * (may be 0: then NULL is accepted); calls that share a workspace must be
  * ordered (same stream). */
@@ -307,6 +326,14 @@ int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const 
                       const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
                       int32_t zp_x, int32_t zp_w, int out_kind, double s_out, void* workspace,
                       size_t workspace_bytes, void* out, void* stream);
+/* The same with the operand types: x_dtype / w_dtype Q8_I8 or Q8_U8 (the
+ * lowering reads Int8Array or Uint8Array elements; the op admits mixed
+ * types, ops/quantization.ts:176-178).  ui8 operands run the direct kernel. */
+int q8_quantized_conv_ex(const void* x, int x_dtype, const void* w, int w_dtype, int spatial_dims,
+                         const int64_t* x_shape, const int64_t* w_shape, const int64_t* strides,
+                         const int64_t* pad_lo, const int64_t* pad_hi, const int64_t* dilation,
+                         int64_t groups, int32_t zp_x, int32_t zp_w, int out_kind, double s_out,
+                         void* workspace, size_t workspace_bytes, void* out, void* stream);
 
 /* ---------------------------------------------------------------- fused */
 

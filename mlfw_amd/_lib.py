@@ -72,6 +72,9 @@ SIGNATURES = {
                 _int, _vp, _vp],
     "q8_gemm_requant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                         _dbl, _vp, _vp],
+    "q8_quantized_dot_workspace": [_i64, _i64, _i64, _int, _int, C.c_int32, C.c_int32, _vp],
+    "q8_quantized_dot": [_vp, _int, _vp, _int, _i64, _i64, _i64, C.c_int32, C.c_int32, _vp, C.c_size_t,
+                         _vp, _vp],
     "q8_qlinear_dynamic": [_vp, _i64, _i64, _int, _vp, _vp, _int, _i64, _vp, _int, _vp, _vp, _vp,
                            _vp],
     "q8_pack_weight_int4": [_vp, _i64, _i64, _i64, _vp, _vp, _vp],
@@ -79,6 +82,8 @@ SIGNATURES = {
     "q8_quantized_conv_workspace": [_int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp],
     "q8_quantized_conv": [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, C.c_int32,
                           C.c_int32, _int, _dbl, _vp, C.c_size_t, _vp, _vp],
+    "q8_quantized_conv_ex": [_vp, _int, _vp, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                             C.c_int32, C.c_int32, _int, _dbl, _vp, C.c_size_t, _vp, _vp],
     "q8_silu_mul_quantize_rows": [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp],
     "q8_observer_state_bytes": [_int, _vp],
     "q8_observer_reset": [_vp, _int, _int, _vp],

@@ -25,7 +25,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CEILING_LIB = os.path.join(HERE, "libq8ceiling.so")
 CEILING_SRC = "q8_ceiling.hip"
 
-SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip", "q8_conv.hip", "q8_w4.hip"]
+SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip", "q8_conv.hip", "q8_w4.hip",
+           "q8_zp.hip"]
 
 # IEEE arithmetic everywhere (the kernels reproduce the reference's f64 /
 # f32 rounding bit for bit), no packed-FP32 instructions, gfx950 only.

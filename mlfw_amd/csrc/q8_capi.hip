@@ -410,6 +410,86 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, c
   return launched(q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream)), "q8_gemv launch");
 }
 
+// Workspace of q8_quantized_dot: int8 copies of ui8 operands, then the
+// row sums the zero-point correction needs, each 256-byte aligned.
+namespace {
+struct QdotPlan {
+  size_t a_off, b_off, rs_off, cs_off, bytes;
+  bool a_u8, b_u8, need_rs, need_cs;
+  int32_t cA, cB;
+};
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+QdotPlan qdot_plan(int64_t M, int64_t N, int64_t K, int a_dtype, int b_dtype, int32_t zpA,
+                   int32_t zpB) {
+  QdotPlan p{};
+  p.a_u8 = a_dtype == Q8_U8;
+  p.b_u8 = b_dtype == Q8_U8;
+  p.cA = (p.a_u8 ? 128 : 0) - zpA;
+  p.cB = (p.b_u8 ? 128 : 0) - zpB;
+  p.need_rs = p.cB != 0;
+  p.need_cs = p.cA != 0;
+  size_t off = 0;
+  p.a_off = off; if (p.a_u8) off = align256(off + (size_t)(M * K));
+  p.b_off = off; if (p.b_u8) off = align256(off + (size_t)(N * K));
+  p.rs_off = off; if (p.need_rs) off = align256(off + 4 * (size_t)M);
+  p.cs_off = off; if (p.need_cs) off = align256(off + 4 * (size_t)N);
+  p.bytes = off;
+  return p;
+}
+}  // namespace
+
+int q8_quantized_dot_workspace(int64_t M, int64_t N, int64_t K, int a_dtype, int b_dtype,
+                               int32_t zpA, int32_t zpB, size_t* bytes) {
+  Q8_REQUIRE(M >= 0 && N >= 0 && K >= 0 && mul_ok(M, K) && mul_ok(N, K) && mul_ok(M, N),
+             "q8_quantized_dot_workspace: bad shape M=%lld N=%lld K=%lld", (long long)M,
+             (long long)N, (long long)K);
+  Q8_REQUIRE((a_dtype == Q8_I8 || a_dtype == Q8_U8) && (b_dtype == Q8_I8 || b_dtype == Q8_U8),
+             "q8_quantized_dot_workspace: operands must be Q8_I8 or Q8_U8");
+  Q8_REQUIRE(bytes != nullptr, "q8_quantized_dot_workspace: bytes is NULL");
+  *bytes = qdot_plan(M, N, K, a_dtype, b_dtype, zpA, zpB).bytes;
+  return Q8_OK;
+}
+
+int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int64_t M,
+                     int64_t N, int64_t K, int32_t zpA, int32_t zpB, void* workspace,
+                     size_t workspace_bytes, int32_t* out, void* stream) {
+  Q8_REQUIRE((a_dtype == Q8_I8 || a_dtype == Q8_U8) && (b_dtype == Q8_I8 || b_dtype == Q8_U8),
+             "q8_quantized_dot: operands must be Q8_I8 or Q8_U8 (got %d, %d)", a_dtype, b_dtype);
+  q8::GemmEpi e;
+  int rc = gemm_common("q8_quantized_dot", (const int8_t*)A, (const int8_t*)B, M, N, K, 0, 0,
+                       nullptr, Q8_PER_TENSOR, nullptr, Q8_PER_TENSOR, Q8_EPI_PT, 0.0, nullptr,
+                       Q8_ACT_NONE, Q8_I32, out, &e);
+  if (rc != Q8_OK) return rc;
+  const QdotPlan p = qdot_plan(M, N, K, a_dtype, b_dtype, zpA, zpB);
+  Q8_REQUIRE(p.bytes == 0 || (workspace && workspace_bytes >= p.bytes),
+             "q8_quantized_dot: needs a workspace of %zu bytes (got %zu)", p.bytes, workspace_bytes);
+  rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  if (M * N == 0) return Q8_OK;
+  hipStream_t st = as_stream(stream);
+  int8_t* ws = static_cast<int8_t*>(workspace);
+  const int8_t* a = static_cast<const int8_t*>(A);
+  const int8_t* b = static_cast<const int8_t*>(B);
+  hipError_t err = hipSuccess;
+  if (p.a_u8 && err == hipSuccess) {
+    err = q8::launch_flip_u8(static_cast<const uint8_t*>(A), ws + p.a_off, M * K, st);
+    a = ws + p.a_off;
+  }
+  if (p.b_u8 && err == hipSuccess) {
+    err = q8::launch_flip_u8(static_cast<const uint8_t*>(B), ws + p.b_off, N * K, st);
+    b = ws + p.b_off;
+  }
+  int32_t* rs = p.need_rs ? reinterpret_cast<int32_t*>(ws + p.rs_off) : nullptr;
+  int32_t* cs = p.need_cs ? reinterpret_cast<int32_t*>(ws + p.cs_off) : nullptr;
+  if (rs && err == hipSuccess) err = q8::launch_row_sums_i8(a, M, K, rs, st);
+  if (cs && err == hipSuccess) err = q8::launch_row_sums_i8(b, N, K, cs, st);
+  if (err == hipSuccess)
+    err = (M <= 16) ? q8::launch_gemv(a, b, M, N, K, e, out, st) : q8::launch_gemm(a, b, M, N, K, e, out, st);
+  if (err == hipSuccess && (p.cA != 0 || p.cB != 0))
+    err = q8::launch_zp_correct(out, M, N, rs, cs, p.cA, p.cB, K, st);
+  return launched(err, "q8_quantized_dot launch");
+}
+
 int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const int8_t* Wq,
                        const double* sW, int sW_mode, int64_t N, const float* bias, int act,
                        float* out, int8_t* xq, double* sx, void* stream) {
@@ -569,34 +649,59 @@ int q8_quantized_conv_workspace(int spatial_dims, const int64_t* x_shape, const 
   return Q8_OK;
 }
 
-int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const int64_t* x_shape,
-                      const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
-                      const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
-                      int32_t zp_x, int32_t zp_w, int out_kind, double s_out, void* workspace,
-                      size_t workspace_bytes, void* out, void* stream) {
+static int conv_impl(const char* who, const void* x, int x_dtype, const void* w, int w_dtype,
+                     int spatial_dims, const int64_t* x_shape, const int64_t* w_shape,
+                     const int64_t* strides, const int64_t* pad_lo, const int64_t* pad_hi,
+                     const int64_t* dilation, int64_t groups, int32_t zp_x, int32_t zp_w,
+                     int out_kind, double s_out, void* workspace, size_t workspace_bytes, void* out,
+                     void* stream) {
   q8::ConvGeom G;
-  int rc = conv_geom("q8_quantized_conv", spatial_dims, x_shape, w_shape, strides, pad_lo, pad_hi,
-                     dilation, groups, &G);
+  int rc = conv_geom(who, spatial_dims, x_shape, w_shape, strides, pad_lo, pad_hi, dilation, groups,
+                     &G);
   if (rc != Q8_OK) return rc;
-  Q8_REQUIRE(out_kind == Q8_F32 || out_kind == Q8_I32,
-             "q8_quantized_conv: out_kind must be Q8_F32 or Q8_I32");
+  Q8_REQUIRE(out_kind == Q8_F32 || out_kind == Q8_I32, "%s: out_kind must be Q8_F32 or Q8_I32", who);
+  Q8_REQUIRE((x_dtype == Q8_I8 || x_dtype == Q8_U8) && (w_dtype == Q8_I8 || w_dtype == Q8_U8),
+             "%s: operands must be Q8_I8 or Q8_U8 (got %d, %d)", who, x_dtype, w_dtype);
+  G.zpx = zp_x;
+  G.zpw = zp_w;
+  G.x_u8 = x_dtype == Q8_U8;
+  G.w_u8 = w_dtype == Q8_U8;
   const bool empty = G.N * G.O * G.Pn == 0;
-  Q8_REQUIRE(empty || (x && w && out), "q8_quantized_conv: NULL pointer");
-  const size_t need = q8::conv_workspace_bytes(G);
+  Q8_REQUIRE(empty || (x && w && out), "%s: NULL pointer", who);
+  const size_t need = q8::conv_direct(G) ? 0 : q8::conv_workspace_bytes(G);
   Q8_REQUIRE(empty || workspace_bytes >= need,
-             "q8_quantized_conv: workspace of %zu bytes is smaller than the %zu bytes required "
-             "(q8_quantized_conv_workspace)", workspace_bytes, need);
-  Q8_REQUIRE(empty || need == 0 || workspace, "q8_quantized_conv: workspace is NULL");
-  if (zp_x != 0 || zp_w != 0)
-    return fail(Q8_ERR_UNSUPPORTED, "q8_quantized_conv: non-zero zero points are not supported by this build");
+             "%s: workspace of %zu bytes is smaller than the %zu bytes required "
+             "(q8_quantized_conv_workspace)", who, workspace_bytes, need);
+  Q8_REQUIRE(empty || need == 0 || workspace, "%s: workspace is NULL", who);
   q8::GemmEpi e{};
   e.mode = 0;
   e.s_out = s_out;
   e.out_i32 = out_kind == Q8_I32;
   rc = ensure_current(nullptr);
   if (rc != Q8_OK) return rc;
-  return launched(q8::launch_conv(x, w, G, e, workspace, out, as_stream(stream)),
-                  "q8_quantized_conv launch");
+  return launched(q8::launch_conv(static_cast<const int8_t*>(x), static_cast<const int8_t*>(w), G,
+                                  e, workspace, out, as_stream(stream)),
+                  "quantized_conv launch");
+}
+
+int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const int64_t* x_shape,
+                      const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
+                      const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                      int32_t zp_x, int32_t zp_w, int out_kind, double s_out, void* workspace,
+                      size_t workspace_bytes, void* out, void* stream) {
+  return conv_impl("q8_quantized_conv", x, Q8_I8, w, Q8_I8, spatial_dims, x_shape, w_shape, strides,
+                   pad_lo, pad_hi, dilation, groups, zp_x, zp_w, out_kind, s_out, workspace,
+                   workspace_bytes, out, stream);
+}
+
+int q8_quantized_conv_ex(const void* x, int x_dtype, const void* w, int w_dtype, int spatial_dims,
+                         const int64_t* x_shape, const int64_t* w_shape, const int64_t* strides,
+                         const int64_t* pad_lo, const int64_t* pad_hi, const int64_t* dilation,
+                         int64_t groups, int32_t zp_x, int32_t zp_w, int out_kind, double s_out,
+                         void* workspace, size_t workspace_bytes, void* out, void* stream) {
+  return conv_impl("q8_quantized_conv_ex", x, x_dtype, w, w_dtype, spatial_dims, x_shape, w_shape,
+                   strides, pad_lo, pad_hi, dilation, groups, zp_x, zp_w, out_kind, s_out, workspace,
+                   workspace_bytes, out, stream);
 }
 
 int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K, float* h_out,

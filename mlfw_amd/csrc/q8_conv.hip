@@ -89,7 +89,9 @@ __global__ __launch_bounds__(256) void k_pad_rows(const int8_t* __restrict__ w, 
 }
 
 // Direct form: one thread per output element, taps in the reference's
-// order (ic, then kernel positions), int32 wrap-around sum.
+// order (ic, then kernel positions), int32 wrap-around sum of
+// (x - zpx) * (w - zpw) over the taps inside the image (a padded tap adds
+// 0), operands read as i8 or ui8.
 __global__ __launch_bounds__(256) void k_conv_direct(const int8_t* __restrict__ x,
                                                      const int8_t* __restrict__ w, ConvGeom G,
                                                      GemmEpi e, void* __restrict__ out) {
@@ -119,8 +121,11 @@ __global__ __launch_bounds__(256) void k_conv_direct(const int8_t* __restrict__ 
         for (int k2 = 0; k2 < G.K[2]; ++k2) {
           const int64_t s2 = (int64_t)o2 * G.st[2] + (int64_t)k2 * G.dl[2] - G.lo[2];
           if (s2 < 0 || s2 >= G.S[2]) continue;
-          acc += (uint32_t)((int)xc[(s0 * G.S[1] + s1) * G.S[2] + s2] *
-                            (int)wc[(k0 * G.K[1] + k1) * G.K[2] + k2]);
+          const int64_t xi = (s0 * G.S[1] + s1) * G.S[2] + s2;
+          const int64_t wi = (k0 * G.K[1] + k1) * G.K[2] + k2;
+          const int xv = G.x_u8 ? (int)reinterpret_cast<const uint8_t*>(xc)[xi] : (int)xc[xi];
+          const int wv = G.w_u8 ? (int)reinterpret_cast<const uint8_t*>(wc)[wi] : (int)wc[wi];
+          acc += (uint32_t)((xv - G.zpx) * (wv - G.zpw));
         }
       }
     }
@@ -130,6 +135,10 @@ __global__ __launch_bounds__(256) void k_conv_direct(const int8_t* __restrict__ 
 }
 
 bool conv_uses_gemm(const ConvGeom& G) { return G.Kc >= 64; }
+
+bool conv_direct(const ConvGeom& G) {
+  return !conv_uses_gemm(G) || G.zpx != 0 || G.zpw != 0 || G.x_u8 || G.w_u8;
+}
 
 size_t conv_workspace_bytes(const ConvGeom& G) {
   if (!conv_uses_gemm(G)) return 0;
@@ -142,7 +151,7 @@ size_t conv_workspace_bytes(const ConvGeom& G) {
 hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, const GemmEpi& e,
                        void* workspace, void* out, hipStream_t st) {
   if (G.N * G.O * G.Pn == 0) return hipSuccess;
-  if (!conv_uses_gemm(G)) {
+  if (conv_direct(G)) {
     const int64_t total = G.N * G.O * G.Pn;
     hipLaunchKernelGGL(k_conv_direct, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x,
                        w, G, e, out);

@@ -52,6 +52,15 @@ hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 // 4-bit per-group weights (q8_w4.hip).
 hipError_t launch_pack_w4(const float* W, int64_t N, int64_t K, int64_t group, uint8_t* wq4,
                           double* scales, hipStream_t st);
+// quantized_dot with zero points / ui8 operands: byte flip of a ui8
+// operand into its int8 form, int8 row sums, and the rank-1 correction of
+// the int32 GEMM result.
+hipError_t launch_flip_u8(const uint8_t* src, int8_t* dst, int64_t n, hipStream_t st);
+hipError_t launch_row_sums_i8(const int8_t* X, int64_t rows, int64_t K, int32_t* out,
+                              hipStream_t st);
+hipError_t launch_zp_correct(int32_t* acc, int64_t M, int64_t N, const int32_t* rsA,
+                             const int32_t* csB, int32_t cA, int32_t cB, int64_t K,
+                             hipStream_t st);
 // Dynamic qlinear for one-token decode in one kernel (per-token or
 // per-tensor quantize of fp32 x + dot4 GEMV + E-rowcol epilogue);
 // qlinear_fused_ok says whether the shape and alignment fit it.
@@ -75,7 +84,12 @@ struct ConvGeom {
   int64_t st[3], lo[3], dl[3];   // stride, leading padding, dilation
   int64_t Sn, Pn;                // prod(S), prod(P)
   int Kn, Kc, Kc16;              // prod(K), Cg * prod(K), Kc rounded up to 16
+  int zpx = 0, zpw = 0;          // input / kernel zero points
+  int x_u8 = 0, w_u8 = 0;        // operands read as ui8 (else i8)
 };
+// Zero points and ui8 operands run the direct kernel (exact, one thread per
+// output); plain i8 convs with Cg * prod(K) >= 64 run im2col + GEMM.
+bool conv_direct(const ConvGeom& G);
 bool conv_uses_gemm(const ConvGeom& G);
 size_t conv_workspace_bytes(const ConvGeom& G);
 hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, const GemmEpi& e,

@@ -73,6 +73,7 @@ function paramIndex(primFunc, buffer) {
   return names.indexOf(buffer.name);
 }
 
+const INT8_DTYPES = new Set(['i8', 'ui8']);
 const isImm = (n) => n && (n.type === 'FloatImmNode' || n.type === 'IntImmNode');
 const isExtern = (n, name) => n && n.type === 'CallExternNode' && n.externName === name;
 const isMath = (n, op) => n && n.type === 'MathOpNode' && n.op === op;
@@ -162,7 +163,7 @@ function detectConv(blocks, primFunc) {
   const acc = blocks.find((b) => b.name.startsWith('qconv_acc'));
   if (!init || !acc || acc.reads.length !== 2 || acc.writes.length !== 1) return null;
   const X = acc.reads[0].buffer, W = acc.reads[1].buffer, Y = acc.writes[0].buffer;
-  if ((X.dtype !== 'i8') || W.dtype !== 'i8' || Y.dtype !== 'i32') return null;
+  if (!INT8_DTYPES.has(X.dtype) || !INT8_DTYPES.has(W.dtype) || Y.dtype !== 'i32') return null;
   const r = X.shape.length, d = r - 2;
   if (d < 1 || d > 3 || W.shape.length !== r || Y.shape.length !== r) return null;
   if (![...X.shape, ...W.shape, ...Y.shape].every((v) => typeof v === 'number')) return null;
@@ -199,7 +200,7 @@ function detectConv(blocks, primFunc) {
   if (xIdx < 0 || wIdx < 0 || outIdx < 0) return null;
   return { op: 'quantized_conv', d, xShape: X.shape.slice(), wShape: W.shape.slice(),
            outShape: Y.shape.slice(), strides, padLo, padHi, dilation, groups, zpX, zpW,
-           xIdx, wIdx, outIdx, outputIndices: [outIdx] };
+           xDtype: X.dtype, wDtype: W.dtype, xIdx, wIdx, outIdx, outputIndices: [outIdx] };
 }
 
 // acc += ((a|0) [- zpA]) * ((b|0) [- zpB])  (rules/quantization.ts:33-39)
@@ -245,7 +246,8 @@ function detectInt8Kernel(primFunc) {
     const acc = blocks.find((b) => b.name.startsWith('qmatmul_acc'));
     if (!init || !acc || acc.reads.length !== 2 || acc.writes.length !== 1) return null;
     const A = acc.reads[0].buffer, B = acc.reads[1].buffer, C = acc.writes[0].buffer;
-    if (A.dtype !== 'i8' || B.dtype !== 'i8' || C.dtype !== 'i32') return null;
+    // the verifier's QUANTIZED_INT_DTYPES (ops/quantization.ts:141-146)
+    if (!INT8_DTYPES.has(A.dtype) || !INT8_DTYPES.has(B.dtype) || C.dtype !== 'i32') return null;
     if (A.shape.length !== 2 || B.shape.length !== 2 || C.shape.length !== 2) return null;
     const [M, K] = A.shape, N = C.shape[1];
     if (C.shape[0] !== M || ![M, N, K].every((d) => typeof d === 'number')) return null;
@@ -270,8 +272,8 @@ function detectInt8Kernel(primFunc) {
     const zpB = product ? zeroPointOf(product, B) : 0;
     const aIdx = paramIndex(primFunc, A), bIdx = paramIndex(primFunc, B), outIdx = paramIndex(primFunc, C);
     if (aIdx < 0 || bIdx < 0 || outIdx < 0) return null;
-    return { op: 'quantized_dot', M, N, K, rhsLayout, zpA, zpB, aIdx, bIdx, outIdx,
-             outputIndices: [outIdx] };
+    return { op: 'quantized_dot', M, N, K, rhsLayout, zpA, zpB, aDtype: A.dtype, bDtype: B.dtype,
+             aIdx, bIdx, outIdx, outputIndices: [outIdx] };
   }
   return null;
 }
@@ -337,33 +339,38 @@ function runDescriptor(d, args, dev) {
   }
   if (d.op === 'quantized_dot') {
     const a = args[d.aIdx], b = args[d.bIdx], out = args[d.outIdx];
-    need(a instanceof Int8Array && a.length === d.M * d.K, 'quantized_dot lhs');
-    need(b instanceof Int8Array && b.length === d.N * d.K, 'quantized_dot rhs');
+    const aT = (d.aDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
+    const bT = (d.bDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
+    need(a instanceof aT && a.length === d.M * d.K, 'quantized_dot lhs');
+    need(b instanceof bT && b.length === d.N * d.K, 'quantized_dot rhs');
     need(out instanceof Int32Array && out.length === d.M * d.N, 'quantized_dot output');
-    // non-zero zero points (asymmetric schemes) are refused by the C ABI
-    // with Q8_ERR_UNSUPPORTED, which the addon throws
+    const aD = aT === Uint8Array ? A.Q8_U8 : A.Q8_I8, bD = bT === Uint8Array ? A.Q8_U8 : A.Q8_I8;
     const da = dev.get('a', d.M * d.K), db = dev.get('b', d.N * d.K), dout = dev.get('out', 4 * d.M * d.N);
+    const wsBytes = A.quantizedDotWorkspace(d.M, d.N, d.K, aD, bD, d.zpA, d.zpB);
+    const dws = wsBytes > 0 ? dev.get('ws', wsBytes) : null;
     A.upload(da, a);
     A.upload(db, d.rhsLayout === 'KN' ? transposeI8(b, d.K, d.N) : b);
-    A.gemm(da, db, d.M, d.N, d.K, d.zpA, d.zpB, null, A.Q8_PER_TENSOR, null, A.Q8_PER_TENSOR,
-           A.Q8_EPI_PT, 0, null, A.Q8_ACT_NONE, A.Q8_I32, dout);
+    // zero points and ui8 operands: the exact correction inside the call
+    A.quantizedDot(da, aD, db, bD, d.M, d.N, d.K, d.zpA, d.zpB, dws, dout);
     A.download(out, dout);
     return out;
   }
   if (d.op === 'quantized_conv') {
     const x = args[d.xIdx], w = args[d.wIdx], out = args[d.outIdx];
     const nx = numel(d.xShape), nw = numel(d.wShape), ny = numel(d.outShape);
-    need(x instanceof Int8Array && x.length === nx, 'quantized_conv input');
-    need(w instanceof Int8Array && w.length === nw, 'quantized_conv kernel');
+    const xT = (d.xDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
+    const wT = (d.wDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
+    need(x instanceof xT && x.length === nx, 'quantized_conv input');
+    need(w instanceof wT && w.length === nw, 'quantized_conv kernel');
     need(out instanceof Int32Array && out.length === ny, 'quantized_conv output');
     const wsBytes = A.convWorkspace(d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups);
     const dx = dev.get('x', nx), dw = dev.get('w', nw), dout = dev.get('out', 4 * ny);
     const dws = wsBytes > 0 ? dev.get('ws', wsBytes) : null;
     A.upload(dx, x);
     A.upload(dw, w);
-    // non-zero zero points are refused by the C ABI (Q8_ERR_UNSUPPORTED)
-    A.quantizedConv(dx, dw, d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation,
-                    d.groups, d.zpX, d.zpW, A.Q8_I32, 0, dws, dout);
+    A.quantizedConvEx(dx, xT === Uint8Array ? A.Q8_U8 : A.Q8_I8, dw, wT === Uint8Array ? A.Q8_U8 : A.Q8_I8,
+                      d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups,
+                      d.zpX, d.zpW, A.Q8_I32, 0, dws, dout);
     A.download(out, dout);
     return out;
   }

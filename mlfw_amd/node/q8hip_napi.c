@@ -512,6 +512,61 @@ static napi_value js_quantized_conv(napi_env env, napi_callback_info info) {
 }
 
 /* siluMulQuantizeRows(g, u, M, K, h, q, scales) */
+/* quantizedConvEx(x, xDtype, w, wDtype, d, xShape, wShape, strides, padLo, padHi, dilation,
+ *                 groups, zpX, zpW, outKind, sOut, workspace, out) */
+static napi_value js_quantized_conv_ex(napi_env env, napi_callback_info info) {
+  napi_value argv[18];
+  void *x, *w, *ws, *out;
+  int64_t xd, wd, d, groups, zpx, zpw, ok;
+  double sOut;
+  ConvArgs c;
+  DevBuf* wsb = NULL;
+  if (!get_args(env, info, 18, argv) || !arg_buf(env, argv[0], 1, &x) || !arg_i64(env, argv[1], &xd) ||
+      !arg_buf(env, argv[2], 1, &w) || !arg_i64(env, argv[3], &wd) || !arg_i64(env, argv[4], &d) ||
+      !conv_args(env, argv + 5, d, &c) || !arg_i64(env, argv[11], &groups) ||
+      !arg_i64(env, argv[12], &zpx) || !arg_i64(env, argv[13], &zpw) || !arg_i64(env, argv[14], &ok) ||
+      !arg_f64(env, argv[15], &sOut) || !arg_buf(env, argv[16], 1, &ws) || !arg_buf(env, argv[17], 1, &out))
+    return NULL;
+  size_t ws_bytes = 0;
+  if (ws != NULL && arg_devbuf(env, argv[16], &wsb)) ws_bytes = wsb->bytes;
+  Q8_CHECK(env, q8_quantized_conv_ex(x, (int)xd, w, (int)wd, (int)d, c.xs, c.ws, c.st, c.lo, c.hi, c.dl,
+                                     groups, (int32_t)zpx, (int32_t)zpw, (int)ok, sOut, ws, ws_bytes, out,
+                                     NULL));
+  return undefined(env);
+}
+
+/* quantizedDotWorkspace(M, N, K, aDtype, bDtype, zpA, zpB) -> bytes */
+static napi_value js_quantized_dot_workspace(napi_env env, napi_callback_info info) {
+  napi_value argv[7], r;
+  int64_t M, N, K, ad, bd, za, zb;
+  size_t bytes = 0;
+  if (!get_args(env, info, 7, argv) || !arg_i64(env, argv[0], &M) || !arg_i64(env, argv[1], &N) ||
+      !arg_i64(env, argv[2], &K) || !arg_i64(env, argv[3], &ad) || !arg_i64(env, argv[4], &bd) ||
+      !arg_i64(env, argv[5], &za) || !arg_i64(env, argv[6], &zb))
+    return NULL;
+  Q8_CHECK(env, q8_quantized_dot_workspace(M, N, K, (int)ad, (int)bd, (int32_t)za, (int32_t)zb, &bytes));
+  napi_create_double(env, (double)bytes, &r);
+  return r;
+}
+
+/* quantizedDot(A, aDtype, B, bDtype, M, N, K, zpA, zpB, workspace, out) */
+static napi_value js_quantized_dot(napi_env env, napi_callback_info info) {
+  napi_value argv[11];
+  void *A, *B, *ws, *out;
+  int64_t ad, bd, M, N, K, za, zb;
+  DevBuf* wsb = NULL;
+  if (!get_args(env, info, 11, argv) || !arg_buf(env, argv[0], 1, &A) || !arg_i64(env, argv[1], &ad) ||
+      !arg_buf(env, argv[2], 1, &B) || !arg_i64(env, argv[3], &bd) || !arg_i64(env, argv[4], &M) ||
+      !arg_i64(env, argv[5], &N) || !arg_i64(env, argv[6], &K) || !arg_i64(env, argv[7], &za) ||
+      !arg_i64(env, argv[8], &zb) || !arg_buf(env, argv[9], 1, &ws) || !arg_buf(env, argv[10], 1, &out))
+    return NULL;
+  size_t ws_bytes = 0;
+  if (ws != NULL && arg_devbuf(env, argv[9], &wsb)) ws_bytes = wsb->bytes;
+  Q8_CHECK(env, q8_quantized_dot(A, (int)ad, B, (int)bd, M, N, K, (int32_t)za, (int32_t)zb, ws, ws_bytes,
+                                 (int32_t*)out, NULL));
+  return undefined(env);
+}
+
 static napi_value js_silu_mul_quantize_rows(napi_env env, napi_callback_info info) {
   napi_value argv[7];
   void *g, *u, *h, *q, *sc;
@@ -556,6 +611,9 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"siluMulQuantizeRows", js_silu_mul_quantize_rows},
       {"convWorkspace", js_conv_workspace},
       {"quantizedConv", js_quantized_conv},
+      {"quantizedConvEx", js_quantized_conv_ex},
+      {"quantizedDotWorkspace", js_quantized_dot_workspace},
+      {"quantizedDot", js_quantized_dot},
   };
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); ++i) {
     napi_value f;

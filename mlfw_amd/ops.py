@@ -263,6 +263,29 @@ def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor
     return out
 
 
+def quantized_dot(A: torch.Tensor, B: torch.Tensor, zpA: int = 0, zpB: int = 0,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference's quantized_dot: int32 [M,N] = sum_k (A[m,k] - zpA) *
+    (B[n,k] - zpB), exact, stored ToInt32.  A [M,K] and B [N,K] are int8
+    (read as i8) or uint8 (read as ui8) tensors."""
+    codes = {torch.int8: L.Q8_I8, torch.uint8: L.Q8_U8}
+    for t, name in ((A, "A"), (B, "B")):
+        if t.dtype not in codes or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError(f"quantized_dot: {name} must be a contiguous 2-D int8 or uint8 tensor")
+    M, K = A.shape
+    N = B.shape[0]
+    if B.shape[1] != K:
+        raise ValueError("quantized_dot: A [M,K] and B [N,K] must share K")
+    ws_bytes = C.c_size_t(0)
+    _call("q8_quantized_dot_workspace", M, N, K, codes[A.dtype], codes[B.dtype], int(zpA), int(zpB),
+           C.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=A.device)
+    out = torch.empty((M, N), dtype=torch.int32, device=A.device) if out is None else out
+    _call("q8_quantized_dot", _ptr(A), codes[A.dtype], _ptr(B), codes[B.dtype], M, N, K, int(zpA),
+           int(zpB), _ptr(ws), ws_bytes.value, _ptr(out), _stream())
+    return out
+
+
 def qlinear_dynamic(x: torch.Tensor, Wq: torch.Tensor, sW: torch.Tensor,
                     bias: torch.Tensor | None = None, act: str | None = None,
                     per_tensor: bool = False, out: torch.Tensor | None = None,
@@ -387,15 +410,20 @@ def conv_out_shape(x_shape, w_shape, strides, padding, dilation=None):
 
 def quantized_conv(x: torch.Tensor, w: torch.Tensor, strides, padding, dilation=None,
                    groups: int = 1, s_out: float | None = None, out: torch.Tensor | None = None,
-                   workspace: torch.Tensor | None = None) -> torch.Tensor:
+                   workspace: torch.Tensor | None = None, zpx: int = 0,
+                   zpw: int = 0) -> torch.Tensor:
     """quantized_conv (src/compiler/ir/graph/ops/quantization.ts:156-190):
-    int8 x [N, C, S..] (NCHW and its 1-D / 3-D forms) and w [O, C/groups, K..]
-    (OIHW), padding as [[lo, hi], ...] per spatial dim.  s_out None: the
+    x [N, C, S..] (NCHW and its 1-D / 3-D forms) and w [O, C/groups, K..]
+    (OIHW), each int8 (read as i8) or uint8 (read as ui8), padding as
+    [[lo, hi], ...] per spatial dim, zero points zpx / zpw.  s_out None: the
     int32 accumulator; otherwise the fused per-tensor dequantize
     fround(acc * s_out) as fp32 (the `dequantize` QuantizationPass appends,
     output_scale = input_scale * kernel_scale)."""
-    _need(x, torch.int8, "quantized_conv x")
-    _need(w, torch.int8, "quantized_conv w")
+    codes = {torch.int8: L.Q8_I8, torch.uint8: L.Q8_U8}
+    for t, name in ((x, "x"), (w, "w")):
+        if t.dtype not in codes:
+            raise ValueError(f"quantized_conv: {name} must be int8 or uint8")
+        _need(t, t.dtype, f"quantized_conv {name}")
     d = len(strides)
     if x.dim() != 2 + d or w.dim() != 2 + d or len(padding) != d:
         raise ValueError(f"quantized_conv: {d} spatial dims need {2 + d}-D x and w and {d} padding pairs")
@@ -415,7 +443,8 @@ def quantized_conv(x: torch.Tensor, w: torch.Tensor, strides, padding, dilation=
             raise ValueError(f"quantized_conv: out must have shape {shape}")
     if need.value and (workspace is None or workspace.numel() < need.value):
         workspace = torch.empty(need.value, dtype=torch.int8, device=x.device)
-    _call("q8_quantized_conv", _ptr(x), _ptr(w), d, xs, ws, st, lo, hi, dl, groups, 0, 0,
+    _call("q8_quantized_conv_ex", _ptr(x), codes[x.dtype], _ptr(w), codes[w.dtype], d, xs, ws, st, lo,
+          hi, dl, groups, int(zpx), int(zpw),
           L.Q8_I32 if s_out is None else L.Q8_F32, 0.0 if s_out is None else float(s_out),
           _ptr(workspace if need.value else None), need.value, _ptr(out), _stream(),
           keep=(xs, ws, st, lo, hi, dl, workspace))

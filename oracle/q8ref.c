@@ -302,18 +302,30 @@ void q8r_dequantize_rows_i8(const int8_t* q, int64_t M, int64_t K, const double*
 /* The JS kernel keeps `_acc` as a double; every partial sum is an integer
  * far below 2^53, so the double sum is exact, and the Int32Array store
  * wraps it modulo 2^32.  An int64 sum followed by the same wrap is equal. */
-void q8r_quantized_dot(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
-                       int b_layout, int32_t zpA, int32_t zpB, int32_t* acc) {
+/* An operand element as the lowering's CastNode(load, dtype, 'i32') reads
+ * it: an Int8Array (i8) or Uint8Array (ui8) element. */
+static int64_t q8r_elem(const int8_t* p, int64_t i, int u8) {
+  return u8 ? (int64_t)((const uint8_t*)p)[i] : (int64_t)p[i];
+}
+
+void q8r_quantized_dot_ex(const int8_t* A, int a_u8, const int8_t* B, int b_u8, int64_t M,
+                          int64_t N, int64_t K, int b_layout, int32_t zpA, int32_t zpB,
+                          int32_t* acc) {
   for (int64_t m = 0; m < M; m++)
     for (int64_t n = 0; n < N; n++) {
       int64_t s = 0;
       for (int64_t k = 0; k < K; k++) {
-        int64_t a = (int64_t)A[m * K + k] - zpA;
-        int64_t b = (int64_t)(b_layout == 0 ? B[k * N + n] : B[n * K + k]) - zpB;
+        int64_t a = q8r_elem(A, m * K + k, a_u8) - zpA;
+        int64_t b = q8r_elem(B, b_layout == 0 ? k * N + n : n * K + k, b_u8) - zpB;
         s += a * b;
       }
       acc[m * N + n] = (int32_t)(uint32_t)(uint64_t)s;
     }
+}
+
+void q8r_quantized_dot(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                       int b_layout, int32_t zpA, int32_t zpB, int32_t* acc) {
+  q8r_quantized_dot_ex(A, 0, B, 0, M, N, K, b_layout, zpA, zpB, acc);
 }
 
 /* quantized_conv: the loop nest buildConvNest emits
@@ -322,10 +334,10 @@ void q8r_quantized_dot(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
  * (x - zpx) * (w - zpw) (rules/quantization.ts:44-62), 0 for a tap in the
  * padding.  The JS accumulation is exact (|sum| < 2^53), the store is
  * ToInt32. */
-void q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* x_shape,
-                        const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
-                        const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
-                        int32_t zpx, int32_t zpw, int32_t* out) {
+void q8r_quantized_conv_ex(const int8_t* x, int x_u8, const int8_t* w, int w_u8, int d,
+                           const int64_t* x_shape, const int64_t* w_shape, const int64_t* strides,
+                           const int64_t* pad_lo, const int64_t* pad_hi, const int64_t* dilation,
+                           int64_t groups, int32_t zpx, int32_t zpw, int32_t* out) {
   const int64_t N = x_shape[0], C = x_shape[1], O = w_shape[0], Cg = w_shape[1];
   const int64_t Og = O / groups;
   int64_t S[3] = {1, 1, 1}, K[3] = {1, 1, 1}, P[3] = {1, 1, 1};
@@ -358,8 +370,8 @@ void q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* 
                   for (int64_t k2 = 0; k2 < K[2]; k2++) {
                     const int64_t s2 = p2 * st[2] + k2 * dl[2] - lo[2];
                     if (s2 < 0 || s2 >= S[2]) continue;
-                    const int64_t a = (int64_t)xc[(s0 * S[1] + s1) * S[2] + s2] - zpx;
-                    const int64_t b = (int64_t)wc[(k0 * K[1] + k1) * K[2] + k2] - zpw;
+                    const int64_t a = q8r_elem(xc, (s0 * S[1] + s1) * S[2] + s2, x_u8) - zpx;
+                    const int64_t b = q8r_elem(wc, (k0 * K[1] + k1) * K[2] + k2, w_u8) - zpw;
                     acc += a * b;
                   }
                 }
@@ -370,6 +382,14 @@ void q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* 
           }
     }
   (void)Pn;
+}
+
+void q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64_t* x_shape,
+                        const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
+                        const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                        int32_t zpx, int32_t zpw, int32_t* out) {
+  q8r_quantized_conv_ex(x, 0, w, 0, d, x_shape, w_shape, strides, pad_lo, pad_hi, dilation, groups,
+                        zpx, zpw, out);
 }
 
 /* W4A8 per-group GEMV as defined in q8ref.h: exact per-group integer

@@ -106,6 +106,11 @@ void     q8r_dequantize_rows_i8(const int8_t* q, int64_t M, int64_t K, const dou
  * b_layout 1: B is [N,K] (rhs_contracting=[1], the nn.Linear weight). */
 void     q8r_quantized_dot(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                            int b_layout, int32_t zpA, int32_t zpB, int32_t* acc);
+/* The same with either operand read as ui8 (a Uint8Array: 0..255), the
+ * verifier's other operand type (ops/quantization.ts:141-146). */
+void     q8r_quantized_dot_ex(const int8_t* A, int a_u8, const int8_t* B, int b_u8, int64_t M,
+                              int64_t N, int64_t K, int b_layout, int32_t zpA, int32_t zpB,
+                              int32_t* acc);
 
 /* ---- quantized_conv, src/compiler/ir/graph/ops/quantization.ts:156-190,
  * lowering rules/quantization.ts:44-62 through buildConvNest
@@ -124,6 +129,13 @@ void     q8r_quantized_conv(const int8_t* x, const int8_t* w, int d, const int64
                             const int64_t* w_shape, const int64_t* strides, const int64_t* pad_lo,
                             const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
                             int32_t zpx, int32_t zpw, int32_t* out);
+/* The same with either operand read as ui8 (buildConvNest's CastNode of a
+ * Uint8Array load). */
+void     q8r_quantized_conv_ex(const int8_t* x, int x_u8, const int8_t* w, int w_u8, int d,
+                               const int64_t* x_shape, const int64_t* w_shape,
+                               const int64_t* strides, const int64_t* pad_lo,
+                               const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
+                               int32_t zpx, int32_t zpw, int32_t* out);
 
 /* ---- W4A8 per-group GEMV (no reference op; composed here) ----
  * Weights: 4-bit codes of fromConstantArrayPerGroup + quantizeArrayPerGroup

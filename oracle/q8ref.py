@@ -87,8 +87,12 @@ def lib():
         "q8r_dequantize_i32": (None, [_i32p, _i64, _dbl, _dbl, _f32p]),
         "q8r_dequantize_rows_i8": (None, [_i8p, _i64, _i64, _f64p, _f32p]),
         "q8r_quantized_dot": (None, [_i8p, _i8p, _i64, _i64, _i64, _int, C.c_int32, C.c_int32, _i32p]),
+        "q8r_quantized_dot_ex": (None, [_i8p, _int, _i8p, _int, _i64, _i64, _i64, _int, C.c_int32,
+                                        C.c_int32, _i32p]),
         "q8r_quantized_conv": (None, [_i8p, _i8p, _int, _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,
                                       _i64, C.c_int32, C.c_int32, _i32p]),
+        "q8r_quantized_conv_ex": (None, [_i8p, _int, _i8p, _int, _int, _i64p, _i64p, _i64p, _i64p, _i64p,
+                                         _i64p, _i64, C.c_int32, C.c_int32, _i32p]),
         "q8r_gemv_w4": (None, [_i8p, _f64p, _i64, _u8p, _f64p, _i64, _i64, _i64, _i64, C.c_void_p,
                                _int, _f32p]),
         "q8r_epilogue": (None, [_i32p, _i64, _i64, _int, _f64p, _i64, _f64p, _i64, _dbl,
@@ -291,13 +295,17 @@ def dequantize_rows(q, scales) -> np.ndarray:
 
 # ---------------------------------------------------------------- M1 + epilogue
 def quantized_dot(A, B, b_layout=1, zpA=0, zpB=0) -> np.ndarray:
-    """quantized_dot (rules/quantization.ts:57-76).  b_layout 1: B is [N,K]."""
-    A = _c(A, np.int8)
-    B = _c(B, np.int8)
+    """quantized_dot (rules/quantization.ts:57-76).  b_layout 1: B is [N,K].
+    A uint8 operand is read as ui8 (0..255), an int8 one as i8."""
+    a_u8 = np.asarray(A).dtype == np.uint8
+    b_u8 = np.asarray(B).dtype == np.uint8
+    A = _c(np.asarray(A).view(np.int8) if a_u8 else A, np.int8)
+    B = _c(np.asarray(B).view(np.int8) if b_u8 else B, np.int8)
     M, K = A.shape
     N = B.shape[1] if b_layout == 0 else B.shape[0]
     acc = np.empty((M, N), np.int32)
-    lib().q8r_quantized_dot(A.reshape(-1), B.reshape(-1), M, N, K, b_layout, zpA, zpB, acc.reshape(-1))
+    lib().q8r_quantized_dot_ex(A.reshape(-1), int(a_u8), B.reshape(-1), int(b_u8), M, N, K, b_layout,
+                               zpA, zpB, acc.reshape(-1))
     return acc
 
 
@@ -313,17 +321,21 @@ def conv_out_shape(x_shape, w_shape, strides, padding, dilation):
 
 def quantized_conv(x, w, strides, padding, dilation=None, groups=1, zpx=0, zpw=0) -> np.ndarray:
     """quantized_conv with NC(spatial) input / OI(spatial) kernel, int32 out
-    (ops/quantization.ts:156-190, buildConvNest lowering_registry.ts:335-449)."""
-    x = _c(x, np.int8)
-    w = _c(w, np.int8)
+    (ops/quantization.ts:156-190, buildConvNest lowering_registry.ts:335-449).
+    A uint8 operand is read as ui8 (0..255), an int8 one as i8."""
+    x_u8 = np.asarray(x).dtype == np.uint8
+    w_u8 = np.asarray(w).dtype == np.uint8
+    x = _c(np.asarray(x).view(np.int8) if x_u8 else x, np.int8)
+    w = _c(np.asarray(w).view(np.int8) if w_u8 else w, np.int8)
     d = len(strides)
     dilation = list(dilation) if dilation is not None else [1] * d
     shp = conv_out_shape(x.shape, w.shape, strides, padding, dilation)
     out = np.empty(shp, np.int32)
     a64 = lambda v: _c(list(v), np.int64)  # noqa: E731
-    lib().q8r_quantized_conv(x.reshape(-1), w.reshape(-1), d, a64(x.shape), a64(w.shape), a64(strides),
-                             a64([p[0] for p in padding]), a64([p[1] for p in padding]),
-                             a64(dilation), groups, zpx, zpw, out.reshape(-1))
+    lib().q8r_quantized_conv_ex(x.reshape(-1), int(x_u8), w.reshape(-1), int(w_u8), d, a64(x.shape),
+                                a64(w.shape), a64(strides), a64([p[0] for p in padding]),
+                                a64([p[1] for p in padding]), a64(dilation), groups, zpx, zpw,
+                                out.reshape(-1))
     return out
 
 

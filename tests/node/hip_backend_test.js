@@ -47,7 +47,7 @@ const buf = (name, shape, dtype) => ({ name, shape, dtype });
 const load = (b, idx) => ({ type: 'BufferLoadNode', buffer: b, indices: idx });
 const ext = (externName, args) => ({ type: 'CallExternNode', externName, args });
 const math = (op, a, b) => ({ type: 'MathOpNode', op, a, b });
-const cast = (expr, toDtype) => ({ type: 'CastNode', expr, toDtype });
+const cast = (expr, toDtype, fromDtype = 'i8') => ({ type: 'CastNode', expr, fromDtype, toDtype });
 function primFunc(name, params, blocks) {
   const attrs = {};
   const bufferMap = new Map(params.map((b, i) => [`v${i}`, b]));
@@ -72,10 +72,10 @@ function dequantizePF(scale, zp, src) {
                   body: { type: 'BufferStoreNode', buffer: y, indices: [V('i'), V('j')], value: math('*', e, F(scale)) } };
   return primFunc('deq', [q, y], [block]);
 }
-function qdotPF(M, N, K, layout, zpA, zpB) {
-  const a = buf('a', [M, K], 'i8'), b = buf('b', layout === 'KN' ? [K, N] : [N, K], 'i8'), c = buf('c', [M, N], 'i32');
+function qdotPF(M, N, K, layout, zpA, zpB, aD = 'i8', bD = 'i8') {
+  const a = buf('a', [M, K], aD), b = buf('b', layout === 'KN' ? [K, N] : [N, K], bD), c = buf('c', [M, N], 'i32');
   const m = V('m'), n = V('n'), k = V('k');
-  let la = cast(load(a, [m, k]), 'i32'), lb = cast(load(b, layout === 'KN' ? [k, n] : [n, k]), 'i32');
+  let la = cast(load(a, [m, k]), 'i32', aD), lb = cast(load(b, layout === 'KN' ? [k, n] : [n, k]), 'i32', bD);
   if (zpA) la = math('-', la, I(zpA));
   if (zpB) lb = math('-', lb, I(zpB));
   const init = { type: 'BlockNode', name: 'qmatmul_init', reads: [], writes: [{ buffer: c }],
@@ -205,6 +205,9 @@ function cpuTests() {
     }
     const z = hip.detectInt8Kernel(qdotPF(8, 8, 16, 'NK', 3, -2));
     assert.deepStrictEqual([z.zpA, z.zpB], [3, -2]);
+    // ui8 operands (an affine activation scheme: zero point 128)
+    const u = hip.detectInt8Kernel(qdotPF(8, 8, 16, 'KN', 128, 0, 'ui8', 'i8'));
+    assert.deepStrictEqual([u.zpA, u.zpB, u.aDtype, u.bDtype, u.rhsLayout], [128, 0, 'ui8', 'i8', 'KN']);
   });
 
   test('annotate tags only the int8 PrimFuncs', () => {
@@ -235,7 +238,11 @@ function cpuTests() {
     assert.throws(() => a.gemm(null, null, 4, 4, 16, 0, 0, null, 0, null, 0, 9, 0, null, 0, a.Q8_F32, null),
                   (e) => e.code === 'Q8_ERR_1' && /bad epi/.test(e.message));
     assert.throws(() => a.upload({}, new Float32Array(1)), TypeError);
-    for (const f of ['gemmRequant', 'packWeightInt4', 'gemvW4', 'qlinearDynamic']) assert.strictEqual(typeof a[f], 'function', f);
+    for (const f of ['gemmRequant', 'packWeightInt4', 'gemvW4', 'qlinearDynamic', 'quantizedDot',
+                     'quantizedDotWorkspace', 'quantizedConvEx']) assert.strictEqual(typeof a[f], 'function', f);
+    assert.strictEqual(a.quantizedDotWorkspace(4, 5, 16, a.Q8_U8, a.Q8_I8, 128, 0), 256);
+    assert.throws(() => a.quantizedDot(null, 7, null, a.Q8_I8, 4, 5, 16, 0, 0, null, null),
+                  (e) => e.code === 'Q8_ERR_1');
     assert.throws(() => a.qlinearDynamic(null, 1, 16, 9, null, null, 0, 4, null, 0, null, null, null),
                   (e) => e.code === 'Q8_ERR_1' && /x_mode/.test(e.message));
     assert.throws(() => a.gemvW4(null, null, a.Q8_PER_TOKEN, null, null, 1, 4, 96, 64, null, 0, null),
@@ -299,6 +306,16 @@ function gpuTests(dir) {
       be.runSync(be.instantiate(kern), [Xq, B, acc], null);
       writeArr(dir, `out_qdot_${layout}.bin`, acc);
     }
+  });
+
+  test('runtime backend: quantized_dot with a ui8 operand and zero points on the GPU', () => {
+    const Au = readArr(dir, 'qdot_u8_a.bin', Uint8Array);
+    const kern = cg.compile({}, hip.hipTarget(), { op: 'quantized_dot', M, N, K, rhsLayout: 'NK', zpA: 128, zpB: 3,
+                                                   aDtype: 'ui8', bDtype: 'i8', aIdx: 0, bIdx: 1, outIdx: 2,
+                                                   outputIndices: [2] });
+    const acc = new Int32Array(M * N);
+    be.runSync(be.instantiate(kern), [Au, Wq, acc], null);
+    writeArr(dir, 'out_qdot_u8.bin', acc);
   });
 
   test('runtime backend: dequantize of int32 accumulators (per-tensor epilogue E-pt)', () => {

@@ -94,10 +94,33 @@ def test_validation_happens_before_any_launch(lib):
 
 
 def test_nonzero_zero_points_are_unsupported_not_wrong(lib):
+    """q8_gemm (the fused-epilogue GEMM) takes no zero points; the
+    reference's quantized_dot with zero points is q8_quantized_dot."""
     fake = C.c_void_p(0x1000)
     rc = lib.load().q8_gemm(fake, fake, 4, 4, 16, 3, 0, None, 0, None, 0, 0, 0.0, None, 0,
                             lib.Q8_I32, fake, None)
     assert rc == lib.Q8_ERR_UNSUPPORTED
+
+
+def test_quantized_dot_workspace_and_validation(lib):
+    """Validation fails before anything is launched."""
+    L = lib.load()
+    need = C.c_size_t(123)
+    # i8 operands without zero points need no workspace
+    assert L.q8_quantized_dot_workspace(4, 5, 16, lib.Q8_I8, lib.Q8_I8, 0, 0, C.byref(need)) == lib.Q8_OK
+    assert need.value == 0
+    # ui8 A: an int8 copy of A (256-aligned) and, for the 128 it shifts by,
+    # the row sums of A
+    assert L.q8_quantized_dot_workspace(4, 5, 16, lib.Q8_U8, lib.Q8_I8, 0, 0, C.byref(need)) == lib.Q8_OK
+    assert need.value == 256 + 256
+    # ui8 A with zero point 128: no shift left, only the copy
+    assert L.q8_quantized_dot_workspace(4, 5, 16, lib.Q8_U8, lib.Q8_I8, 128, 0, C.byref(need)) == lib.Q8_OK
+    assert need.value == 256
+    fake = C.c_void_p(0x1000)
+    expect_invalid(lib, "q8_quantized_dot_workspace", 4, 5, 16, 7, lib.Q8_I8, 0, 0, C.byref(need))
+    expect_invalid(lib, "q8_quantized_dot", fake, 7, fake, lib.Q8_I8, 4, 5, 16, 0, 0, None, 0, fake, None)
+    expect_invalid(lib, "q8_quantized_dot", fake, lib.Q8_U8, fake, lib.Q8_I8, 4, 5, 16, 0, 0, fake, 16,
+                   fake, None, match="workspace")
 
 
 def test_python_ops_refuse_cpu_tensors():
@@ -145,8 +168,8 @@ def test_conv_workspace_query_and_validation(lib):
                    fake, 16, fake, None, match="workspace")                          # workspace too small
     expect_invalid(lib, "q8_quantized_conv", fake, fake, 4, *args, 1, 0, 0, lib.Q8_I32, 0.0,
                    fake, 1 << 20, fake, None)                                        # rank 4
-    rc = L.q8_quantized_conv(fake, fake, 2, *args, 1, 2, 0, lib.Q8_I32, 0.0, fake, 1 << 20, fake, None)
-    assert rc == lib.Q8_ERR_UNSUPPORTED
+    expect_invalid(lib, "q8_quantized_conv_ex", fake, 9, fake, lib.Q8_I8, 2, *args, 1, 2, 0, lib.Q8_I32,
+                   0.0, fake, 1 << 20, fake, None)                                   # bad operand type
 
 
 def test_requant_validation(lib):

@@ -5,9 +5,9 @@ The cases cover both device paths (direct kernel for contractions shorter
 than 64, im2col + MFMA GEMM otherwise, with and without a contraction that
 is a multiple of 16), the GEMV and the GEMM kernels behind the latter
 (<= 16 and > 16 output channels per group), groups / depthwise, strides,
-asymmetric padding, dilation, batch > 1 and spatial ranks 1 to 3; then the
-whole pipeline QuantizationPass builds for a conv (quantize input, quantize
-kernel, quantized_conv, dequantize).
+asymmetric padding, dilation, batch > 1 and spatial ranks 1 to 3; zero
+points and ui8 operands; then the whole pipeline QuantizationPass builds
+for a conv (quantize input, quantize kernel, quantized_conv, dequantize).
 """
 import numpy as np
 import pytest
@@ -87,6 +87,24 @@ def test_quantized_conv_dequant_epilogue(ops, oracle, case):
     acc = oracle.quantized_conv(x, w, st, pd, dl, g)
     want = oracle.dequantize(acc.reshape(-1), s_out).reshape(acc.shape)
     same_bits(host(got), want)
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[7]])
+@pytest.mark.parametrize("x_u8,w_u8", [(False, False), (True, False), (True, True)])
+def test_quantized_conv_zero_points_and_ui8(ops, oracle, case, x_u8, w_u8):
+    """input_zero_point / kernel_zero_point and ui8 operands (the direct
+    kernel), int32 bit for bit; a padded tap adds 0."""
+    xs, ws, st, pd, dl, g = case
+    rng = np.random.default_rng(len(xs) * 13 + g + 2 * x_u8 + w_u8)
+    x = rng.integers(0, 256, xs).astype(np.uint8)
+    w = rng.integers(0, 256, ws).astype(np.uint8)
+    x = x if x_u8 else x.view(np.int8)
+    w = w if w_u8 else w.view(np.int8)
+    for zpx, zpw in ((0, 0), (128, 0), (3, -2), (128, 128)):
+        print(f"conv zp {xs} {ws} x_u8={x_u8} w_u8={w_u8} zp=({zpx},{zpw})", flush=True)
+        want = oracle.quantized_conv(x, w, st, pd, dl, g, zpx, zpw)
+        got = ops.quantized_conv(dev(x), dev(w), st, pd, dl, g, zpx=zpx, zpw=zpw)
+        same_bits(host(got), want)
 
 
 def test_conv_pipeline_of_the_quantization_pass(ops, oracle):

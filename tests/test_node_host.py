@@ -74,7 +74,9 @@ def test_node_host_gpu_c1(tmp_path, oracle):
     from mlfw_amd.checkpoint import pack_int4
     sw4 = oracle.scales_per_group(W.reshape(-1), w4_group, num_bits=4)
     wq4 = pack_int4(oracle.weight_quantize_per_group(W.reshape(-1), w4_group, sw4, lo=-8, hi=7).reshape(W.shape))
-    for name, arr in (("sx_tok", s_tok), ("xq_tok", q_tok), ("w4_q", wq4), ("w4_s", sw4)):
+    qdot_u8_a = np.random.default_rng(12).integers(0, 256, (M, K)).astype(np.uint8)
+    for name, arr in (("sx_tok", s_tok), ("xq_tok", q_tok), ("w4_q", wq4), ("w4_s", sw4),
+                      ("qdot_u8_a", qdot_u8_a)):
         np.ascontiguousarray(arr).tofile(tmp_path / f"{name}.bin")
     (tmp_path / "meta.json").write_text(json.dumps({"M": M, "N": N, "K": K, "sX": sX, "sOut": s_out,
                                                     "sNext": s_next, "w4Group": w4_group, "w4M": w4_m}))
@@ -94,6 +96,8 @@ def test_node_host_gpu_c1(tmp_path, oracle):
     acc = oracle.quantized_dot(Xq, Wq, b_layout=1)
     same_bits(out("out_qdot_NK", np.int32, (M, N)), acc, "quantized_dot [N,K]")
     same_bits(out("out_qdot_KN", np.int32, (M, N)), acc, "quantized_dot [K,N]")
+    same_bits(out("out_qdot_u8", np.int32, (M, N)), oracle.quantized_dot(qdot_u8_a, Wq, 1, 128, 3),
+              "quantized_dot ui8 x i8 with zero points")
     same_bits(out("out_dequant_i32", np.float32, (M, N)), oracle.dequantize(acc, s_out), "E-pt")
     same_bits(out("out_c1", np.float32, (M, N)), y_ref, "C1 fused qlinear")
     same_bits(out("out_qpt_q", np.int8, (M, K)), q_tok, "eager quantize_per_token codes")

@@ -211,6 +211,31 @@ def test_quantized_dot_brute_force(oracle):
         same_bits(oracle.quantized_dot(A, B, 1, zpA, zpB), want_zp)
 
 
+def test_quantized_dot_ui8_operands_and_zero_points(oracle):
+    """ui8 operands are read as 0..255 (CastNode of a Uint8Array load,
+    rules/quantization.ts:33-36; the verifier admits i8 and ui8,
+    ops/quantization.ts:141-146); checked against an int64 brute force.  A
+    mistake that reads ui8 bytes as signed, or drops a zero point, changes
+    the result for bytes >= 128."""
+    rng = np.random.default_rng(3)
+    for M, N, K in [(1, 1, 1), (4, 6, 33), (7, 3, 128)]:
+        for a_u8 in (False, True):
+            for b_u8 in (False, True):
+                A = rng.integers(0, 256, (M, K)).astype(np.uint8)
+                B = rng.integers(0, 256, (N, K)).astype(np.uint8)
+                A_ = A if a_u8 else A.view(np.int8)
+                B_ = B if b_u8 else B.view(np.int8)
+                for zpA, zpB in ((0, 0), (128, 0), (0, -7), (131, 255), (-128, 127)):
+                    want = ((A_.astype(np.int64) - zpA) @ (B_.astype(np.int64) - zpB).T).astype(np.int32)
+                    same_bits(oracle.quantized_dot(A_, B_, 1, zpA, zpB), want)
+                    same_bits(oracle.quantized_dot(A_, np.ascontiguousarray(B_.T), 0, zpA, zpB), want)
+    # the signed and unsigned readings of the same bytes differ
+    A = np.full((1, 4), 200, np.uint8)
+    B = np.ones((1, 4), np.int8)
+    assert oracle.quantized_dot(A, B)[0, 0] == 800
+    assert oracle.quantized_dot(A.view(np.int8), B)[0, 0] == -224
+
+
 def test_quantized_dot_int32_wrap(oracle):
     """The JS double accumulator is exact; the Int32Array store wraps mod 2^32."""
     K = 1 << 17
@@ -245,6 +270,24 @@ def _conv_windows(x, w, strides, padding, dilation, groups, zpx=0, zpw=0):
             ws = wz[(slice(g * Og, (g + 1) * Og), slice(None)) + tuple(kk)]
             out[:, g * Og:(g + 1) * Og] += np.einsum("nc...,oc->no...", xs, ws)
     return out.astype(np.int32)
+
+
+def test_conv_ui8_operands_and_zero_points(oracle):
+    """ui8 inputs / kernels read as 0..255, with zero points, against the
+    independent windowed formulation (which pads with zpx, so a padded tap
+    adds 0)."""
+    rng = np.random.default_rng(5)
+    for xs, ws, st, pad, dl, g in [((2, 4, 9, 7), (6, 2, 3, 2), [2, 1], [[1, 2], [0, 1]], [2, 1], 2),
+                                   ((1, 3, 8), (4, 3, 3), [1], [[2, 1]], [1], 1)]:
+        for x_u8 in (False, True):
+            for w_u8 in (False, True):
+                x = rng.integers(0, 256, xs).astype(np.uint8)
+                w = rng.integers(0, 256, ws).astype(np.uint8)
+                x = x if x_u8 else x.view(np.int8)
+                w = w if w_u8 else w.view(np.int8)
+                for zpx, zpw in ((0, 0), (128, 0), (5, 130)):
+                    want = _conv_windows(x, w, st, pad, dl, g, zpx, zpw)
+                    same_bits(oracle.quantized_conv(x, w, st, pad, dl, g, zpx, zpw), want)
 
 
 CONV_CASES = [
