@@ -268,6 +268,139 @@ __global__ __launch_bounds__(256) void k_gemv_w4(const int8_t* __restrict__ xq,
     run_block(blockIdx.x + gs, wb, sb, bb, tg + G * pitch);
 }
 
+// ---- MFMA W4A8 GEMV, 2 <= M <= 16 tokens.  One v_mfma_i32_16x16x32_i8 per
+// 16 weight rows x 32 K elements x all 16 token columns: lane l holds row
+// (resp. token) l % 16 and 8 of the 32 elements, in A and B alike (the
+// order of K inside an instruction is free as long as both operands use
+// the same one).  The 4 packed weight bytes of a lane become two dot
+// operands without sign extension -- the low nibbles (elements 0, 2, 4, 6)
+// and the high ones (1, 3, 5, 7), each `(n ^ 8)` = q + 8 -- and the
+// activations are regrouped into the same even / odd order (v_perm); a
+// second MFMA with the constant -8 as A adds -8 * sum(x) to the same
+// accumulator, so it holds sum x * q exactly.
+//
+// A step of a wave covers SPAN = 32 (narrow) or 128 (WIDE, groups of a
+// multiple of 128) elements: in the wide form lane (r, q) loads 16 packed
+// bytes (32 elements) of row r and the 32 matching activation bytes of
+// token r, and runs four MFMA pairs on them.  The workgroup's 4 waves take
+// quarters of K (whole groups); at the end of each group a wave writes its
+// int32 accumulators to LDS [group][output], then one lane per output adds
+// acc_g * sw_g (f64) over the groups in order.  All of a wave's weight and
+// activation loads are issued before its first MFMA.
+__device__ __forceinline__ v4i w4_mma8(int w, int x0, int x1, v4i acc) {
+  const long minus8 = (long)0xF8F8F8F8F8F8F8F8ull;
+  const int lo = (w & 0x0F0F0F0F) ^ 0x08080808;         // elements 0,2,4,6 of 8: q + 8
+  const int hi = ((w >> 4) & 0x0F0F0F0F) ^ 0x08080808;  // elements 1,3,5,7
+  const long a = (long)(uint32_t)lo | ((long)(uint32_t)hi << 32);
+  const int xe = (int)__builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x06040200u);
+  const int xo = (int)__builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x07050301u);
+  const long b = (long)(uint32_t)xe | ((long)(uint32_t)xo << 32);
+  acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(minus8, b, acc, 0, 0, 0);
+}
+
+template <int STEPS, bool WIDE>
+__global__ __launch_bounds__(256) void k_gemv_w4_mfma(const int8_t* __restrict__ xq,
+                                                      const double* __restrict__ sx, int sx_stride,
+                                                      const uint8_t* __restrict__ wq4,
+                                                      const double* __restrict__ sw, int M, int N,
+                                                      int K, int group,
+                                                      const float* __restrict__ bias, int act,
+                                                      float* __restrict__ y) {
+  constexpr int SPAN = WIDE ? 128 : 32;                 // elements per wave step
+  constexpr int LANE = SPAN / 4;                        // elements per lane and step
+  extern __shared__ double lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int G = K / group, KB = K >> 1;
+  const int NO = 16 * M;                                // outputs of the workgroup
+  double* sc = lds;                                     // [16][G] group scales
+  int* accs = reinterpret_cast<int*>(lds + 16 * G);     // [G][NO] group sums
+
+  const int steps = (K >> 2) / SPAN;                    // steps per wave (<= STEPS)
+  const int kbase = wave * (K >> 2);
+  const uint32_t rows = (uint32_t)min(16, N - n0);
+  const __amdgpu_buffer_rsrc_t rw = w4_rsrc(wq4 + (int64_t)n0 * KB, rows * (uint32_t)KB);
+  const __amdgpu_buffer_rsrc_t rx = w4_rsrc(xq, (uint32_t)M * (uint32_t)K);
+  // lane's weight row r16 (past the last row: offset past the end) and
+  // token r16 (>= M: past the end): both read zero
+  const uint32_t wrow = (uint32_t)r16 < rows ? (uint32_t)r16 : rows;
+  const uint32_t xtok = r16 < M ? (uint32_t)r16 : (uint32_t)M;
+  v4i wv[WIDE ? STEPS : 1];
+  v4i xv[WIDE ? 2 * STEPS : 1];
+  int wn[WIDE ? 1 : STEPS];
+  v2i xn[WIDE ? 1 : STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint32_t k = (uint32_t)(kbase + SPAN * (s < steps ? s : 0) + LANE * q);
+    const uint32_t wo = wrow * (uint32_t)KB + k / 2, xo = xtok * (uint32_t)K + k;
+    if constexpr (WIDE) {
+      wv[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
+      xv[2 * s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
+      xv[2 * s + 1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0));
+    } else {
+      wn[s] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rw, wo, 0, 2));
+      xn[s] = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rx, xo, 0, 0));
+    }
+  }
+  // group scales of the workgroup's 16 rows
+  for (int i = tid; i < 16 * G; i += 256) {
+    const int r = i / G, g = i - r * G;
+    sc[i] = n0 + r < N ? sw[(int64_t)(n0 + r) * G + g] : 0.0;
+  }
+  // this lane's output: (row o / M, token o % M)
+  const int o = tid, orow = o / M, otok = o - orow * M;
+  const bool out_lane = o < NO && n0 + orow < N;
+  const double sxo = out_lane ? sx[(int64_t)otok * sx_stride] : 0.0;
+  const float bo = (out_lane && bias) ? bias[n0 + orow] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int gsteps = group / SPAN;                      // steps per group
+  int g = kbase / group, left = 0;                      // the wave starts on a group boundary
+  v4i acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    if (s < steps) {                                    // uniform
+      if (left == 0) {                                  // a group starts
+        acc = v4i{0, 0, 0, 0};
+        left = gsteps;
+      }
+      if constexpr (WIDE) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc = w4_mma8(wv[s][j], xv[2 * s + j / 2][2 * (j & 1)], xv[2 * s + j / 2][2 * (j & 1) + 1], acc);
+      } else {
+        acc = w4_mma8(wn[s], xn[s].x, xn[s].y, acc);
+      }
+      if (--left == 0) {                                // a group ends: D[4q + r][r16]
+        if (r16 < M) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) accs[g * NO + (4 * q + r) * M + r16] = acc[r];
+        }
+        ++g;
+      }
+    }
+  }
+  __syncthreads();
+  if (out_lane) {
+    double S = -0.0;                                    // -0.0 + t = t exactly
+    for (int gi = 0; gi < G; ++gi) S = S + (double)accs[gi * NO + o] * sc[orow * G + gi];
+    float v = (float)(S * sxo);
+    if (bias) v = v + bo;
+    if (act == 1) v = relu_js(v);
+    else if (act == 2) v = silu_js(v);
+    y[(int64_t)otok * N + n0 + orow] = v;
+  }
+}
+
+bool gemv_w4_mfma_ok(int64_t M, int64_t K, int64_t group) {
+  if (M < 2 || M > 16 || K % 128 != 0 || K > 4096 || group % 32 != 0 || K % group != 0) return false;
+  const int64_t G = K / group;
+  if ((K / 4) % group != 0) return false;               // whole groups per wave
+  return (size_t)16 * G * 8 + (size_t)G * 16 * M * 4 <= 65536;
+}
+
 __global__ __launch_bounds__(256) void k_gemv_w4_generic(const int8_t* __restrict__ xq,
                                                          const double* __restrict__ sx,
                                                          int sx_stride,
@@ -347,7 +480,30 @@ hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, con
                           const float* bias, int act, float* y, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
   W4Plan pl;
-  if (!w4_plan(M, K, group, &pl)) {
+  const bool dot4 = w4_plan(M, K, group, &pl);
+  // the MFMA kernel from 3 tokens on with 16-byte weight loads (groups of a
+  // multiple of 128); dot4 below that, or where the MFMA kernel does not apply
+  if (gemv_w4_mfma_ok(M, K, group) && (!dot4 || (M >= 3 && group % 128 == 0))) {
+    const int64_t G = K / group;
+    const size_t lds = (size_t)16 * G * 8 + (size_t)G * 16 * M * 4;
+    const dim3 grid((unsigned)((N + 15) / 16)), block(256);
+#define Q8_W4M(ST, WD)                                                                          \
+  hipLaunchKernelGGL((k_gemv_w4_mfma<ST, WD>), grid, block, lds, st, xq, sx, sx_stride, wq4, sw, \
+                     (int)M, (int)N, (int)K, (int)group, bias, act, y)
+    if (group % 128 == 0) {                             // 16-byte weight loads
+      const int steps = (int)(K >> 9);
+      if (steps <= 4) Q8_W4M(4, true);
+      else Q8_W4M(8, true);
+    } else {
+      const int steps = (int)(K >> 7);
+      if (steps <= 8) Q8_W4M(8, false);
+      else if (steps <= 16) Q8_W4M(16, false);
+      else Q8_W4M(32, false);
+    }
+#undef Q8_W4M
+    return hipGetLastError();
+  }
+  if (!dot4) {
     hipLaunchKernelGGL(k_gemv_w4_generic, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, st,
                        xq, sx, sx_stride, wq4, sw, M, N, K, group, bias, act, y);
     return hipGetLastError();

@@ -4,7 +4,8 @@ Packing is compared with the oracle's fromConstantArrayPerGroup /
 quantizeArrayPerGroup restatement (codes and f64 scales bit for bit, NaN and
 zero groups included); the W4A8 GEMV with the oracle's definition of it
 (exact per-group sums, f64 sum over groups in order), bit for bit, on the
-fast kernel (M <= 4, power-of-two groups) and the generic one.
+MFMA kernel (2 <= M <= 16, K <= 4096), the dot4 kernel (M <= 4,
+power-of-two groups) and the generic one.
 """
 import numpy as np
 import pytest
@@ -63,11 +64,15 @@ def test_pack_int4_matches_oracle(ops, oracle, N, K, g):
     same_bits(host(wq), want_q)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
-# (11008, 4096) and (5000, 8192) make every workgroup of the fast kernel walk
-# two blocks of rows (prefetch path); (19, 96) has 256-row blocks
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 16])
+# (11008, 4096) and (5000, 8192) make every workgroup of the dot4 kernel walk
+# two blocks of rows (prefetch path); (19, 96) has 256-row blocks; for
+# 2 <= M <= 16 the MFMA kernel takes K <= 4096 with whole groups per quarter
+# of K: 8, 16 and 32 steps per wave, a non-power-of-two group (96), one
+# group per wave (1024), N not a multiple of 16
 @pytest.mark.parametrize("N,K,g", [(4096, 4096, 128), (1000, 4096, 32), (77, 2048, 2048), (33, 8192, 64),
-                                   (19, 96, 32), (11, 160, 80), (11008, 4096, 128), (5000, 8192, 64)])
+                                   (19, 96, 32), (11, 160, 80), (11008, 4096, 128), (5000, 8192, 64),
+                                   (77, 1536, 96), (11, 4096, 1024), (5, 128, 32), (300, 1024, 64)])
 def test_gemv_w4_matches_oracle(ops, oracle, M, N, K, g):
     r = oracle.Rng(M * 1000 + N + g)
     x = r.normal((M, K))
