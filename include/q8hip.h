@@ -288,9 +288,11 @@ int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size
  *   y     = fround(S * sx[m]), then fround(y + bias[n]) and act (Q8_ACT_*)
  * xq: int8 [M, K] (q8_quantize_rows codes); sx: f64, sx_mode Q8_PER_TOKEN
  * ([M]) or Q8_PER_TENSOR ([1]); Wq4 / sw as written by q8_pack_weight_int4.
- * Fast kernel for M <= 4, power-of-two group_size in [32, 2048] and
- * K <= 8192 (half the weight bytes of int8); any other shape runs a simple
- * exact kernel. */
+ * Kernels: packed dot products for M <= 2 (M <= 4 where K or the group
+ * rule out the MFMA kernel) with a power-of-two group_size in [32, 2048]
+ * and K <= 8192; the MFMA kernel for any M (blocks of 16 tokens) with K and
+ * group_size multiples of 32; any other shape (a group that is not a
+ * multiple of 32) runs a simple exact kernel.  All give the same bits. */
 int q8_gemv_w4(const int8_t* xq, const double* sx, int sx_mode, const uint8_t* Wq4,
                const double* sw, int64_t M, int64_t N, int64_t K, int64_t group_size,
                const float* bias, int act, float* out, void* stream);

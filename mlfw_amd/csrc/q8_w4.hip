@@ -268,29 +268,40 @@ __global__ __launch_bounds__(256) void k_gemv_w4(const int8_t* __restrict__ xq,
     run_block(blockIdx.x + gs, wb, sb, bb, tg + G * pitch);
 }
 
-// ---- MFMA W4A8 GEMV, 2 <= M <= 16 tokens.  One v_mfma_i32_16x16x32_i8 per
-// 16 weight rows x 32 K elements x all 16 token columns: lane l holds row
-// (resp. token) l % 16 and 8 of the 32 elements, in A and B alike (the
-// order of K inside an instruction is free as long as both operands use
-// the same one).  The 4 packed weight bytes of a lane become two dot
-// operands without sign extension -- the low nibbles (elements 0, 2, 4, 6)
-// and the high ones (1, 3, 5, 7), each `(n ^ 8)` = q + 8 -- and the
-// activations are regrouped into the same even / odd order (v_perm); a
-// second MFMA with the constant -8 as A adds -8 * sum(x) to the same
-// accumulator, so it holds sum x * q exactly.
+// ---- MFMA W4A8 GEMV: any M (blocks of 16 tokens), K a multiple of 32,
+// groups of a multiple of 32.  One v_mfma_i32_16x16x32_i8 per 16 weight
+// rows x 32 codes x 16 token columns: lane l holds row (resp. token) l % 16
+// and 8 of the 32 codes, in A and B alike (the order of K inside an
+// instruction is free as long as both operands use the same one).  The 4
+// packed bytes of a lane become two dot operands without sign extension --
+// the low nibbles (codes 0, 2, 4, 6) and the high ones (1, 3, 5, 7), each
+// `(n ^ 8)` = q + 8 -- and the activations are regrouped into the same
+// even / odd order (v_perm); a second MFMA with the constant -8 as A adds
+// -8 * sum(x), so the accumulator holds sum x * q exactly.
 //
-// A step of a wave covers SPAN = 32 (narrow) or 128 (WIDE, groups of a
-// multiple of 128) elements: in the wide form lane (r, q) loads 16 packed
-// bytes (32 elements) of row r and the 32 matching activation bytes of
-// token r, and runs four MFMA pairs on them.  The workgroup's 4 waves take
-// quarters of K (whole groups); at the end of each group a wave writes its
-// int32 accumulators to LDS [group][output], then one lane per output adds
-// acc_g * sw_g (f64) over the groups in order.  All of a wave's weight and
-// activation loads are issued before its first MFMA.
+// Loads: lane (r, q) of a wave reads 16 packed bytes (a 32-code chunk) of
+// row r, so one instruction covers 64 contiguous bytes of each of 16 rows.
+// A step of a wave is 4 such chunks (128 codes); the 4 x 4 transpose of the
+// chunk dwords between the 4 lanes of a row (v_permlane32_swap, then
+// v_permlane16_swap) makes MFMA j consume chunk j whole, so a chunk never
+// mixes two groups.  Lane (t, q) loads codes 8q..8q+7 of chunk j of token
+// t's activations to match.
+//
+// K is walked in rounds: in round r, wave w of the workgroup's NW takes the
+// span of PS codes at (NW r + w) * PS (PS a multiple of the group, or a
+// divisor of it, of at most 128 * RS codes: one round covers K = 4096 with
+// groups of 128),
+// and splits it into segments of SL = min(PS, group) codes; each segment's
+// int32 sum (exact) goes to LDS [segment][token][row], with the scales of
+// the groups that end in the round.  After one barrier, lane o = (token,
+// row) walks the round's segments in order, adds the pieces of a group in
+// int32 and, when the group is complete, adds acc_g * sw_g to its f64 sum --
+// groups in ascending order, as the definition asks.  LDS holds two round
+// windows, so one barrier per round suffices.
 __device__ __forceinline__ v4i w4_mma8(int w, int x0, int x1, v4i acc) {
   const long minus8 = (long)0xF8F8F8F8F8F8F8F8ull;
-  const int lo = (w & 0x0F0F0F0F) ^ 0x08080808;         // elements 0,2,4,6 of 8: q + 8
-  const int hi = ((w >> 4) & 0x0F0F0F0F) ^ 0x08080808;  // elements 1,3,5,7
+  const int lo = (w & 0x0F0F0F0F) ^ 0x08080808;         // codes 0,2,4,6 of 8: q + 8
+  const int hi = ((w >> 4) & 0x0F0F0F0F) ^ 0x08080808;  // codes 1,3,5,7
   const long a = (long)(uint32_t)lo | ((long)(uint32_t)hi << 32);
   const int xe = (int)__builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x06040200u);
   const int xo = (int)__builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x07050301u);
@@ -299,107 +310,244 @@ __device__ __forceinline__ v4i w4_mma8(int w, int x0, int x1, v4i acc) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(minus8, b, acc, 0, 0, 0);
 }
 
-template <int STEPS, bool WIDE>
-__global__ __launch_bounds__(256) void k_gemv_w4_mfma(const int8_t* __restrict__ xq,
-                                                      const double* __restrict__ sx, int sx_stride,
-                                                      const uint8_t* __restrict__ wq4,
-                                                      const double* __restrict__ sw, int M, int N,
-                                                      int K, int group,
-                                                      const float* __restrict__ bias, int act,
-                                                      float* __restrict__ y) {
-  constexpr int SPAN = WIDE ? 128 : 32;                 // elements per wave step
-  constexpr int LANE = SPAN / 4;                        // elements per lane and step
+// Register j of lane (r, q) <- dword q of lane (r, j)'s v[0..3].
+__device__ __forceinline__ v4i w4_transpose4(v4i v) {
+  const auto s02 = __builtin_amdgcn_permlane32_swap((unsigned)v[0], (unsigned)v[2], false, false);
+  const auto s13 = __builtin_amdgcn_permlane32_swap((unsigned)v[1], (unsigned)v[3], false, false);
+  const auto t01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  const auto t23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  return v4i{(int)t01[0], (int)t01[1], (int)t23[0], (int)t23[1]};
+}
+
+template <int NW, int RS, bool TR>
+__global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restrict__ xq,
+                                                          const double* __restrict__ sx,
+                                                          int sx_stride,
+                                                          const uint8_t* __restrict__ wq4,
+                                                          const double* __restrict__ sw, int M,
+                                                          int N, int K, int group, int PS,
+                                                          int segw, int ng,
+                                                          const float* __restrict__ bias, int act,
+                                                          float* __restrict__ y) {
+  constexpr int NT = 64 * NW;
   extern __shared__ double lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+  const int MB = min(16, M - t0);                       // tokens of this block
+  const int NO = 16 * MB;                               // outputs: o = token * 16 + row
   const int G = K / group, KB = K >> 1;
-  const int NO = 16 * M;                                // outputs of the workgroup
-  double* sc = lds;                                     // [16][G] group scales
-  int* accs = reinterpret_cast<int*>(lds + 16 * G);     // [G][NO] group sums
+  const int SL = min(PS, group);                        // segment length (codes)
+  const int nseg = NW * segw;                           // segments per round
+  const int win = nseg * NO + 2 * 16 * ng;              // ints per LDS window: sums, then the
+                                                        // scales of the <= ng groups that end
+  const int RC = NW * PS;                               // codes per round
+  const int rounds = (K + RC - 1) / RC;
 
-  const int steps = (K >> 2) / SPAN;                    // steps per wave (<= STEPS)
-  const int kbase = wave * (K >> 2);
   const uint32_t rows = (uint32_t)min(16, N - n0);
   const __amdgpu_buffer_rsrc_t rw = w4_rsrc(wq4 + (int64_t)n0 * KB, rows * (uint32_t)KB);
-  const __amdgpu_buffer_rsrc_t rx = w4_rsrc(xq, (uint32_t)M * (uint32_t)K);
-  // lane's weight row r16 (past the last row: offset past the end) and
-  // token r16 (>= M: past the end): both read zero
-  const uint32_t wrow = (uint32_t)r16 < rows ? (uint32_t)r16 : rows;
-  const uint32_t xtok = r16 < M ? (uint32_t)r16 : (uint32_t)M;
-  v4i wv[WIDE ? STEPS : 1];
-  v4i xv[WIDE ? 2 * STEPS : 1];
-  int wn[WIDE ? 1 : STEPS];
-  v2i xn[WIDE ? 1 : STEPS];
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const uint32_t k = (uint32_t)(kbase + SPAN * (s < steps ? s : 0) + LANE * q);
-    const uint32_t wo = wrow * (uint32_t)KB + k / 2, xo = xtok * (uint32_t)K + k;
-    if constexpr (WIDE) {
-      wv[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
-      xv[2 * s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
-      xv[2 * s + 1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0));
-    } else {
-      wn[s] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rw, wo, 0, 2));
-      xn[s] = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rx, xo, 0, 0));
-    }
-  }
-  // group scales of the workgroup's 16 rows
-  for (int i = tid; i < 16 * G; i += 256) {
-    const int r = i / G, g = i - r * G;
-    sc[i] = n0 + r < N ? sw[(int64_t)(n0 + r) * G + g] : 0.0;
-  }
-  // this lane's output: (row o / M, token o % M)
-  const int o = tid, orow = o / M, otok = o - orow * M;
-  const bool out_lane = o < NO && n0 + orow < N;
-  const double sxo = out_lane ? sx[(int64_t)otok * sx_stride] : 0.0;
-  const float bo = (out_lane && bias) ? bias[n0 + orow] : 0.0f;
-  __builtin_amdgcn_sched_barrier(0);
+  const __amdgpu_buffer_rsrc_t rx = w4_rsrc(xq + (int64_t)t0 * K, (uint32_t)MB * (uint32_t)K);
+  const __amdgpu_buffer_rsrc_t rs = w4_rsrc(sw + (int64_t)n0 * G, rows * (uint32_t)G * 8u);
+  const uint32_t wrow = (uint32_t)r16 < rows ? (uint32_t)r16 : rows;    // past the end: zero
+  const uint32_t xtok = r16 < MB ? (uint32_t)r16 : (uint32_t)MB;
 
-  const int gsteps = group / SPAN;                      // steps per group
-  int g = kbase / group, left = 0;                      // the wave starts on a group boundary
-  v4i acc = {0, 0, 0, 0};
+  // this lane's output
+  const int o = tid, otok = o >> 4, orow = o & 15;
+  const bool out_lane = o < NO && n0 + orow < N;
+  const double sxo = out_lane ? sx[(int64_t)(t0 + otok) * sx_stride] : 0.0;
+  const float bo = (out_lane && bias) ? bias[n0 + orow] : 0.0f;
+  // scale slots u = tid + NT * u2 of a window: row u / ng, group u % ng
+  constexpr int NSC = (16 * 64 + NT - 1) / NT;          // ng <= 64
+  uint32_t sc_off[NSC];
+  int sc_g[NSC];
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    if (s < steps) {                                    // uniform
-      if (left == 0) {                                  // a group starts
-        acc = v4i{0, 0, 0, 0};
-        left = gsteps;
-      }
-      if constexpr (WIDE) {
+  for (int u2 = 0; u2 < NSC; ++u2) {
+    const int u = tid + NT * u2, rr = u / ng;
+    sc_g[u2] = u < 16 * ng ? u - rr * ng : G;          // G: past the end
+    sc_off[u2] = (uint32_t)(rr < 16 ? rr : 16) * (uint32_t)G;
+  }
+
+  double S = -0.0;                                      // -0.0 + t = t exactly
+  int gacc = 0, pieces = 0, gdone = 0;                  // groups split over spans
+  const int P = group > PS ? group / PS : 1;            // spans per group
+  int* const win0 = reinterpret_cast<int*>(lds);
+  for (int r = 0; r < rounds; ++r) {
+    int* wbuf = win0 + (r & 1) * win;                   // two windows (one if one round):
+                                                        // one barrier per round
+    const int k0 = (NW * r + wave) * PS;                // this wave's span
+    const int gfirst = (NW * r * PS) / group;           // first group that can end in round r
+    v4i wv[RS], xv[RS][2];
+    double scv[NSC];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc = w4_mma8(wv[s][j], xv[2 * s + j / 2][2 * (j & 1)], xv[2 * s + j / 2][2 * (j & 1) + 1], acc);
-      } else {
-        acc = w4_mma8(wn[s], xn[s].x, xn[s].y, acc);
-      }
-      if (--left == 0) {                                // a group ends: D[4q + r][r16]
-        if (r16 < M) {
+    for (int s = 0; s < RS; ++s) {
+      const int kc = k0 + 128 * s + 32 * q;             // the lane's chunk
+      // a chunk outside the span or K reads from the row (token) past the
+      // end: selecting the row, not the offset, keeps the load unconditional
+      const bool ok = 128 * s + 32 * q < PS && kc < K;
+      const uint32_t kk = ok ? (uint32_t)kc : 0u;
+      const uint32_t wr = ok ? wrow : rows, xt = ok ? xtok : (uint32_t)MB;
+      wv[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wr * (uint32_t)KB + kk / 2, 0, 0));
+      const uint32_t xo = xt * (uint32_t)K + kk;
+      xv[s][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
+      xv[s][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0));
+    }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) accs[g * NO + (4 * q + r) * M + r16] = acc[r];
+    for (int u2 = 0; u2 < NSC; ++u2) {
+      const int g = gfirst + sc_g[u2] < G ? gfirst + sc_g[u2] : G;          // G: past the row
+      scv[u2] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(
+                    rs, (sc_off[u2] + (uint32_t)g) * 8u, 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // MFMAs over the span's chunks; segment sums to LDS [segment][token][row]
+    const int nch = max(0, min(PS, K - k0)) >> 5;       // chunks of this span inside K
+    v4i acc = {0, 0, 0, 0};
+    int seg = wave * segw, left = 0;
+    auto seg_end = [&]() {
+      if (r16 < MB) *reinterpret_cast<v4i*>(wbuf + seg * NO + r16 * 16 + 4 * q) = acc;
+      ++seg;
+    };
+    if constexpr (!TR) {
+      // groups of a multiple of 128 codes, spans of whole steps: MFMA j takes
+      // dword j (codes 8j..8j+7) of every lane's chunk, all in one group
+#pragma unroll
+      for (int s = 0; s < RS; ++s) {
+        if (4 * s < nch) {                              // uniform
+          if (left == 0) {                              // a segment starts
+            acc = v4i{0, 0, 0, 0};
+            left = SL >> 7;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc = w4_mma8(wv[s][j], xv[s][j >> 1][2 * (j & 1)], xv[s][j >> 1][2 * (j & 1) + 1], acc);
+          if (--left == 0) seg_end();
         }
-        ++g;
+      }
+    } else {
+#pragma unroll
+    for (int s = 0; s < RS; ++s) {
+      if (4 * s < nch) {                                // uniform
+        const v4i wt = w4_transpose4(wv[s]);
+        // chunk j's codes 8q..8q+7 = dwords 2q, 2q+1 of lane (t, j)'s 32 bytes
+        const v4i xe = w4_transpose4(v4i{xv[s][0][0], xv[s][0][2], xv[s][1][0], xv[s][1][2]});
+        const v4i xo = w4_transpose4(v4i{xv[s][0][1], xv[s][0][3], xv[s][1][1], xv[s][1][3]});
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (4 * s + j < nch) {                        // uniform
+            if (left == 0) {                            // a segment starts
+              acc = v4i{0, 0, 0, 0};
+              left = SL >> 5;
+            }
+            acc = w4_mma8(wt[j], xe[j], xo[j], acc);
+            if (--left == 0) seg_end();                 // segment complete
+          }
+        }
+      }
+    }
+    }
+    double* scw = reinterpret_cast<double*>(wbuf + nseg * NO);
+#pragma unroll
+    for (int u2 = 0; u2 < NSC; ++u2)
+      if (tid + NT * u2 < 16 * ng) scw[tid + NT * u2] = scv[u2];
+    w4_lds_barrier();
+
+    // lane o adds the round's groups in order
+    if (out_lane) {
+      const double* sco = scw + orow * ng;
+      const int kr = NW * r * PS;                       // the round's first code
+      if (group <= PS) {                                // uniform: every segment is a group
+        const int nv = min(nseg, (K - kr) / group);
+        for (int i = 0; i < nv; i += 8) {
+          int a8[8];
+          double t8[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {                 // reads stay inside the window
+            const int iu = min(i + u, nseg - 1);
+            a8[u] = wbuf[iu * NO + o];
+            t8[u] = sco[iu];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (i + u < nv) S = S + (double)a8[u] * t8[u];
+        }
+      } else {                                          // a group spans P wave spans
+        for (int w = 0; w < NW; ++w) {
+          if (kr + w * PS >= K) break;
+          gacc += wbuf[w * NO + o];                     // int32, exact
+          if (++pieces == P) {
+            S = S + (double)gacc * sco[gdone - gfirst];
+            gacc = 0;
+            pieces = 0;
+            ++gdone;
+          }
+        }
       }
     }
   }
-  __syncthreads();
   if (out_lane) {
-    double S = -0.0;                                    // -0.0 + t = t exactly
-    for (int gi = 0; gi < G; ++gi) S = S + (double)accs[gi * NO + o] * sc[orow * G + gi];
     float v = (float)(S * sxo);
     if (bias) v = v + bo;
     if (act == 1) v = relu_js(v);
     else if (act == 2) v = silu_js(v);
-    y[(int64_t)otok * N + n0 + orow] = v;
+    y[(int64_t)(t0 + otok) * N + n0 + orow] = v;
   }
 }
 
-bool gemv_w4_mfma_ok(int64_t M, int64_t K, int64_t group) {
-  if (M < 2 || M > 16 || K % 128 != 0 || K > 4096 || group % 32 != 0 || K % group != 0) return false;
-  const int64_t G = K / group;
-  if ((K / 4) % group != 0) return false;               // whole groups per wave
-  return (size_t)16 * G * 8 + (size_t)G * 16 * M * 4 <= 65536;
+namespace {
+struct W4MPlan {
+  int nw, rs;                             // waves per workgroup, 128-code steps per span
+  int PS, segw, ng;                       // span per wave and round, segments per span,
+  size_t lds;                             // groups that can end in a round; LDS bytes
+  bool tr;                                // chunk transpose (groups not a multiple of 128)
+};
+
+// Span per wave and round: a multiple of the group (as many groups as fit
+// in 4 steps = 512 codes and the LDS budget) or, for groups above 512
+// codes, the largest divisor of the group of at most 512 codes.
+// Workgroup shape: 8 waves of 4-step spans (94 VGPRs: two workgroups per
+// CU) while the grid fits the chip at two per CU, else 4 waves of 8-step
+// spans (152 VGPRs: three per CU) for groups of a multiple of 128.
+bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl) {
+  if (M < 1 || K < 32 || K % 32 != 0 || group < 32 || group % 32 != 0 || K % group != 0) return false;
+  if (K > (int64_t)1 << 24) return false;                     // 32-bit buffer offsets
+  if ((M + 15) / 16 > 65535) return false;                    // token blocks: grid.y
+  const int64_t NO = 16 * std::min<int64_t>(M, 16);
+  // groups of a multiple of 128 codes need no chunk transpose, with spans of
+  // whole 128-code steps; other groups work in 32-code chunks
+  pl->tr = group % 128 != 0;
+  const int64_t blocks = ((N + 15) / 16) * ((M + 15) / 16);
+  const bool wide = !pl->tr && blocks > 2 * (int64_t)cu_count();
+  pl->nw = wide ? 4 : 8;
+  pl->rs = wide ? 8 : 4;
+  const int64_t NW = pl->nw, span = 128 * pl->rs;
+  const int64_t unit = pl->tr ? 32 : 128;
+  // LDS: one window of segment sums and scales per round in flight (two
+  // when there is more than one round)
+  auto lds_of = [&](int64_t PS, int64_t segw, int64_t ng) {
+    const int64_t nwin = K > NW * PS ? 2 : 1;
+    return nwin * (NW * segw * NO + 2 * 16 * ng) * 4;
+  };
+  int64_t PS = 0;
+  if (group <= span) {
+    // as many whole groups per span as fit (ng <= 64)
+    for (int64_t k = span / group; k >= 1; --k)
+      if (NW * k <= 64 && lds_of(k * group, k, NW * k) <= 65536) { PS = k * group; break; }
+  } else {
+    // the largest divisor of the group of at most `span` codes, in whole units
+    for (int64_t c = span / unit; c >= 1; --c)
+      if ((group / unit) % c == 0) { PS = unit * c; break; }
+  }
+  if (PS == 0) return false;
+  pl->PS = (int)PS;
+  pl->segw = PS >= group ? (int)(PS / group) : 1;
+  // a round of NW * PS codes holds NW * PS / group group ends when the group
+  // divides it, else at most one more
+  const int64_t rc = NW * PS;
+  pl->ng = (int)(rc / group + (rc % group != 0));
+  pl->lds = (size_t)lds_of(PS, pl->segw, pl->ng);
+  return pl->ng <= 64 && pl->lds <= 65536;
 }
+}  // namespace
 
 __global__ __launch_bounds__(256) void k_gemv_w4_generic(const int8_t* __restrict__ xq,
                                                          const double* __restrict__ sx,
@@ -470,36 +618,24 @@ bool w4_plan(int64_t M, int64_t K, int64_t group, W4Plan* pl) {
 }
 }  // namespace
 
-bool gemv_w4_fast_ok(int64_t M, int64_t K, int64_t group) {
-  W4Plan pl;
-  return w4_plan(M, K, group, &pl);
-}
-
 hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, const uint8_t* wq4,
                           const double* sw, int64_t M, int64_t N, int64_t K, int64_t group,
                           const float* bias, int act, float* y, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
   W4Plan pl;
   const bool dot4 = w4_plan(M, K, group, &pl);
-  // the MFMA kernel from 3 tokens on with 16-byte weight loads (groups of a
-  // multiple of 128); dot4 below that, or where the MFMA kernel does not apply
-  if (gemv_w4_mfma_ok(M, K, group) && (!dot4 || (M >= 3 && group % 128 == 0))) {
-    const int64_t G = K / group;
-    const size_t lds = (size_t)16 * G * 8 + (size_t)G * 16 * M * 4;
-    const dim3 grid((unsigned)((N + 15) / 16)), block(256);
-#define Q8_W4M(ST, WD)                                                                          \
-  hipLaunchKernelGGL((k_gemv_w4_mfma<ST, WD>), grid, block, lds, st, xq, sx, sx_stride, wq4, sw, \
-                     (int)M, (int)N, (int)K, (int)group, bias, act, y)
-    if (group % 128 == 0) {                             // 16-byte weight loads
-      const int steps = (int)(K >> 9);
-      if (steps <= 4) Q8_W4M(4, true);
-      else Q8_W4M(8, true);
-    } else {
-      const int steps = (int)(K >> 7);
-      if (steps <= 8) Q8_W4M(8, false);
-      else if (steps <= 16) Q8_W4M(16, false);
-      else Q8_W4M(32, false);
-    }
+  W4MPlan mp;
+  const bool mfma = w4m_plan(M, N, K, group, &mp);
+  // dot4 for one and two tokens (and up to four where the MFMA kernel does
+  // not apply), the MFMA kernel from three tokens on
+  if (mfma && (!dot4 || M >= 3)) {
+    const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16)), block(64 * mp.nw);
+#define Q8_W4M(NW, RS, TR)                                                                        \
+  hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR>), grid, block, mp.lds, st, xq, sx, sx_stride, wq4, \
+                     sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw, mp.ng, bias, act, y)
+    if (mp.nw == 4) Q8_W4M(4, 8, false);
+    else if (mp.tr) Q8_W4M(8, 4, true);
+    else Q8_W4M(8, 4, false);
 #undef Q8_W4M
     return hipGetLastError();
   }

@@ -11,6 +11,7 @@ check dtype, shape and device before calling, and the C ABI validates again.
 from __future__ import annotations
 
 import ctypes as C
+import math
 
 import torch
 
@@ -96,6 +97,20 @@ def _need(t: torch.Tensor, dtype: torch.dtype, name: str, ndim: int | None = Non
         raise ValueError(f"{name}: expected {ndim}-D, got shape {tuple(t.shape)}")
 
 
+def _out(t, shape, dtype: torch.dtype, like: torch.Tensor, name: str = "out") -> torch.Tensor:
+    """The caller's output tensor, checked (dtype, device, contiguity, element
+    count -- the kernels write exactly that many elements), or a new one."""
+    shape = tuple(shape) if isinstance(shape, (tuple, list, torch.Size)) else (int(shape),)
+    if t is None:
+        return torch.empty(shape, dtype=dtype, device=like.device)
+    _need(t, dtype, name)
+    if t.numel() != math.prod(shape):
+        raise ValueError(f"{name}: expected {math.prod(shape)} elements (shape {shape}), got {tuple(t.shape)}")
+    if t.device != like.device:
+        raise ValueError(f"{name}: must be on {like.device}, got {t.device}")
+    return t
+
+
 def _rows(x: torch.Tensor):
     """[..., K] viewed as [M, K] with M the product of the leading dims."""
     if x.dim() == 0:
@@ -151,8 +166,8 @@ def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
     quantization_types.ts:248-254).  Returns (int8 codes, f64 scales[M])."""
     _need(x, torch.float32, "quantize_per_token")
     M, K = _rows(x)
-    q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
-    scales = torch.empty(M, dtype=torch.float64, device=x.device) if scales is None else scales
+    q = _out(q, x.shape, torch.int8, x, "q")
+    scales = _out(scales, M, torch.float64, x, "scales")
     _call("q8_quantize_rows", _ptr(x), M, K, L.Q8_PER_TOKEN, _ptr(q), _ptr(scales), _stream())
     return q, scales
 
@@ -162,8 +177,8 @@ def quantize_per_tensor(x: torch.Tensor, q: torch.Tensor | None = None,
     """Dynamic symmetric int8 quantize with one scale for the whole tensor.
     Returns (int8 codes, f64 scale tensor of one element)."""
     _need(x, torch.float32, "quantize_per_tensor")
-    q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
-    scales = torch.empty(1, dtype=torch.float64, device=x.device) if scales is None else scales
+    q = _out(q, x.shape, torch.int8, x, "q")
+    scales = _out(scales, 1, torch.float64, x, "scales")
     _call("q8_quantize_rows", _ptr(x), 1, x.numel(), L.Q8_PER_TENSOR, _ptr(q), _ptr(scales),
            _stream())
     return q, scales
@@ -191,7 +206,7 @@ def dequantize(q: torch.Tensor, scale, zero_point: float = 0.0,
     else:
         gran = L.Q8_PER_TENSOR
         s = torch.tensor([float(scale)], dtype=torch.float64, device=q.device)
-    y = torch.empty(q.shape, dtype=torch.float32, device=q.device) if out is None else out
+    y = _out(out, q.shape, torch.float32, q, "out")
     _call("q8_dequantize", _ptr(q), _SRC[q.dtype], M, K, _ptr(s), gran, float(zero_point),
           _ptr(y), _stream(), keep=(s,))
     return y
@@ -230,16 +245,6 @@ def _mk(A, B):
     return M, N, K
 
 
-def quantized_dot(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """quantized_dot (ops/quantization.ts:103-155) with lhs_contracting=[1],
-    rhs_contracting=[1]: int32 acc[m,n] = sum_k A[m,k] * B[n,k]."""
-    M, N, K = _mk(A, B)
-    out = torch.empty((M, N), dtype=torch.int32, device=A.device) if out is None else out
-    _call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT, 0.0,
-           None, L.Q8_ACT_NONE, L.Q8_I32, _ptr(out), _stream())
-    return out
-
-
 def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor,
             bias: torch.Tensor | None = None, act: str | None = None,
             out: torch.Tensor | None = None) -> torch.Tensor:
@@ -255,7 +260,7 @@ def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor
         _need(bias, torch.float32, "bias")
         if bias.numel() != N:
             raise ValueError("qlinear: bias must have N elements")
-    out = torch.empty((M, N), dtype=torch.float32, device=A.device) if out is None else out
+    out = _out(out, (M, N), torch.float32, A, "out")
     _call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0,
            _ptr(sA), L.Q8_PER_TOKEN if sA.numel() == M and M != 1 else L.Q8_PER_TENSOR,
            _ptr(sB), L.Q8_PER_CHANNEL if sB.numel() == N and N != 1 else L.Q8_PER_TENSOR,
@@ -280,7 +285,7 @@ def quantized_dot(A: torch.Tensor, B: torch.Tensor, zpA: int = 0, zpB: int = 0,
     _call("q8_quantized_dot_workspace", M, N, K, codes[A.dtype], codes[B.dtype], int(zpA), int(zpB),
            C.byref(ws_bytes))
     ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=A.device)
-    out = torch.empty((M, N), dtype=torch.int32, device=A.device) if out is None else out
+    out = _out(out, (M, N), torch.int32, A, "out")
     _call("q8_quantized_dot", _ptr(A), codes[A.dtype], _ptr(B), codes[B.dtype], M, N, K, int(zpA),
            int(zpB), _ptr(ws), ws_bytes.value, _ptr(out), _stream())
     return out
@@ -308,9 +313,9 @@ def qlinear_dynamic(x: torch.Tensor, Wq: torch.Tensor, sW: torch.Tensor,
         _need(bias, torch.float32, "bias")
         if bias.numel() != N:
             raise ValueError("qlinear_dynamic: bias must have N elements")
-    out = torch.empty((M, N), dtype=torch.float32, device=x.device) if out is None else out
-    xq = torch.empty((M, K), dtype=torch.int8, device=x.device) if xq is None else xq
-    sx = torch.empty(1 if per_tensor else M, dtype=torch.float64, device=x.device) if sx is None else sx
+    out = _out(out, (M, N), torch.float32, x, "out")
+    xq = _out(xq, (M, K), torch.int8, x, "xq")
+    sx = _out(sx, 1 if per_tensor else M, torch.float64, x, "sx")
     _call("q8_qlinear_dynamic", _ptr(x), M, K, L.Q8_PER_TENSOR if per_tensor else L.Q8_PER_TOKEN,
            _ptr(Wq), _ptr(sW), L.Q8_PER_CHANNEL if sW.numel() == N and N != 1 else L.Q8_PER_TENSOR,
            N, _ptr(bias), _ACT[act], _ptr(out), _ptr(xq), _ptr(sx), _stream())
@@ -323,7 +328,7 @@ def qlinear_pt(A: torch.Tensor, B: torch.Tensor, s_out: float,
     """Per-tensor form (quantization_pass.ts:335-355): y = fround(acc * s_out),
     s_out = lhs_scale * rhs_scale in f64."""
     M, N, K = _mk(A, B)
-    out = torch.empty((M, N), dtype=torch.float32, device=A.device) if out is None else out
+    out = _out(out, (M, N), torch.float32, A, "out")
     _call("q8_gemm", _ptr(A), _ptr(B), M, N, K, 0, 0, None, 0, None, 0, L.Q8_EPI_PT,
            float(s_out), _ptr(bias), _ACT[act], L.Q8_F32, _ptr(out), _stream())
     return out
@@ -342,7 +347,7 @@ def qlinear_requant(A: torch.Tensor, sA: torch.Tensor | None, B: torch.Tensor,
         _need(bias, torch.float32, "bias")
         if bias.numel() != N:
             raise ValueError("qlinear_requant: bias must have N elements")
-    out = torch.empty((M, N), dtype=torch.int8, device=A.device) if out is None else out
+    out = _out(out, (M, N), torch.int8, A, "out")
     _need(out, torch.int8, "qlinear_requant out")
     if s_out is None:
         _need(sA, torch.float64, "sA")
@@ -385,7 +390,7 @@ def qlinear_w4(xq: torch.Tensor, sx: torch.Tensor, Wq4: torch.Tensor, sw: torch.
         raise ValueError("qlinear_w4: shapes do not match K")
     if bias is not None:
         _need(bias, torch.float32, "bias")
-    out = torch.empty((M, N), dtype=torch.float32, device=xq.device) if out is None else out
+    out = _out(out, (M, N), torch.float32, xq, "out")
     _call("q8_gemv_w4", _ptr(xq), _ptr(sx), L.Q8_PER_TOKEN if sx.numel() == M and M != 1 else L.Q8_PER_TENSOR,
           _ptr(Wq4), _ptr(sw), M, N, K, group_size, _ptr(bias), _ACT[act], _ptr(out), _stream())
     return out

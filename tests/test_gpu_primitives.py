@@ -137,6 +137,25 @@ def test_quantize_static_rejects_nonpositive_scale(ops):
         ops.quantize(torch.zeros(4, device=DEV), -1.0)
 
 
+
+def test_caller_outputs_are_checked(ops):
+    """Caller-supplied output tensors of the wrong dtype, size or device are
+    refused before any launch (the kernels write M*N elements)."""
+    A = torch.zeros((32, 64), dtype=torch.int8, device=DEV)
+    B = torch.zeros((48, 64), dtype=torch.int8, device=DEV)
+    sA = torch.ones(32, dtype=torch.float64, device=DEV)
+    sB = torch.ones(48, dtype=torch.float64, device=DEV)
+    with pytest.raises(ValueError):
+        ops.qlinear(A, sA, B, sB, out=torch.empty((32, 47), dtype=torch.float32, device=DEV))
+    with pytest.raises(TypeError):
+        ops.quantized_dot(A, B, out=torch.empty((32, 48), dtype=torch.float32, device=DEV))
+    with pytest.raises(ValueError):
+        ops.quantized_dot(A, B, out=torch.empty((32, 48), dtype=torch.int32))
+    x = torch.zeros((8, 64), dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError):
+        ops.quantize_per_token(x, scales=torch.empty(7, dtype=torch.float64, device=DEV))
+    assert ops.quantized_dot(A, B, out=torch.empty((32, 48), dtype=torch.int32, device=DEV)).shape == (32, 48)
+
 # ------------------------------------------------------------------ dequantize
 def test_dequantize_rows_i8(ops, oracle):
     x = edge_rows(oracle, 1024)

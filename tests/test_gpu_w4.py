@@ -66,10 +66,11 @@ def test_pack_int4_matches_oracle(ops, oracle, N, K, g):
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 16])
 # (11008, 4096) and (5000, 8192) make every workgroup of the dot4 kernel walk
-# two blocks of rows (prefetch path); (19, 96) has 256-row blocks; for
-# 2 <= M <= 16 the MFMA kernel takes K <= 4096 with whole groups per quarter
-# of K: 8, 16 and 32 steps per wave, a non-power-of-two group (96), one
-# group per wave (1024), N not a multiple of 16
+# two blocks of rows (prefetch path); (19, 96) has 256-row blocks; the MFMA
+# kernel (M >= 3) sees spans of several groups (32, 64, 128), a group of 96
+# (spans of 480 codes: a partial last step), groups of 1024 and 2048 (one
+# span per group or half a group), K below one round (96, 128), many rounds
+# (8192), N not a multiple of 16
 @pytest.mark.parametrize("N,K,g", [(4096, 4096, 128), (1000, 4096, 32), (77, 2048, 2048), (33, 8192, 64),
                                    (19, 96, 32), (11, 160, 80), (11008, 4096, 128), (5000, 8192, 64),
                                    (77, 1536, 96), (11, 4096, 1024), (5, 128, 32), (300, 1024, 64)])
@@ -83,6 +84,31 @@ def test_gemv_w4_matches_oracle(ops, oracle, M, N, K, g):
     bias = r.uniform((N,), -0.1, 0.1)
     print(f"gemv_w4 M={M} N={N} K={K} g={g}", flush=True)
     for b, act in ((None, "none"), (bias, "silu")):
+        want = oracle.gemv_w4(xq, sx, wq4, sw, K, g, bias=b, act=act)
+        got = ops.qlinear_w4(dev(xq), dev(sx), dev(wq4), dev(sw), K, g,
+                             bias=None if b is None else dev(b), act=act)
+        same_bits(host(got), want)
+
+
+@pytest.mark.parametrize("M", [1, 3, 16, 20, 33])
+# K above 8192 / non-power-of-two groups (no dot4 plan: the MFMA kernel for
+# every M, also M = 1), groups split over spans (1536: 3 spans of 512, so a
+# round of 2048 codes sees up to two group ends; 640: spans of 320), an odd
+# round count, and token blocks (M = 20, 33: a partial block of 16)
+# (3000, 11008) with M = 20, 33: more blocks than two per CU, the 4-wave shape
+@pytest.mark.parametrize("N,K,g", [(300, 11008, 128), (70, 11008, 32), (40, 3072, 1536), (33, 1280, 640),
+                                   (17, 12288, 64), (129, 4096, 4096), (3000, 11008, 128)])
+def test_gemv_w4_mfma_rounds(ops, oracle, M, N, K, g):
+    r = oracle.Rng(M * 7 + N + K + g)
+    x = r.normal((M, K))
+    W = r.normal((N, K), 0.0, 0.02)
+    W[1, :g] = 0.0                      # an all-zero group
+    sx = oracle.scales_per_token(x)
+    xq = oracle.quantize_rows(x, sx)
+    wq4, sw = ref_pack(oracle, W, g)
+    bias = r.uniform((N,), -0.1, 0.1)
+    print(f"gemv_w4 rounds M={M} N={N} K={K} g={g}", flush=True)
+    for b, act in ((None, "none"), (bias, "relu")):
         want = oracle.gemv_w4(xq, sx, wq4, sw, K, g, bias=b, act=act)
         got = ops.qlinear_w4(dev(xq), dev(sx), dev(wq4), dev(sw), K, g,
                              bias=None if b is None else dev(b), act=act)
