@@ -320,8 +320,11 @@ def cpu_baseline(rows=256):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the part ramps its clocks over the first few tens of milliseconds of
+    # load: 400 warm steps (~40 ms) reach the steady state, 5 leave the
+    # timed steps on the ramp (up to ~15% slower, varying run to run)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceilings", action="store_true",
