@@ -276,7 +276,8 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
  * per byte (element 2j in the low nibble, two's complement) into
  * Wq4 [N, K/2].  group_size must be even and divide K, so every group lies
  * in one row; scales has N * K / group_size entries (row n's groups at
- * n * K / group_size). */
+ * n * K / group_size).  N * K / 2 must stay below 2^31 (q8_gemv_w4's
+ * limit). */
 int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size,
                         uint8_t* Wq4, double* scales, void* stream);
 

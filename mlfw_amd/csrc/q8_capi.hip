@@ -546,6 +546,8 @@ int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size
   Q8_REQUIRE(group_size >= 2 && group_size % 2 == 0 && K % group_size == 0,
              "q8_pack_weight_int4: group_size (%lld) must be even and divide K (%lld)",
              (long long)group_size, (long long)K);
+  Q8_REQUIRE(N * (K / 2) < (1LL << 31), "q8_pack_weight_int4: weight too large (%lld x %lld; "
+             "q8_gemv_w4 addresses N * K / 2 bytes with 32-bit offsets)", (long long)N, (long long)K);
   Q8_REQUIRE(N * K == 0 || (W && Wq4 && scales), "q8_pack_weight_int4: NULL pointer");
   int rc = ensure_current(nullptr);
   if (rc != Q8_OK) return rc;

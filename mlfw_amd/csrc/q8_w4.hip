@@ -48,25 +48,41 @@ __device__ __forceinline__ int w4_code(float w, double s) {
   return (int)r;
 }
 
-// One thread per group: absmax, scale, then codes (two per byte).
+// A team of L lanes per group (L = the largest power of two <= 64 that
+// divides group / 2, teams aligned within the wave): lane j of the team
+// takes the code pairs j, j + L, j + 2L, ... so the team's loads and byte
+// stores are contiguous; the absmax is combined across the team by xor
+// shuffles (NaN never compares greater, so it never becomes the max), then
+// every lane rounds its own pairs.
 __global__ __launch_bounds__(256) void k_pack_w4(const float* __restrict__ W, int64_t total,
-                                                 int64_t group, uint8_t* __restrict__ wq,
+                                                 int64_t group, int L, uint8_t* __restrict__ wq,
                                                  double* __restrict__ scales) {
-  const int64_t g = blockIdx.x * 256LL + threadIdx.x;
+  const int64_t t = blockIdx.x * 256LL + threadIdx.x;
   const int64_t ngroups = total / group;
-  if (g >= ngroups) return;
-  const float* w = W + g * group;
+  const int64_t g = t / L;
+  const int j = (int)(t - g * L);
+  const bool live = g < ngroups;                 // dead lanes still join the shuffles
+  const int64_t pairs = group / 2;
+  const float* w = W + (live ? g : 0) * group;   // 4-byte aligned only: two dword loads per pair
   double amax = 0.0;
-  for (int64_t i = 0; i < group; ++i) {
-    const double a = fabs((double)w[i]);
-    if (a > amax) amax = a;                      // NaN never compares greater
+  if (live) {
+    for (int64_t p = j; p < pairs; p += L) {
+      const double a = fabs((double)w[2 * p]), b = fabs((double)w[2 * p + 1]);
+      if (a > amax) amax = a;
+      if (b > amax) amax = b;
+    }
   }
+  for (int o = L >> 1; o >= 1; o >>= 1) {
+    const double other = __shfl_xor(amax, o, 64);
+    if (other > amax) amax = other;
+  }
+  if (!live) return;
   double s = amax / 7.0;
   if (s == 0.0 || s != s) s = 1e-10;
-  scales[g] = s;
-  uint8_t* out = wq + (g * group) / 2;
-  for (int64_t i = 0; i < group; i += 2)
-    out[i / 2] = (uint8_t)((w4_code(w[i], s) & 0xF) | ((w4_code(w[i + 1], s) & 0xF) << 4));
+  if (j == 0) scales[g] = s;
+  uint8_t* out = wq + g * pairs;
+  for (int64_t p = j; p < pairs; p += L)
+    out[p] = (uint8_t)((w4_code(w[2 * p], s) & 0xF) | ((w4_code(w[2 * p + 1], s) & 0xF) << 4));
 }
 
 // Activation chunk (32 bytes) -> even / odd element dwords and 8 * sum.
@@ -582,8 +598,11 @@ hipError_t launch_pack_w4(const float* W, int64_t N, int64_t K, int64_t group, u
                           double* scales, hipStream_t st) {
   const int64_t ngroups = N * K / group;
   if (ngroups == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_pack_w4, dim3((unsigned)((ngroups + 255) / 256)), dim3(256), 0, st, W,
-                     N * K, group, wq4, scales);
+  int L = 1;                                     // lanes per group: a power of two dividing group / 2
+  while (L < 64 && (group / 2) % (2 * L) == 0) L *= 2;
+  const int64_t threads = ngroups * L;
+  hipLaunchKernelGGL(k_pack_w4, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, W,
+                     N * K, group, L, wq4, scales);
   return hipGetLastError();
 }
 

@@ -51,7 +51,9 @@ def ref_pack(oracle, W, g):
     return pack_int4(q), s
 
 
-@pytest.mark.parametrize("N,K,g", [(64, 4096, 128), (37, 1024, 32), (5, 96, 48), (300, 8192, 2048)])
+# lane teams of 64 (g = 128, 2048), 16 (32), 8 (48), 2 (12) and 1 (2, 6)
+@pytest.mark.parametrize("N,K,g", [(64, 4096, 128), (37, 1024, 32), (5, 96, 48), (300, 8192, 2048),
+                                   (3, 12, 2), (7, 30, 6), (9, 36, 12)])
 def test_pack_int4_matches_oracle(ops, oracle, N, K, g):
     r = oracle.Rng(N + K + g)
     W = r.normal((N, K), 0.0, 0.02)
@@ -59,6 +61,21 @@ def test_pack_int4_matches_oracle(ops, oracle, N, K, g):
     W[1, 3] = np.nan                    # NaN: never the max, code 0
     W[2, 5] = 7.0                       # outlier
     wq, s = ops.pack_weight_int4(dev(W), g)
+    want_q, want_s = ref_pack(oracle, W, g)
+    same_bits(host(s), want_s)
+    same_bits(host(wq), want_q)
+
+
+def test_pack_int4_unaligned_source(ops, oracle):
+    """A weight that starts 4 bytes into an allocation (4-byte aligned only)."""
+    N, K, g = 33, 256, 64
+    r = oracle.Rng(91)
+    W = r.normal((N, K), 0.0, 0.02)
+    buf = torch.empty(N * K + 1, dtype=torch.float32, device=DEV)
+    Wd = buf[1:].view(N, K)
+    Wd.copy_(torch.from_numpy(W))
+    assert Wd.data_ptr() % 8 == 4
+    wq, s = ops.pack_weight_int4(Wd, g)
     want_q, want_s = ref_pack(oracle, W, g)
     same_bits(host(s), want_s)
     same_bits(host(wq), want_q)
