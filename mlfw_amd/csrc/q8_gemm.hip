@@ -227,7 +227,9 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   constexpr bool OUT_I32 = Epi<EPI>::OUT_I32;
   constexpr int MODE = Epi<EPI>::MODE;
   extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is uniform: kept in an SGPR, the LDS destinations of the
+  // copies (M0) follow without a VGPR round trip
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -273,6 +275,14 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   const uint32_t bytes_a = (uint32_t)rows_a * (uint32_t)K;
   const uint32_t bytes_b = (uint32_t)rows_b * (uint32_t)K;
   const int KT = (K + BK - 1) / BK;
+  // offsets for the last stage when K is not a multiple of BK: the lane's
+  // chunk past K reads past the buffer's end (zero) instead of the next row
+  const int kb_last = (KT - 1) * BK;
+  uint32_t offa_t[C::A_LOADS], offb_t[C::B_LOADS];
+#pragma unroll
+  for (int j = 0; j < C::A_LOADS; ++j) offa_t[j] = kb_last + kca[j] >= K ? OOB : offa[j];
+#pragma unroll
+  for (int j = 0; j < C::B_LOADS; ++j) offb_t[j] = kb_last + kcb[j] >= K ? OOB : offb[j];
 
   // Copies of the A (resp. B) half of K stage kt into `stage`.  kt >= KT
   // copies nothing: with num_records 0 every lane is out of range and
@@ -286,7 +296,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const bool tail = kb + BK > K;
 #pragma unroll
     for (int j = 0; j < C::A_LOADS; ++j)
-      copy16_to_lds(ra, sa + j * 16 * BK, (tail && kb + kca[j] >= K) ? OOB : offa[j]);
+      copy16_to_lds(ra, sa + j * 16 * BK, tail ? offa_t[j] : offa[j]);
   };
   auto issue_b = [&](int kt, int8_t* stage) {
     const bool live = kt < KT;
@@ -296,7 +306,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const bool tail = kb + BK > K;
 #pragma unroll
     for (int j = 0; j < C::B_LOADS; ++j)
-      copy16_to_lds(rb, sb + j * 16 * BK, (tail && kb + kcb[j] >= K) ? OOB : offb[j]);
+      copy16_to_lds(rb, sb + j * 16 * BK, tail ? offb_t[j] : offb[j]);
   };
 
   // Fragment addresses: byte offset of the fragment row within a stage and
