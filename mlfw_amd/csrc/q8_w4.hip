@@ -295,25 +295,27 @@ __global__ __launch_bounds__(256) void k_gemv_w4(const int8_t* __restrict__ xq,
 // even / odd order (v_perm); a second MFMA with the constant -8 as A adds
 // -8 * sum(x), so the accumulator holds sum x * q exactly.
 //
-// Loads: lane (r, q) of a wave reads 16 packed bytes (a 32-code chunk) of
-// row r, so one instruction covers 64 contiguous bytes of each of 16 rows.
-// A step of a wave is 4 such chunks (128 codes); the 4 x 4 transpose of the
-// chunk dwords between the 4 lanes of a row (v_permlane32_swap, then
-// v_permlane16_swap) makes MFMA j consume chunk j whole, so a chunk never
-// mixes two groups.  Lane (t, q) loads codes 8q..8q+7 of chunk j of token
-// t's activations to match.
+// Loads: in a step of 128 codes, lane (r, q) of a wave reads the 16 packed
+// bytes of chunk q (32 codes) of row r, so one instruction covers 64
+// contiguous bytes of each of 16 rows, and lane (t, q) the 32 activation
+// bytes of the same chunk of token t.  With groups of a multiple of 128
+// codes the whole step lies in one group and MFMA j takes dword j (codes
+// 8j..8j+7) of every lane's chunk.  Otherwise (TR) a 4 x 4 transpose of the
+// dwords between the 4 lanes of a row (v_permlane32_swap, then
+// v_permlane16_swap), of codes and activations alike, makes MFMA j consume
+// chunk j whole, so no MFMA mixes two groups.
 //
 // K is walked in rounds: in round r, wave w of the workgroup's NW takes the
-// span of PS codes at (NW r + w) * PS (PS a multiple of the group, or a
-// divisor of it, of at most 128 * RS codes: one round covers K = 4096 with
-// groups of 128),
-// and splits it into segments of SL = min(PS, group) codes; each segment's
-// int32 sum (exact) goes to LDS [segment][token][row], with the scales of
-// the groups that end in the round.  After one barrier, lane o = (token,
-// row) walks the round's segments in order, adds the pieces of a group in
-// int32 and, when the group is complete, adds acc_g * sw_g to its f64 sum --
-// groups in ascending order, as the definition asks.  LDS holds two round
-// windows, so one barrier per round suffices.
+// span of PS codes at (NW r + w) * PS -- PS a multiple of the group, or a
+// divisor of it, of at most 128 * RS codes (one round covers K = 4096 with
+// groups of 128) -- and splits it into segments of SL = min(PS, group)
+// codes.  Each segment's int32 sum (exact) goes to an LDS window
+// [segment][token][row], with the scales of the groups that end in the
+// round.  After one barrier, lane o = (token, row) walks the round's
+// segments in order, adds the pieces of a group in int32 and, when the
+// group is complete, adds acc_g * sw_g to its f64 sum -- groups in
+// ascending order, as the definition asks.  With more than one round, LDS
+// holds two windows used alternately, so one barrier per round suffices.
 __device__ __forceinline__ v4i w4_mma8(int w, int x0, int x1, v4i acc) {
   const long minus8 = (long)0xF8F8F8F8F8F8F8F8ull;
   const int lo = (w & 0x0F0F0F0F) ^ 0x08080808;         // codes 0,2,4,6 of 8: q + 8
