@@ -130,3 +130,18 @@ def test_gemv_w4_mfma_rounds(ops, oracle, M, N, K, g):
         got = ops.qlinear_w4(dev(xq), dev(sx), dev(wq4), dev(sw), K, g,
                              bias=None if b is None else dev(b), act=act)
         same_bits(host(got), want)
+
+
+@pytest.mark.parametrize("M,N,K,g", [(6, 300, 4096, 128), (1, 70, 11008, 32), (20, 33, 1024, 64)])
+def test_gemv_w4_per_tensor_scale(ops, oracle, M, N, K, g):
+    """One activation scale for every token (sx [1], read with stride 0)."""
+    r = oracle.Rng(M + N + K + g + 5)
+    x = r.normal((M, K))
+    W = r.normal((N, K), 0.0, 0.02)
+    s = oracle.scale_per_tensor(x)
+    xq = oracle.quantize(x.reshape(-1), s).reshape(M, K)
+    wq4, sw = ref_pack(oracle, W, g)
+    print(f"gemv_w4 per-tensor M={M} N={N} K={K} g={g}", flush=True)
+    want = oracle.gemv_w4(xq, np.full(M, s), wq4, sw, K, g, act="silu")
+    got = ops.qlinear_w4(dev(xq), dev(np.array([s])), dev(wq4), dev(sw), K, g, act="silu")
+    same_bits(host(got), want)
