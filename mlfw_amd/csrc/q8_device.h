@@ -134,11 +134,16 @@ __device__ __forceinline__ float relu_js(float v) {
 
 // SiLU decomposed (decomposition_pass.ts:197-203, 224-230), each op rounded:
 // fround(x * fround(1 / fround(1 + fround(exp(-x))))), exp evaluated in f64.
+// The add, divide and multiply are binary32 operations: for +, / and * of
+// binary32 operands, rounding the binary64 result to binary32 gives the
+// correctly rounded binary32 result (53 >= 2 * 24 + 2), which is what the
+// IEEE binary32 instructions compute (no fast-math: the division is the
+// correctly rounded sequence).
 __device__ __forceinline__ float silu_js(float x) {
-  float e = (float)exp(-(double)x);
-  float d = (float)(1.0 + (double)e);
-  float r = (float)(1.0 / (double)d);
-  return (float)((double)x * (double)r);
+  const float e = (float)exp(-(double)x);
+  const float d = 1.0f + e;
+  const float r = 1.0f / d;
+  return x * r;
 }
 
 // Wave64 reductions.

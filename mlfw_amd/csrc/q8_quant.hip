@@ -706,10 +706,9 @@ __global__ __launch_bounds__(TPB) void k_silu_mul_quant_rows(const float* __rest
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t i = tid + (int64_t)j * NT;
-      v[j] = make_float4((float)((double)silu_js(a[j].x) * (double)b[j].x),
-                         (float)((double)silu_js(a[j].y) * (double)b[j].y),
-                         (float)((double)silu_js(a[j].z) * (double)b[j].z),
-                         (float)((double)silu_js(a[j].w) * (double)b[j].w));
+      // fround(silu * up): a binary32 multiply (the exact product, rounded once)
+      v[j] = make_float4(silu_js(a[j].x) * b[j].x, silu_js(a[j].y) * b[j].y,
+                         silu_js(a[j].z) * b[j].z, silu_js(a[j].w) * b[j].w);
       if (i < K4) {
         if (h) reinterpret_cast<float4*>(h + row * K)[i] = v[j];
         const int k = key4(v[j]);
@@ -739,7 +738,7 @@ __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows_scalar(
   for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
     int key = -1;
     for (int64_t i = threadIdx.x; i < K; i += NT) {
-      float v = (float)((double)silu_js(g[row * K + i]) * (double)u[row * K + i]);
+      float v = silu_js(g[row * K + i]) * u[row * K + i];
       if (h) h[row * K + i] = v;
       int k = absmax_key(v);
       key = key > k ? key : k;
@@ -750,7 +749,7 @@ __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows_scalar(
     const bool fast = fast_scale_ok(s);
     const float r32 = (float)(1.0 / s);
     for (int64_t i = threadIdx.x; i < K; i += NT) {
-      float v = (float)((double)silu_js(g[row * K + i]) * (double)u[row * K + i]);
+      float v = silu_js(g[row * K + i]) * u[row * K + i];
       q[row * K + i] = (int8_t)(fast ? quant_sym_fast(v, r32, s) : quant_exact(v, s, 0.0, -128, 127));
     }
   }
