@@ -302,6 +302,32 @@ def test_qlinear_large_rowcol_exact(ops, oracle, M, N, K):
     same_bits(host(y), ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 260, 4096), (8, 300, 4096), (2, 77, 8192)])
+def test_qlinear_large_accumulators(ops, oracle, M, N, K):
+    """Saturated rows and columns (|acc| up to K * 128 * 128 = 2^26 at
+    K = 4096, beyond 2^24 where an int32 stops being exactly a binary32):
+    the epilogue's f64 path, in strips that also hold small accumulators,
+    on the MFMA GEMM (M > 16) and the GEMV kernels."""
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    A = torch.randint(-128, 128, (M, K), dtype=torch.int8, device=DEV, generator=g)
+    B = torch.randint(-128, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    A[0, :] = 127
+    A[M - 1, :] = -128
+    B[:5, :] = 127
+    B[5:9, :] = -128
+    B[N - 1, : K // 2] = -128
+    sA = torch.rand(M, dtype=torch.float64, device=DEV, generator=g) * 1e-2 + 1e-4
+    sB = torch.rand(N, dtype=torch.float64, device=DEV, generator=g) * 1e-3 + 1e-5
+    bias = torch.rand(N, dtype=torch.float32, device=DEV, generator=g) - 0.5
+    for act in (None, "silu"):
+        y = ops.qlinear(A, sA, B, sB, bias=bias, act=act)
+        acc = (A.double() @ B.double().t().contiguous()).to(torch.int32)
+        a = host(acc)
+        assert np.abs(a).max() > (1 << 24)
+        ref = oracle.epilogue(a, "rowcol", host(sA), host(sB), bias=host(bias), act=act or "none")
+        same_bits(host(y), ref)
+
+
 def test_qlinear_pt_epilogue(ops, oracle):
     rng = np.random.default_rng(3)
     A, B = rand_i8(rng, (48, 256)), rand_i8(rng, (72, 256))
