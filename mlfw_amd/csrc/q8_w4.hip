@@ -415,6 +415,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
       scv[u2] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(
                     rs, (sc_off[u2] + (uint32_t)g) * 8u, 0, 0));
     }
+    // an unconditional use of every loaded value: the compiler would
+    // otherwise sink a step's loads into the branch that consumes them,
+    // behind all the others, and wait for every load before the first MFMA
+#pragma unroll
+    for (int s = 0; s < RS; ++s) asm volatile("" ::"v"(wv[s]), "v"(xv[s][0]), "v"(xv[s][1]));
     __builtin_amdgcn_sched_barrier(0);
 
     // MFMAs over the span's chunks; segment sums to LDS [segment][token][row]
