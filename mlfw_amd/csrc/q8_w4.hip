@@ -337,7 +337,7 @@ __device__ __forceinline__ v4i w4_transpose4(v4i v) {
   return v4i{(int)t01[0], (int)t01[1], (int)t23[0], (int)t23[1]};
 }
 
-template <int NW, int RS, bool TR>
+template <int NW, int RS, bool TR, bool ONE>
 __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restrict__ xq,
                                                           const double* __restrict__ sx,
                                                           int sx_stride,
@@ -389,8 +389,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
   int gacc = 0, pieces = 0, gdone = 0;                  // groups split over spans
   const int P = group > PS ? group / PS : 1;            // spans per group
   int* const win0 = reinterpret_cast<int*>(lds);
-  for (int r = 0; r < rounds; ++r) {
-    int* wbuf = win0 + (r & 1) * win;                   // two windows (one if one round):
+  // ONE: a single round (K <= NW * PS), known at compile time: no loop, and
+  // the registers of the round are allocated as straight-line code
+  for (int r = 0; r < (ONE ? 1 : rounds); ++r) {
+    int* wbuf = ONE ? win0 : win0 + (r & 1) * win;     // two windows (one if one round):
                                                         // one barrier per round
     const int k0 = (NW * r + wave) * PS;                // this wave's span
     const int gfirst = (NW * r * PS) / group;           // first group that can end in round r
@@ -522,15 +524,19 @@ struct W4MPlan {
   int PS, segw, ng;                       // span per wave and round, segments per span,
   size_t lds;                             // groups that can end in a round; LDS bytes
   bool tr;                                // chunk transpose (groups not a multiple of 128)
+  bool one;                               // one round covers K
 };
 
 // Span per wave and round: a multiple of the group (as many groups as fit
 // in 4 steps = 512 codes and the LDS budget) or, for groups above 512
 // codes, the largest divisor of the group of at most 512 codes.
-// Workgroup shape: 8 waves of 4-step spans (94 VGPRs: two workgroups per
-// CU) while the grid fits the chip at two per CU, else 4 waves of 8-step
-// spans (152 VGPRs: three per CU) for groups of a multiple of 128.
-bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl) {
+// Workgroup shape: 8 waves of 4-step spans while the grid fits the chip
+// (two workgroups per CU at 94 VGPRs, three when one round covers K and the
+// kernel needs 68), else 4 waves of 8-step spans (three per CU) for groups
+// of a multiple of 128.
+bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int nw = 8);
+
+bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int nw) {
   if (M < 1 || K < 32 || K % 32 != 0 || group < 32 || group % 32 != 0 || K % group != 0) return false;
   if (K > (int64_t)1 << 24) return false;                     // 32-bit buffer offsets
   if ((M + 15) / 16 > 65535) return false;                    // token blocks: grid.y
@@ -538,10 +544,8 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl) {
   // groups of a multiple of 128 codes need no chunk transpose, with spans of
   // whole 128-code steps; other groups work in 32-code chunks
   pl->tr = group % 128 != 0;
-  const int64_t blocks = ((N + 15) / 16) * ((M + 15) / 16);
-  const bool wide = !pl->tr && blocks > 2 * (int64_t)cu_count();
-  pl->nw = wide ? 4 : 8;
-  pl->rs = wide ? 8 : 4;
+  pl->nw = nw;
+  pl->rs = nw == 8 ? 4 : 8;
   const int64_t NW = pl->nw, span = 128 * pl->rs;
   const int64_t unit = pl->tr ? 32 : 128;
   // LDS: one window of segment sums and scales per round in flight (two
@@ -568,7 +572,16 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl) {
   const int64_t rc = NW * PS;
   pl->ng = (int)(rc / group + (rc % group != 0));
   pl->lds = (size_t)lds_of(PS, pl->segw, pl->ng);
-  return pl->ng <= 64 && pl->lds <= 65536;
+  pl->one = K <= NW * PS;
+  if (!(pl->ng <= 64 && pl->lds <= 65536)) return false;
+  if (nw == 8 && !pl->tr) {
+    const int64_t blocks = ((N + 15) / 16) * ((M + 15) / 16);
+    if (blocks > (pl->one ? 3 : 2) * (int64_t)cu_count()) {
+      W4MPlan p4;
+      if (w4m_plan(M, N, K, group, &p4, 4)) *pl = p4;
+    }
+  }
+  return true;
 }
 }  // namespace
 
@@ -657,8 +670,16 @@ hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, con
   if (mfma && (!dot4 || M >= 3)) {
     const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16)), block(64 * mp.nw);
 #define Q8_W4M(NW, RS, TR)                                                                        \
-  hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR>), grid, block, mp.lds, st, xq, sx, sx_stride, wq4, \
-                     sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw, mp.ng, bias, act, y)
+  do {                                                                                            \
+    if (mp.one)                                                                                   \
+      hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR, true>), grid, block, mp.lds, st, xq, sx,     \
+                         sx_stride, wq4, sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw,  \
+                         mp.ng, bias, act, y);                                                    \
+    else                                                                                          \
+      hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR, false>), grid, block, mp.lds, st, xq, sx,    \
+                         sx_stride, wq4, sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw,  \
+                         mp.ng, bias, act, y);                                                    \
+  } while (0)
     if (mp.nw == 4) Q8_W4M(4, 8, false);
     else if (mp.tr) Q8_W4M(8, 4, true);
     else Q8_W4M(8, 4, false);

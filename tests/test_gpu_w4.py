@@ -112,9 +112,12 @@ def test_gemv_w4_matches_oracle(ops, oracle, M, N, K, g):
 # every M, also M = 1), groups split over spans (1536: 3 spans of 512, so a
 # round of 2048 codes sees up to two group ends; 640: spans of 320), an odd
 # round count, and token blocks (M = 20, 33: a partial block of 16)
-# (3000, 11008) with M = 20, 33: more blocks than two per CU, the 4-wave shape
+# (3000, 11008) with M = 33: more blocks than two per CU over several rounds,
+# the 4-wave shape; (11008, 4096) with M = 20, 33: more than three per CU in
+# one round, the 4-wave one-round kernel
 @pytest.mark.parametrize("N,K,g", [(300, 11008, 128), (70, 11008, 32), (40, 3072, 1536), (33, 1280, 640),
-                                   (17, 12288, 64), (129, 4096, 4096), (3000, 11008, 128)])
+                                   (17, 12288, 64), (129, 4096, 4096), (3000, 11008, 128),
+                                   (11008, 4096, 128)])
 def test_gemv_w4_mfma_rounds(ops, oracle, M, N, K, g):
     r = oracle.Rng(M * 7 + N + K + g)
     x = r.normal((M, K))
