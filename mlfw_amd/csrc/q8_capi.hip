@@ -241,7 +241,10 @@ int q8_d2h(void* dst, const void* src, size_t bytes, void* stream) {
 int q8_memset(void* dst, int value, size_t bytes, void* stream) {
   if (bytes == 0) return Q8_OK;
   Q8_REQUIRE(dst != nullptr, "q8_memset: dst is NULL");
-  return launched(hipMemsetAsync(dst, value, bytes, as_stream(stream)), "q8_memset");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  // a fill kernel, not hipMemsetAsync: callers may capture this in a HIP graph
+  return launched(q8::launch_fill_u8(dst, value, (int64_t)bytes, as_stream(stream)), "q8_memset");
 }
 
 int q8_stream_sync(void* stream) {

@@ -56,6 +56,7 @@ hipError_t launch_pack_w4(const float* W, int64_t N, int64_t K, int64_t group, u
 // operand into its int8 form, int8 row sums, and the rank-1 correction of
 // the int32 GEMM result.
 hipError_t launch_flip_u8(const uint8_t* src, int8_t* dst, int64_t n, hipStream_t st);
+hipError_t launch_fill_u8(void* dst, int value, int64_t n, hipStream_t st);
 hipError_t launch_row_sums_i8(const int8_t* X, int64_t rows, int64_t K, int32_t* out,
                               hipStream_t st);
 hipError_t launch_zp_correct(int32_t* acc, int64_t M, int64_t N, const int32_t* rsA,

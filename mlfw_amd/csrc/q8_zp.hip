@@ -78,6 +78,35 @@ __global__ __launch_bounds__(256) void k_zp_correct(int32_t* __restrict__ acc, i
   }
 }
 
+// dst[0..n) = value (a byte): 16-byte stores over the aligned middle, byte
+// stores at the ends.  A kernel rather than hipMemsetAsync, so that a
+// caller may capture q8_memset in a HIP graph.
+__global__ __launch_bounds__(256) void k_fill_u8(uint8_t* __restrict__ dst, int64_t head,
+                                                 int64_t n16, int64_t n, uint32_t v4) {
+  const int64_t t0 = blockIdx.x * 256LL + threadIdx.x, stride = (int64_t)gridDim.x * 256;
+  v4i* mid = reinterpret_cast<v4i*>(dst + head);
+  const v4i v = {(int)v4, (int)v4, (int)v4, (int)v4};
+  for (int64_t j = t0; j < n16; j += stride) mid[j] = v;
+  const int64_t tail0 = head + 16 * n16;
+  for (int64_t j = t0; j < head + (n - tail0); j += stride) {
+    const int64_t i = j < head ? j : tail0 + (j - head);
+    dst[i] = (uint8_t)(v4 & 0xffu);
+  }
+}
+
+hipError_t launch_fill_u8(void* dst, int value, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  uint8_t* d = static_cast<uint8_t*>(dst);
+  int64_t head = (int64_t)((16 - (reinterpret_cast<uintptr_t>(d) & 15)) & 15);
+  if (head > n) head = n;
+  const int64_t n16 = (n - head) / 16;
+  const uint32_t b = (uint32_t)value & 0xffu;
+  const int64_t items = n16 > 0 ? n16 : n;
+  hipLaunchKernelGGL(k_fill_u8, dim3((unsigned)zp_grid(items, 8 * cu_count())), dim3(256), 0, st, d,
+                     head, n16, n, b * 0x01010101u);
+  return hipGetLastError();
+}
+
 hipError_t launch_flip_u8(const uint8_t* src, int8_t* dst, int64_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
   const int vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;

@@ -156,6 +156,47 @@ def test_caller_outputs_are_checked(ops):
         ops.quantize_per_token(x, scales=torch.empty(7, dtype=torch.float64, device=DEV))
     assert ops.quantized_dot(A, B, out=torch.empty((32, 48), dtype=torch.int32, device=DEV)).shape == (32, 48)
 
+
+@pytest.mark.parametrize("off,n", [(0, 0), (3, 1), (1, 15), (0, 4096), (5, 100003)])
+def test_memset_fill_kernel(ops, off, n):
+    """q8_memset writes exactly [off, off + n) (unaligned heads and tails)."""
+    from mlfw_amd import _lib
+    import ctypes as C
+    buf = torch.full((n + 64,), 7, dtype=torch.uint8, device=DEV)
+    _lib.call("q8_memset", C.c_void_p(buf.data_ptr() + off), 0xAB, n, ops._stream())
+    want = np.full(n + 64, 7, np.uint8)
+    want[off:off + n] = 0xAB
+    np.testing.assert_array_equal(host(buf), want)
+
+
+def test_memset_in_a_graph(ops):
+    """q8_memset captured in a HIP graph (with a quantize after it) gives the
+    right bytes on every replay, with eager writes to the buffer between."""
+    from mlfw_amd import _lib
+    import ctypes as C
+    buf = torch.zeros(5000, dtype=torch.uint8, device=DEV)
+    x = torch.linspace(-3, 3, 8 * 64, device=DEV).reshape(8, 64)
+    q = torch.empty((8, 64), dtype=torch.int8, device=DEV)
+    s = torch.empty(8, dtype=torch.float64, device=DEV)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            _lib.call("q8_memset", C.c_void_p(buf.data_ptr() + 1), 0x5A, 4099, ops._stream())
+            ops.quantize_per_token(x, q, s)
+    q_eager, s_eager = ops.quantize_per_token(x)
+    for rep in range(3):
+        buf.fill_(rep)
+        q.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        b = host(buf)
+        assert b[0] == rep and b[4100] == rep and (b[1:4100] == 0x5A).all(), rep
+        np.testing.assert_array_equal(host(q), host(q_eager))
+        np.testing.assert_array_equal(host(s), host(s_eager))
+
 # ------------------------------------------------------------------ dequantize
 def test_dequantize_rows_i8(ops, oracle):
     x = edge_rows(oracle, 1024)
