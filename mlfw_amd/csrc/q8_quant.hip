@@ -191,7 +191,7 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // reads zeros without touching memory; the loads in flight are then the
 // same on every path and the wait before a row's reduction leaves the
 // next row's loads outstanding.
-template <int VPT, bool FULL>
+template <int VPT, bool FULL, bool NTS>
 __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t M,
                                                    int64_t K, int8_t* __restrict__ q,
                                                    double* __restrict__ scales) {
@@ -236,13 +236,18 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int i = tid + j * NT;
-      if (FULL || i < K4) __builtin_nontemporal_store(quant4_sym(v[j], fast, r32, s), qr + i);
+      if (FULL || i < K4) {
+        const int c = quant4_sym(v[j], fast, r32, s);
+        if constexpr (NTS) __builtin_nontemporal_store(c, qr + i);
+        else qr[i] = c;
+      }
     }
     if constexpr (!FULL) {
       for (int64_t i = tid + (int64_t)VPT * NT; i < K4; i += NT) {
         const v4f t = xr[i];
-        __builtin_nontemporal_store(quant4_sym(make_float4(t.x, t.y, t.z, t.w), fast, r32, s),
-                                    qr + i);
+        const int c = quant4_sym(make_float4(t.x, t.y, t.z, t.w), fast, r32, s);
+        if constexpr (NTS) __builtin_nontemporal_store(c, qr + i);
+        else qr[i] = c;
       }
     }
   };
@@ -305,14 +310,21 @@ hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, do
   // workgroup: equal for 2048-4096 rows, 10-20% slower for 16384); a grid
   // capped at 2^20 workgroups walks the rest with the pipelined loop.
   const int workers = (int)(M < 1048576 ? M : 1048576);
+  // The codes are read next by the GEMM.  Up to 32 MiB (an eighth of the
+  // 256 MB MALL) they are stored normally and stay in the cache for it (C3
+  // step, 16 MiB of codes: 86.5 -> 85.1 us); larger outputs gain nothing
+  // there and use non-temporal stores, faster for this kernel (64 MiB:
+  // 53.9 us instead of 57.2 us).
+  const bool nts = M * K > ((int64_t)32 << 20);
+#define Q8_QROWS_S(V, FULLK, S)                                                                   \
+  hipLaunchKernelGGL((k_quant_rows<V, FULLK, S>), dim3(workers), dim3(NT), 0, st, x, M, K, q, scales)
 #define Q8_QROWS(V)                                                                          \
   do {                                                                                       \
-    if (K4 == (V) * NT)                                                                      \
-      hipLaunchKernelGGL((k_quant_rows<V, true>), dim3(workers), dim3(NT), 0, st, x, M, K, q, \
-                         scales);                                                            \
-    else                                                                                     \
-      hipLaunchKernelGGL((k_quant_rows<V, false>), dim3(workers), dim3(NT), 0, st, x, M, K,  \
-                         q, scales);                                                         \
+    if (K4 == (V) * NT) {                                                                    \
+      if (nts) Q8_QROWS_S(V, true, true); else Q8_QROWS_S(V, true, false);                   \
+    } else {                                                                                 \
+      if (nts) Q8_QROWS_S(V, false, true); else Q8_QROWS_S(V, false, false);                 \
+    }                                                                                        \
   } while (0)
   if (K4 <= 1 * NT) Q8_QROWS(1);
   else if (K4 <= 2 * NT) Q8_QROWS(2);
@@ -320,6 +332,7 @@ hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, do
   else if (K4 <= 8 * NT) Q8_QROWS(8);
   else Q8_QROWS(12);
 #undef Q8_QROWS
+#undef Q8_QROWS_S
   return hipGetLastError();
 }
 
