@@ -335,7 +335,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the int8 path has no multi-GPU code (DESIGN.md describes how it would shard)",
+              "the int8 path has no multi-GPU code: every kernel runs on one GPU's share at its real shape",
               file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
