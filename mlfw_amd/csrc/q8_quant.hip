@@ -182,8 +182,10 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // One block per row (grid-stride over rows).  The first VPT*1024 elements
 // of the row stay in registers between the absmax reduction and the
 // quantize, so such rows are read once; longer rows re-read the tail.
-// Loads and stores are non-temporal: the stream is touched once, and
-// keeping it out of the caches measured ~5-10% faster than plain accesses.
+// Loads are non-temporal: the input is touched once, and keeping it out of
+// the caches measured ~5-10% faster than plain loads.  Stores are
+// non-temporal too (NTS) unless the codes are small enough to stay in the
+// MALL for the GEMM that reads them next (see launch_quant_rows).
 // A block with several rows loads the next row while it reduces and
 // quantizes the current one (two register sets, used alternately).  Every
 // row is loaded through its own buffer resource whose size is 0 past the
