@@ -156,6 +156,14 @@ int q8_quantize_static(const float* x, int64_t n, double scale, double zero_poin
 int q8_quantize_rows(const float* x, int64_t M, int64_t K, int mode,
                      int8_t* q, double* scales, void* stream);
 
+/* q8_quantize_rows with Q8_PER_TOKEN for a row-strided input: row m of x
+ * starts at x + m * ldx (ldx >= K), e.g. one slice of a wider projection
+ * output; q stays [M, K] contiguous.  No counterpart in the reference (its
+ * tensors are contiguous); the codes and scales are those of the
+ * contiguous copy. */
+int q8_quantize_rows_ld(const float* x, int64_t ldx, int64_t M, int64_t K, int8_t* q,
+                        double* scales, void* stream);
+
 /* ---------------------------------------------------------------- dequantize */
 
 /* The compiled `dequantize` op (quant_math.ts:29-34, rule
@@ -347,6 +355,15 @@ int q8_quantized_conv_ex(const void* x, int x_dtype, const void* w, int w_dtype,
  * NULL (the fp32 h is then not written). */
 int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K,
                               float* h_out, int8_t* q, double* scales, void* stream);
+
+/* As q8_silu_mul_quantize_rows, with g and u rows ldg and ldu floats apart
+ * (>= K): g and u may be the two halves of one [M, 2K] output, so gate and
+ * up come from a single GEMM over the concatenated weights.  h_out and q
+ * stay [M, K] contiguous.  No counterpart in the reference (its gate and up
+ * are two separate projections); each h element is the same. */
+int q8_silu_mul_quantize_rows_ld(const float* g, int64_t ldg, const float* u, int64_t ldu,
+                                 int64_t M, int64_t K, float* h_out, int8_t* q, double* scales,
+                                 void* stream);
 
 /* ------------------------------------------------------------ calibration */
 

@@ -85,6 +85,8 @@ SIGNATURES = {
     "q8_quantized_conv_ex": [_vp, _int, _vp, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                              C.c_int32, C.c_int32, _int, _dbl, _vp, C.c_size_t, _vp, _vp],
     "q8_silu_mul_quantize_rows": [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp],
+    "q8_silu_mul_quantize_rows_ld": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
+    "q8_quantize_rows_ld": [_vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "q8_observer_state_bytes": [_int, _vp],
     "q8_observer_reset": [_vp, _int, _int, _vp],
     "q8_observer_update": [_vp, _vp, _i64, _vp],

@@ -121,18 +121,23 @@ def c4_inputs(device="cuda", tokens=2048):
 
 
 def c4_prepare(W):
-    return {k: ops.pack_weight(w, axis=0) for k, w in W.items()}
+    """Per-channel int8 weights of the projection set.  Gate and up are packed
+    as one [2 * 11008, 4096] weight (codes and scales are per row, so each
+    row is what packing them apart gives): one GEMM computes both."""
+    P = {k: ops.pack_weight(w, axis=0) for k, w in W.items() if k not in ("gate", "up")}
+    P["gate_up"] = ops.pack_weight(torch.cat([W["gate"], W["up"]], 0), axis=0)
+    return P
 
 
 def c4_step(X, P):
     xq, sx = ops.quantize_per_token(X)
     qkv = ops.qlinear(xq, sx, *P["qkv"])
-    v = qkv[:, 8192:].contiguous()
-    vq, sv = ops.quantize_per_token(v)
+    vq, sv = ops.quantize_per_token(qkv[:, 8192:])         # row-strided V slice
     o = ops.qlinear(vq, sv, *P["o"])
     oq, so = ops.quantize_per_token(o)
-    g = ops.qlinear(oq, so, *P["gate"])
-    u = ops.qlinear(oq, so, *P["up"])
+    gu = ops.qlinear(oq, so, *P["gate_up"])               # [tokens, gate | up]
+    nf = gu.shape[1] // 2
+    g, u = gu[:, :nf], gu[:, nf:]                          # row-strided halves
     hq, sh = ops.silu_mul_quantize(g, u)
     d = ops.qlinear(hq, sh, *P["down"])
     return {"qkv": qkv, "o": o, "gate": g, "up": u, "down": d}

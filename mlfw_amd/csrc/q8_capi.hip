@@ -307,9 +307,23 @@ int q8_quantize_rows(const float* x, int64_t M, int64_t K, int mode, int8_t* q, 
   int rc = ensure_current(&work);
   if (rc != Q8_OK) return rc;
   hipError_t e = mode == Q8_PER_TOKEN
-                     ? q8::launch_quant_rows(x, M, K, q, scales, as_stream(stream))
+                     ? q8::launch_quant_rows(x, K, M, K, q, scales, as_stream(stream))
                      : q8::launch_quant_tensor(x, M * K, q, scales, work, as_stream(stream));
   return launched(e, "q8_quantize_rows launch");
+}
+
+int q8_quantize_rows_ld(const float* x, int64_t ldx, int64_t M, int64_t K, int8_t* q,
+                        double* scales, void* stream) {
+  Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_quantize_rows_ld: bad shape [%lld,%lld]",
+             (long long)M, (long long)K);
+  Q8_REQUIRE(ldx >= K && mul_ok(M, ldx), "q8_quantize_rows_ld: row stride %lld must be >= K (%lld)",
+             (long long)ldx, (long long)K);
+  Q8_REQUIRE(M == 0 || scales, "q8_quantize_rows_ld: scales is NULL");
+  Q8_REQUIRE(M * K == 0 || (x && q), "q8_quantize_rows_ld: NULL pointer");
+  int rc = ensure_current(nullptr);
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_quant_rows(x, ldx, M, K, q, scales, as_stream(stream)),
+                  "q8_quantize_rows_ld launch");
 }
 
 int q8_dequantize(const void* q, int src, int64_t M, int64_t K, const double* scales,
@@ -512,7 +526,7 @@ int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const i
     return launched(q8::launch_qlinear_fused(x, M, K, x_mode == Q8_PER_TENSOR ? 1 : 0, Wq, sW,
                                              e.sB_stride, N, bias, act, out, sx, xq, st),
                     "q8_qlinear_dynamic launch");
-  hipError_t err = x_mode == Q8_PER_TOKEN ? q8::launch_quant_rows(x, M, K, xq, sx, st)
+  hipError_t err = x_mode == Q8_PER_TOKEN ? q8::launch_quant_rows(x, K, M, K, xq, sx, st)
                                           : q8::launch_quant_tensor(x, M * K, xq, sx, work, st);
   if (err != hipSuccess || M * N == 0) return launched(err, "q8_qlinear_dynamic quantize launch");
   err = (M <= 16) ? q8::launch_gemv(xq, Wq, M, N, K, e, out, st)
@@ -709,15 +723,25 @@ int q8_quantized_conv_ex(const void* x, int x_dtype, const void* w, int w_dtype,
                    workspace_bytes, out, stream);
 }
 
-int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K, float* h_out,
-                              int8_t* q, double* scales, void* stream) {
+int q8_silu_mul_quantize_rows_ld(const float* g, int64_t ldg, const float* u, int64_t ldu,
+                                 int64_t M, int64_t K, float* h_out, int8_t* q, double* scales,
+                                 void* stream) {
   Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_silu_mul_quantize_rows: bad shape");
+  Q8_REQUIRE(ldg >= K && ldu >= K && mul_ok(M, ldg) && mul_ok(M, ldu),
+             "q8_silu_mul_quantize_rows: row strides (%lld, %lld) must be >= K (%lld)",
+             (long long)ldg, (long long)ldu, (long long)K);
   Q8_REQUIRE(M == 0 || scales, "q8_silu_mul_quantize_rows: scales is NULL");
   Q8_REQUIRE(M * K == 0 || (g && u && q), "q8_silu_mul_quantize_rows: NULL pointer");
   int rc = ensure_current(nullptr);
   if (rc != Q8_OK) return rc;
-  return launched(q8::launch_silu_mul_quant_rows(g, u, M, K, h_out, q, scales, as_stream(stream)),
+  return launched(q8::launch_silu_mul_quant_rows(g, ldg, u, ldu, M, K, h_out, q, scales,
+                                                 as_stream(stream)),
                   "q8_silu_mul_quantize_rows launch");
+}
+
+int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t K, float* h_out,
+                              int8_t* q, double* scales, void* stream) {
+  return q8_silu_mul_quantize_rows_ld(g, K, u, K, M, K, h_out, q, scales, stream);
 }
 
 int q8_observer_state_bytes(int num_bins, size_t* bytes) {

@@ -194,7 +194,8 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // same on every path and the wait before a row's reduction leaves the
 // next row's loads outstanding.
 template <int VPT, bool FULL, bool NTS>
-__global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t M,
+__global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, int64_t ldx,
+                                                   int64_t M,
                                                    int64_t K, int8_t* __restrict__ q,
                                                    double* __restrict__ scales) {
   __shared__ int red[NT / 64];
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
   auto load_row = [&](int64_t row, float4* v) {
     const bool in = row < M;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(x + (in ? row : 0) * K), (short)0, in ? (int)(K * 4) : 0, 0x00020000);
+        const_cast<float*>(x + (in ? row : 0) * ldx), (short)0, in ? (int)(K * 4) : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int i = tid + j * NT;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
     }
   };
   auto process_row = [&](int64_t row, const float4* v) {
-    const v4f* xr = reinterpret_cast<const v4f*>(x + row * K);
+    const v4f* xr = reinterpret_cast<const v4f*>(x + row * ldx);
     int* qr = reinterpret_cast<int*>(q + row * K);
     int key = -1;
 #pragma unroll
@@ -269,13 +270,14 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
   }
 }
 
-// Any K / alignment: two passes over the row with scalar loads.
-__global__ __launch_bounds__(NT) void k_quant_rows_scalar(const float* __restrict__ x, int64_t M,
+// Any K / row stride / alignment: two passes over the row with scalar loads.
+__global__ __launch_bounds__(NT) void k_quant_rows_scalar(const float* __restrict__ x, int64_t ldx,
+                                                          int64_t M,
                                                           int64_t K, int8_t* __restrict__ q,
                                                           double* __restrict__ scales) {
   __shared__ int red[NT / 64];
   for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
-    const float* xr = x + row * K;
+    const float* xr = x + row * ldx;
     int key = -1;
     for (int64_t i = threadIdx.x; i < K; i += NT) {
       int k = absmax_key(xr[i]);
@@ -292,19 +294,19 @@ __global__ __launch_bounds__(NT) void k_quant_rows_scalar(const float* __restric
   }
 }
 
-hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, double* scales,
-                             hipStream_t st) {
+hipError_t launch_quant_rows(const float* x, int64_t ldx, int64_t M, int64_t K, int8_t* q,
+                             double* scales, hipStream_t st) {
   if (M == 0) return hipSuccess;
   const int grid = (int)(M < 1048576 ? M : 1048576);
-  const bool vec = (K % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+  const bool vec = (K % 4 == 0) && (ldx % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
   if (!vec) {
-    hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+    hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, ldx, M, K, q, scales);
     return hipGetLastError();
   }
   const int64_t K4 = K / 4;
   if (K4 == 0) {        // rows of zero length: only the scales are written
-    hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, M, K, q, scales);
+    hipLaunchKernelGGL(k_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, x, ldx, M, K, q, scales);
     return hipGetLastError();
   }
   // Row workers: one workgroup per row (measured against resident grids of
@@ -318,8 +320,9 @@ hipError_t launch_quant_rows(const float* x, int64_t M, int64_t K, int8_t* q, do
   // there and use non-temporal stores, faster for this kernel (64 MiB:
   // 53.9 us instead of 57.2 us).
   const bool nts = M * K > ((int64_t)32 << 20);
-#define Q8_QROWS_S(V, FULLK, S)                                                                   \
-  hipLaunchKernelGGL((k_quant_rows<V, FULLK, S>), dim3(workers), dim3(NT), 0, st, x, M, K, q, scales)
+#define Q8_QROWS_S(V, FULLK, S)                                                             \
+  hipLaunchKernelGGL((k_quant_rows<V, FULLK, S>), dim3(workers), dim3(NT), 0, st, x, ldx, M, K, q, \
+                     scales)
 #define Q8_QROWS(V)                                                                          \
   do {                                                                                       \
     if (K4 == (V) * NT) {                                                                    \
@@ -692,6 +695,7 @@ hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int ax
 template <int VPT, int TPB>
 __global__ __launch_bounds__(TPB) void k_silu_mul_quant_rows(const float* __restrict__ g,
                                                              const float* __restrict__ u,
+                                                             int64_t ldg, int64_t ldu,
                                                              int64_t M, int64_t K,
                                                              float* __restrict__ h,
                                                              int8_t* __restrict__ q,
@@ -701,8 +705,8 @@ __global__ __launch_bounds__(TPB) void k_silu_mul_quant_rows(const float* __rest
   const int tid = threadIdx.x;
   const int64_t K4 = K >> 2;
   for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
-    const float4* gr = reinterpret_cast<const float4*>(g + row * K);
-    const float4* ur = reinterpret_cast<const float4*>(u + row * K);
+    const float4* gr = reinterpret_cast<const float4*>(g + row * ldg);
+    const float4* ur = reinterpret_cast<const float4*>(u + row * ldu);
     float4 v[VPT];
     int key = -1;
     // loads issued unconditionally (a lane past the row end reloads the
@@ -744,16 +748,18 @@ __global__ __launch_bounds__(TPB) void k_silu_mul_quant_rows(const float* __rest
   }
 }
 
-// Fallback for K % 4 != 0, misaligned pointers or rows above 12 Ki elements:
-// h is formed twice (scan, then quantize) from g and u.
+// Fallback for K % 4 != 0, a row stride that is not a multiple of 4,
+// misaligned pointers or rows above 12 Ki elements: h is formed twice (scan,
+// then quantize) from g and u.
 __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows_scalar(
-    const float* __restrict__ g, const float* __restrict__ u, int64_t M, int64_t K,
+    const float* __restrict__ g, const float* __restrict__ u, int64_t ldg, int64_t ldu, int64_t M,
+    int64_t K,
     float* __restrict__ h, int8_t* __restrict__ q, double* __restrict__ scales) {
   __shared__ int red[NT / 64];
   for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
     int key = -1;
     for (int64_t i = threadIdx.x; i < K; i += NT) {
-      float v = silu_js(g[row * K + i]) * u[row * K + i];
+      float v = silu_js(g[row * ldg + i]) * u[row * ldu + i];
       if (h) h[row * K + i] = v;
       int k = absmax_key(v);
       key = key > k ? key : k;
@@ -764,28 +770,31 @@ __global__ __launch_bounds__(NT) void k_silu_mul_quant_rows_scalar(
     const bool fast = fast_scale_ok(s);
     const float r32 = (float)(1.0 / s);
     for (int64_t i = threadIdx.x; i < K; i += NT) {
-      float v = silu_js(g[row * K + i]) * u[row * K + i];
+      float v = silu_js(g[row * ldg + i]) * u[row * ldu + i];
       q[row * K + i] = (int8_t)(fast ? quant_sym_fast(v, r32, s) : quant_exact(v, s, 0.0, -128, 127));
     }
   }
 }
 
-hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M, int64_t K,
+hipError_t launch_silu_mul_quant_rows(const float* g, int64_t ldg, const float* u, int64_t ldu,
+                                      int64_t M, int64_t K,
                                       float* h, int8_t* q, double* scales, hipStream_t st) {
   if (M == 0) return hipSuccess;
   const int grid = (int)(M < 1048576 ? M : 1048576);
-  const bool vec = (K % 4 == 0) && (K / 4 <= 6 * 512) &&
+  const bool vec = (K % 4 == 0) && (ldg % 4 == 0) && (ldu % 4 == 0) && (K / 4 <= 6 * 512) &&
                    ((reinterpret_cast<uintptr_t>(g) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(u) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(h) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(q) & 3) == 0);
   if (!vec) {
-    hipLaunchKernelGGL(k_silu_mul_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    hipLaunchKernelGGL(k_silu_mul_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, g, u, ldg, ldu, M,
+                       K, h, q, scales);
     return hipGetLastError();
   }
   const int64_t K4 = K / 4;
   if (K4 == 0) {
-    hipLaunchKernelGGL(k_silu_mul_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, g, u, M, K, h, q, scales);
+    hipLaunchKernelGGL(k_silu_mul_quant_rows_scalar, dim3(grid), dim3(NT), 0, st, g, u, ldg, ldu, M,
+                       K, h, q, scales);
     return hipGetLastError();
   }
   const int workers = (int)(M < 8 * cu_count() ? M : 8 * cu_count());
@@ -793,14 +802,14 @@ hipError_t launch_silu_mul_quant_rows(const float* g, const float* u, int64_t M,
   // [2048, 8192] and [2048, 11008] against 256 threads x 8-12 and 1024
   // threads x 2-3 per lane, with and without occupancy limits)
   if (K4 <= 4 * 256)
-    hipLaunchKernelGGL((k_silu_mul_quant_rows<4, 256>), dim3(workers), dim3(256), 0, st, g, u, M, K, h,
-                       q, scales);
+    hipLaunchKernelGGL((k_silu_mul_quant_rows<4, 256>), dim3(workers), dim3(256), 0, st, g, u, ldg, ldu, M, K,
+                       h, q, scales);
   else if (K4 <= 4 * 512)
-    hipLaunchKernelGGL((k_silu_mul_quant_rows<4, 512>), dim3(workers), dim3(512), 0, st, g, u, M, K, h,
-                       q, scales);
+    hipLaunchKernelGGL((k_silu_mul_quant_rows<4, 512>), dim3(workers), dim3(512), 0, st, g, u, ldg, ldu, M, K,
+                       h, q, scales);
   else
-    hipLaunchKernelGGL((k_silu_mul_quant_rows<6, 512>), dim3(workers), dim3(512), 0, st, g, u, M, K, h,
-                       q, scales);
+    hipLaunchKernelGGL((k_silu_mul_quant_rows<6, 512>), dim3(workers), dim3(512), 0, st, g, u, ldg, ldu, M, K,
+                       h, q, scales);
   return hipGetLastError();
 }
 

@@ -163,7 +163,18 @@ def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
                        scales: torch.Tensor | None = None):
     """Dynamic symmetric int8 quantize with one f64 scale per row of the last
     dimension (calibration scale of each row, calibration.ts:24-34 +
-    quantization_types.ts:248-254).  Returns (int8 codes, f64 scales[M])."""
+    quantization_types.ts:248-254).  x is contiguous, or a 2-D row-strided
+    view (e.g. a column slice of a wider projection output); the codes are
+    [M, K] contiguous either way.  Returns (int8 codes, f64 scales[M])."""
+    if isinstance(x, torch.Tensor) and not x.is_contiguous():
+        if x.dtype != torch.float32 or not x.is_cuda or x.dim() != 2 or x.stride(1) != 1:
+            raise ValueError("quantize_per_token: x must be contiguous or a 2-D fp32 device view "
+                             "with unit column stride")
+        M, K = x.shape
+        q = _out(q, (M, K), torch.int8, x, "q")
+        scales = _out(scales, M, torch.float64, x, "scales")
+        _call("q8_quantize_rows_ld", _ptr(x), x.stride(0), M, K, _ptr(q), _ptr(scales), _stream())
+        return q, scales
     _need(x, torch.float32, "quantize_per_token")
     M, K = _rows(x)
     q = _out(q, x.shape, torch.int8, x, "q")
@@ -458,16 +469,27 @@ def quantized_conv(x: torch.Tensor, w: torch.Tensor, strides, padding, dilation=
 
 def silu_mul_quantize(g: torch.Tensor, u: torch.Tensor, h_out: torch.Tensor | None = None):
     """h = fround(silu(g) * u), then per-token int8 quantize of h.
-    Returns (int8 codes, f64 scales[M])."""
-    _need(g, torch.float32, "g")
-    _need(u, torch.float32, "u")
+    g and u are contiguous, or 2-D row-strided views (e.g. the two halves of
+    one [M, 2K] GEMM output).  Returns (int8 codes [M, K], f64 scales[M])."""
     if g.shape != u.shape:
         raise ValueError("silu_mul_quantize: g and u shapes differ")
-    M, K = _rows(g)
+    lds = []
+    for t, name in ((g, "g"), (u, "u")):
+        if t.is_contiguous():
+            _need(t, torch.float32, name)
+            lds.append(None)
+        else:
+            if t.dtype != torch.float32 or not t.is_cuda or t.dim() != 2 or t.stride(1) != 1:
+                raise ValueError(f"silu_mul_quantize: {name} must be contiguous or a 2-D fp32 device "
+                                 "view with unit column stride")
+            lds.append(t.stride(0))
+    M, K = _rows(g) if g.is_contiguous() else g.shape
+    ldg = K if lds[0] is None else lds[0]
+    ldu = K if lds[1] is None else lds[1]
     q = torch.empty(g.shape, dtype=torch.int8, device=g.device)
     scales = torch.empty(M, dtype=torch.float64, device=g.device)
     if h_out is not None:
-        _need(h_out, torch.float32, "h_out")
-    _call("q8_silu_mul_quantize_rows", _ptr(g), _ptr(u), M, K, _ptr(h_out), _ptr(q),
-           _ptr(scales), _stream())
+        _out(h_out, (M, K), torch.float32, g, "h_out")
+    _call("q8_silu_mul_quantize_rows_ld", _ptr(g), ldg, _ptr(u), ldu, M, K, _ptr(h_out), _ptr(q),
+          _ptr(scales), _stream())
     return q, scales

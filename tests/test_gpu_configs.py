@@ -95,6 +95,8 @@ def test_c4_decoder_projections(mods, oracle):
     inp = OC.c4_inputs()
     packed_ref = {k: OC.pack_pc(w, 0) for k, w in inp["W"].items()}
     P = C.c4_prepare({k: dev(w) for k, w in inp["W"].items()})
+    # gate and up run as one GEMM over the concatenated weight
+    packed_ref["gate_up"] = tuple(np.concatenate([packed_ref["gate"][i], packed_ref["up"][i]]) for i in (0, 1))
     for k in P:
         same_bits(host(P[k][1]), packed_ref[k][1], f"C4 {k} scales")
         same_bits(host(P[k][0]), packed_ref[k][0], f"C4 {k} codes")

@@ -412,6 +412,53 @@ def test_silu_mul_quantize(ops, oracle, M, K):
     same_bits(host(q), oracle.quantize_rows(h, s_ref))
 
 
+
+@pytest.mark.parametrize("M,K,pad", [(4, 11008, 11008), (3, 1000, 1000), (2, 64, 4), (3, 6000, 2), (2, 30, 3)])
+def test_silu_mul_quantize_strided(ops, oracle, M, K, pad):
+    """g and u as row-strided views: the two halves of one [M, 2K] output
+    (pad = K) or of a wider buffer; odd strides take the scalar kernel."""
+    rng = oracle.Rng(K + pad)
+    g = rng.normal((M, K), 0.0, 3.0)
+    u = rng.normal((M, K))
+    buf = np.zeros((M, 2 * K + pad), np.float32)
+    buf[:, :K] = g
+    buf[:, K + pad:] = u
+    d = dev(buf)
+    gv, uv = d[:, :K], d[:, K + pad:]
+    assert not gv.is_contiguous() and gv.stride(0) == 2 * K + pad
+    h_out = torch.empty((M, K), dtype=torch.float32, device=DEV)
+    q, s = ops.silu_mul_quantize(gv, uv, h_out)
+    h = oracle.silu_mul(g, u)
+    same_bits(host(h_out), h)
+    s_ref = oracle.scales_per_token(h)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(h, s_ref))
+
+@pytest.mark.parametrize("M,K,off,tail", [(5, 4096, 8192, 0), (3, 1000, 3, 1), (7, 64, 4, 0),
+                                          (2, 30, 1, 2), (4, 20000, 4, 4)])
+def test_quantize_per_token_strided(ops, oracle, M, K, off, tail):
+    """x as a column slice of a wider buffer (the V third of a fused qkv
+    output is off = 2K of a [M, 3K] row); odd strides take the scalar kernel.
+    A zero row and a row with one large outlier are included."""
+    rng = oracle.Rng(K + off)
+    x = rng.normal((M, K))
+    x[0] = 0.0
+    x[-1, K // 2] = 5000.0
+    buf = rng.normal((M, off + K + tail))
+    buf[:, off:off + K] = x
+    d = dev(buf)
+    v = d[:, off:off + K]
+    assert not v.is_contiguous() and v.stride(0) == off + K + tail
+    q, s = ops.quantize_per_token(v)
+    s_ref = oracle.scales_per_token(x)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(x, s_ref))
+    q2, s2 = ops.quantize_per_token(v.contiguous())
+    same_bits(host(q), host(q2))
+    with pytest.raises(ValueError):
+        ops.quantize_per_token(d.t()[:K])                 # column stride != 1
+
+
 def test_fill_uniform_matches_oracle(ops, oracle):
     r = oracle.Rng(11)
     ref = r.uniform((10001,), -0.1, 0.1)
