@@ -72,6 +72,14 @@ def test_validation_happens_before_any_launch(lib):
     expect_invalid(lib, "q8_quantize_rows", fake, 4, 8, 7, fake, fake, nil)
     expect_invalid(lib, "q8_quantize_rows", fake, -4, 8, lib.Q8_PER_TOKEN, fake, fake, nil)
     expect_invalid(lib, "q8_quantize_rows", nil, 4, 8, lib.Q8_PER_TOKEN, fake, fake, nil)
+    # row-strided forms: the row stride may not be below the row length
+    expect_invalid(lib, "q8_quantize_rows_ld", fake, 7, 4, 8, fake, fake, nil)
+    expect_invalid(lib, "q8_quantize_rows_ld", fake, -1, 4, 8, fake, fake, nil)
+    expect_invalid(lib, "q8_quantize_rows_ld", nil, 16, 4, 8, fake, fake, nil)
+    expect_invalid(lib, "q8_quantize_rows_ld", fake, 16, 4, 8, fake, nil, nil)
+    expect_invalid(lib, "q8_silu_mul_quantize_rows_ld", fake, 7, fake, 8, 4, 8, nil, fake, fake, nil)
+    expect_invalid(lib, "q8_silu_mul_quantize_rows_ld", fake, 8, fake, 3, 4, 8, nil, fake, fake, nil)
+    expect_invalid(lib, "q8_silu_mul_quantize_rows_ld", fake, 16, nil, 16, 4, 8, nil, fake, fake, nil)
     expect_invalid(lib, "q8_dequantize", fake, lib.Q8_F32, 4, 8, fake, lib.Q8_PER_TENSOR, 0.0,
                    fake, nil)
     expect_invalid(lib, "q8_dequantize", fake, lib.Q8_I8, 4, 8, fake, 9, 0.0, fake, nil)
