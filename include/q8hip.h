@@ -93,7 +93,7 @@ const char* q8_last_error(void);
 int q8_device_count(int* count);
 
 /* Make `device` current for this thread and prepare it (checks the device is
- * gfx950, allocates the library's small per-device work area).  Entry points
+ * gfx950 and sets kernel attributes).  Entry points
  * below call it for the current device on first use.  Replaces the CUDA
  * backend's context/stream set-up (src/runtime/node/cuda/device.ts:14-35). */
 int q8_init(int device);
@@ -152,7 +152,11 @@ int q8_quantize_static(const float* x, int64_t n, double scale, double zero_poin
  * Codes are then the compiled quantize above with that scale.  The
  * reference has this scale only as a static, calibrated one; the dynamic
  * per-token / per-tensor op is this library's composition of the two.
- * scales: f64 device array of M (per token) or 1 (per tensor) entries. */
+ * scales: 8-byte aligned f64 device array of M (per token) or 1 (per
+ * tensor) entries.  The per-tensor reduction keeps its running key in
+ * scales[0] until the final scale replaces it, so the call uses no memory
+ * besides its arguments: calls with distinct outputs may run concurrently
+ * on any streams. */
 int q8_quantize_rows(const float* x, int64_t M, int64_t K, int mode,
                      int8_t* q, double* scales, void* stream);
 
@@ -188,7 +192,9 @@ int q8_dequantize(const void* q, int src, int64_t M, int64_t K,
  * nn.Linear weight [N,K]); axis 1: channel = column (a [K,N] weight).
  * Output Wq is always [N, K] (channel-major, K contiguous: the GEMM's B
  * layout), i.e. W itself for axis 0 and its transpose for axis 1.
- * scales: f64 device array of N entries (per channel) or 1 (per tensor). */
+ * scales: 8-byte aligned f64 device array of N entries (per channel) or 1
+ * (per tensor; its min / max keys are kept in scales[0] until the scale
+ * replaces them, as in q8_quantize_rows). */
 int q8_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int granularity,
                    int8_t* Wq, double* scales, void* stream);
 
@@ -252,7 +258,8 @@ int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int
  * bit for bit.  For one-token decode (M == 1, K <= 4096, K % 16 == 0,
  * 16-byte aligned x and Wq) both steps run in one kernel; otherwise as
  * two (the same kernels as the separate calls).
- * xq: int8 [M,K]; sx: f64 [M] (per token) or [1] (per tensor). */
+ * xq: int8 [M,K]; sx: 8-byte aligned f64 [M] (per token) or [1] (per
+ * tensor; holds the reduction key until the scale replaces it). */
 int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const int8_t* Wq,
                        const double* sW, int sW_mode, int64_t N, const float* bias, int act,
                        float* out, int8_t* xq, double* sx, void* stream);

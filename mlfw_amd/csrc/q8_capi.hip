@@ -34,12 +34,12 @@ int hip_fail(hipError_t e, const char* what) {
               hipGetErrorString(e), (int)e);
 }
 
-// Per-device state: initialised once, holds the small work area used by
-// the two-phase per-tensor reductions (a few int32 keys).
+// Per-device state: initialised once.  The library allocates no device
+// memory for the ops: per-tensor reductions keep their keys in the caller's
+// scales output and workspaces come from the caller.
 constexpr int kMaxDevices = 64;
 struct DevState {
   std::atomic<int> ready{0};
-  int* work = nullptr;
 };
 DevState g_dev[kMaxDevices];
 std::mutex g_init_mu;
@@ -61,7 +61,6 @@ int init_device(int dev) {
   if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   e = q8::setup_kernel_attributes();
   (void)q8::cu_count();
-  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&g_dev[dev].work), 256);
   if (cur != dev) (void)hipSetDevice(cur);
   if (e != hipSuccess) return hip_fail(e, "device set-up");
   g_dev[dev].ready.store(1, std::memory_order_release);
@@ -69,13 +68,12 @@ int init_device(int dev) {
 }
 
 // Initialise the calling thread's current device on first use.
-int ensure_current(int** work) {
+int ensure_current() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice (no HIP device?)");
   int rc = init_device(dev);
   if (rc != Q8_OK) return rc;
-  if (work) *work = g_dev[dev].work;
   return Q8_OK;
 }
 
@@ -209,7 +207,7 @@ int q8_init(int device) {
 
 int q8_alloc(void** dptr, size_t bytes) {
   Q8_REQUIRE(dptr != nullptr, "q8_alloc: dptr is NULL");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   *dptr = nullptr;
   if (bytes == 0) return Q8_OK;
@@ -241,7 +239,7 @@ int q8_d2h(void* dst, const void* src, size_t bytes, void* stream) {
 int q8_memset(void* dst, int value, size_t bytes, void* stream) {
   if (bytes == 0) return Q8_OK;
   Q8_REQUIRE(dst != nullptr, "q8_memset: dst is NULL");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   // a fill kernel, not hipMemsetAsync: callers may capture this in a HIP graph
   return launched(q8::launch_fill_u8(dst, value, (int64_t)bytes, as_stream(stream)), "q8_memset");
@@ -255,7 +253,7 @@ int q8_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset, double
                    double std, void* stream) {
   Q8_REQUIRE(n >= 0, "q8_fill_normal: n < 0");
   Q8_REQUIRE(n == 0 || out, "q8_fill_normal: out is NULL");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_fill_normal(out, n, seed, offset, mean, std, as_stream(stream)),
                   "q8_fill_normal launch");
@@ -265,7 +263,7 @@ int q8_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset, doubl
                     void* stream) {
   Q8_REQUIRE(n >= 0, "q8_fill_uniform: n < 0");
   Q8_REQUIRE(n == 0 || out, "q8_fill_uniform: out is NULL");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_fill_uniform(out, n, seed, offset, a, b, as_stream(stream)),
                   "q8_fill_uniform launch");
@@ -274,7 +272,7 @@ int q8_fill_uniform(float* out, int64_t n, uint32_t seed, uint64_t offset, doubl
 int q8_apply_outliers(float* x, int64_t n, uint32_t seed, double p, double factor, void* stream) {
   Q8_REQUIRE(n >= 0, "q8_apply_outliers: n < 0");
   Q8_REQUIRE(n == 0 || x, "q8_apply_outliers: x is NULL");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_apply_outliers(x, n, seed, p, factor, as_stream(stream)),
                   "q8_apply_outliers launch");
@@ -288,7 +286,7 @@ int q8_quantize_static(const float* x, int64_t n, double scale, double zero_poin
              "q8_quantize_static: target must be Q8_I8 or Q8_U8 (got %d)", target);
   // quantize op verifier: `scale <= 0` is rejected (ops/quantization.ts:44-47)
   Q8_REQUIRE(!(scale <= 0.0), "q8_quantize_static: quantize scale must be positive (got %g)", scale);
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_quant_static(x, n, scale, zero_point, target == Q8_U8, q,
                                           as_stream(stream)),
@@ -303,12 +301,13 @@ int q8_quantize_rows(const float* x, int64_t M, int64_t K, int mode, int8_t* q, 
              "q8_quantize_rows: mode must be Q8_PER_TOKEN or Q8_PER_TENSOR (got %d)", mode);
   Q8_REQUIRE(scales != nullptr || (mode == Q8_PER_TOKEN && M == 0), "q8_quantize_rows: scales is NULL");
   Q8_REQUIRE(M * K == 0 || (x && q), "q8_quantize_rows: NULL pointer");
-  int* work = nullptr;
-  int rc = ensure_current(&work);
+  Q8_REQUIRE((reinterpret_cast<uintptr_t>(scales) & 7) == 0,
+             "q8_quantize_rows: scales must be 8-byte aligned");
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   hipError_t e = mode == Q8_PER_TOKEN
                      ? q8::launch_quant_rows(x, K, M, K, q, scales, as_stream(stream))
-                     : q8::launch_quant_tensor(x, M * K, q, scales, work, as_stream(stream));
+                     : q8::launch_quant_tensor(x, M * K, q, scales, as_stream(stream));
   return launched(e, "q8_quantize_rows launch");
 }
 
@@ -320,7 +319,7 @@ int q8_quantize_rows_ld(const float* x, int64_t ldx, int64_t M, int64_t K, int8_
              (long long)ldx, (long long)K);
   Q8_REQUIRE(M == 0 || scales, "q8_quantize_rows_ld: scales is NULL");
   Q8_REQUIRE(M * K == 0 || (x && q), "q8_quantize_rows_ld: NULL pointer");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_quant_rows(x, ldx, M, K, q, scales, as_stream(stream)),
                   "q8_quantize_rows_ld launch");
@@ -335,7 +334,7 @@ int q8_dequantize(const void* q, int src, int64_t M, int64_t K, const double* sc
   Q8_REQUIRE(granularity == Q8_PER_TENSOR || granularity == Q8_PER_TOKEN,
              "q8_dequantize: granularity must be Q8_PER_TENSOR or Q8_PER_TOKEN (got %d)", granularity);
   Q8_REQUIRE(M * K == 0 || (q && y && scales), "q8_dequantize: NULL pointer");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_dequant(q, src, M, K, scales, granularity == Q8_PER_TOKEN,
                                      zero_point, y, as_stream(stream)),
@@ -352,11 +351,12 @@ int q8_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int gra
              granularity);
   Q8_REQUIRE(rows * cols == 0 || (W && Wq), "q8_pack_weight: NULL pointer");
   Q8_REQUIRE(scales != nullptr, "q8_pack_weight: scales is NULL");
-  int* work = nullptr;
-  int rc = ensure_current(&work);
+  Q8_REQUIRE((reinterpret_cast<uintptr_t>(scales) & 7) == 0,
+             "q8_pack_weight: scales must be 8-byte aligned");
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_pack_weight(W, rows, cols, axis, granularity == Q8_PER_TENSOR, Wq,
-                                         scales, work, as_stream(stream)),
+                                         scales, as_stream(stream)),
                   "q8_pack_weight launch");
 }
 
@@ -407,7 +407,7 @@ int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, i
   int rc = gemm_common("q8_gemm", A, B, M, N, K, zpA, zpB, sA, sA_mode, sB, sB_mode, epi, s_out,
                        bias, act, out_kind, out, &e);
   if (rc != Q8_OK) return rc;
-  rc = ensure_current(nullptr);
+  rc = ensure_current();
   if (rc != Q8_OK) return rc;
   hipError_t err = (M <= 16) ? q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream))
                              : q8::launch_gemm(A, B, M, N, K, e, out, as_stream(stream));
@@ -422,7 +422,7 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, c
   int rc = gemm_common("q8_gemv", A, B, M, N, K, 0, 0, sA, sA_mode, sB, sB_mode, epi, s_out, bias,
                        act, out_kind, out, &e);
   if (rc != Q8_OK) return rc;
-  rc = ensure_current(nullptr);
+  rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream)), "q8_gemv launch");
 }
@@ -480,7 +480,7 @@ int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int
   const QdotPlan p = qdot_plan(M, N, K, a_dtype, b_dtype, zpA, zpB);
   Q8_REQUIRE(p.bytes == 0 || (workspace && workspace_bytes >= p.bytes),
              "q8_quantized_dot: needs a workspace of %zu bytes (got %zu)", p.bytes, workspace_bytes);
-  rc = ensure_current(nullptr);
+  rc = ensure_current();
   if (rc != Q8_OK) return rc;
   if (M * N == 0) return Q8_OK;
   hipStream_t st = as_stream(stream);
@@ -507,6 +507,23 @@ int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int
   return launched(err, "q8_quantized_dot launch");
 }
 
+// Body of the dynamic linear once the arguments are checked.
+static hipError_t qlinear_dynamic_run(const float* x, int64_t M, int64_t K, int x_mode,
+                                      const int8_t* Wq, const double* sW, int64_t N,
+                                      const float* bias, int act, float* out, int8_t* xq,
+                                      double* sx, q8::GemmEpi& e, hipStream_t st) {
+  if (M * N == 0 && M * K == 0) return hipSuccess;
+  if (N > 0 && q8::qlinear_fused_ok(x, Wq, M, K))
+    return q8::launch_qlinear_fused(x, M, K, x_mode == Q8_PER_TENSOR ? 1 : 0, Wq, sW,
+                                    e.sB_stride, N, bias, act, out, sx, xq, st);
+  hipError_t err = x_mode == Q8_PER_TOKEN ? q8::launch_quant_rows(x, K, M, K, xq, sx, st)
+                                          : q8::launch_quant_tensor(x, M * K, xq, sx, st);
+  if (err != hipSuccess || M * N == 0) return err;
+  e.sA = sx;
+  return (M <= 16) ? q8::launch_gemv(xq, Wq, M, N, K, e, out, st)
+                   : q8::launch_gemm(xq, Wq, M, N, K, e, out, st);
+}
+
 int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const int8_t* Wq,
                        const double* sW, int sW_mode, int64_t N, const float* bias, int act,
                        float* out, int8_t* xq, double* sx, void* stream) {
@@ -517,21 +534,13 @@ int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const i
                        Q8_EPI_ROWCOL, 0.0, bias, act, Q8_F32, out, &e);
   if (rc != Q8_OK) return rc;
   Q8_REQUIRE(M * K == 0 || x, "q8_qlinear_dynamic: x is NULL");
-  int* work = nullptr;
-  rc = ensure_current(&work);
+  Q8_REQUIRE((reinterpret_cast<uintptr_t>(sx) & 7) == 0,
+             "q8_qlinear_dynamic: sx must be 8-byte aligned");
+  rc = ensure_current();
   if (rc != Q8_OK) return rc;
-  hipStream_t st = as_stream(stream);
-  if (M * N == 0 && M * K == 0) return Q8_OK;
-  if (N > 0 && q8::qlinear_fused_ok(x, Wq, M, K))
-    return launched(q8::launch_qlinear_fused(x, M, K, x_mode == Q8_PER_TENSOR ? 1 : 0, Wq, sW,
-                                             e.sB_stride, N, bias, act, out, sx, xq, st),
-                    "q8_qlinear_dynamic launch");
-  hipError_t err = x_mode == Q8_PER_TOKEN ? q8::launch_quant_rows(x, K, M, K, xq, sx, st)
-                                          : q8::launch_quant_tensor(x, M * K, xq, sx, work, st);
-  if (err != hipSuccess || M * N == 0) return launched(err, "q8_qlinear_dynamic quantize launch");
-  err = (M <= 16) ? q8::launch_gemv(xq, Wq, M, N, K, e, out, st)
-                  : q8::launch_gemm(xq, Wq, M, N, K, e, out, st);
-  return launched(err, "q8_qlinear_dynamic launch");
+  return launched(qlinear_dynamic_run(x, M, K, x_mode, Wq, sW, N, bias, act, out, xq, sx, e,
+                                      as_stream(stream)),
+                  "q8_qlinear_dynamic launch");
 }
 
 int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
@@ -549,7 +558,7 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
   e.s_q = s_next;
   e.rq32 = (float)(1.0 / s_next);
   e.q_fast = (s_next >= 0x1p-100 && s_next <= 0x1p100) ? 1 : 0;
-  rc = ensure_current(nullptr);
+  rc = ensure_current();
   if (rc != Q8_OK) return rc;
   hipError_t err = (M <= 16) ? q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream))
                              : q8::launch_gemm(A, B, M, N, K, e, out, as_stream(stream));
@@ -566,7 +575,7 @@ int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size
   Q8_REQUIRE(N * (K / 2) < (1LL << 31), "q8_pack_weight_int4: weight too large (%lld x %lld; "
              "q8_gemv_w4 addresses N * K / 2 bytes with 32-bit offsets)", (long long)N, (long long)K);
   Q8_REQUIRE(N * K == 0 || (W && Wq4 && scales), "q8_pack_weight_int4: NULL pointer");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_pack_w4(W, N, K, group_size, Wq4, scales, as_stream(stream)),
                   "q8_pack_weight_int4 launch");
@@ -585,7 +594,7 @@ int q8_gemv_w4(const int8_t* xq, const double* sx, int sx_mode, const uint8_t* W
   Q8_REQUIRE(sx_mode == Q8_PER_TENSOR || sx_mode == Q8_PER_TOKEN, "q8_gemv_w4: bad sx_mode %d", sx_mode);
   Q8_REQUIRE(act == Q8_ACT_NONE || act == Q8_ACT_RELU || act == Q8_ACT_SILU, "q8_gemv_w4: bad act %d", act);
   Q8_REQUIRE(M * N == 0 || (xq && sx && Wq4 && sw && out), "q8_gemv_w4: NULL pointer");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_gemv_w4(xq, sx, sx_mode == Q8_PER_TOKEN ? 1 : 0, Wq4, sw, M, N, K,
                                      group_size, bias, act, out, as_stream(stream)),
@@ -696,7 +705,7 @@ static int conv_impl(const char* who, const void* x, int x_dtype, const void* w,
   e.mode = 0;
   e.s_out = s_out;
   e.out_i32 = out_kind == Q8_I32;
-  rc = ensure_current(nullptr);
+  rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_conv(static_cast<const int8_t*>(x), static_cast<const int8_t*>(w), G,
                                   e, workspace, out, as_stream(stream)),
@@ -732,7 +741,7 @@ int q8_silu_mul_quantize_rows_ld(const float* g, int64_t ldg, const float* u, in
              (long long)ldg, (long long)ldu, (long long)K);
   Q8_REQUIRE(M == 0 || scales, "q8_silu_mul_quantize_rows: scales is NULL");
   Q8_REQUIRE(M * K == 0 || (g && u && q), "q8_silu_mul_quantize_rows: NULL pointer");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_silu_mul_quant_rows(g, ldg, u, ldu, M, K, h_out, q, scales,
                                                  as_stream(stream)),
@@ -758,7 +767,7 @@ int q8_observer_reset(void* state, int num_bins, int histogram, void* stream) {
   Q8_REQUIRE((reinterpret_cast<uintptr_t>(state) & 7) == 0, "q8_observer_reset: state must be 8-byte aligned");
   Q8_REQUIRE(num_bins >= 1 && num_bins <= Q8_OBS_MAX_BINS,
              "q8_observer_reset: num_bins must be in [1, %d] (got %d)", Q8_OBS_MAX_BINS, num_bins);
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_obs_reset(static_cast<q8::ObsState*>(state), num_bins,
                                        histogram ? 1 : 0, as_stream(stream)),
@@ -770,7 +779,7 @@ int q8_observer_update(void* state, const float* x, int64_t n, void* stream) {
   Q8_REQUIRE((reinterpret_cast<uintptr_t>(state) & 7) == 0, "q8_observer_update: state must be 8-byte aligned");
   Q8_REQUIRE(n >= 0, "q8_observer_update: n must be >= 0");
   Q8_REQUIRE(n == 0 || x != nullptr, "q8_observer_update: x is NULL");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   return launched(q8::launch_obs_update(static_cast<q8::ObsState*>(state), x, n, as_stream(stream)),
                   "q8_observer_update launch");
@@ -778,7 +787,7 @@ int q8_observer_update(void* state, const float* x, int64_t n, void* stream) {
 
 int q8_observer_read(const void* state, double* summary, double* bins, void* stream) {
   Q8_REQUIRE(state != nullptr && summary != nullptr, "q8_observer_read: NULL pointer");
-  int rc = ensure_current(nullptr);
+  int rc = ensure_current();
   if (rc != Q8_OK) return rc;
   q8::ObsState h;
   hipStream_t s = as_stream(stream);

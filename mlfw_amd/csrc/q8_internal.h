@@ -36,13 +36,13 @@ hipError_t launch_quant_static(const float* x, int64_t n, double s, double zp, i
 // x rows start ldx floats apart (K for a contiguous input)
 hipError_t launch_quant_rows(const float* x, int64_t ldx, int64_t M, int64_t K, int8_t* q,
                              double* scales, hipStream_t st);
+// per-tensor dynamic quantize; its reduction key lives in scales[0]
 hipError_t launch_quant_tensor(const float* x, int64_t n, int8_t* q, double* scales,
-                               int* work, hipStream_t st);
+                               hipStream_t st);
 hipError_t launch_dequant(const void* q, int src, int64_t M, int64_t K, const double* scales,
                           int per_row, double zp, float* y, hipStream_t st);
 hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int axis,
-                              int per_tensor, int8_t* Wq, double* scales, int* work,
-                              hipStream_t st);
+                              int per_tensor, int8_t* Wq, double* scales, hipStream_t st);
 // g and u rows start ldg / ldu floats apart (K for contiguous inputs)
 hipError_t launch_silu_mul_quant_rows(const float* g, int64_t ldg, const float* u, int64_t ldu,
                                       int64_t M, int64_t K, float* h, int8_t* q, double* scales,

@@ -203,10 +203,15 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const float* __restrict__ x, 
   const int64_t K4 = K >> 2;       // FULL: K4 == VPT * NT, no bounds to test
   const int last = (int)K4 - 1;
   const int64_t G = gridDim.x;
+  // The resource spans only the part of the row the VPT register loads
+  // cover (at most VPT * NT float4, 48 KiB), so num_records never wraps
+  // however long the row is; the rest of a long row is read directly.
+  constexpr int64_t SPAN = (int64_t)VPT * NT * 16;
+  const int rec = (int)(K * 4 < SPAN ? K * 4 : SPAN);
   auto load_row = [&](int64_t row, float4* v) {
     const bool in = row < M;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(x + (in ? row : 0) * ldx), (short)0, in ? (int)(K * 4) : 0, 0x00020000);
+        const_cast<float*>(x + (in ? row : 0) * ldx), (short)0, in ? rec : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int i = tid + j * NT;
@@ -342,13 +347,32 @@ hipError_t launch_quant_rows(const float* x, int64_t ldx, int64_t M, int64_t K, 
 }
 
 // ------------------------------------------------------------------ per-tensor quantize
-// Phase 1: NaN-ignoring absmax of the whole tensor into work[0] (an int key,
-// combined with a vector atomic max).  Phase 2: every block derives the
-// scale from the key and quantizes its share.
-__global__ void k_set_i32(int* p, int v) { p[0] = v; }
+// The reduction key lives in the caller's own scales[0] (8 bytes), so calls
+// with distinct outputs share no memory and may run concurrently on any
+// streams.  The key is the binary64 bit pattern of a candidate scale,
+// amax_b / 127 for a block's NaN-ignoring absmax amax_b, combined with a
+// 64-bit atomic max: non-negative doubles order like their bit patterns,
+// and x -> x / 127 (one rounding) is non-decreasing, so the max of the
+// candidates is exactly max(amax) / 127.  It starts at -1 ("no non-NaN
+// value seen").  Phase 1 raises it; phase 2 turns it into the final scale
+//   s = key < 0 ? Infinity : (key == 0 ? 1e-10 : key)
+// (S-abs with fromRange's `|| 1e-10`, and the (+inf, -inf) range of an
+// observer that saw only NaNs), quantizes its share with s, and block 0
+// stores s back into scales[0].  That mapping is idempotent (s maps to s),
+// so a block that reads scales[0] after block 0's store derives the same s;
+// every access to the key is atomic.
+__global__ void k_set_i64(long long* p, long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ double scale_from_dkey(long long key) {
+  if (key < 0) return __builtin_inf();
+  const double s = __longlong_as_double(key);
+  return s == 0.0 ? 1e-10 : s;
+}
 
 __global__ __launch_bounds__(NT) void k_absmax_tensor(const float* __restrict__ x, int64_t n,
-                                                      int* __restrict__ work) {
+                                                      long long* __restrict__ dkey) {
   __shared__ int red[NT / 64];
   int key = -1;
   const int64_t stride = (int64_t)gridDim.x * NT;
@@ -371,15 +395,20 @@ __global__ __launch_bounds__(NT) void k_absmax_tensor(const float* __restrict__ 
     }
   }
   key = block_max_i32(key, red);
-  if (threadIdx.x == 0 && key >= 0) atomicMax(work, key);
+  if (threadIdx.x == 0 && key >= 0) {
+    const double s = (double)__uint_as_float((unsigned)key) / 127.0;
+    __hip_atomic_fetch_max(dkey, __double_as_longlong(s), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 __global__ __launch_bounds__(NT) void k_quant_tensor(const float* __restrict__ x, int64_t n,
-                                                     const int* __restrict__ work,
-                                                     int8_t* __restrict__ q,
-                                                     double* __restrict__ scales) {
-  const double s = n == 0 ? 6.0 / 127.0 : scale_from_key(work[0]);
-  if (blockIdx.x == 0 && threadIdx.x == 0) scales[0] = s;
+                                                     long long* dkey, int8_t* __restrict__ q) {
+  const double s = n == 0 ? 6.0 / 127.0
+                          : scale_from_dkey(__hip_atomic_load(dkey, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT));
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(dkey, __double_as_longlong(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const bool fast = fast_scale_ok(s);
   const float r32 = (float)(1.0 / s);
   const int64_t stride = (int64_t)gridDim.x * NT;
@@ -397,15 +426,15 @@ __global__ __launch_bounds__(NT) void k_quant_tensor(const float* __restrict__ x
   }
 }
 
-hipError_t launch_quant_tensor(const float* x, int64_t n, int8_t* q, double* scales, int* work,
+hipError_t launch_quant_tensor(const float* x, int64_t n, int8_t* q, double* scales,
                                hipStream_t st) {
-  // The key starts at -1 ("only NaNs seen"); blocks that saw a non-NaN
-  // value raise it.  A fill kernel (not a memset) keeps the sequence
-  // capturable in a HIP graph.
-  hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, work, -1);
+  // A fill kernel (not a memset) starts the key, so the sequence can be
+  // captured in a HIP graph.
+  long long* dkey = reinterpret_cast<long long*>(scales);
+  hipLaunchKernelGGL(k_set_i64, dim3(1), dim3(1), 0, st, dkey, -1LL);
   const int grid = grid_for((n + 3) / 4, NT * 4, 2048);
-  if (n > 0) hipLaunchKernelGGL(k_absmax_tensor, dim3(grid), dim3(NT), 0, st, x, n, work);
-  hipLaunchKernelGGL(k_quant_tensor, dim3(grid), dim3(NT), 0, st, x, n, work, q, scales);
+  if (n > 0) hipLaunchKernelGGL(k_absmax_tensor, dim3(grid), dim3(NT), 0, st, x, n, dkey);
+  hipLaunchKernelGGL(k_quant_tensor, dim3(grid), dim3(NT), 0, st, x, n, dkey, q);
   return hipGetLastError();
 }
 
@@ -576,7 +605,9 @@ __global__ __launch_bounds__(NT) void k_wscale_cols(const float* __restrict__ W,
   }
 }
 
-// per tensor: order-key min / max of the whole array into work[0], work[1].
+// per tensor: order-key min / max of the whole array into work[0], work[1],
+// the two 32-bit halves of the caller's scales[0]; k_wscale_tensor (one
+// thread) reads both keys and then overwrites them with the f64 scale.
 __global__ void k_set_minmax_init(int* work) {
   work[0] = 0x7fffffff;             // key of +NaN-free max -> min starts high
   work[1] = (int)0x80000000;        // max starts low
@@ -610,10 +641,13 @@ __global__ __launch_bounds__(NT) void k_wminmax_tensor(const float* __restrict__
 }
 
 // fromConstantArray (quantization_types.ts:287-297) on the reduced keys.
-__global__ void k_wscale_tensor(const int* __restrict__ work, double* __restrict__ scales) {
-  const bool none = work[0] == 0x7fffffff && work[1] == (int)0x80000000;
-  double mn = none ? __builtin_inf() : (double)from_order_key(work[0]);
-  double mx = none ? -__builtin_inf() : (double)from_order_key(work[1]);
+// The keys are read before the scale overwrites them (one thread).
+__global__ void k_wscale_tensor(double* scales) {
+  const int* work = reinterpret_cast<const int*>(scales);
+  const int kmn = work[0], kmx = work[1];
+  const bool none = kmn == 0x7fffffff && kmx == (int)0x80000000;
+  double mn = none ? __builtin_inf() : (double)from_order_key(kmn);
+  double mx = none ? -__builtin_inf() : (double)from_order_key(kmx);
   scales[0] = channel_scale(mn, mx);
 }
 
@@ -659,16 +693,17 @@ __global__ __launch_bounds__(NT) void k_wquant_cols_t(const float* __restrict__ 
 }
 
 hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int per_tensor,
-                              int8_t* Wq, double* scales, int* work, hipStream_t st) {
+                              int8_t* Wq, double* scales, hipStream_t st) {
   // An empty channel keeps the (inf, -inf) start values, which the fix-ups
   // turn into (-1, 1) -> 1/127; the scale kernels below produce that too.
   const int64_t nch = per_tensor ? 1 : (axis == 0 ? rows : cols);
   if (nch == 0) return hipSuccess;
   if (per_tensor) {
+    int* work = reinterpret_cast<int*>(scales);
     hipLaunchKernelGGL(k_set_minmax_init, dim3(1), dim3(1), 0, st, work);
     hipLaunchKernelGGL(k_wminmax_tensor, dim3(grid_for(rows * cols, NT * 8, 2048)), dim3(NT), 0, st,
                        W, rows * cols, work);
-    hipLaunchKernelGGL(k_wscale_tensor, dim3(1), dim3(1), 0, st, work, scales);
+    hipLaunchKernelGGL(k_wscale_tensor, dim3(1), dim3(1), 0, st, scales);
   } else if (axis == 0) {
     hipLaunchKernelGGL(k_wscale_rows, dim3((unsigned)(rows < 1048576 ? rows : 1048576)), dim3(NT),
                        0, st, W, rows, cols, scales);

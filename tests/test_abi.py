@@ -101,6 +101,18 @@ def test_validation_happens_before_any_launch(lib):
     assert gv(fake, fake, 17, 4, 16, fake, 0, fake, 0, 1, 0.0, nil, 0, lib.Q8_F32, fake, nil) == 1
 
 
+def test_per_tensor_key_needs_an_aligned_scale_slot(lib):
+    """Per-tensor reductions keep their running key in the caller's scales
+    output (a 64-bit atomic), so that slot must be 8-byte aligned."""
+    fake, odd, nil = C.c_void_p(0x1000), C.c_void_p(0x1004), None
+    expect_invalid(lib, "q8_quantize_rows", fake, 4, 8, lib.Q8_PER_TENSOR, fake, odd, nil,
+                   match="aligned")
+    expect_invalid(lib, "q8_pack_weight", fake, 4, 8, 0, lib.Q8_PER_TENSOR, fake, odd, nil,
+                   match="aligned")
+    expect_invalid(lib, "q8_qlinear_dynamic", fake, 4, 16, lib.Q8_PER_TENSOR, fake, fake,
+                   lib.Q8_PER_CHANNEL, 8, nil, 0, fake, fake, odd, nil, match="aligned")
+
+
 def test_nonzero_zero_points_are_unsupported_not_wrong(lib):
     """q8_gemm (the fused-epilogue GEMM) takes no zero points; the
     reference's quantized_dot with zero points is q8_quantized_dot."""

@@ -117,6 +117,84 @@ def test_quantize_per_tensor(ops, oracle, n):
     same_bits(host(q), oracle.quantize(x, s_ref))
 
 
+@pytest.mark.parametrize("fill", ["zeros", "nans", "nan_and_zero", "inf"])
+def test_quantize_per_tensor_degenerate(ops, oracle, fill):
+    # all zeros -> 1e-10, only NaNs -> +inf (an observer that saw no value),
+    # an infinity -> +inf; the key's start value and the final mapping
+    x = np.zeros(5000, np.float32)
+    if fill == "nans":
+        x[:] = np.nan
+    elif fill == "nan_and_zero":
+        x[::2] = np.nan
+    elif fill == "inf":
+        x = oracle.Rng(4).normal((5000,))
+        x[77] = -np.inf
+    q, s = ops.quantize_per_tensor(dev(x))
+    s_ref = oracle.scale_per_tensor(x)
+    same_bits(host(s), np.array([s_ref]))
+    same_bits(host(q), oracle.quantize(x, s_ref))
+
+
+def test_quantize_per_tensor_concurrent_streams(ops, oracle):
+    # Per-tensor reductions keep their key in the call's own scales output,
+    # so calls on different streams with different outputs never interfere.
+    # Each stream's tensor has its own absmax; all calls are enqueued before
+    # any is waited for, several rounds in a row.
+    n = 1 << 20
+    xs = []
+    for i in range(4):
+        x = oracle.Rng(40 + i).normal((n,))
+        x[1000 * i + 3] = 10.0 * (i + 2)
+        xs.append(x)
+    streams = [torch.cuda.Stream() for _ in xs]
+    xd = [dev(x) for x in xs]
+    torch.cuda.synchronize()
+    outs = [(torch.empty(n, dtype=torch.int8, device=DEV),
+             torch.empty(1, dtype=torch.float64, device=DEV)) for _ in xs]
+    for _ in range(5):
+        for st, x, (q, s) in zip(streams, xd, outs):
+            with torch.cuda.stream(st):
+                ops.quantize_per_tensor(x, q, s)
+        torch.cuda.synchronize()
+        for x, (q, s) in zip(xs, outs):
+            s_ref = oracle.scale_per_tensor(x)
+            same_bits(host(s), np.array([s_ref]))
+            same_bits(host(q), oracle.quantize(x, s_ref))
+
+
+def test_pack_weight_per_tensor_concurrent_streams(ops, oracle):
+    Ws = [oracle.Rng(60 + i).normal((256, 512), 0.0, 0.5 + i) for i in range(3)]
+    streams = [torch.cuda.Stream() for _ in Ws]
+    Wd = [dev(W) for W in Ws]
+    torch.cuda.synchronize()
+    res = []
+    for st, W in zip(streams, Wd):
+        with torch.cuda.stream(st):
+            res.append(ops.pack_weight(W, axis=0, granularity="per_tensor"))
+    torch.cuda.synchronize()
+    for W, (Wq, s) in zip(Ws, res):
+        s_ref = oracle.scale_const_array(W)
+        same_bits(host(s), np.array([s_ref]))
+        same_bits(host(Wq), oracle.weight_quantize_per_tensor(W, s_ref, -127, 127))
+
+
+@pytest.mark.parametrize("ldx", [8, 12])
+def test_quantize_per_token_many_rows(ops, oracle, ldx):
+    # More rows than the 2^20 row workers of one launch: the pipelined loop
+    # (two register sets, the prefetch of row + G, the early exit), with
+    # contiguous and row-strided rows.
+    M, K = (1 << 20) + 3, 8
+    x = oracle.Rng(77).normal((M, ldx))
+    x[::4099, 1] = 9.0
+    x[5::7001, :K] = 0.0
+    xd = dev(x)
+    q, s = ops.quantize_per_token(xd[:, :K] if ldx != K else xd)
+    xc = np.ascontiguousarray(x[:, :K])
+    s_ref = oracle.scales_per_token(xc)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(xc, s_ref))
+
+
 @pytest.mark.parametrize("scale,zp,tgt", [(6 / 127, 0.0, "i8"), (0.0123, 0.0, "i8"),
                                           (6 / 255, -128.0, "i8"), (1 / 255, 0.0, "ui8"),
                                           (6 / 255, 3.0, "ui8"), (1e-10, 0.0, "i8"),
