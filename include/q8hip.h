@@ -264,6 +264,23 @@ int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const i
                        const double* sW, int sW_mode, int64_t N, const float* bias, int act,
                        float* out, int8_t* xq, double* sx, void* stream);
 
+/* q8_qlinear_dynamic without caller buffers for xq / sx and without any
+ * allocation.  No counterpart in the reference: this entry point is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The codes and
+ * scales of x are staged in a file-scope device array of
+ * Q8_NOALLOC_SCRATCH_BYTES bytes that each GPU holds until the process
+ * ends; x needs round_up(M*K, 256) + 8*M bytes of it (8 for per tensor),
+ * and a larger x is rejected with Q8_ERR_INVALID.  out is bit for bit that
+ * of q8_qlinear_dynamic.  Every call on one GPU shares that GPU's array and
+ * leaves the last call's staging in it: calls that overlap in time on one
+ * GPU (two streams, or two host threads) race, so order them on one
+ * stream. */
+#define Q8_NOALLOC_SCRATCH_BYTES (4u << 20)
+int q8_qlinear_dynamic_noalloc(const float* x, int64_t M, int64_t K, int x_mode,
+                               const int8_t* Wq, const double* sW, int sW_mode, int64_t N,
+                               const float* bias, int act, float* out, void* stream);
+
 /* q8_gemm's fp32 result, requantized in the epilogue with the next layer's
  * static scale and stored as int8: QuantizationPass's calibrated chain
  * dequantize -> [add bias] -> [relu] -> quantize(s_next)

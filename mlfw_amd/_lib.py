@@ -32,6 +32,7 @@ Q8_CALIB_MINMAX, Q8_CALIB_PERCENTILE, Q8_CALIB_ENTROPY = 0, 1, 2
 Q8_SCHEME_PER_TENSOR_SYMMETRIC, Q8_SCHEME_PER_TENSOR_ASYMMETRIC, Q8_SCHEME_PER_CHANNEL = 0, 1, 2
 Q8_OBS_MAX_BINS = 8192
 Q8_OBS_SUMMARY = 9
+Q8_NOALLOC_SCRATCH_BYTES = 4 << 20   # scratch of q8_qlinear_dynamic_noalloc
 
 
 class Q8Error(RuntimeError):
@@ -77,6 +78,8 @@ SIGNATURES = {
                          _vp, _vp],
     "q8_qlinear_dynamic": [_vp, _i64, _i64, _int, _vp, _vp, _int, _i64, _vp, _int, _vp, _vp, _vp,
                            _vp],
+    "q8_qlinear_dynamic_noalloc": [_vp, _i64, _i64, _int, _vp, _vp, _int, _i64, _vp, _int, _vp,
+                                   _vp],
     "q8_pack_weight_int4": [_vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "q8_gemv_w4": [_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _int, _vp, _vp],
     "q8_quantized_conv_workspace": [_int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp],

@@ -36,13 +36,22 @@ int hip_fail(hipError_t e, const char* what) {
 
 // Per-device state: initialised once.  The library allocates no device
 // memory for the ops: per-tensor reductions keep their keys in the caller's
-// scales output and workspaces come from the caller.
+// scales output and workspaces come from the caller.  The one exception is
+// `scratch` below, a file-scope device array (no allocation call) that only
+// q8_qlinear_dynamic_noalloc uses.
 constexpr int kMaxDevices = 64;
 struct DevState {
   std::atomic<int> ready{0};
+  unsigned char* scratch = nullptr;   // this device's copy of `scratch`
 };
 DevState g_dev[kMaxDevices];
 std::mutex g_init_mu;
+
+// Staging of q8_qlinear_dynamic_noalloc: the int8 codes of x and their f64
+// scales.  Every device the library runs on holds its own copy until the
+// process ends.  In host code the name is only a stand-in for the symbol:
+// its device address comes from hipGetSymbolAddress (g_dev[dev].scratch).
+static __device__ __align__(256) unsigned char scratch[Q8_NOALLOC_SCRATCH_BYTES];
 
 int init_device(int dev) {
   if (dev < 0 || dev >= kMaxDevices) return fail(Q8_ERR_INVALID, "device %d out of range", dev);
@@ -61,19 +70,25 @@ int init_device(int dev) {
   if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   e = q8::setup_kernel_attributes();
   (void)q8::cu_count();
+  void* sp = nullptr;
+  if (e == hipSuccess) e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
   if (cur != dev) (void)hipSetDevice(cur);
   if (e != hipSuccess) return hip_fail(e, "device set-up");
+  if (sp == nullptr) return fail(Q8_ERR_DEVICE, "device %d: no address for the scratch array", dev);
+  g_dev[dev].scratch = static_cast<unsigned char*>(sp);
   g_dev[dev].ready.store(1, std::memory_order_release);
   return Q8_OK;
 }
 
-// Initialise the calling thread's current device on first use.
-int ensure_current() {
+// Initialise the calling thread's current device on first use; `scratch`
+// (may be NULL) receives that device's address of the scratch array.
+int ensure_current(unsigned char** scratch_out = nullptr) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice (no HIP device?)");
   int rc = init_device(dev);
   if (rc != Q8_OK) return rc;
+  if (scratch_out) *scratch_out = g_dev[dev].scratch;
   return Q8_OK;
 }
 
@@ -507,7 +522,9 @@ int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int
   return launched(err, "q8_quantized_dot launch");
 }
 
-// Body of the dynamic linear once the arguments are checked.
+// Body of the dynamic linear once the arguments are checked; xq / sx are
+// the caller's outputs (q8_qlinear_dynamic) or the scratch staging
+// (q8_qlinear_dynamic_noalloc).
 static hipError_t qlinear_dynamic_run(const float* x, int64_t M, int64_t K, int x_mode,
                                       const int8_t* Wq, const double* sW, int64_t N,
                                       const float* bias, int act, float* out, int8_t* xq,
@@ -541,6 +558,42 @@ int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const i
   return launched(qlinear_dynamic_run(x, M, K, x_mode, Wq, sW, N, bias, act, out, xq, sx, e,
                                       as_stream(stream)),
                   "q8_qlinear_dynamic launch");
+}
+
+int q8_qlinear_dynamic_noalloc(const float* x, int64_t M, int64_t K, int x_mode,
+                               const int8_t* Wq, const double* sW, int sW_mode, int64_t N,
+                               const float* bias, int act, float* out, void* stream) {
+  Q8_REQUIRE(x_mode == Q8_PER_TOKEN || x_mode == Q8_PER_TENSOR,
+             "q8_qlinear_dynamic_noalloc: x_mode must be Q8_PER_TOKEN or Q8_PER_TENSOR (got %d)",
+             x_mode);
+  Q8_REQUIRE(M >= 0 && K >= 0 && mul_ok(M, K), "q8_qlinear_dynamic_noalloc: bad shape [%lld,%lld]",
+             (long long)M, (long long)K);
+  // staging: codes at offset 0, scales at the next 256-byte boundary
+  const int64_t codes = (M * K + 255) / 256 * 256;
+  const int64_t nsc = x_mode == Q8_PER_TOKEN ? M : 1;
+  Q8_REQUIRE(M <= (int64_t)Q8_NOALLOC_SCRATCH_BYTES &&
+                 codes + 8 * nsc <= (int64_t)Q8_NOALLOC_SCRATCH_BYTES,
+             "q8_qlinear_dynamic_noalloc: x of [%lld,%lld] needs %lld bytes of staging; the "
+             "scratch holds %lld (use q8_qlinear_dynamic with caller buffers)",
+             (long long)M, (long long)K, (long long)(codes + 8 * nsc),
+             (long long)Q8_NOALLOC_SCRATCH_BYTES);
+  // a stand-in, non-NULL, 8-aligned pointer lets gemm_common check the
+  // other arguments; the real staging addresses are set below
+  int8_t* const fake_xq = reinterpret_cast<int8_t*>(static_cast<uintptr_t>(256));
+  double* const fake_sx = reinterpret_cast<double*>(static_cast<uintptr_t>(256));
+  q8::GemmEpi e;
+  int rc = gemm_common("q8_qlinear_dynamic_noalloc", fake_xq, Wq, M, N, K, 0, 0, fake_sx, x_mode,
+                       sW, sW_mode, Q8_EPI_ROWCOL, 0.0, bias, act, Q8_F32, out, &e);
+  if (rc != Q8_OK) return rc;
+  Q8_REQUIRE(M * K == 0 || x, "q8_qlinear_dynamic_noalloc: x is NULL");
+  unsigned char* sp = nullptr;
+  rc = ensure_current(&sp);
+  if (rc != Q8_OK) return rc;
+  int8_t* xq = reinterpret_cast<int8_t*>(sp);
+  double* sx = reinterpret_cast<double*>(sp + codes);
+  return launched(qlinear_dynamic_run(x, M, K, x_mode, Wq, sW, N, bias, act, out, xq, sx, e,
+                                      as_stream(stream)),
+                  "q8_qlinear_dynamic_noalloc launch");
 }
 
 int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
