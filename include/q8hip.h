@@ -389,6 +389,95 @@ int q8_silu_mul_quantize_rows_ld(const float* g, int64_t ldg, const float* u, in
                                  int64_t M, int64_t K, float* h_out, int8_t* q, double* scales,
                                  void* stream);
 
+/* ------------------------------------------------------------ elementwise */
+
+/* One elementwise loop nest -- a PrimFunc the reference lowers to a loop nest
+ * with a single store, e.g. the per-channel tail convert -> broadcast ->
+ * mul that QuantizationPass emits after quantized_dot
+ * (quantization_pass.ts:431-456), the bias add, ReLU (max) or a `quantize`
+ * fused into such a group (rules/fusion.ts:66-79) -- evaluated on the device
+ * with the reference CPU backend's arithmetic (src/backend/cpu/codegen.ts:
+ * 428-552): every value is an f64, an f32-typed MathOp or non-exact extern
+ * is rounded once to binary32 (Math.fround), exact externs (max, min, abs,
+ * floor, ceil, round, sign, sqrt, fmod) are not rounded, a cast to an
+ * integer type is ToInt32 (`| 0`), and the store converts like a typed-array
+ * store (Float32Array: RNE; Int32Array / Int8Array / Uint8Array: the low
+ * 32 / 8 bits of ToInt32).
+ *
+ * The loop nest has `ndims` loops of the given extents (row-major, the last
+ * fastest); loop index i_d.  Input j is read at element offset
+ * in_coef[j][0..ndims-1] . i + in_coef[j][Q8_EW_MAX_DIMS] (broadcasts have
+ * zero coefficients); the output is written at the row-major offset of i.
+ * The program is straight-line code over Q8_EW_MAX_REGS f64 registers; the
+ * value of register `result` is stored. */
+#define Q8_F64 4                 /* element type of q8_ewise inputs / output */
+#define Q8_EW_MAX_DIMS   6
+#define Q8_EW_MAX_INPUTS 8
+#define Q8_EW_MAX_CODE   96
+#define Q8_EW_MAX_REGS   16
+#define Q8_EW_MAX_CONST  32
+
+/* opcodes: r[dst] = ... ; `rnd` = 1 rounds the result to binary32 */
+#define Q8_EW_LOAD     0   /* input[aux] at its offset */
+#define Q8_EW_CONST    1   /* konst[aux] */
+#define Q8_EW_INDEX    2   /* (double) i_aux, a loop index */
+#define Q8_EW_ADD      3   /* a + b */
+#define Q8_EW_SUB      4   /* a - b */
+#define Q8_EW_MUL      5   /* a * b */
+#define Q8_EW_DIV      6   /* a / b */
+#define Q8_EW_IDIV     7   /* Math.trunc(a / b) (int-typed '/') */
+#define Q8_EW_MOD      8   /* ((a % b + b) % b) */
+#define Q8_EW_FLOORDIV 9   /* Math.floor(a / b) */
+#define Q8_EW_TMOD     10  /* a % b */
+#define Q8_EW_TDIV     11  /* ((a / b) | 0) */
+#define Q8_EW_NEG      12  /* -a */
+#define Q8_EW_CMP      13  /* (a OP b) ? 1 : 0, OP = aux: 0 ==, 1 !=, 2 <, 3 <=, 4 >, 5 >= */
+#define Q8_EW_SELECT   14  /* a ? b : c (a truthy: not 0, not NaN) */
+#define Q8_EW_TOINT32  15  /* a | 0 */
+#define Q8_EW_TOBOOL   16  /* a ? 1 : 0 */
+#define Q8_EW_MAX      17  /* Math.max(a, b) */
+#define Q8_EW_MIN      18  /* Math.min(a, b) */
+#define Q8_EW_ABS      19
+#define Q8_EW_FLOOR    20
+#define Q8_EW_CEIL     21
+#define Q8_EW_ROUND    22  /* Math.round */
+#define Q8_EW_SIGN     23
+#define Q8_EW_SQRT     24
+#define Q8_EW_FMOD     25  /* ((a % b + b) % b) */
+#define Q8_EW_EXP      26
+#define Q8_EW_LOG      27
+#define Q8_EW_TANH     28
+#define Q8_EW_RSQRT    29  /* 1 / Math.sqrt(a) */
+#define Q8_EW_POW      30
+#define Q8_EW_NOPS     31
+
+typedef struct {
+  uint8_t op, dst, a, b, c, aux, rnd, pad;
+} q8_ew_instr;
+
+typedef struct {
+  int32_t ndims;
+  int32_t ninputs;
+  int64_t extent[Q8_EW_MAX_DIMS];
+  int32_t in_dtype[Q8_EW_MAX_INPUTS];     /* Q8_I8, Q8_U8, Q8_I32, Q8_F32, Q8_F64 */
+  int64_t in_coef[Q8_EW_MAX_INPUTS][Q8_EW_MAX_DIMS + 1];
+  int32_t out_dtype;
+  int32_t ncode;
+  int32_t result;
+  int32_t nconst;
+  q8_ew_instr code[Q8_EW_MAX_CODE];
+  double konst[Q8_EW_MAX_CONST];
+} q8_ew_prog;
+
+/* Runs `prog` over its loop nest: inputs[j] is a device array of
+ * in_numel[j] elements of prog->in_dtype[j], out a device array of
+ * out_numel elements of prog->out_dtype (out_numel = product of the
+ * extents).  Every input offset the nest can form is checked against
+ * in_numel on the host before the launch.  Inputs may alias each other but
+ * not the output. */
+int q8_ewise(const q8_ew_prog* prog, const void* const* inputs, const int64_t* in_numel,
+             void* out, int64_t out_numel, void* stream);
+
 /* ------------------------------------------------------------ calibration */
 
 /* An observer is a device buffer of q8_observer_state_bytes(num_bins) bytes

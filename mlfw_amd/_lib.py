@@ -32,6 +32,7 @@ Q8_CALIB_MINMAX, Q8_CALIB_PERCENTILE, Q8_CALIB_ENTROPY = 0, 1, 2
 Q8_SCHEME_PER_TENSOR_SYMMETRIC, Q8_SCHEME_PER_TENSOR_ASYMMETRIC, Q8_SCHEME_PER_CHANNEL = 0, 1, 2
 Q8_OBS_MAX_BINS = 8192
 Q8_OBS_SUMMARY = 9
+Q8_F64 = 4
 Q8_NOALLOC_SCRATCH_BYTES = 4 << 20   # scratch of q8_qlinear_dynamic_noalloc
 
 
@@ -90,6 +91,7 @@ SIGNATURES = {
     "q8_silu_mul_quantize_rows": [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp],
     "q8_silu_mul_quantize_rows_ld": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
     "q8_quantize_rows_ld": [_vp, _i64, _i64, _i64, _vp, _vp, _vp],
+    "q8_ewise": [_vp, _vp, _vp, _vp, _i64, _vp],
     "q8_observer_state_bytes": [_int, _vp],
     "q8_observer_reset": [_vp, _int, _int, _vp],
     "q8_observer_update": [_vp, _vp, _i64, _vp],

@@ -26,7 +26,7 @@ CEILING_LIB = os.path.join(HERE, "libq8ceiling.so")
 CEILING_SRC = "q8_ceiling.hip"
 
 SOURCES = ["q8_capi.hip", "q8_quant.hip", "q8_gemm.hip", "q8_calib.hip", "q8_conv.hip", "q8_w4.hip",
-           "q8_zp.hip"]
+           "q8_zp.hip", "q8_ewise.hip"]
 
 # IEEE arithmetic everywhere (the kernels reproduce the reference's f64 /
 # f32 rounding bit for bit), no packed-FP32 instructions, gfx950 only.

@@ -806,6 +806,24 @@ int q8_silu_mul_quantize_rows(const float* g, const float* u, int64_t M, int64_t
   return q8_silu_mul_quantize_rows_ld(g, K, u, K, M, K, h_out, q, scales, stream);
 }
 
+int q8_ewise(const q8_ew_prog* prog, const void* const* inputs, const int64_t* in_numel,
+             void* out, int64_t out_numel, void* stream) {
+  Q8_REQUIRE(prog != nullptr, "q8_ewise: prog is NULL");
+  Q8_REQUIRE(out_numel >= 0, "q8_ewise: negative out_numel");
+  Q8_REQUIRE(prog->ninputs == 0 || (inputs && in_numel), "q8_ewise: inputs / in_numel is NULL");
+  const char* why = q8::ewise_check(*prog, in_numel, out_numel);
+  Q8_REQUIRE(why == nullptr, "q8_ewise: %s", why);
+  if (out_numel > 0) {
+    Q8_REQUIRE(out != nullptr, "q8_ewise: out is NULL");
+    for (int j = 0; j < prog->ninputs; ++j)
+      Q8_REQUIRE(inputs[j] != nullptr, "q8_ewise: input %d is NULL", j);
+  }
+  int rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_ewise(*prog, inputs, out, out_numel, as_stream(stream)),
+                  "q8_ewise launch");
+}
+
 int q8_observer_state_bytes(int num_bins, size_t* bytes) {
   Q8_REQUIRE(num_bins >= 1 && num_bins <= Q8_OBS_MAX_BINS,
              "q8_observer_state_bytes: num_bins must be in [1, %d] (got %d)", Q8_OBS_MAX_BINS,

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/q8hip.h"
+
 namespace q8 {
 
 // Epilogue description passed by value to the GEMM / GEMV kernels.
@@ -128,5 +130,10 @@ hipError_t setup_kernel_attributes();
 
 // Compute units of the current device (cached per device).
 int cu_count();
+
+// elementwise loop nests (q8_ewise.hip); q8_ew_prog comes from q8hip.h
+const char* ewise_check(const q8_ew_prog& p, const int64_t* in_numel, int64_t out_numel);
+hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* out, int64_t n,
+                        hipStream_t st);
 
 }  // namespace q8

@@ -278,13 +278,51 @@ function detectInt8Kernel(primFunc) {
   return null;
 }
 
+// ---------------------------------------------------------------- device residency
+// Constant tensors (a kernel's constant buffers: QuantizationPass's int8
+// weights and f32 scale vectors, src/compiler/passes/lowering/graph_to_tensor.ts:
+// 210-239) keep one device copy per host typed array, uploaded on first use
+// -- the rule of the reference CUDA runtime's resident mirrors
+// (src/runtime/node/cuda/resident.ts:129-140, cuda_runtime.ts:123-146).  A
+// derived form (the [N,K] transpose of a [K,N] weight, f64 widening of an
+// f32 scale vector) is cached beside it.  markHostDirty(array) drops the
+// copies of an array the host rewrote.
+const stats = { uploadBytes: 0, constUploadBytes: 0, downloadBytes: 0, launches: 0, fusedLinears: 0 };
+const _resident = new WeakMap();
+
+function resetStats() { for (const k of Object.keys(stats)) stats[k] = 0; }
+
+function upload(dbuf, host, isConst) {
+  q8().upload(dbuf, host);
+  stats.uploadBytes += host.byteLength;
+  if (isConst) stats.constUploadBytes += host.byteLength;
+}
+
+function download(host, dbuf) {
+  q8().download(host, dbuf);
+  stats.downloadBytes += host.byteLength;
+}
+
+function residentConst(arr, variant, derive) {
+  let m = _resident.get(arr);
+  if (!m) { m = new Map(); _resident.set(arr, m); }
+  let b = m.get(variant);
+  if (!b) {
+    const host = derive ? derive(arr) : arr;
+    b = q8().alloc(Math.max(host.byteLength, 1));
+    upload(b, host, true);
+    m.set(variant, b);
+  }
+  return b;
+}
+
+function markHostDirty(arr) { _resident.delete(arr); }
+
 // ---------------------------------------------------------------- runtime backend
 const SRC_CODE = { i8: 'Q8_I8', ui8: 'Q8_U8', i32: 'Q8_I32' };
 const ACT_CODE = { none: 'Q8_ACT_NONE', relu: 'Q8_ACT_RELU', silu: 'Q8_ACT_SILU' };
 
-function bytesOf(a) { return a.byteLength; }
-
-/** Device buffers of one kernel instance, reused across runs. */
+/** Device buffers of one kernel instance (or plan), reused across runs. */
 class DeviceArgs {
   constructor() { this.bufs = new Map(); }
   get(key, bytes) {
@@ -294,6 +332,12 @@ class DeviceArgs {
       b = q8().alloc(Math.max(bytes, 1));
       this.bufs.set(key, b);
     }
+    return b;
+  }
+  f64(key, values) {                    // a small constant f64 array, uploaded once
+    const k = `${key}:${values.join(',')}`;
+    let b = this.bufs.get(k);
+    if (!b) { b = q8().alloc(8 * values.length); upload(b, new Float64Array(values), true); this.bufs.set(k, b); }
     return b;
   }
   release() {
@@ -307,150 +351,333 @@ function need(cond, msg) {
 }
 
 function transposeI8(b, rows, cols) {
-  const t = new Int8Array(rows * cols);
+  const t = new b.constructor(rows * cols);
   for (let r = 0; r < rows; r++) for (let c = 0; c < cols; c++) t[c * rows + r] = b[r * cols + c];
   return t;
 }
 
-function f64(v) { return new Float64Array([v]); }
+const CTOR = { i8: Int8Array, ui8: Uint8Array, i32: Int32Array, f32: Float32Array, f64: Float64Array };
+const ELEM_BYTES = { i8: 1, ui8: 1, i32: 4, f32: 4, f64: 8 };
+const EW_DT = ['i8', 'ui8', 'i32', 'f32', 'f64'];          // Q8_I8 .. Q8_F64
 
-/** Runs one descriptor on typed arrays (host in, host out, device in between). */
-function runDescriptor(d, args, dev) {
+/** Which tensor arguments a descriptor reads ({index: {ctor, n, what}}). */
+function inputSpecs(d) {
+  const s = new Map();
+  const add = (i, ctor, n, what) => { if (i !== undefined && i >= 0) s.set(i, { ctor, n, what: `${d.op} ${what}` }); };
+  switch (d.op) {
+    case 'quantize': add(d.inIdx, Float32Array, d.n, 'input'); break;
+    case 'dequantize': add(d.inIdx, CTOR[d.srcDtype], d.n, 'input'); break;
+    case 'quantized_dot':
+      add(d.aIdx, CTOR[d.aDtype || 'i8'], d.M * d.K, 'lhs');
+      add(d.bIdx, CTOR[d.bDtype || 'i8'], d.N * d.K, 'rhs');
+      break;
+    case 'quantized_conv':
+      add(d.xIdx, CTOR[d.xDtype || 'i8'], numel(d.xShape), 'input');
+      add(d.wIdx, CTOR[d.wDtype || 'i8'], numel(d.wShape), 'kernel');
+      break;
+    case 'qlinear':
+      add(d.xIdx, Float32Array, d.M * d.K, 'x'); add(d.wqIdx, Int8Array, d.N * d.K, 'wq');
+      add(d.wsIdx, Float64Array, d.N, 'weight scales'); add(d.biasIdx, Float32Array, d.N, 'bias');
+      break;
+    case 'qlinear_requant':
+      need(typeof d.sNext === 'number', 'qlinear_requant needs the static scale sNext');
+      add(d.xqIdx, Int8Array, d.M * d.K, 'xq');
+      add(d.sxIdx, Float64Array, d.granularity === 'per_tensor' ? 1 : d.M, 'activation scales');
+      add(d.wqIdx, Int8Array, d.N * d.K, 'wq'); add(d.wsIdx, Float64Array, d.N, 'weight scales');
+      add(d.biasIdx, Float32Array, d.N, 'bias');
+      break;
+    case 'qlinear_w4':
+      need(d.group > 0 && d.K % d.group === 0, 'qlinear_w4 group must divide K');
+      add(d.xIdx, Float32Array, d.M * d.K, 'x'); add(d.wqIdx, Uint8Array, d.N * d.K / 2, 'packed weights');
+      add(d.swIdx, Float64Array, d.N * d.K / d.group, 'group scales'); add(d.biasIdx, Float32Array, d.N, 'bias');
+      break;
+    case 'ewise':
+      d.inputIdx.forEach((p, j) => {
+        if (!s.has(p)) s.set(p, { ctor: CTOR[EW_DT[d.prog.inDtype[j]]], n: d.inNumel[j], min: true, what: `ewise input ${j}` });
+      });
+      break;
+    default: throw new Error(`hip backend: unknown op '${d.op}'`);
+  }
+  return s;
+}
+
+/** Output arguments of a descriptor ({index: {ctor, n, what}}). */
+function outputSpecs(d) {
+  const s = new Map();
+  const set = (ctor, n) => s.set(d.outIdx, { ctor, n, what: `${d.op} out` });
+  switch (d.op) {
+    case 'quantize': set(d.targetDtype === 'ui8' ? Uint8Array : Int8Array, d.n); break;
+    case 'dequantize': set(Float32Array, d.n); break;
+    case 'quantized_dot': set(Int32Array, d.M * d.N); break;
+    case 'quantized_conv': set(Int32Array, numel(d.outShape)); break;
+    case 'qlinear': case 'qlinear_w4': set(Float32Array, d.M * d.N); break;
+    case 'qlinear_requant': set(Int8Array, d.M * d.N); break;
+    case 'ewise': set(CTOR[EW_DT[d.prog.outDtype]], d.outNumel); break;
+    default: throw new Error(`hip backend: unknown op '${d.op}'`);
+  }
+  return s;
+}
+
+function checkArg(a, spec) {
+  need(a instanceof spec.ctor, `${spec.what} must be a ${spec.ctor.name}`);
+  need(spec.min ? a.length >= spec.n : a.length === spec.n,
+       `${spec.what} has ${a.length} elements, expected ${spec.n}`);
+}
+
+/**
+ * Runs a descriptor on device buffers: `dv[i]` is the device buffer of
+ * tensor argument i; `rhsNK` (quantized_dot) is the weight already in the
+ * [N,K] layout when the caller has it.
+ */
+function execDevice(d, dv, dev, rhsNK) {
   const A = q8();
-  if (d.op === 'quantize') {
-    const x = args[d.inIdx], q = args[d.outIdx];
-    need(x instanceof Float32Array && x.length === d.n, 'quantize input must be a Float32Array of n');
-    need(q.length === d.n && (q instanceof Int8Array || q instanceof Uint8Array), 'quantize output');
-    const dx = dev.get('x', bytesOf(x)), dq = dev.get('q', d.n);
-    A.upload(dx, x);
-    A.quantizeStatic(dx, d.n, d.scale, d.zeroPoint, A[d.targetDtype === 'ui8' ? 'Q8_U8' : 'Q8_I8'], dq);
-    A.download(q, dq);
-    return q;
+  stats.launches++;
+  switch (d.op) {
+    case 'quantize':
+      A.quantizeStatic(dv[d.inIdx], d.n, d.scale, d.zeroPoint, A[d.targetDtype === 'ui8' ? 'Q8_U8' : 'Q8_I8'], dv[d.outIdx]);
+      return;
+    case 'dequantize':
+      A.dequantize(dv[d.inIdx], A[SRC_CODE[d.srcDtype]], 1, d.n, dev.f64('s', [d.scale]), A.Q8_PER_TENSOR,
+                   d.zeroPoint, dv[d.outIdx]);
+      return;
+    case 'quantized_dot': {
+      const aD = (d.aDtype || 'i8') === 'ui8' ? A.Q8_U8 : A.Q8_I8, bD = (d.bDtype || 'i8') === 'ui8' ? A.Q8_U8 : A.Q8_I8;
+      let b = rhsNK;
+      if (!b) {
+        b = dv[d.bIdx];
+        if (d.rhsLayout === 'KN') {        // [K,N] -> [N,K] on the device
+          const t = dev.get('bT', d.N * d.K);
+          A.ewise(transposeProg(d.K, d.N, bD === A.Q8_U8 ? 1 : 0), [b], [d.N * d.K], t, d.N * d.K);
+          b = t;
+        }
+      }
+      const ws = A.quantizedDotWorkspace(d.M, d.N, d.K, aD, bD, d.zpA, d.zpB);
+      A.quantizedDot(dv[d.aIdx], aD, b, bD, d.M, d.N, d.K, d.zpA, d.zpB, ws > 0 ? dev.get('ws', ws) : null,
+                     dv[d.outIdx]);
+      return;
+    }
+    case 'quantized_conv': {
+      const xD = (d.xDtype || 'i8') === 'ui8' ? A.Q8_U8 : A.Q8_I8, wD = (d.wDtype || 'i8') === 'ui8' ? A.Q8_U8 : A.Q8_I8;
+      const ws = A.convWorkspace(d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups);
+      A.quantizedConvEx(dv[d.xIdx], xD, dv[d.wIdx], wD, d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi,
+                        d.dilation, d.groups, d.zpX, d.zpW, A.Q8_I32, 0, ws > 0 ? dev.get('ws', ws) : null,
+                        dv[d.outIdx]);
+      return;
+    }
+    case 'qlinear': {
+      // dynamic per-token int8 linear: x fp32 [M,K]; wq int8 [N,K] + f64 scales [N];
+      // quantize + GEMM + epilogue in one call (one kernel for a single token)
+      const perTensor = d.granularity === 'per_tensor';
+      A.qlinearDynamic(dv[d.xIdx], d.M, d.K, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN, dv[d.wqIdx], dv[d.wsIdx],
+                       A.Q8_PER_CHANNEL, d.N, d.biasIdx >= 0 ? dv[d.biasIdx] : null, A[ACT_CODE[d.act || 'none']],
+                       dv[d.outIdx], dev.get('xq', d.M * d.K), dev.get('sx', 8 * (perTensor ? 1 : d.M)));
+      return;
+    }
+    case 'qlinear_requant': {
+      // int8 codes in, the next layer's static-scale codes out (the calibrated
+      // chain ... mul(sv) -> add(b) -> max -> quantize)
+      const perTensor = d.granularity === 'per_tensor';
+      A.gemmRequant(dv[d.xqIdx], dv[d.wqIdx], d.M, d.N, d.K, dv[d.sxIdx], perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN,
+                    dv[d.wsIdx], A.Q8_PER_CHANNEL, A.Q8_EPI_ROWCOL, 0, d.biasIdx >= 0 ? dv[d.biasIdx] : null,
+                    A[ACT_CODE[d.act || 'none']], d.sNext, dv[d.outIdx]);
+      return;
+    }
+    case 'qlinear_w4': {
+      // decode linear with 4-bit per-group weights: per-token int8 quantize of
+      // x, then the W4A8 GEMV
+      const dxq = dev.get('xq', d.M * d.K), dsx = dev.get('sx', 8 * d.M);
+      A.quantizeRows(dv[d.xIdx], d.M, d.K, A.Q8_PER_TOKEN, dxq, dsx);
+      A.gemvW4(dxq, dsx, A.Q8_PER_TOKEN, dv[d.wqIdx], dv[d.swIdx], d.M, d.N, d.K, d.group,
+               d.biasIdx >= 0 ? dv[d.biasIdx] : null, A[ACT_CODE[d.act || 'none']], dv[d.outIdx]);
+      return;
+    }
+    case 'ewise':
+      A.ewise(d.progBytes || (d.progBytes = ew().packProg(d.prog)), d.inputIdx.map((p) => dv[p]), d.inNumel,
+              dv[d.outIdx], d.outNumel);
+      return;
+    default:
+      throw new Error(`hip backend: unknown op '${d.op}'`);
   }
-  if (d.op === 'dequantize') {
-    const q = args[d.inIdx], y = args[d.outIdx];
-    need(q.length === d.n && y instanceof Float32Array && y.length === d.n, 'dequantize shapes');
-    const dq = dev.get('q', bytesOf(q)), ds = dev.get('s', 8), dy = dev.get('y', 4 * d.n);
-    A.upload(dq, q);
-    A.upload(ds, f64(d.scale));
-    A.dequantize(dq, A[SRC_CODE[d.srcDtype]], 1, d.n, ds, A.Q8_PER_TENSOR, d.zeroPoint, dy);
-    A.download(y, dy);
-    return y;
+}
+
+// [N,K] <- [K,N] gather as an elementwise program (out[n,k] = in[k,n])
+const _tpCache = new Map();
+function transposeProg(K, N, unsigned) {
+  const key = `${K}x${N}:${unsigned}`;
+  let p = _tpCache.get(key);
+  if (!p) {
+    const dt = unsigned ? 1 : 0;
+    const coef = [1, N, 0, 0, 0, 0, 0];
+    p = ew().packProg({ ndims: 2, ninputs: 1, extent: [N, K], inDtype: [dt], inCoef: [coef], outDtype: dt,
+                        ncode: 1, result: 0, nconst: 0, code: [{ op: ew().OP.LOAD, dst: 0, a: 0, b: 0, c: 0, aux: 0, rnd: 0 }],
+                        konst: [] });
+    _tpCache.set(key, p);
   }
-  if (d.op === 'quantized_dot') {
-    const a = args[d.aIdx], b = args[d.bIdx], out = args[d.outIdx];
-    const aT = (d.aDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
-    const bT = (d.bDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
-    need(a instanceof aT && a.length === d.M * d.K, 'quantized_dot lhs');
-    need(b instanceof bT && b.length === d.N * d.K, 'quantized_dot rhs');
-    need(out instanceof Int32Array && out.length === d.M * d.N, 'quantized_dot output');
-    const aD = aT === Uint8Array ? A.Q8_U8 : A.Q8_I8, bD = bT === Uint8Array ? A.Q8_U8 : A.Q8_I8;
-    const da = dev.get('a', d.M * d.K), db = dev.get('b', d.N * d.K), dout = dev.get('out', 4 * d.M * d.N);
-    const wsBytes = A.quantizedDotWorkspace(d.M, d.N, d.K, aD, bD, d.zpA, d.zpB);
-    const dws = wsBytes > 0 ? dev.get('ws', wsBytes) : null;
-    A.upload(da, a);
-    A.upload(db, d.rhsLayout === 'KN' ? transposeI8(b, d.K, d.N) : b);
-    // zero points and ui8 operands: the exact correction inside the call
-    A.quantizedDot(da, aD, db, bD, d.M, d.N, d.K, d.zpA, d.zpB, dws, dout);
-    A.download(out, dout);
-    return out;
+  return p;
+}
+
+function ew() { return require('./ewise.js'); }
+
+/**
+ * Runs one descriptor on host typed arrays: inputs are uploaded (constant
+ * buffers only once, see residentConst), the op runs on the device, the
+ * outputs are downloaded into the caller's arrays (the outputIndices rule of
+ * the reference CUDA runtime, cuda_runtime.ts:85-121).
+ */
+function runDescriptor(d, args, dev, consts) {
+  const ins = inputSpecs(d), outs = outputSpecs(d);
+  // every argument is checked before the first device call
+  for (const [i, spec] of ins) checkArg(args[i], spec);
+  for (const [i, spec] of outs) checkArg(args[i], spec);
+  const dv = [];
+  let rhsNK = null;
+  for (const [i] of ins) {
+    const a = args[i];
+    const isConst = !!(consts && consts.has(a));
+    if (d.op === 'quantized_dot' && i === d.bIdx && d.rhsLayout === 'KN') {
+      rhsNK = isConst ? residentConst(a, 'T', (w) => transposeI8(w, d.K, d.N)) : null;
+      if (!rhsNK) {
+        rhsNK = dev.get('bT', d.N * d.K);
+        upload(rhsNK, transposeI8(a, d.K, d.N), false);
+      }
+      continue;
+    }
+    if (isConst) { dv[i] = residentConst(a, 'plain'); continue; }
+    dv[i] = dev.get(`in${i}`, a.byteLength);
+    upload(dv[i], a, false);
   }
-  if (d.op === 'quantized_conv') {
-    const x = args[d.xIdx], w = args[d.wIdx], out = args[d.outIdx];
-    const nx = numel(d.xShape), nw = numel(d.wShape), ny = numel(d.outShape);
-    const xT = (d.xDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
-    const wT = (d.wDtype || 'i8') === 'ui8' ? Uint8Array : Int8Array;
-    need(x instanceof xT && x.length === nx, 'quantized_conv input');
-    need(w instanceof wT && w.length === nw, 'quantized_conv kernel');
-    need(out instanceof Int32Array && out.length === ny, 'quantized_conv output');
-    const wsBytes = A.convWorkspace(d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups);
-    const dx = dev.get('x', nx), dw = dev.get('w', nw), dout = dev.get('out', 4 * ny);
-    const dws = wsBytes > 0 ? dev.get('ws', wsBytes) : null;
-    A.upload(dx, x);
-    A.upload(dw, w);
-    A.quantizedConvEx(dx, xT === Uint8Array ? A.Q8_U8 : A.Q8_I8, dw, wT === Uint8Array ? A.Q8_U8 : A.Q8_I8,
-                      d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups,
-                      d.zpX, d.zpW, A.Q8_I32, 0, dws, dout);
-    A.download(out, dout);
-    return out;
+  for (const [i] of outs) dv[i] = dev.get(`out${i}`, args[i].byteLength);
+  execDevice(d, dv, dev, rhsNK);
+  for (const [i] of outs) download(args[i], dv[i]);
+  return args[d.outIdx];
+}
+
+/** Constant-buffer arrays of a compiled kernel (metadata.constBuffers). */
+function constSet(kernel) {
+  const s = new Set();
+  const cbs = kernel && kernel.metadata && kernel.metadata.constBuffers;
+  if (cbs) for (const cb of cbs) if (cb && cb.data) s.add(cb.data);
+  return s;
+}
+
+// ---------------------------------------------------------------- plan execution
+/**
+ * runPlan (backend_registry.ts:14-20, RuntimeModule.runPlanAsync,
+ * runtime.ts:290-329): every step is a hip kernel, so the whole plan runs
+ * with its slots resident on the device.  Plan inputs are uploaded once,
+ * intermediates never leave the device, and the slots the caller reads back
+ * (plan outputs and the sources of return fix-ups) are downloaded at the
+ * end.  A quantized_dot whose int32 result feeds only the per-channel
+ * epilogue group of the next step (matchEpilogue: convert -> mul(sv)
+ * [-> add(b)] [-> max(0)] [-> quantize]) runs as one fused GEMM launch
+ * (q8_gemm / q8_gemm_requant), and the int32 tensor is never written.
+ */
+const _planState = new WeakMap();
+
+function slotBytes(t) { return t && t.data ? t.data.byteLength : 0; }
+
+function runPlanOnDevice(plan, slots, steps, opts) {
+  let st = _planState.get(plan);
+  if (!st) { st = { dev: new DeviceArgs(), inst: new Map() }; _planState.set(plan, st); }
+  const dev = st.dev;
+  const instOf = (kernel) => {
+    let i = st.inst.get(kernel);
+    if (!i) {
+      const d = kernel && kernel.metadata && kernel.metadata.q8;
+      need(kernel && kernel.metadata && kernel.metadata.kind === HIP_KIND && d, `plan step is not a hip kernel`);
+      i = { desc: d, consts: constSet(kernel), constData: (kernel.metadata.constBuffers || []).map((c) => c.data) };
+      st.inst.set(kernel, i);
+    }
+    return i;
+  };
+  const produced = new Map(), readers = new Map();
+  steps.forEach((s, k) => {
+    for (const o of s.outputSlots) if (!produced.has(o)) produced.set(o, k);
+    for (const i of s.inputSlots) { if (!readers.has(i)) readers.set(i, []); readers.get(i).push(k); }
+  });
+  const argSet = new Set(plan.argSlots);
+  const hostNeeds = new Set();
+  for (const a of plan.argSlots) if (produced.has(a)) hostNeeds.add(a);
+  for (const fx of plan.returnFixups || []) if (fx.kind === 'copy') hostNeeds.add(fx.srcSlot);
+  const slotBuf = (s) => dev.get(`slot${s}`, slotBytes(slots[s]));
+  // plan inputs: argument slots read before any step writes them
+  for (const a of plan.argSlots) {
+    const first = produced.has(a) ? produced.get(a) : Infinity;
+    const rd = readers.get(a) || [];
+    if (rd.some((k) => k <= first) && slots[a] && slots[a].data) upload(slotBuf(a), slots[a].data, false);
   }
-  if (d.op === 'qlinear') {
-    // dynamic per-token int8 linear: x fp32 [M,K]; wq int8 [N,K] + f64 scales [N]
-    const x = args[d.xIdx], wq = args[d.wqIdx], ws = args[d.wsIdx], out = args[d.outIdx];
-    const bias = d.biasIdx === undefined || d.biasIdx < 0 ? null : args[d.biasIdx];
-    need(x instanceof Float32Array && x.length === d.M * d.K, 'qlinear x');
-    need(wq instanceof Int8Array && wq.length === d.N * d.K, 'qlinear wq');
-    need(ws instanceof Float64Array && ws.length === d.N, 'qlinear weight scales');
-    need(out instanceof Float32Array && out.length === d.M * d.N, 'qlinear out');
-    need(bias === null || (bias instanceof Float32Array && bias.length === d.N), 'qlinear bias');
-    const perTensor = d.granularity === 'per_tensor';
-    const dx = dev.get('x', 4 * d.M * d.K), dxq = dev.get('xq', d.M * d.K);
-    const dsx = dev.get('sx', 8 * (perTensor ? 1 : d.M));
-    const dwq = dev.get('wq', d.N * d.K), dws = dev.get('ws', 8 * d.N);
-    const db = bias ? dev.get('bias', 4 * d.N) : null, dout = dev.get('out', 4 * d.M * d.N);
-    A.upload(dx, x);
-    A.upload(dwq, wq);
-    A.upload(dws, ws);
-    if (bias) A.upload(db, bias);
-    // quantize + GEMM + epilogue in one call (one kernel for a single token)
-    A.qlinearDynamic(dx, d.M, d.K, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN, dwq, dws, A.Q8_PER_CHANNEL,
-                     d.N, db, A[ACT_CODE[d.act || 'none']], dout, dxq, dsx);
-    A.download(out, dout);
-    return out;
+  const devArgs = (s, inst) => {
+    const dv = [];
+    const all = s.inputSlots.concat(s.outputSlots);
+    all.forEach((slot, i) => { dv[i] = slotBuf(slot); });
+    inst.constData.forEach((data, j) => { dv[all.length + j] = residentConst(data, 'plain'); });
+    return dv;
+  };
+  const hostArgs = (s, inst) => s.inputSlots.concat(s.outputSlots).map((slot) => slots[slot] && slots[slot].data)
+    .concat(inst.constData);
+  for (let k = 0; k < steps.length; k++) {
+    const s = steps[k], inst = instOf(s.kernel), d = inst.desc;
+    need(!s.shapeValues || s.shapeValues.length === 0, 'dynamic shapes are not supported by the int8 kernels');
+    const fused = !(opts && opts.fuse === false) && k + 1 < steps.length &&
+                  tryFusedLinear(s, inst, steps[k + 1], instOf(steps[k + 1].kernel), slots, readers, argSet, hostNeeds,
+                                 slotBuf, dev, hostArgs);
+    if (fused) { k++; continue; }
+    const dv = devArgs(s, inst);
+    let rhsNK = null;
+    if (d.op === 'quantized_dot' && d.rhsLayout === 'KN') {
+      const b = hostArgs(s, inst)[d.bIdx];
+      if (inst.consts.has(b)) rhsNK = residentConst(b, 'T', (w) => transposeI8(w, d.K, d.N));
+    }
+    execDevice(d, dv, dev, rhsNK);
   }
-  if (d.op === 'qlinear_requant') {
-    // int8 linear whose output is requantized with the next layer's static
-    // scale (the calibrated chain ... mul(sv) -> add(b) -> max -> quantize):
-    // xq int8 [M,K] + f64 scale(s), wq int8 [N,K] + f64 scales [N] -> int8 [M,N]
-    const xq = args[d.xqIdx], sx = args[d.sxIdx], wq = args[d.wqIdx], ws = args[d.wsIdx];
-    const out = args[d.outIdx];
-    const bias = d.biasIdx === undefined || d.biasIdx < 0 ? null : args[d.biasIdx];
-    const perTensor = d.granularity === 'per_tensor';
-    need(xq instanceof Int8Array && xq.length === d.M * d.K, 'qlinear_requant xq');
-    need(sx instanceof Float64Array && sx.length === (perTensor ? 1 : d.M), 'qlinear_requant activation scales');
-    need(wq instanceof Int8Array && wq.length === d.N * d.K, 'qlinear_requant wq');
-    need(ws instanceof Float64Array && ws.length === d.N, 'qlinear_requant weight scales');
-    need(out instanceof Int8Array && out.length === d.M * d.N, 'qlinear_requant out');
-    need(bias === null || (bias instanceof Float32Array && bias.length === d.N), 'qlinear_requant bias');
-    need(typeof d.sNext === 'number', 'qlinear_requant needs the static scale sNext');
-    const dxq = dev.get('xq', d.M * d.K), dsx = dev.get('sx', bytesOf(sx));
-    const dwq = dev.get('wq', d.N * d.K), dws = dev.get('ws', 8 * d.N);
-    const db = bias ? dev.get('bias', 4 * d.N) : null, dout = dev.get('out', d.M * d.N);
-    A.upload(dxq, xq);
-    A.upload(dsx, sx);
-    A.upload(dwq, wq);
-    A.upload(dws, ws);
-    if (bias) A.upload(db, bias);
-    A.gemmRequant(dxq, dwq, d.M, d.N, d.K, dsx, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN,
-                  dws, A.Q8_PER_CHANNEL, A.Q8_EPI_ROWCOL, 0, db, A[ACT_CODE[d.act || 'none']], d.sNext, dout);
-    A.download(out, dout);
-    return out;
+  for (const s of hostNeeds) if (slots[s] && slots[s].data) download(slots[s].data, slotBuf(s));
+}
+
+function tryFusedLinear(s0, i0, s1, i1, slots, readers, argSet, hostNeeds, slotBuf, dev, hostArgs) {
+  const d0 = i0.desc, e = i1.desc;
+  if (d0.op !== 'quantized_dot' || e.op !== 'ewise' || !e.epilogue) return false;
+  if ((d0.aDtype || 'i8') !== 'i8' || (d0.bDtype || 'i8') !== 'i8' || d0.zpA || d0.zpB) return false;
+  const accSlot = s0.outputSlots[d0.outIdx - s0.inputSlots.length];
+  const ep = e.epilogue;
+  const args1 = s1.inputSlots.concat(s1.outputSlots);
+  if (args1[ep.accParam] !== accSlot || ep.M !== d0.M || ep.N !== d0.N) return false;
+  if ((readers.get(accSlot) || []).length !== 1 || argSet.has(accSlot) || hostNeeds.has(accSlot)) return false;
+  const h1 = hostArgs(s1, i1);
+  const sv = h1[ep.svParam];
+  if (!(sv instanceof Float32Array) || !i1.consts.has(sv) || sv.length !== d0.N) return false;
+  const A = q8();
+  const h0 = hostArgs(s0, i0);
+  const a = slotBuf(s0.inputSlots[d0.aIdx]);
+  const bHost = h0[d0.bIdx];
+  let b;
+  if (i0.consts.has(bHost)) {
+    b = d0.rhsLayout === 'KN' ? residentConst(bHost, 'T', (w) => transposeI8(w, d0.K, d0.N)) : residentConst(bHost, 'plain');
+  } else {
+    b = d0.bIdx < s0.inputSlots.length ? slotBuf(s0.inputSlots[d0.bIdx]) : null;
+    if (!b || d0.rhsLayout === 'KN') return false;
   }
-  if (d.op === 'qlinear_w4') {
-    // decode linear with 4-bit per-group weights: x fp32 [M,K], per-token
-    // int8 quantize, then the W4A8 GEMV; wq4 uint8 [N, K/2] (two codes per
-    // byte), sw f64 [N * K / group]
-    const x = args[d.xIdx], wq = args[d.wqIdx], sw = args[d.swIdx], out = args[d.outIdx];
-    const bias = d.biasIdx === undefined || d.biasIdx < 0 ? null : args[d.biasIdx];
-    need(x instanceof Float32Array && x.length === d.M * d.K, 'qlinear_w4 x');
-    need(wq instanceof Uint8Array && wq.length === d.N * d.K / 2, 'qlinear_w4 packed weights');
-    need(d.group > 0 && d.K % d.group === 0, 'qlinear_w4 group must divide K');
-    need(sw instanceof Float64Array && sw.length === d.N * d.K / d.group, 'qlinear_w4 group scales');
-    need(out instanceof Float32Array && out.length === d.M * d.N, 'qlinear_w4 out');
-    need(bias === null || (bias instanceof Float32Array && bias.length === d.N), 'qlinear_w4 bias');
-    const dx = dev.get('x', 4 * d.M * d.K), dxq = dev.get('xq', d.M * d.K), dsx = dev.get('sx', 8 * d.M);
-    const dwq = dev.get('wq', bytesOf(wq)), dsw = dev.get('sw', bytesOf(sw));
-    const db = bias ? dev.get('bias', 4 * d.N) : null, dout = dev.get('out', 4 * d.M * d.N);
-    A.upload(dx, x);
-    A.upload(dwq, wq);
-    A.upload(dsw, sw);
-    if (bias) A.upload(db, bias);
-    A.quantizeRows(dx, d.M, d.K, A.Q8_PER_TOKEN, dxq, dsx);
-    A.gemvW4(dxq, dsx, A.Q8_PER_TOKEN, dwq, dsw, d.M, d.N, d.K, d.group, db, A[ACT_CODE[d.act || 'none']], dout);
-    A.download(out, dout);
-    return out;
+  // E-pc as q8_gemm's row x column epilogue: fround(acc * fround(1 * sv[n]))
+  const sB = residentConst(sv, 'f64', (x) => Float64Array.from(x));
+  const sA = dev.f64('one', [1]);
+  let bias = null;
+  if (ep.biasParam >= 0) {
+    const bh = h1[ep.biasParam];
+    if (!(bh instanceof Float32Array) || bh.length !== d0.N) return false;
+    bias = i1.consts.has(bh) ? residentConst(bh, 'plain') : (ep.biasParam < s1.inputSlots.length ? slotBuf(s1.inputSlots[ep.biasParam]) : null);
+    if (!bias) return false;
   }
-  throw new Error(`hip backend: unknown op '${d.op}'`);
+  const out = slotBuf(args1[e.outIdx]);
+  const act = ep.relu ? A.Q8_ACT_RELU : A.Q8_ACT_NONE;
+  stats.launches++;
+  stats.fusedLinears++;
+  if (ep.quant) {
+    A.gemmRequant(a, b, d0.M, d0.N, d0.K, sA, A.Q8_PER_TENSOR, sB, A.Q8_PER_CHANNEL, A.Q8_EPI_ROWCOL, 0, bias, act,
+                  ep.quant.scale, out);
+  } else {
+    A.gemm(a, b, d0.M, d0.N, d0.K, 0, 0, sA, A.Q8_PER_TENSOR, sB, A.Q8_PER_CHANNEL, A.Q8_EPI_ROWCOL, 0, bias, act,
+           A.Q8_F32, out);
+  }
+  return true;
 }
 
 /** The object registerBackend('hip', ...) takes (backend_registry.ts:14-20). */
@@ -460,34 +687,79 @@ function createHipRuntimeBackend() {
       const d = kernel && kernel.metadata && kernel.metadata.q8;
       need(kernel && kernel.metadata && kernel.metadata.kind === HIP_KIND, 'kernel kind is not hip');
       need(d && typeof d.op === 'string', 'kernel metadata carries no q8 descriptor');
-      return { kernel, desc: d, dev: new DeviceArgs() };
+      inputSpecs(d);                     // rejects unknown ops before any device call
+      return { kernel, desc: d, dev: new DeviceArgs(), consts: constSet(kernel) };
     },
     runSync(inst, tensorArgs, shapeValues) {
       need(shapeValues === null || shapeValues === undefined || shapeValues.length === 0,
            'dynamic shapes are not supported by the int8 kernels');
-      return runDescriptor(inst.desc, tensorArgs, inst.dev);
+      return runDescriptor(inst.desc, tensorArgs, inst.dev, inst.consts);
     },
     runAsync(inst, tensorArgs, shapeValues) {
       return Promise.resolve().then(() => this.runSync(inst, tensorArgs, shapeValues));
+    },
+    // runs the plan before returning (the device work is ordered on one
+    // stream and its outputs are already downloaded); the promise is the
+    // registry's contract (backend_registry.ts:19)
+    runPlan(plan, slots, steps, opts) {
+      try {
+        runPlanOnDevice(plan, slots, steps, opts);
+        return Promise.resolve();
+      } catch (e) {
+        return Promise.reject(e);
+      }
     },
     isAsync() { return false; },
   };
 }
 
-/** registerExternalCodegen('hip_int8', ...) entry (codegen_registry.ts:17-21). */
-function createHipExternalCodegen() {
+/** registerExternalCodegen('hip_int8', ...) entry (codegen_registry.ts:17-21).
+ * The kernel's constant buffers travel in metadata.constBuffers, as
+ * BackendPipeline.compile attaches them for the non-external path
+ * (backend/pipeline.ts:49-55), so RuntimeModule appends them to the
+ * kernel's arguments (runtime.ts:76-81, 246-258). */
+function createHipExternalCodegen(CONST_BUFFERS_ATTR) {
+  const cattr = CONST_BUFFERS_ATTR || 'const_buffers';
   return {
     targetKind: HIP_KIND,
     runtimeKind: HIP_KIND,
     compile(primFunc, target, info) {
-      return { source: '', metadata: { kind: HIP_KIND, q8: info, outputIndices: info.outputIndices } };
+      const metadata = { kind: HIP_KIND, q8: info, outputIndices: info.outputIndices };
+      const cbs = primFunc && typeof primFunc.getAttr === 'function' ? primFunc.getAttr(cattr) : null;
+      if (cbs && cbs.length > 0) {
+        metadata.constBuffers = cbs.map((cb) => ({ name: cb.buffer.name, dtype: cb.buffer.dtype, data: cb.data }));
+      }
+      return { source: '', metadata };
     },
   };
 }
 
+/** Descriptor of a PrimFunc for the hip provider: an int8 op of the path,
+ * or an elementwise loop nest (q8_ewise), or null. */
+function describe(primFunc, constBuffers) {
+  const info = detectInt8Kernel(primFunc);
+  if (info) return info;
+  const tr = ew().translateEwise(primFunc);
+  if (!tr) return null;
+  const zeroData = new Map();
+  for (const cb of constBuffers || []) {
+    const data = cb.data;
+    let allZero = data && data.length > 0;
+    for (let i = 0; allZero && i < data.length; i++) allZero = Object.is(+data[i], 0);
+    zeroData.set(cb.buffer.name, allZero);
+  }
+  const params = [];
+  for (const [, buf] of primFunc.bufferMap) params.push(buf);
+  const isZero = (p) => !!zeroData.get(params[p] && params[p].name);
+  const epilogue = ew().matchEpilogue(tr, isZero);
+  return { op: 'ewise', prog: tr.prog, inputIdx: tr.inputIdx, inNumel: tr.inNumel, outIdx: tr.outIdx,
+           outNumel: tr.outNumel, outputIndices: [tr.outIdx], epilogue };
+}
+
 /** registerExternalCodegenProvider(...) entry (external_codegen.ts:11-17). */
-function createHipProvider(EXTERNAL_CODEGEN_ATTR) {
+function createHipProvider(EXTERNAL_CODEGEN_ATTR, CONST_BUFFERS_ATTR) {
   const attr = EXTERNAL_CODEGEN_ATTR || 'external_codegen';    // FuncAttr.EXTERNAL_CODEGEN
+  const cattr = CONST_BUFFERS_ATTR || 'const_buffers';         // FuncAttr.CONST_BUFFERS
   return {
     name: PROVIDER,
     enabled(config, target) {
@@ -496,16 +768,50 @@ function createHipProvider(EXTERNAL_CODEGEN_ATTR) {
     },
     annotate(tirModule) {
       for (const primFunc of tirModule) {
-        const info = detectInt8Kernel(primFunc);
+        const cbs = typeof primFunc.getAttr === 'function' ? primFunc.getAttr(cattr) : null;
+        const info = describe(primFunc, cbs);
         if (info) primFunc.setAttr(attr, { name: PROVIDER, info });
       }
     },
   };
 }
 
-/** A compile target for the hip kind (support/target.ts: kind is a free string). */
-function hipTarget() {
-  return { kind: HIP_KIND, isGPU: () => true, supportsInt8: true };
+/**
+ * Codegen entry for target kind 'hip' (registerCodegen,
+ * codegen_registry.ts:26-28).  BackendPipeline.compile consults it for every
+ * PrimFunc the provider did not tag (backend/pipeline.ts:46-47): ops outside
+ * the int8 path that are not elementwise loop nests (reductions, softmax,
+ * gathers).  They go to the target's host codegen entry -- the CPU one by
+ * default -- and run on the JS runtime; the kernel's metadata records
+ * hipRoute: 'host' so callers can see which kernels left the GPU.
+ */
+function createHipCodegenEntry(getCodegenEntry, hostKind) {
+  const host = hostKind || 'cpu';
+  return {
+    runtimeKind: 'js',
+    compile(primFunc, target, pipeline) {
+      const entry = getCodegenEntry(host);
+      need(entry, `no codegen entry for the host target kind '${host}'`);
+      const out = entry.compile(primFunc, target, pipeline);
+      out.metadata.hipRoute = 'host';
+      return out;
+    },
+  };
+}
+
+/**
+ * A compile target of kind 'hip'.  With the reference's target factory
+ * (CPUTarget, support/target.ts:187-205) it is a real TargetFeatures whose
+ * scheduling and layout choices are the host's (isGPU() is false for a
+ * kind other than cuda / webgpu, so no thread binding is planned for the
+ * host-routed kernels); int8 and constant buffers are supported.  Without
+ * one, a plain object with the fields the provider and QuantizationPass
+ * read.
+ */
+function hipTarget(CPUTarget, overrides) {
+  const f = { kind: HIP_KIND, name: 'hip_mi355x', supportsInt8: true, supportsConstBuffers: true };
+  if (typeof CPUTarget === 'function') return CPUTarget(Object.assign(f, overrides || {}));
+  return Object.assign({ isGPU: () => false, isCPU: () => false, getAttr: () => null }, f, overrides || {});
 }
 
 // ---------------------------------------------------------------- eager library
@@ -560,14 +866,22 @@ function defineEagerLibrary(Library, DispatchKey, tensors) {
 /**
  * Plugs the hip int8 path into a running mlfw.  `r` carries the reference's
  * registry functions: { registerBackend, registerExternalCodegen,
- * registerExternalCodegenProvider, FuncAttr?, Library?, DispatchKey?, tensors? }.
+ * registerExternalCodegenProvider, registerCodegen?, getCodegenEntry?,
+ * FuncAttr?, Library?, DispatchKey?, tensors? }.  With registerCodegen and
+ * getCodegenEntry it also registers the 'hip' codegen entry, so the PrimFuncs
+ * the provider leaves untagged compile for the host instead of throwing
+ * 'Unsupported target kind: hip' (backend/pipeline.ts:46-47).
  */
 function registerHip(r) {
   need(r && typeof r.registerBackend === 'function', 'registerBackend is required');
+  const fa = r.FuncAttr || {};
   r.registerBackend(HIP_KIND, createHipRuntimeBackend());
-  if (r.registerExternalCodegen) r.registerExternalCodegen(PROVIDER, createHipExternalCodegen());
+  if (r.registerExternalCodegen) r.registerExternalCodegen(PROVIDER, createHipExternalCodegen(fa.CONST_BUFFERS));
   if (r.registerExternalCodegenProvider) {
-    r.registerExternalCodegenProvider(createHipProvider(r.FuncAttr && r.FuncAttr.EXTERNAL_CODEGEN));
+    r.registerExternalCodegenProvider(createHipProvider(fa.EXTERNAL_CODEGEN, fa.CONST_BUFFERS));
+  }
+  if (r.registerCodegen && r.getCodegenEntry) {
+    r.registerCodegen(HIP_KIND, createHipCodegenEntry(r.getCodegenEntry, r.hostKind));
   }
   let library = null;
   if (r.Library && r.DispatchKey && r.tensors) library = defineEagerLibrary(r.Library, r.DispatchKey, r.tensors);
@@ -575,6 +889,7 @@ function registerHip(r) {
 }
 
 module.exports = {
-  HIP_KIND, PROVIDER, registerHip, createHipRuntimeBackend, createHipExternalCodegen,
-  createHipProvider, defineEagerLibrary, detectInt8Kernel, runDescriptor, hipTarget, DeviceArgs,
+  HIP_KIND, PROVIDER, registerHip, createHipRuntimeBackend, createHipExternalCodegen, createHipCodegenEntry,
+  createHipProvider, defineEagerLibrary, detectInt8Kernel, describe, runDescriptor, hipTarget, DeviceArgs,
+  markHostDirty, stats, resetStats,
 };

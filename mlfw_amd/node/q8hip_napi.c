@@ -582,6 +582,55 @@ static napi_value js_silu_mul_quantize_rows(napi_env env, napi_callback_info inf
 
 /* ---------------------------------------------------------------- module */
 
+/* ewise(progBytes, [inputs], [inNumel], out, outNumel): one elementwise loop
+ * nest (q8_ewise); progBytes holds a q8_ew_prog exactly (ewise.js packs it). */
+static napi_value js_ewise(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  void* pb = NULL;
+  size_t pbytes = 0;
+  void* out = NULL;
+  int64_t onum = 0;
+  if (!get_args(env, info, 5, argv) || !arg_host(env, argv[0], &pb, &pbytes) ||
+      !arg_buf(env, argv[3], 1, &out) || !arg_i64(env, argv[4], &onum))
+    return NULL;
+  if (pbytes != sizeof(q8_ew_prog)) {
+    napi_throw_range_error(env, NULL, "q8hip: program bytes differ from sizeof(q8_ew_prog)");
+    return NULL;
+  }
+  q8_ew_prog prog;
+  memcpy(&prog, pb, sizeof(prog));
+  bool is;
+  uint32_t n = 0;
+  if (napi_is_array(env, argv[1], &is) != napi_ok || !is || napi_get_array_length(env, argv[1], &n) != napi_ok ||
+      n > Q8_EW_MAX_INPUTS) {
+    napi_throw_type_error(env, NULL, "q8hip: inputs must be an array of at most 8 device buffers");
+    return NULL;
+  }
+  const void* ins[Q8_EW_MAX_INPUTS] = {0};
+  int64_t nums[Q8_EW_MAX_INPUTS] = {0};
+  uint32_t nn = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    napi_value e;
+    void* p = NULL;
+    if (napi_get_element(env, argv[1], i, &e) != napi_ok || !arg_buf(env, e, 0, &p)) return NULL;
+    ins[i] = p;
+  }
+  if (!arg_i64_array(env, argv[2], nums, Q8_EW_MAX_INPUTS, &nn)) return NULL;
+  if (nn != n || (int64_t)n != prog.ninputs) {
+    napi_throw_range_error(env, NULL, "q8hip: inputs / inNumel do not match the program");
+    return NULL;
+  }
+  Q8_CHECK(env, q8_ewise(&prog, ins, nums, out, onum, NULL));
+  return undefined(env);
+}
+
+static napi_value js_ewise_prog_bytes(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value r;
+  NAPI_CALL(env, napi_create_int32(env, (int32_t)sizeof(q8_ew_prog), &r));
+  return r;
+}
+
 static napi_value init_module(napi_env env, napi_value exports) {
   const struct {
     const char* name;
@@ -614,6 +663,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"quantizedConvEx", js_quantized_conv_ex},
       {"quantizedDotWorkspace", js_quantized_dot_workspace},
       {"quantizedDot", js_quantized_dot},
+      {"ewise", js_ewise},
+      {"ewiseProgBytes", js_ewise_prog_bytes},
   };
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); ++i) {
     napi_value f;
@@ -624,7 +675,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
     const char* name;
     int value;
   } consts[] = {
-      {"Q8_I8", Q8_I8}, {"Q8_U8", Q8_U8}, {"Q8_I32", Q8_I32}, {"Q8_F32", Q8_F32},
+      {"Q8_I8", Q8_I8}, {"Q8_U8", Q8_U8}, {"Q8_I32", Q8_I32}, {"Q8_F32", Q8_F32}, {"Q8_F64", Q8_F64},
       {"Q8_PER_TENSOR", Q8_PER_TENSOR}, {"Q8_PER_TOKEN", Q8_PER_TOKEN},
       {"Q8_PER_CHANNEL", Q8_PER_CHANNEL}, {"Q8_EPI_PT", Q8_EPI_PT}, {"Q8_EPI_ROWCOL", Q8_EPI_ROWCOL},
       {"Q8_ACT_NONE", Q8_ACT_NONE}, {"Q8_ACT_RELU", Q8_ACT_RELU}, {"Q8_ACT_SILU", Q8_ACT_SILU},

@@ -1,0 +1,550 @@
+'use strict';
+/*
+ * Elementwise PrimFuncs and whole-plan execution on the 'hip' target
+ * (run by tests/test_node_ewise.py).
+ *   node ewise_test.js cpu    oracle pinning, translation, epilogue matching,
+ *                             compile routing (no GPU)
+ *   node ewise_test.js gpu    every PrimFunc through runSync, and the per-channel
+ *                             Linear + bias + ReLU PrimFunc set through runPlan
+ *                             (fused and unfused), bit for bit against the oracle
+ * TIR nodes are plain objects with the reference's field names
+ * (src/compiler/ir/tensor/nodes.ts); loop nests are built the way
+ * lowerPointwise builds them (src/compiler/passes/lowering/lowering_registry.ts:
+ * 277-306, 521-576): loop vars i_d, block iter vars v_d bound to them, loads
+ * through computeBroadcastIndices.
+ */
+const path = require('path');
+const assert = require('assert');
+
+const ROOT = path.join(__dirname, '..', '..');
+const hip = require(path.join(ROOT, 'mlfw_amd', 'node', 'hip_backend.js'));
+const ew = require(path.join(ROOT, 'mlfw_amd', 'node', 'ewise.js'));
+const ref = require(path.join(ROOT, 'oracle', 'ewise_ref.js'));        // the checker
+const q8ref = require(path.join(ROOT, 'oracle', 'q8ref.js'));          // the checker
+
+let failures = 0;
+function test(name, fn) {
+  try { fn(); console.log(`ok   ${name}`); } catch (e) { failures++; console.log(`FAIL ${name}\n     ${e.stack}`); }
+}
+
+// ---------------------------------------------------------------- TIR builders
+const V = (name, dtype = 'index') => ({ type: 'VariableNode', name, dtype });
+const I = (value) => ({ type: 'IntImmNode', value });
+const F = (value) => ({ type: 'FloatImmNode', value });
+const buf = (name, shape, dtype) => ({ name, shape, dtype });
+const load = (b, indices) => ({ type: 'BufferLoadNode', buffer: b, indices });
+const math = (op, a, b = null) => ({ type: 'MathOpNode', op, a, b });
+const ext = (externName, args, dtype = 'f32') => ({ type: 'CallExternNode', externName, args, dtype });
+const cast = (expr, fromDtype, toDtype) => ({ type: 'CastNode', expr, fromDtype, toDtype });
+const cmp = (direction, a, b) => ({ type: 'CompareNode', direction, a, b });
+const sel = (condition, thenBody, elseBody) => ({ type: 'IfThenElseNode', condition, thenBody, elseBody });
+
+let uid = 0;
+function primFunc(name, params, body, consts) {
+  const attrs = new Map();
+  const bufferMap = new Map();
+  params.forEach((b) => bufferMap.set(V(`p${uid++}`, 'handle'), b));
+  if (consts && consts.length) attrs.set('const_buffers', consts);
+  return {
+    name, params: [...bufferMap.keys()], body, bufferMap, attrs,
+    getAttr(k) { return attrs.has(k) ? attrs.get(k) : null; },
+    setAttr(k, v) { attrs.set(k, v); return this; },
+  };
+}
+
+/** lowerPointwise: loops over out's shape, loads through broadcast indices. */
+function pointwise(name, out, inputs, exprBuilder, consts) {
+  const n = out.shape.length, tag = uid++;
+  const loopVars = [], ivs = [], indices = [];
+  for (let d = 0; d < n; d++) {
+    loopVars.push(V(`i${d}_${tag}`));
+    const iv = V(`v${d}_${tag}`);
+    ivs.push({ type: 'BlockRealizeNode', iterVar: iv, binding: loopVars[d], kind: 0 });
+    indices.push(iv);
+  }
+  const loads = inputs.map((b) => {
+    const off = n - b.shape.length;
+    return load(b, b.shape.map((s, j) => (s === 1 ? I(0) : indices[off + j])));
+  });
+  const store = { type: 'BufferStoreNode', buffer: out, indices, value: exprBuilder(loads, indices) };
+  let body = { type: 'BlockNode', name: `${name}_block`, iterVars: ivs, reads: inputs.map((b) => ({ buffer: b })),
+               writes: [{ buffer: out }], body: store, initBody: null };
+  for (let d = n - 1; d >= 0; d--) {
+    body = { type: 'ForNode', loopVar: loopVars[d], min: I(0), extent: I(out.shape[d]), kind: 'serial', body };
+  }
+  const constBufs = (consts || []).map((c) => c.buffer);
+  const params = inputs.filter((b) => !constBufs.includes(b)).concat([out], constBufs);
+  return primFunc(name, params, body, consts);
+}
+
+/** quantize_block (quant_math.ts:16-27) around an inner expression. */
+function quantizeExpr(e, scale, zp = 0, tgt = 'i8') {
+  let s = math('/', e, F(scale));
+  if (zp !== 0) s = math('+', s, F(zp));
+  const lo = tgt === 'ui8' ? 0 : -128, hi = tgt === 'ui8' ? 255 : 127;
+  return cast(ext('min', [ext('max', [ext('round', [s]), F(lo)]), F(hi)]), 'f32', tgt);
+}
+
+/** qmatmul_init / qmatmul_acc (rules/quantization.ts:23-42) with W [N,K]. */
+function qmatmulPF(M, N, K, a, w, out, consts) {
+  const tag = uid++;
+  const m = V(`vm_${tag}`), n = V(`vn_${tag}`), k = V(`vk_${tag}`);
+  const init = { type: 'BlockNode', name: 'qmatmul_init', iterVars: [], reads: [], writes: [{ buffer: out }],
+                 body: { type: 'BufferStoreNode', buffer: out, indices: [m, n], value: I(0) } };
+  const acc = { type: 'BlockNode', name: 'qmatmul_acc_1', iterVars: [], reads: [{ buffer: a }, { buffer: w }],
+                writes: [{ buffer: out }],
+                body: { type: 'BufferStoreNode', buffer: out, indices: [m, n],
+                        value: math('+', load(out, [m, n]), math('*', cast(load(a, [m, k]), 'i8', 'i32'),
+                                                               cast(load(w, [n, k]), 'i8', 'i32'))) } };
+  return primFunc('qmatmul', [a, out, w], { type: 'ForNode', body: { type: 'SeqNode', stmts: [init, acc] } }, consts);
+}
+
+// ---------------------------------------------------------------- data
+function rng(seed) { return q8ref.makeRng(seed); }
+function normal(seed, n, std = 1) { const a = new Float32Array(n); q8ref.normalFill(rng(seed), a, 0, std); return a; }
+function withEdges(a) {
+  const e = [NaN, Infinity, -Infinity, -0, 0, 0.5, -0.5, 2.5, -2.5, 1e-40, -1e-40, 3.4e38, -3.4e38, 127.5, -128.5];
+  for (let i = 0; i < e.length && i < a.length; i++) a[(i * 7919) % a.length] = e[i];
+  return a;
+}
+function randI8(seed, n) { const r = rng(seed), a = new Int8Array(n); for (let i = 0; i < n; i++) a[i] = Math.floor(r() * 256) - 128; return a; }
+function randI32(seed, n, span) { const r = rng(seed), a = new Int32Array(n); for (let i = 0; i < n; i++) a[i] = Math.floor((r() - 0.5) * span); return a; }
+
+function sameBits(got, want, what) {
+  assert.strictEqual(got.length, want.length, `${what}: length`);
+  const isF = got instanceof Float32Array || got instanceof Float64Array;
+  let bad = 0, first = -1;
+  for (let i = 0; i < got.length; i++) {
+    const g = got[i], w = want[i];
+    // a NaN stored into a float array may take any encoding (ECMA-262
+    // NumericToRawBytes), so any NaN equals any NaN
+    const eq = isF ? (Number.isNaN(g) && Number.isNaN(w)) || Object.is(g, w) : g === w;
+    if (!eq) { bad++; if (first < 0) first = i; }
+  }
+  assert.strictEqual(bad, 0, `${what}: ${bad} of ${got.length} differ, first at ${first}: ${got[first]} vs ${want[first]}`);
+}
+
+// JS interpreter of a translated program (the device kernel's semantics), so
+// the translation can be checked on the CPU against the oracle.
+function emulate(tr, args) {
+  const p = tr.prog, OP = ew.OP, out = args[tr.outIdx];
+  const n = p.extent.reduce((a, b) => a * b, 1);
+  const toI32 = (x) => x | 0;
+  const jsmax = Math.max, jsmin = Math.min;
+  const idx = new Array(6).fill(0);
+  for (let e = 0; e < n; e++) {
+    let rem = e;
+    for (let d = p.ndims - 1; d >= 0; d--) { idx[d] = rem % p.extent[d]; rem = Math.floor(rem / p.extent[d]); }
+    const R = new Array(16).fill(0);
+    for (let pc = 0; pc < p.ncode; pc++) {
+      const c = p.code[pc], a = R[c.a], b = R[c.b];
+      let v;
+      switch (c.op) {
+        case OP.LOAD: { const j = c.aux; let off = p.inCoef[j][6]; for (let d = 0; d < 6; d++) off += p.inCoef[j][d] * idx[d]; v = args[tr.inputIdx[j]][off]; break; }
+        case OP.CONST: v = p.konst[c.aux]; break;
+        case OP.INDEX: v = idx[c.aux]; break;
+        case OP.ADD: v = a + b; break;
+        case OP.SUB: v = a - b; break;
+        case OP.MUL: v = a * b; break;
+        case OP.DIV: v = a / b; break;
+        case OP.IDIV: v = Math.trunc(a / b); break;
+        case OP.MOD: v = ((a % b + b) % b); break;
+        case OP.FLOORDIV: v = Math.floor(a / b); break;
+        case OP.TMOD: v = a % b; break;
+        case OP.TDIV: v = (a / b) | 0; break;
+        case OP.NEG: v = -a; break;
+        case OP.CMP: v = [a === b, a !== b, a < b, a <= b, a > b, a >= b][c.aux] ? 1 : 0; break;
+        case OP.SELECT: v = a ? b : R[c.c]; break;
+        case OP.TOINT32: v = toI32(a); break;
+        case OP.TOBOOL: v = a ? 1 : 0; break;
+        case OP.MAX: v = jsmax(a, b); break;
+        case OP.MIN: v = jsmin(a, b); break;
+        case OP.ABS: v = Math.abs(a); break;
+        case OP.FLOOR: v = Math.floor(a); break;
+        case OP.CEIL: v = Math.ceil(a); break;
+        case OP.ROUND: v = Math.round(a); break;
+        case OP.SIGN: v = Math.sign(a); break;
+        case OP.SQRT: v = Math.sqrt(a); break;
+        case OP.FMOD: v = ((a % b + b) % b); break;
+        case OP.EXP: v = Math.exp(a); break;
+        case OP.LOG: v = Math.log(a); break;
+        case OP.TANH: v = Math.tanh(a); break;
+        case OP.RSQRT: v = 1.0 / Math.sqrt(a); break;
+        case OP.POW: v = Math.pow(a, b); break;
+        default: throw new Error(`op ${c.op}`);
+      }
+      if (c.rnd) v = Math.fround(v);
+      R[c.dst] = v;
+    }
+    out[e] = R[p.result];
+  }
+}
+
+// ---------------------------------------------------------------- the cases
+const M = 37, N = 96, K = 256;
+function linearSet() {
+  const x = buf('x', [M, K], 'f32'), xq = buf('xq', [M, K], 'i8'), W = buf('w', [N, K], 'i8');
+  const acc = buf('acc', [M, N], 'i32'), sv = buf('sv', [N], 'f32'), b = buf('b', [N], 'f32');
+  const y = buf('y', [M, N], 'f32'), y2 = buf('y2', [M, N], 'f32'), y3 = buf('y3', [M, N], 'f32');
+  const zero = buf('zero', [1, 1], 'f32'), q2 = buf('q2', [M, N], 'i8');
+  const sX = 4.9 / 127, sNext = 0.0371;
+  const Wdata = randI8(5, N * K);
+  const svData = new Float32Array(N);
+  for (let i = 0; i < N; i++) svData[i] = Math.fround(sX * (0.001 + 0.0002 * ((i * 37) % 17)));
+  const consts = { W: { buffer: W, data: Wdata }, sv: { buffer: sv, data: svData },
+                   zero: { buffer: zero, data: new Float32Array([0]) } };
+  const pf = {
+    quantize: pointwise('quantize', xq, [x], (l) => quantizeExpr(l[0], sX)),
+    qmatmul: qmatmulPF(M, N, K, xq, W, acc, [consts.W]),
+    tail: pointwise('fused_convert_mul', y, [acc, sv], (l) => math('*', cast(l[0], 'i32', 'f32'), l[1]), [consts.sv]),
+    add: pointwise('add', y2, [y, b], (l) => math('+', l[0], l[1])),
+    max: pointwise('maximum', y3, [y2, zero], (l) => ext('max', [l[0], l[1]]), [consts.zero]),
+    fused: pointwise('fused_convert_mul_add_maximum', y3, [acc, sv, b, zero],
+                     (l) => ext('max', [math('+', math('*', cast(l[0], 'i32', 'f32'), l[1]), l[2]), l[3]]),
+                     [consts.sv, consts.zero]),
+    reluQuant: pointwise('fused_maximum_quantize', q2, [y2, zero],
+                         (l) => quantizeExpr(ext('max', [l[0], l[1]]), sNext), [consts.zero]),
+    fusedRq: pointwise('fused_convert_mul_add_maximum_quantize', q2, [acc, sv, b, zero],
+                       (l) => quantizeExpr(ext('max', [math('+', math('*', cast(l[0], 'i32', 'f32'), l[1]), l[2]), l[3]]),
+                                           sNext), [consts.sv, consts.zero]),
+  };
+  return { bufs: { x, xq, W, acc, sv, b, y, y2, y3, zero, q2 }, pf, consts, sX, sNext };
+}
+
+// extra elementwise shapes: broadcasts, casts, compare/select, externs, lets
+function extraCases() {
+  const A = buf('a', [3, 5, 7], 'f32'), B = buf('b', [5, 1], 'f32'), C = buf('c', [7], 'f32');
+  const O = buf('o', [3, 5, 7], 'f32'), OI = buf('oi', [3, 5, 7], 'i32'), OB = buf('ob', [3, 5, 7], 'ui8');
+  const Q = buf('q', [3, 5, 7], 'i8'), D = buf('d', [3, 5, 7], 'f64');
+  const cases = [
+    ['broadcast add/mul chain', pointwise('fused', O, [A, B, C], (l) => math('*', math('+', l[0], l[1]), math('-', l[2], F(0.25))))],
+    ['x - 0 and x * 1 folds', pointwise('fold', O, [A], (l) => math('+', math('*', math('-', l[0], I(0)), I(1)), F(0)))],
+    ['silu', pointwise('silu', O, [A], (l) => math('*', l[0], math('/', F(1), math('+', F(1), ext('exp', [math('-', l[0])])))))],
+    ['compare/select', pointwise('sel', O, [A, C], (l) => sel(cmp('gt', l[0], l[1]), l[0], math('*', l[1], F(2))))],
+    ['cast to i32 (| 0)', pointwise('cvt', OI, [A], (l) => cast(math('*', l[0], F(1e9)), 'f32', 'i32'))],
+    ['cast to bool', pointwise('cvtb', OB, [A], (l) => cast(l[0], 'f32', 'bool'))],
+    ['exact externs', pointwise('ex', O, [A, C], (l) => ext('min', [ext('abs', [ext('floor', [math('*', l[0], F(3))])]),
+                                                                    ext('sqrt', [ext('sign', [l[1]])])]))],
+    ['round / ceil / fmod', pointwise('rnd', O, [A, C], (l) => math('+', ext('round', [math('*', l[0], F(2))]),
+                                                                      ext('fmod', [ext('ceil', [l[0]]), F(3)])))],
+    ['tanh / rsqrt / log / pow', pointwise('tr', O, [A], (l) => math('+', math('+', ext('tanh', [l[0]]), ext('rsqrt', [ext('abs', [l[0]])])),
+                                                                   math('+', ext('log', [ext('abs', [l[0]])]), ext('pow', [ext('abs', [l[0]]), F(0.75)]))))],
+    ['quantize ui8 with zero point', pointwise('q8u', OB, [A], (l) => quantizeExpr(l[0], 0.0123, 128, 'ui8'))],
+    ['quantize i8', pointwise('q8', Q, [A], (l) => quantizeExpr(l[0], 0.02))],
+    ['f64 output', pointwise('f64', D, [A, C], (l) => cast(math('*', l[0], l[1]), 'f32', 'f64'))],
+    ['index arithmetic (iota)', pointwise('iota', OI, [], (l, ix) => math('+', math('*', ix[0], I(7)), math('-', ix[2], ix[1])))],
+  ];
+  return { cases, A, B, C };
+}
+
+function argsFor(pf, fill) {
+  const args = [];
+  for (const [, b] of pf.bufferMap) args.push(fill(b));
+  return args;
+}
+function alloc(b) {
+  const T = { f32: Float32Array, f64: Float64Array, i32: Int32Array, i8: Int8Array, ui8: Uint8Array }[b.dtype];
+  return new T(b.shape.reduce((a, c) => a * c, 1));
+}
+
+// ---------------------------------------------------------------- CPU tests
+function cpuTests() {
+  // expected strings of tests/backend/cpu/codegen-internals.test.js
+  test('oracle exprToJS reproduces the reference codegen-internals vectors', () => {
+    const e = (n) => ref.exprToJS(n, new Map());
+    const idx = (n) => V(n, 'index');
+    const vectors = [
+      [I(42), '42'], [I(0), '0'], [I(-7), '-7'], [F(3.14), '3.14'], [F(0), '0'], [F(-1.5), '-1.5'],
+      [V('i0', 'index'), 'i0'], [math('+', I(3), I(4)), '(3 + 4)'], [math('*', idx('i'), I(8)), '(i * 8)'],
+      [math('-', I(10), I(3)), '(10 - 3)'], [math('-', V('x', 'f32')), '(-x)'],
+      [math('%', idx('x'), I(4)), '((x % 4 + 4) % 4)'], [math('//', idx('x'), I(4)), 'Math.floor(x / 4)'],
+      [math('tdiv', idx('x'), I(4)), '((x / 4) | 0)'], [math('+', idx('x'), I(0)), 'x'], [math('+', I(0), idx('x')), 'x'],
+      [math('+', V('x', 'f32'), I(0)), 'Math.fround(x + 0)'], [math('+', I(0), V('x', 'f32')), 'Math.fround(0 + x)'],
+      [math('-', V('x', 'f32'), I(0)), 'x'], [math('*', idx('x'), I(0)), '0'], [math('*', I(0), idx('x')), '0'],
+      [math('*', V('x', 'i64'), I(0)), '0n'], [math('*', V('x', 'f32'), I(0)), 'Math.fround(x * 0)'],
+      [math('*', I(0), V('x', 'f32')), 'Math.fround(0 * x)'], [math('*', V('x', 'f32'), I(1)), 'x'],
+      [math('*', I(1), V('x', 'f32')), 'x'], [math('*', math('+', idx('i'), I(1)), I(4)), '((i + 1) * 4)'],
+      [cmp('ge', idx('x'), I(0)), '(x >= 0)'], [cmp('eq', idx('a'), idx('b')), '(a === b)'],
+      [sel(cmp('gt', V('x', 'f32'), I(0)), F(1), F(0)), '((x > 0) ? 1 : 0)'],
+      [cast(F(3.7), 'f32', 'i32'), '(3.7 | 0)'], [cast(I(5), 'i32', 'f32'), '(+5)'], [cast(idx('x'), 'index', 'bool'), '(x ? 1 : 0)'],
+      [ext('exp', [V('x', 'f32')], 'f32'), 'Math.fround(Math.exp(x))'], [ext('sqrt', [V('x', 'f32')], 'f32'), 'Math.sqrt(x)'],
+      [ext('rsqrt', [V('x', 'f32')], 'f32'), 'Math.fround(1.0 / Math.sqrt(x))'],
+      [ext('max', [V('a', 'f32'), V('b', 'f32')], 'f32'), 'Math.max(a, b)'],
+      [ext('fmod', [V('a', 'f32'), V('b', 'f32')], 'f32'), '((a % b + b) % b)'],
+      [load(buf('buf_1', [4], 'f32'), [V('i', 'index')]), 'buf_1[i]'],
+    ];
+    for (const [node, want] of vectors) assert.strictEqual(e(node), want);
+    assert.throws(() => e(ext('fake_func', [V('x', 'f32')], 'f32')), /unsupported extern function "fake_func"/);
+    assert.strictEqual(e(null), '0');
+    // _flatIndex vectors
+    const fi = (b, ix) => ref.flatIndex(b, ix, new Map());
+    assert.strictEqual(fi(buf('s', [], 'f32'), []), '0');
+    assert.strictEqual(fi(buf('v', [8], 'f32'), [idx('i')]), 'i');
+    assert.strictEqual(fi(buf('m', [3, 4], 'f32'), [idx('i'), idx('j')]), 'i * 4 + j');
+    assert.strictEqual(fi(buf('t', [2, 3, 4], 'f32'), [idx('i'), idx('j'), idx('k')]), 'i * 12 + j * 4 + k');
+    assert.strictEqual(fi(buf('m', [3, 4], 'f32'), [I(0), idx('j')]), 'j');
+    assert.strictEqual(fi(buf('m', [3, 4], 'f32'), [I(0), I(0)]), '0');
+  });
+
+  test('the oracle per-channel tail agrees with q8ref.js (two restatements, one engine)', () => {
+    const L = linearSet();
+    const accD = randI32(7, M * N, 1 << 22), bD = normal(8, N, 0.1);
+    const y1 = new Float32Array(M * N), y2 = new Float32Array(M * N);
+    q8ref.buildEpiloguePerChannel(M, N, false, false)(accD, L.consts.sv.data, null, y1);
+    ref.compilePrimFunc(L.pf.tail).fn(accD, y2, L.consts.sv.data);
+    sameBits(y2, y1, 'tail');
+    const z1 = new Float32Array(M * N), z2 = new Float32Array(M * N);
+    q8ref.buildEpiloguePerChannel(M, N, true, true)(accD, L.consts.sv.data, bD, z1);
+    ref.compilePrimFunc(L.pf.fused).fn(accD, bD, z2, L.consts.sv.data, L.consts.zero.data);
+    sameBits(z2, z1, 'tail + bias + relu');
+  });
+
+  test('program layout matches the addon (sizeof q8_ew_prog)', () => {
+    const a = require(path.join(ROOT, 'mlfw_amd', 'node', 'index.js'));
+    assert.strictEqual(a.ewiseProgBytes(), ew.LAYOUT.bytes);
+  });
+
+  test('translated programs evaluate like the oracle (JS emulation of the device program)', () => {
+    const L = linearSet();
+    const { cases } = extraCases();
+    const all = Object.entries(L.pf).filter(([k]) => k !== 'qmatmul').map(([k, pf]) => [k, pf]).concat(cases);
+    let seed = 100;
+    for (const [name, pf] of all) {
+      const tr = ew.translateEwise(pf);
+      assert.ok(tr, `${name}: not translated`);
+      const consts = pf.getAttr('const_buffers') || [];
+      const fill = (b) => {
+        const c = consts.find((x) => x.buffer === b);
+        if (c) return c.data;
+        const a = alloc(b);
+        if (a instanceof Float32Array) { a.set(withEdges(normal(seed++, a.length, 3))); }
+        else if (a instanceof Int32Array) a.set(randI32(seed++, a.length, 1 << 26));
+        else if (a instanceof Int8Array) a.set(randI8(seed++, a.length));
+        return a;
+      };
+      const args = argsFor(pf, fill);
+      const want = args.slice(), got = args.slice();
+      want[tr.outIdx] = alloc(pf.bufferMap.get([...pf.bufferMap.keys()][tr.outIdx]));
+      got[tr.outIdx] = alloc(pf.bufferMap.get([...pf.bufferMap.keys()][tr.outIdx]));
+      ref.compilePrimFunc(pf).fn(...want);
+      emulate(tr, got);
+      sameBits(got[tr.outIdx], want[tr.outIdx], name);
+    }
+  });
+
+  test('matchEpilogue finds the per-channel tail, bias, ReLU and requant forms only', () => {
+    const L = linearSet();
+    const zeroParam = (pf) => (p) => [...pf.bufferMap.values()][p] === L.bufs.zero;
+    const m = (pf) => ew.matchEpilogue(ew.translateEwise(pf), zeroParam(pf));
+    const t = m(L.pf.tail);
+    assert.ok(t && !t.relu && t.biasParam < 0 && !t.quant && t.M === M && t.N === N);
+    const f = m(L.pf.fused);
+    assert.ok(f && f.relu && f.biasParam >= 0 && !f.quant);
+    const r = m(L.pf.fusedRq);
+    assert.ok(r && r.relu && r.quant && r.quant.scale === 0.0371);
+    assert.strictEqual(m(L.pf.add), null);
+    assert.strictEqual(m(L.pf.reluQuant), null);
+    const { cases } = extraCases();
+    for (const [, pf] of cases) assert.strictEqual(ew.matchEpilogue(ew.translateEwise(pf), () => false), null);
+  });
+
+  test('the provider tags every PrimFunc of the linear set; nothing reaches the host codegen', () => {
+    const L = linearSet();
+    const p = hip.createHipProvider('external_codegen', 'const_buffers');
+    const pfs = Object.values(L.pf);
+    p.annotate(pfs);
+    for (const pf of pfs) {
+      const a = pf.getAttr('external_codegen');
+      assert.ok(a && a.name === 'hip_int8', `${pf.name} untagged`);
+    }
+    assert.strictEqual(L.pf.qmatmul.getAttr('external_codegen').info.op, 'quantized_dot');
+    assert.strictEqual(L.pf.quantize.getAttr('external_codegen').info.op, 'quantize');
+    assert.ok(L.pf.fused.getAttr('external_codegen').info.epilogue.relu);
+  });
+
+  test('BackendPipeline.compile with the hip entries: tagged -> hip kernels, the rest -> host codegen', () => {
+    // restates src/backend/pipeline.ts:37-57
+    const externals = new Map(), entries = new Map();
+    entries.set('cpu', { runtimeKind: 'js', compile: (pf) => ({ source: `function ${pf.name}(){}`, metadata: { kind: 'js' } }) });
+    const r = { registerBackend() {}, registerExternalCodegen: (n, e) => externals.set(n, e),
+                registerExternalCodegenProvider() {}, registerCodegen: (k, e) => entries.set(k, e),
+                getCodegenEntry: (k) => entries.get(k) || null, FuncAttr: { EXTERNAL_CODEGEN: 'external_codegen', CONST_BUFFERS: 'const_buffers' } };
+    hip.registerHip(r);
+    const target = hip.hipTarget();
+    function compile(pf) {
+      const x = pf.getAttr('external_codegen');
+      if (x) {
+        const e = externals.get(x.name);
+        if (e && e.targetKind === target.kind) return e.compile(pf, target, x.info);
+      }
+      const entry = r.getCodegenEntry(target.kind);
+      if (!entry) throw new Error(`Unsupported target kind: ${target.kind}`);
+      return entry.compile(pf, target);
+    }
+    const L = linearSet();
+    hip.createHipProvider('external_codegen', 'const_buffers').annotate(Object.values(L.pf));
+    for (const pf of Object.values(L.pf)) {
+      const k = compile(pf);
+      assert.strictEqual(k.metadata.kind, 'hip', pf.name);
+    }
+    const qk = compile(L.pf.qmatmul);
+    assert.ok(qk.metadata.constBuffers && qk.metadata.constBuffers[0].data === L.consts.W.data, 'const buffers travel');
+    // a reduction (not an elementwise nest): compiled for the host, labelled
+    const s = buf('s', [M], 'f32'), x = buf('x', [M, K], 'f32');
+    const red = primFunc('sum', [x, s], { type: 'ForNode', loopVar: V('r0'), min: I(0), extent: I(M), kind: 'serial',
+      body: { type: 'BlockNode', name: 'reduce', iterVars: [], reads: [], writes: [], initBody: { type: 'SeqNode', stmts: [] },
+              body: { type: 'BufferStoreNode', buffer: s, indices: [V('r0')], value: F(0) } } });
+    hip.createHipProvider('external_codegen', 'const_buffers').annotate([red]);
+    const rk = compile(red);
+    assert.strictEqual(rk.metadata.kind, 'js');
+    assert.strictEqual(rk.metadata.hipRoute, 'host');
+  });
+
+  test('hipTarget builds on the reference factory when given one', () => {
+    const seen = [];
+    const t = hip.hipTarget((cfg) => { seen.push(cfg); return { kind: cfg.kind, made: true }; });
+    assert.ok(t.made);
+    assert.strictEqual(seen[0].kind, 'hip');
+    assert.strictEqual(seen[0].supportsInt8, true);
+    assert.strictEqual(hip.hipTarget().isGPU(), false);
+  });
+}
+
+// ---------------------------------------------------------------- GPU tests
+/** RuntimeModule.runPlanAsync (runtime.ts:290-329) for a uniform plan. */
+function makePlan(steps, argSlots, numSlots) {
+  return { numSlots, argSlots, intermediates: [], steps: steps.map((s) => ({ name: s.name, inputSlots: s.inputSlots,
+                                                                           outputSlots: s.outputSlots })) };
+}
+
+function gpuTests() {
+  const A = require(path.join(ROOT, 'mlfw_amd', 'node', 'index.js'));
+  A.init(0);
+  const codegen = hip.createHipExternalCodegen('const_buffers');
+  const provider = hip.createHipProvider('external_codegen', 'const_buffers');
+  const be = hip.createHipRuntimeBackend();
+  const kernelOf = (pf) => {
+    provider.annotate([pf]);
+    const x = pf.getAttr('external_codegen');
+    assert.ok(x, `${pf.name} not tagged`);
+    return codegen.compile(pf, hip.hipTarget(), x.info);
+  };
+  // RuntimeModule.run: tensor args + const buffers appended (runtime.ts:246-268)
+  const runKernel = (kernel, inst, args) => {
+    const all = args.concat((kernel.metadata.constBuffers || []).map((c) => c.data));
+    be.runSync(inst, all, null);
+  };
+
+  test('GPU: every elementwise PrimFunc through runSync, bit for bit', () => {
+    const L = linearSet();
+    const { cases } = extraCases();
+    const all = Object.entries(L.pf).filter(([k]) => k !== 'qmatmul').concat(cases);
+    let seed = 300;
+    for (const [name, pf] of all) {
+      const consts = pf.getAttr('const_buffers') || [];
+      const fill = (b) => {
+        const c = consts.find((x) => x.buffer === b);
+        if (c) return c.data;
+        const a = alloc(b);
+        if (a instanceof Float32Array) a.set(withEdges(normal(seed++, a.length, 3)));
+        else if (a instanceof Int32Array) a.set(randI32(seed++, a.length, 1 << 26));
+        else if (a instanceof Int8Array) a.set(randI8(seed++, a.length));
+        return a;
+      };
+      const args = argsFor(pf, fill);
+      const kernel = kernelOf(pf);
+      const d = kernel.metadata.q8;
+      const outIdx = d.outIdx;
+      const want = args.slice();
+      want[outIdx] = alloc([...pf.bufferMap.values()][outIdx]);
+      ref.compilePrimFunc(pf).fn(...want);
+      const nParams = [...pf.bufferMap.values()].length - consts.length;
+      const got = args.slice(0, nParams);
+      got[outIdx] = alloc([...pf.bufferMap.values()][outIdx]);
+      runKernel(kernel, be.instantiate(kernel), got);
+      sameBits(got[outIdx], want[outIdx], name);
+    }
+  });
+
+  // the whole per-channel Linear + bias + ReLU set, layer output requantized
+  function linearRun(which, fuse) {
+    const L = linearSet();
+    const xD = withEdges(normal(21, M * K, 1.5)), bD = normal(22, N, 0.05);
+    // oracle: every step on the host
+    const h = {};
+    const run = (pf, args) => ref.compilePrimFunc(pf).fn(...args);
+    h.xq = new Int8Array(M * K); run(L.pf.quantize, [xD, h.xq]);
+    h.acc = new Int32Array(M * N); q8ref.buildQuantizedDot(M, N, K, 1, 0, 0)(h.xq, L.consts.W.data, h.acc);
+    const sv = L.consts.sv.data, zero = L.consts.zero.data;
+    h.y = new Float32Array(M * N); run(L.pf.tail, [h.acc, h.y, sv]);
+    h.y2 = new Float32Array(M * N); run(L.pf.add, [h.y, bD, h.y2]);
+    h.y3 = new Float32Array(M * N); run(L.pf.max, [h.y2, h.y3, zero]);
+    h.q2 = new Int8Array(M * N); run(L.pf.reluQuant, [h.y2, h.q2, zero]);
+    // slots: 0 x, 1 b, 2 xq, 3 acc, 4 y, 5 y2, 6 y3 / q2
+    let steps, outSlot, want;
+    const S = (pf, ins, outs) => ({ name: pf.name, inputSlots: ins, outputSlots: outs, kernel: kernelOf(pf), shapeValues: null });
+    if (which === 'unfused') {
+      steps = [S(L.pf.quantize, [0], [2]), S(L.pf.qmatmul, [2], [3]), S(L.pf.tail, [3], [4]),
+               S(L.pf.add, [4, 1], [5]), S(L.pf.max, [5], [6])];
+      outSlot = 6; want = h.y3;
+    } else if (which === 'fused') {
+      steps = [S(L.pf.quantize, [0], [2]), S(L.pf.qmatmul, [2], [3]), S(L.pf.fused, [3, 1], [6])];
+      outSlot = 6; want = h.y3;
+    } else {
+      steps = [S(L.pf.quantize, [0], [2]), S(L.pf.qmatmul, [2], [3]), S(L.pf.fusedRq, [3, 1], [6])];
+      outSlot = 6; want = h.q2;
+    }
+    const plan = makePlan(steps, [0, 1, outSlot], 7);
+    const mk = (data, shape, dtype) => ({ data, shape, dtype });
+    const out = which === 'requant' ? new Int8Array(M * N) : new Float32Array(M * N);
+    const slots = [mk(xD, [M, K], 'f32'), mk(bD, [N], 'f32'), mk(new Int8Array(M * K), [M, K], 'i8'),
+                   mk(new Int32Array(M * N), [M, N], 'i32'), mk(new Float32Array(M * N), [M, N], 'f32'),
+                   mk(new Float32Array(M * N), [M, N], 'f32'), mk(out, [M, N], which === 'requant' ? 'i8' : 'f32')];
+    return { plan, slots, steps, out, want, h, fuse };
+  }
+
+  for (const [which, fuse, fusedCount] of [['unfused', true, 1], ['unfused', false, 0], ['fused', true, 1],
+                                            ['fused', false, 0], ['requant', true, 1], ['requant', false, 0]]) {
+    test(`GPU: runPlan of the per-channel linear set (${which}, fusion ${fuse ? 'on' : 'off'})`, () => {
+      const t = linearRun(which, fuse);
+      hip.resetStats();
+      let err = null;
+      be.runPlan(t.plan, t.slots, t.steps, { fuse }).catch((e) => { err = e; });
+      const first = Object.assign({}, hip.stats);
+      sameBits(t.out, t.want, `${which} plan output`);
+      assert.strictEqual(first.fusedLinears, fusedCount);
+      // intermediates stay on the device: only plan outputs come back
+      assert.strictEqual(t.slots[3].data.some((v) => v !== 0), false, 'acc slot was never downloaded');
+      // a second run uploads no constant bytes and only the plan inputs
+      hip.resetStats();
+      t.out.fill(0);
+      be.runPlan(t.plan, t.slots, t.steps, { fuse }).catch((e) => { err = e; });
+      assert.strictEqual(err, null);
+      sameBits(t.out, t.want, `${which} plan output, second run`);
+      assert.strictEqual(hip.stats.constUploadBytes, 0, 'weights uploaded again');
+      assert.strictEqual(hip.stats.uploadBytes, 4 * M * K + 4 * N, 'second run uploads only x and b');
+    });
+  }
+
+  test('GPU: runSync of the linear set step by step, weights resident after the first call', () => {
+    const t = linearRun('unfused', true);
+    const insts = t.steps.map((s) => be.instantiate(s.kernel));
+    const host = (slot) => t.slots[slot].data;
+    const once = () => t.steps.forEach((s, k) => runKernel(s.kernel, insts[k], s.inputSlots.concat(s.outputSlots).map(host)));
+    hip.resetStats();
+    once();
+    sameBits(host(3), t.h.acc, 'acc');
+    sameBits(host(6), t.want, 'y3');
+    assert.ok(hip.stats.constUploadBytes >= N * K, 'the int8 weight was uploaded once');
+    hip.resetStats();
+    once();
+    assert.strictEqual(hip.stats.constUploadBytes, 0, 'second call uploads no weight bytes');
+    sameBits(host(6), t.want, 'y3, second call');
+  });
+}
+
+const mode = process.argv[2] || 'cpu';
+if (mode === 'cpu') cpuTests();
+else gpuTests();
+console.log(failures ? `${failures} failed` : 'all passed');
+process.exit(failures ? 1 : 0);
