@@ -243,12 +243,19 @@ def bench_c4():
     P = C.c4_prepare(inp["W"])
     del inp["W"]
     X = inp["X"]
+    from mlfw_amd import ops as O
     us, how = graph_time_us(lambda i: C.c4_step(X, P), 1, replays=5)
     ms = us / 1e3
+    # the same step with the O projection's per-token requant fused into its
+    # GEMM epilogue (no fp32 intermediate; one cooperative launch)
+    nb, fused = O.requant_dynamic_workspace(X.shape[0], *C.C4_SHAPES["o"])
+    ws = torch.empty(nb, dtype=torch.int8, device="cuda")
+    us_f, _ = graph_time_us(lambda i: C.c4_step(X, P, fused_requant=True, ws=ws), 1, replays=5)
     return {"c4_projection_set": {"avg_ms": ms, "ops": C.C4_OPS,
                                   "TOPS": C.C4_OPS / (ms * 1e-3) / 1e12,
                                   "frac_mfma": C.C4_OPS / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
-                                  "timing": how}}
+                                  "timing": how,
+                                  "fused_o_requant_ms": us_f / 1e3, "fused_o_route": fused}}
 
 
 # ---------------------------------------------------------------- ceilings

@@ -298,6 +298,36 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
                     int epi, double s_out, const float* bias, int act,
                     double s_next, int8_t* out, void* stream);
 
+/* q8_gemm's fp32 result requantized per row with the row's own dynamic
+ * scale, as the next layer's per-token quantize would take it:
+ *   y[m,n]   = act(bias + epilogue(acc))          (exactly q8_gemm's Q8_F32 output)
+ *   scale[m] = S-abs of row m of y                (q8_quantize_rows, Q8_PER_TOKEN)
+ *   out[m,n] = the compiled quantize of y[m,n] with scale[m]
+ * bit for bit equal to q8_gemm followed by q8_quantize_rows, without the
+ * fp32 tensor reaching memory when the fused route applies: every 256x256
+ * tile of the MFMA GEMM is resident at once (cooperative launch), the tiles
+ * of a row block publish their rows' absmax through atomics in the
+ * workspace, meet once grid-wide (a bounded wait) and quantize the values
+ * they hold.  Otherwise (M <= 16, more tiles than fit the chip, K not a
+ * multiple of 16) the GEMM writes y into the workspace and q8_quantize_rows
+ * follows.  No counterpart in the reference, whose scales are static (it
+ * composes quantization_pass.ts:390-459 with a per-token scale); the
+ * reference chain it replaces is dequantize -> [add] -> [max] -> quantize.
+ * q8_gemm_requant_dynamic_workspace gives the workspace bytes and whether
+ * the fused route applies (it then needs 16-byte aligned A and B); calls that
+ * share a workspace must be ordered.  q8_gemm_requant_dynamic_status reads
+ * (synchronously) whether the fused route's bounded wait ran out -- never
+ * expected, since co-residency is guaranteed; out is then unreliable.  The
+ * environment variable Q8_DQ_TEST_TIMEOUT=1 (read at each call; tests only)
+ * makes every wait run out, to exercise that report. */
+int q8_gemm_requant_dynamic_workspace(int64_t M, int64_t N, int64_t K, size_t* bytes, int* fused);
+int q8_gemm_requant_dynamic(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                            const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
+                            double s_out, const float* bias, int act, int8_t* out,
+                            double* out_scales, void* workspace, size_t workspace_bytes,
+                            void* stream);
+int q8_gemm_requant_dynamic_status(const void* workspace, int64_t M, int* timed_out, void* stream);
+
 /* ---------------------------------------------------------------- 4-bit weights */
 
 /* fromConstantArrayPerGroup (quantization_types.ts:319-340, numBits 4) +

@@ -129,18 +129,31 @@ def c4_prepare(W):
     return P
 
 
-def c4_step(X, P):
+def c4_step(X, P, fused_requant=False, ws=None):
+    """One pass of the projection set.  With fused_requant the O projection
+    writes its per-token int8 codes and scales directly from the GEMM
+    epilogue (q8_gemm_requant_dynamic: 128 co-resident tiles, one
+    cooperative launch), so its fp32 output never reaches memory; otherwise
+    (the default, faster on MI355X at this shape: the cooperative launch
+    alone costs ~20 us) it is written and quantized by a second kernel.
+    Returns every stage's tensors."""
     xq, sx = ops.quantize_per_token(X)
     qkv = ops.qlinear(xq, sx, *P["qkv"])
     vq, sv = ops.quantize_per_token(qkv[:, 8192:])         # row-strided V slice
-    o = ops.qlinear(vq, sv, *P["o"])
-    oq, so = ops.quantize_per_token(o)
+    out = {"xq": xq, "sx": sx, "qkv": qkv, "vq": vq, "sv": sv}
+    if fused_requant:
+        oq, so = ops.qlinear_requant_dynamic(vq, sv, *P["o"], workspace=ws)
+    else:
+        o = ops.qlinear(vq, sv, *P["o"])
+        oq, so = ops.quantize_per_token(o)
+        out["o"] = o
     gu = ops.qlinear(oq, so, *P["gate_up"])               # [tokens, gate | up]
     nf = gu.shape[1] // 2
     g, u = gu[:, :nf], gu[:, nf:]                          # row-strided halves
     hq, sh = ops.silu_mul_quantize(g, u)
     d = ops.qlinear(hq, sh, *P["down"])
-    return {"qkv": qkv, "o": o, "gate": g, "up": u, "down": d}
+    out.update({"oq": oq, "so": so, "gate": g, "up": u, "hq": hq, "sh": sh, "down": d})
+    return out
 
 
 C4_OPS = sum(2 * 2048 * n * k for n, k in C4_SHAPES.values())

@@ -418,7 +418,7 @@ static int gemm_common(const char* who, const int8_t* A, const int8_t* B, int64_
 int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, int32_t zpA,
             int32_t zpB, const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
             double s_out, const float* bias, int act, int out_kind, void* out, void* stream) {
-  q8::GemmEpi e;
+  q8::GemmEpi e{};
   int rc = gemm_common("q8_gemm", A, B, M, N, K, zpA, zpB, sA, sA_mode, sB, sB_mode, epi, s_out,
                        bias, act, out_kind, out, &e);
   if (rc != Q8_OK) return rc;
@@ -433,7 +433,7 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, c
             int sA_mode, const double* sB, int sB_mode, int epi, double s_out, const float* bias,
             int act, int out_kind, void* out, void* stream) {
   Q8_REQUIRE(M >= 0 && M <= 16, "q8_gemv: M must be in [0, 16] (got %lld)", (long long)M);
-  q8::GemmEpi e;
+  q8::GemmEpi e{};
   int rc = gemm_common("q8_gemv", A, B, M, N, K, 0, 0, sA, sA_mode, sB, sB_mode, epi, s_out, bias,
                        act, out_kind, out, &e);
   if (rc != Q8_OK) return rc;
@@ -487,7 +487,7 @@ int q8_quantized_dot(const void* A, int a_dtype, const void* B, int b_dtype, int
                      size_t workspace_bytes, int32_t* out, void* stream) {
   Q8_REQUIRE((a_dtype == Q8_I8 || a_dtype == Q8_U8) && (b_dtype == Q8_I8 || b_dtype == Q8_U8),
              "q8_quantized_dot: operands must be Q8_I8 or Q8_U8 (got %d, %d)", a_dtype, b_dtype);
-  q8::GemmEpi e;
+  q8::GemmEpi e{};
   int rc = gemm_common("q8_quantized_dot", (const int8_t*)A, (const int8_t*)B, M, N, K, 0, 0,
                        nullptr, Q8_PER_TENSOR, nullptr, Q8_PER_TENSOR, Q8_EPI_PT, 0.0, nullptr,
                        Q8_ACT_NONE, Q8_I32, out, &e);
@@ -546,7 +546,7 @@ int q8_qlinear_dynamic(const float* x, int64_t M, int64_t K, int x_mode, const i
                        float* out, int8_t* xq, double* sx, void* stream) {
   Q8_REQUIRE(x_mode == Q8_PER_TOKEN || x_mode == Q8_PER_TENSOR,
              "q8_qlinear_dynamic: x_mode must be Q8_PER_TOKEN or Q8_PER_TENSOR (got %d)", x_mode);
-  q8::GemmEpi e;
+  q8::GemmEpi e{};
   int rc = gemm_common("q8_qlinear_dynamic", xq, Wq, M, N, K, 0, 0, sx, x_mode, sW, sW_mode,
                        Q8_EPI_ROWCOL, 0.0, bias, act, Q8_F32, out, &e);
   if (rc != Q8_OK) return rc;
@@ -581,7 +581,7 @@ int q8_qlinear_dynamic_noalloc(const float* x, int64_t M, int64_t K, int x_mode,
   // other arguments; the real staging addresses are set below
   int8_t* const fake_xq = reinterpret_cast<int8_t*>(static_cast<uintptr_t>(256));
   double* const fake_sx = reinterpret_cast<double*>(static_cast<uintptr_t>(256));
-  q8::GemmEpi e;
+  q8::GemmEpi e{};
   int rc = gemm_common("q8_qlinear_dynamic_noalloc", fake_xq, Wq, M, N, K, 0, 0, fake_sx, x_mode,
                        sW, sW_mode, Q8_EPI_ROWCOL, 0.0, bias, act, Q8_F32, out, &e);
   if (rc != Q8_OK) return rc;
@@ -600,7 +600,7 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
                     const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
                     double s_out, const float* bias, int act, double s_next, int8_t* out,
                     void* stream) {
-  q8::GemmEpi e;
+  q8::GemmEpi e{};
   int rc = gemm_common("q8_gemm_requant", A, B, M, N, K, 0, 0, sA, sA_mode, sB, sB_mode, epi,
                        s_out, bias, act, Q8_F32, out, &e);
   if (rc != Q8_OK) return rc;
@@ -616,6 +616,75 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
   hipError_t err = (M <= 16) ? q8::launch_gemv(A, B, M, N, K, e, out, as_stream(stream))
                              : q8::launch_gemm(A, B, M, N, K, e, out, as_stream(stream));
   return launched(err, "q8_gemm_requant launch");
+}
+
+// Route of q8_gemm_requant_dynamic: the fused cooperative kernel needs the
+// MFMA GEMM (M > 16, K a multiple of 16, 256-row tile offsets in 32 bits)
+// and every 256 x 256 tile resident at once.
+static bool dq_fused_route(int64_t M, int64_t N, int64_t K) {
+  return M > 16 && K > 0 && K % 16 == 0 && 256 * K < (1LL << 31) && q8::gemm_dq_fits(M, N);
+}
+
+static size_t dq_fallback_bytes(int64_t M, int64_t N) { return (size_t)((M * N * 4 + 255) / 256 * 256); }
+
+int q8_gemm_requant_dynamic_workspace(int64_t M, int64_t N, int64_t K, size_t* bytes, int* fused) {
+  Q8_REQUIRE(M >= 0 && N >= 0 && K >= 0 && mul_ok(M, N) && mul_ok(M, 4 * N),
+             "q8_gemm_requant_dynamic_workspace: bad shape M=%lld N=%lld K=%lld", (long long)M,
+             (long long)N, (long long)K);
+  Q8_REQUIRE(bytes != nullptr, "q8_gemm_requant_dynamic_workspace: bytes is NULL");
+  int rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  const bool f = dq_fused_route(M, N, K);
+  *bytes = f ? q8::gemm_dq_ws_bytes(M) : dq_fallback_bytes(M, N);
+  if (fused) *fused = f ? 1 : 0;
+  return Q8_OK;
+}
+
+int q8_gemm_requant_dynamic(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                            const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
+                            double s_out, const float* bias, int act, int8_t* out,
+                            double* out_scales, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  q8::GemmEpi e{};
+  int rc = gemm_common("q8_gemm_requant_dynamic", A, B, M, N, K, 0, 0, sA, sA_mode, sB, sB_mode, epi,
+                       s_out, bias, act, Q8_F32, out, &e);
+  if (rc != Q8_OK) return rc;
+  Q8_REQUIRE(M == 0 || out_scales, "q8_gemm_requant_dynamic: out_scales is NULL");
+  Q8_REQUIRE(mul_ok(M, 4 * N), "q8_gemm_requant_dynamic: bad shape");
+  rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  if (M == 0) return Q8_OK;
+  const bool fused = dq_fused_route(M, N, K);
+  const size_t need = fused ? q8::gemm_dq_ws_bytes(M) : dq_fallback_bytes(M, N);
+  Q8_REQUIRE(workspace && workspace_bytes >= need,
+             "q8_gemm_requant_dynamic: needs a workspace of %zu bytes (got %zu)", need, workspace_bytes);
+  hipStream_t st = as_stream(stream);
+  if (fused) {
+    Q8_REQUIRE((reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0,
+               "q8_gemm_requant_dynamic: the fused route needs 16-byte aligned A and B");
+    return launched(q8::launch_gemm_dq(A, B, M, N, K, e, out, out_scales, workspace, st),
+                    "q8_gemm_requant_dynamic launch");
+  }
+  // fp32 result in the workspace, then the per-token quantize of it
+  float* y = static_cast<float*>(workspace);
+  hipError_t err = (M <= 16) ? q8::launch_gemv(A, B, M, N, K, e, y, st) : q8::launch_gemm(A, B, M, N, K, e, y, st);
+  if (err == hipSuccess) err = q8::launch_quant_rows(y, N, M, N, out, out_scales, st);
+  return launched(err, "q8_gemm_requant_dynamic launch");
+}
+
+int q8_gemm_requant_dynamic_status(const void* workspace, int64_t M, int* timed_out, void* stream) {
+  Q8_REQUIRE(workspace && timed_out && M >= 0, "q8_gemm_requant_dynamic_status: NULL argument");
+  int rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  hipStream_t st = as_stream(stream);
+  hipError_t e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  const size_t off = q8::gemm_dq_ws_bytes(M) - 256 + 4;
+  int v = 0;
+  e = hipMemcpy(&v, static_cast<const char*>(workspace) + off, sizeof(int), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
+  *timed_out = v;
+  return Q8_OK;
 }
 
 int q8_pack_weight_int4(const float* W, int64_t N, int64_t K, int64_t group_size,

@@ -17,13 +17,14 @@
 //     the buffer resource's num_records, which the hardware returns as
 //     zero -- edge tiles need no separate code.
 //   * LDS layout: tile row r occupies 64 B; its logical 16-byte K chunk c
-//     is stored at chunk position c ^ swz(r), swz(r) = ((r>>1) ^ (r>>3)) & 3.
-//     The lanes that read one K chunk of 32 consecutive rows then hit
-//     distinct 16-byte bank groups within every 8-row group (32 banks)
-//     and every 16-row group (64 banks), so fragment reads are
-//     conflict-free.  The swizzle is applied on the global side (each lane
-//     fetches the chunk its LDS slot must hold), so the DMA writes stay
-//     linear.
+//     is stored at chunk position c ^ swz(r), swz(r) = (r>>2) & 3: rows
+//     r, r+4, r+8, r+12 start on the same bank (64-byte rows over 256 bytes
+//     of banks) and the swizzle puts their chunks on four distinct 16-byte
+//     bank groups.  Measured on the 2048 x 4096 x 4096 int8 GEMM:
+//     SQ_LDS_BANK_CONFLICT 0 (the earlier ((r>>1) ^ (r>>3)) & 3 read 4.2M
+//     conflict cycles, with no difference in run time).  The swizzle is
+//     applied on the global side (each lane fetches the chunk its LDS slot
+//     must hold), so the DMA writes stay linear.
 //   * Pipeline: one barrier per stage, between its two 32-byte K sub-steps;
 //     a stage's refill is spread over the following two sub-steps, so each
 //     sub-step issues a quarter of a stage's copies between its MFMAs (a
@@ -42,6 +43,8 @@
 // (v_dot4_i32_i8), no MFMA; 4 < M <= 16: one 16x16x64 MFMA per 16 weight
 // rows x 64 K-bytes (dot4 would make it VALU-bound); see the kernels' own
 // comments.
+#include <atomic>
+#include <cstdlib>
 #include <type_traits>
 
 #include "q8_device.h"
@@ -110,7 +113,7 @@ struct GemmCfg {
   static_assert(TM >= 1 && TN >= 1 && BM % 64 == 0 && BN % 64 == 0, "tile shape");
 };
 
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 // Buffer resource (V#) of a raw byte range: base, stride 0, num_records
 // bytes, gfx9 data-format word.
@@ -203,17 +206,21 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 //   bit 3 MODE (0: fround(acc * s_out), 1: fround(acc * fround(sA[m] * sB[n]))),
 //   bit 2 bias, bits 0-1 activation (0 none, 1 ReLU, 2 SiLU);
 //   bit 5 int8 output: the fp32 value (MODE as above, bias and activation
-//   taken from the runtime epilogue) requantized with a static scale.
+//   taken from the runtime epilogue) requantized with a static scale;
+//   bit 6 int8 output requantized per row with the row's dynamic absmax
+//   scale (cooperative launch; the OUT_DQ branch of k_qgemm's epilogue).
 template <int EPI>
 struct Epi {
   static constexpr bool OUT_I32 = (EPI & 16) != 0;
   static constexpr bool OUT_Q8 = (EPI & 32) != 0;
+  static constexpr bool OUT_DQ = (EPI & 64) != 0;
   static constexpr int MODE = (EPI >> 3) & 1;
   static constexpr bool BIAS = (EPI & 4) != 0;
   static constexpr int ACT = EPI & 3;
 };
 
 inline int epi_code(const GemmEpi& e) {
+  if (e.out_dq) return 64 | (e.mode << 3);
   if (e.out_i32) return 16;
   if (e.out_q8) return 32 | (e.mode << 3);
   return (e.mode << 3) | (e.bias ? 4 : 0) | e.act;
@@ -424,7 +431,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const int lc = wn + 32 * j + r32;
     sbj[j] = (!OUT_I32 && MODE == 1) ? s_cols[lc] : 0.0;
     if constexpr (P::BIAS) bj[j] = e.bias[n0 + lc < N ? n0 + lc : N - 1];
-    else if constexpr (P::OUT_Q8) bj[j] = e.bias ? e.bias[n0 + lc < N ? n0 + lc : N - 1] : 0.0f;
+    else if constexpr (P::OUT_Q8 || P::OUT_DQ) bj[j] = e.bias ? e.bias[n0 + lc < N ? n0 + lc : N - 1] : 0.0f;
     else bj[j] = 0.0f;
   }
   auto strip_out = [&](auto ic) {
@@ -531,11 +538,252 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     }
     }
   };
-  strip_out(std::integral_constant<int, 0>{});
-  if constexpr (C::TM > 1) strip_out(std::integral_constant<int, 1>{});
-  if constexpr (C::TM > 2) strip_out(std::integral_constant<int, 2>{});
-  if constexpr (C::TM > 3) strip_out(std::integral_constant<int, 3>{});
-  static_assert(C::TM <= 4, "strip_out calls cover TM <= 4");
+  if constexpr (P::OUT_DQ) {
+    // Dynamic per-row requant: the row's scale is S-abs over all N columns,
+    // so every tile of a row block must have seen its values first.
+    //  A. per strip: the accumulators go to the wave's LDS strip; a rolled
+    //     loop over the lane's 4-column quads (one row each) applies the
+    //     scales, bias and activation, takes the quad's absmax key, reduces
+    //     it over the lanes of the row and max-es it into the tile's row
+    //     keys (LDS); the fp32 values go back to the accumulator registers
+    //     in quad order;
+    //  B. the tile's row keys are max-ed into the caller's workspace (one
+    //     32-bit atomic per row) and all workgroups (co-resident by the
+    //     cooperative launch) meet once: an arrival counter, polled with a
+    //     bound (a timed-out wait sets the status word and carries on with
+    //     the keys it sees);
+    //  C. each row's scale, and its binary32 reciprocal (NaN where the f32
+    //     fast path does not apply), is computed once into LDS; per strip
+    //     the values return to the LDS strip and a rolled loop quantizes
+    //     each quad like q8_quantize_rows does (R1 with the row scale) and
+    //     stores its 4 codes; the tiles of column 0 store the scales.
+    // The per-element work runs in rolled loops reading LDS, so the code a
+    // wave executes stays small: unrolled over the 256 values a lane holds
+    // (with the exact-path and activation code between them) it overflows
+    // the instruction cache and costs more than the main loop.
+    constexpr int STRIP_WORDS = 4 * 32 * PITCH;
+    static_assert((STRIP_WORDS + BM) % 2 == 0, "row scales are 8-byte aligned");
+    static_assert((STRIP_WORDS + BM) * 4 + BM * 12 <= C::LDS, "row keys and scales fit in the stage buffers");
+    int* tkey = reinterpret_cast<int32_t*>(lds) + STRIP_WORDS;                 // [BM] row keys
+    double* rscale = reinterpret_cast<double*>(lds + (STRIP_WORDS + BM) * 4);  // [BM] row scales
+    float* rrcp = reinterpret_cast<float*>(rscale + BM);                      // [BM] f32 reciprocals
+    if (tid < BM) tkey[tid] = -1;
+    __syncthreads();
+    // the lane's four columns, the same in every quad it handles
+    double sc4[4];
+    float b4[4];
+    bool col_ok[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int lc = wn + qcol + c;
+      col_ok[c] = n0 + lc < N;
+      sc4[c] = MODE == 1 ? s_cols[lc] : 0.0;
+      b4[c] = e.bias ? e.bias[col_ok[c] ? n0 + lc : N - 1] : 0.0f;
+    }
+    auto quad_ptr = [&](int it) { return reinterpret_cast<v4i*>(strip + (it * RPI + qrow) * PITCH + qcol); };
+    // U quads per iteration: U independent LDS / shuffle chains in flight
+    // (one wave per SIMD leaves nothing else to hide their latency), each
+    // step a straight-line block over the U quads.
+    constexpr int U = 8;
+    static_assert(NQ % U == 0, "whole groups of quads");
+    auto dq_values = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) strip[((r >> 2) * 8 + kh * 4 + (r & 3)) * PITCH + 32 * j + r32] = acc[i][j][r];
+#pragma unroll 1
+      for (int it0 = 0; it0 < NQ; it0 += U) {
+        const int trow0 = wm + 32 * i + it0 * RPI + qrow;    // tile row of quad it0 (+ RPI per quad)
+        v4i a[U];
+        double sr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          a[u] = *quad_ptr(it0 + u);
+          sr[u] = MODE == 1 ? s_rows[trow0 + u * RPI] : 0.0;
+        }
+        float y[U][4];
+        bool exact = true;
+        if constexpr (MODE == 1) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) exact &= (unsigned)(a[u][c] + (1 << 24)) <= (2u << 24);
+        }
+        if (MODE == 0 || __all(exact)) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              if constexpr (MODE == 0) y[u][c] = (float)((double)a[u][c] * e.s_out);
+              else y[u][c] = (float)a[u][c] * (float)(sr[u] * sc4[c]);
+            }
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[u][c] = mul_acc_f32scale(a[u][c], (float)(sr[u] * sc4[c]));
+        }
+        if (e.bias) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[u][c] = y[u][c] + b4[c];
+        }
+        if (e.act == 1) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[u][c] = relu_js(y[u][c]);
+        } else if (e.act == 2) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[u][c] = silu_js(y[u][c]);
+        }
+        // columns past N are never stored and rows past M never published,
+        // so neither changes a real row's key
+        int k[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          k[u] = -1;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int kc = col_ok[c] ? absmax_key(y[u][c]) : -1;
+            k[u] = kc > k[u] ? kc : k[u];
+          }
+        }
+#pragma unroll
+        for (int off = 1; off < LPR; off <<= 1)
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int o = __shfl_xor(k[u], off, 64);
+            k[u] = o > k[u] ? o : k[u];
+          }
+        if (lane % LPR == 0) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) atomicMax(&tkey[trow0 + u * RPI], k[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          *quad_ptr(it0 + u) = v4i{__float_as_int(y[u][0]), __float_as_int(y[u][1]), __float_as_int(y[u][2]),
+                                   __float_as_int(y[u][3])};
+      }
+#pragma unroll
+      for (int it = 0; it < NQ; ++it) {
+        const v4i v = *quad_ptr(it);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[i][(4 * it + c) >> 4][(4 * it + c) & 15] = v[c];
+      }
+    };
+    dq_values(std::integral_constant<int, 0>{});
+    if constexpr (C::TM > 1) dq_values(std::integral_constant<int, 1>{});
+    if constexpr (C::TM > 2) dq_values(std::integral_constant<int, 2>{});
+    if constexpr (C::TM > 3) dq_values(std::integral_constant<int, 3>{});
+    static_assert(C::TM <= 4 && C::TN * 16 == 4 * NQ, "dq_values covers TM <= 4; a strip is NQ quads per lane");
+    __syncthreads();
+    // Agent-scope atomics; the workgroup barrier orders them before thread
+    // 0's release increment of the arrival counter.  The counter is polled
+    // relaxed (an acquire per poll would invalidate this XCD's L2 each
+    // time) and a single acquire fence follows the wait.
+    if (tid < rows_a && tkey[tid] >= 0)
+      __hip_atomic_fetch_max(&e.row_keys[m0 + tid], tkey[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (tid == 0) {
+      __hip_atomic_fetch_add(e.sync, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      int polls = 0;
+      while (__hip_atomic_load(e.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)e.nwg) {
+        if (++polls > e.spin_limit) {
+          __hip_atomic_store(e.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (tid < BM) {
+      const int key = tid < rows_a
+                          ? __hip_atomic_load(&e.row_keys[m0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : -1;
+      const double s = scale_from_key(key);
+      rscale[tid] = s;
+      rrcp[tid] = fast_scale_ok(s) ? (float)(1.0 / s) : __builtin_nanf("");
+      if (tn == 0 && tid < rows_a) e.q_scales[m0 + tid] = s;
+    }
+    __syncthreads();
+    int8_t* o8 = static_cast<int8_t*>(out);
+    auto dq_store = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+#pragma unroll
+      for (int it = 0; it < NQ; ++it) {
+        v4i v;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = acc[i][(4 * it + c) >> 4][(4 * it + c) & 15];
+        *quad_ptr(it) = v;
+      }
+#pragma unroll 1
+      for (int it0 = 0; it0 < NQ; it0 += U) {
+        const int trow0 = wm + 32 * i + it0 * RPI + qrow;
+        float f[U][4];
+        float rcp[U];
+        double sc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const v4i v = *quad_ptr(it0 + u);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) f[u][c] = __int_as_float(v[c]);
+          rcp[u] = rrcp[trow0 + u * RPI];
+          sc[u] = rscale[trow0 + u * RPI];
+        }
+        // the f32 decision for every value; a NaN reciprocal (scale outside
+        // the fast path's range) flags all of its row's values
+        int code[U][4];
+        bool bad[U][4];
+        bool any_bad = false;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            code[u][c] = quant_sym_try(f[u][c], rcp[u], bad[u][c]);
+            any_bad |= bad[u][c];
+          }
+        if (__any(any_bad)) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (bad[u][c]) code[u][c] = quant_exact(f[u][c], sc[u], 0.0, -128, 127);
+        }
+        if (interior) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            *reinterpret_cast<int*>(o8 + (m0 + trow0 + u * RPI) * (int64_t)N + gcol) =
+                pack4(code[u][0], code[u][1], code[u][2], code[u][3]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int64_t row = m0 + trow0 + u * RPI;
+            if (row < M) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                if (gcol + c < N) o8[row * N + gcol + c] = (int8_t)code[u][c];
+            }
+          }
+        }
+      }
+    };
+    dq_store(std::integral_constant<int, 0>{});
+    if constexpr (C::TM > 1) dq_store(std::integral_constant<int, 1>{});
+    if constexpr (C::TM > 2) dq_store(std::integral_constant<int, 2>{});
+    if constexpr (C::TM > 3) dq_store(std::integral_constant<int, 3>{});
+  } else {
+    strip_out(std::integral_constant<int, 0>{});
+    if constexpr (C::TM > 1) strip_out(std::integral_constant<int, 1>{});
+    if constexpr (C::TM > 2) strip_out(std::integral_constant<int, 2>{});
+    if constexpr (C::TM > 3) strip_out(std::integral_constant<int, 3>{});
+    static_assert(C::TM <= 4, "strip_out calls cover TM <= 4");
+  }
 }
 
 template <int BM, int BN>
@@ -612,6 +860,76 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
     case 2: return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
     default: return launch_qgemm_tile<64, 64>(A, B, (int)M, (int)N, (int)K, e, out, st);
   }
+}
+
+// ------------------------------------------------------------------ dynamic requant GEMM
+// Workspace: [M] int32 row keys (rounded up to 256 bytes), then the arrival
+// counter and the status word.
+size_t gemm_dq_ws_bytes(int64_t M) { return (size_t)((M * 4 + 255) / 256 * 256) + 256; }
+
+__global__ void k_dq_init(int* keys, int64_t M, unsigned* sync, int* status) {
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < M; i += (int64_t)gridDim.x * 256) keys[i] = -1;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *sync = 0u;
+    *status = 0;
+  }
+}
+
+// Workgroups of the 256 x 256 dynamic-requant kernel that fit the chip at
+// once (one per CU at its LDS size), cached per device.
+static int dq_capacity() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_qgemm<256, 256, 72>,
+                                                     GEMM_THREADS, qgemm_lds<256, 256>()) != hipSuccess)
+      per_cu = 0;
+    c = per_cu * cu_count();
+    cache[dev].store(c > 0 ? c : -1, std::memory_order_relaxed);
+  }
+  return c > 0 ? c : 0;
+}
+
+bool gemm_dq_fits(int64_t M, int64_t N) {
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  return tiles <= dq_capacity();
+}
+
+hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                          GemmEpi e, int8_t* out, double* scales, void* ws, hipStream_t st) {
+  if (M == 0 || N == 0) return hipSuccess;
+  const int tm = (int)((M + 255) / 256), tn = (int)((N + 255) / 256);
+  const int nwg = tm * tn;
+  if (nwg > dq_capacity()) return hipErrorCooperativeLaunchTooLarge;
+  char* w = static_cast<char*>(ws);
+  const size_t keys_bytes = (size_t)((M * 4 + 255) / 256 * 256);
+  e.out_dq = 1;
+  e.row_keys = reinterpret_cast<int*>(w);
+  e.sync = reinterpret_cast<unsigned*>(w + keys_bytes);
+  e.status = reinterpret_cast<int*>(w + keys_bytes + 4);
+  e.q_scales = scales;
+  e.nwg = nwg;
+  e.spin_limit = 1 << 18;      // a poll is a device-coherent load (~1 us) and a short sleep: < 1 s in all
+  // Test hook for the timeout report: the arrival count can never reach
+  // nwg + 1, so every workgroup's wait runs out after a few polls (the
+  // kernel still ends normally; its output is then unreliable).
+  const char* t = getenv("Q8_DQ_TEST_TIMEOUT");
+  if (t && t[0] == '1') {
+    e.nwg = nwg + 1;
+    e.spin_limit = 64;
+  }
+  const int ig = (int)((M + 255) / 256 < 1024 ? (M + 255) / 256 : 1024);
+  hipLaunchKernelGGL(k_dq_init, dim3(ig), dim3(256), 0, st, e.row_keys, M, e.sync, e.status);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+  void* args[] = {(void*)&A, (void*)&B, &Mi, &Ni, &Ki, (void*)&tm, (void*)&tn, &e, (void*)&out};
+  const void* kern = e.mode == 1 ? (const void*)k_qgemm<256, 256, 72> : (const void*)k_qgemm<256, 256, 64>;
+  return hipLaunchCooperativeKernel(kern, dim3((unsigned)nwg), dim3(GEMM_THREADS), args,
+                                    (unsigned)qgemm_lds<256, 256>(), st);
 }
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
@@ -1049,6 +1367,8 @@ hipError_t setup_kernel_attributes() {
   Q8_EPI_CODES(Q8_SET_256x128)
   Q8_EPI_CODES(Q8_SET_128)
   Q8_EPI_CODES(Q8_SET_64)
+  Q8_SET_256(64)
+  Q8_SET_256(72)
 #undef Q8_SET_256
 #undef Q8_SET_256x128
 #undef Q8_SET_128

@@ -25,6 +25,17 @@ struct GemmEpi {
   double s_q;           // next layer's quantize scale (out_q8)
   float rq32;           // (float)(1 / s_q), for the f32 fast path of R1
   int q_fast;           // s_q admits the fast path (normal, in [2^-100, 2^100])
+  // out_dq: the fp32 value is requantized per row with the row's own
+  // absmax scale (q8_gemm_requant_dynamic).  All workgroups are co-resident
+  // (cooperative launch): each publishes its rows' absmax keys, they meet
+  // once grid-wide, then quantize the values they still hold.
+  int out_dq;
+  int* row_keys;        // [M] absmax keys, -1 at launch
+  unsigned* sync;       // arrival counter, 0 at launch
+  int* status;          // set to 1 if the bounded wait ran out
+  double* q_scales;     // [M] row scales, written by the tiles of column 0
+  int nwg;              // workgroups of the launch
+  int spin_limit;       // bound of the wait (polls)
 };
 
 hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
@@ -51,6 +62,14 @@ hipError_t launch_silu_mul_quant_rows(const float* g, int64_t ldg, const float* 
                                       hipStream_t st);
 hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
+// GEMM with the dynamic per-row requant epilogue (e.out_dq fields filled by
+// the caller except the meeting point, which comes from `ws`).  Returns
+// hipErrorCooperativeLaunchTooLarge when the tiles do not fit the chip at
+// once; gemm_dq_fits tells beforehand.
+bool gemm_dq_fits(int64_t M, int64_t N);
+size_t gemm_dq_ws_bytes(int64_t M);
+hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                          GemmEpi e, int8_t* out, double* scales, void* ws, hipStream_t st);
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
 

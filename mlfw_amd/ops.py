@@ -375,6 +375,46 @@ def qlinear_requant(A: torch.Tensor, sA: torch.Tensor | None, B: torch.Tensor,
     return out
 
 
+def requant_dynamic_workspace(M: int, N: int, K: int):
+    """(bytes, fused) of q8_gemm_requant_dynamic for this shape."""
+    nb, fused = C.c_size_t(0), C.c_int(0)
+    L.call("q8_gemm_requant_dynamic_workspace", M, N, K, C.byref(nb), C.byref(fused))
+    return nb.value, bool(fused.value)
+
+
+def qlinear_requant_dynamic(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor,
+                            bias: torch.Tensor | None = None, act: str | None = None,
+                            out: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                            workspace: torch.Tensor | None = None):
+    """int8 linear whose fp32 result (the qlinear epilogue) is requantized per
+    row with the row's own dynamic absmax scale, as the next layer's
+    per-token quantize takes it: returns (int8 codes [M, N], f64 scales [M]),
+    bit for bit qlinear followed by quantize_per_token.  When every tile of
+    the MFMA GEMM fits the chip at once the fp32 tensor never reaches memory
+    (one cooperative launch); the workspace holds the row keys then, or the
+    fp32 result on the fallback route."""
+    M, N, K = _mk(A, B)
+    _need(sA, torch.float64, "sA")
+    _need(sB, torch.float64, "sB")
+    if sA.numel() not in (1, M) or sB.numel() not in (1, N):
+        raise ValueError("qlinear_requant_dynamic: scale sizes must be 1 or M (sA) and 1 or N (sB)")
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.numel() != N:
+            raise ValueError("qlinear_requant_dynamic: bias must have N elements")
+    out = _out(out, (M, N), torch.int8, A, "out")
+    scales = _out(scales, M, torch.float64, A, "scales")
+    nb, _ = requant_dynamic_workspace(M, N, K)
+    if workspace is None or workspace.numel() < nb:
+        workspace = torch.empty(max(nb, 1), dtype=torch.int8, device=A.device)
+    _call("q8_gemm_requant_dynamic", _ptr(A), _ptr(B), M, N, K,
+          _ptr(sA), L.Q8_PER_TOKEN if sA.numel() == M and M != 1 else L.Q8_PER_TENSOR,
+          _ptr(sB), L.Q8_PER_CHANNEL if sB.numel() == N and N != 1 else L.Q8_PER_TENSOR,
+          L.Q8_EPI_ROWCOL, 0.0, _ptr(bias), _ACT[act], _ptr(out), _ptr(scales), _ptr(workspace),
+          workspace.numel(), _stream(), keep=(workspace,))
+    return out, scales
+
+
 def pack_weight_int4(W: torch.Tensor, group_size: int):
     """4-bit per-group weight packing (fromConstantArrayPerGroup +
     quantizeArrayPerGroup, quantization_types.ts:319-340, :143-153) of an

@@ -90,7 +90,19 @@ def test_c3_gemm_4096(mods, oracle):
     same_bits(y_h, oracle.epilogue(host(acc), "rowcol", s_ref, sB_ref), "C3 epilogue")
 
 
-def test_c4_decoder_projections(mods, oracle):
+def exact_acc(Aq, Bq):
+    """int32 accumulators of int8 [M,K] x [N,K]^T through an f64 matmul:
+    every partial sum is an integer below 2^53 (|acc| <= K * 128 * 128)."""
+    return (Aq.astype(np.float64) @ Bq.astype(np.float64).T).astype(np.int32)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_c4_decoder_projections(mods, oracle, fused):
+    """Every stage of the projection set on all 2048 tokens, each fed the
+    device's own inputs: int32 accumulators against an exact f64 matmul, the
+    per-channel epilogue, the per-token quantizes (the O projection's fused
+    into its GEMM when `fused`) and SiLU*up requant against the oracle; plus
+    8 tokens end to end from X."""
     C, O, OC = mods
     inp = OC.c4_inputs()
     packed_ref = {k: OC.pack_pc(w, 0) for k, w in inp["W"].items()}
@@ -100,11 +112,38 @@ def test_c4_decoder_projections(mods, oracle):
     for k in P:
         same_bits(host(P[k][1]), packed_ref[k][1], f"C4 {k} scales")
         same_bits(host(P[k][0]), packed_ref[k][0], f"C4 {k} codes")
-    out = C.c4_step(dev(inp["X"]), P)
+    out = C.c4_step(dev(inp["X"]), P, fused_requant=fused)
+    h = {k: host(v) for k, v in out.items()}
+
+    def quant(x, q, s, what):
+        s_ref = oracle.scales_per_token(x)
+        same_bits(s, s_ref, f"{what} scales")
+        same_bits(q, oracle.quantize_rows(x, s_ref), f"{what} codes")
+
+    def linear(xq, sx, wname, y, what):
+        Wq, sW = packed_ref[wname]
+        same_bits(y, oracle.epilogue(exact_acc(xq, Wq), "rowcol", sx, sW), what)
+
+    quant(inp["X"], h["xq"], h["sx"], "C4 x quantize")
+    linear(h["xq"], h["sx"], "qkv", h["qkv"], "C4 qkv (all rows)")
+    quant(np.ascontiguousarray(h["qkv"][:, 8192:]), h["vq"], h["sv"], "C4 v quantize")
+    o_ref = oracle.epilogue(exact_acc(h["vq"], packed_ref["o"][0]), "rowcol", h["sv"], packed_ref["o"][1])
+    if not fused:
+        same_bits(h["o"], o_ref, "C4 o (all rows)")
+    quant(o_ref, h["oq"], h["so"], "C4 o requant" + (" (fused in the GEMM)" if fused else ""))
+    gu = np.concatenate([h["gate"], h["up"]], 1)
+    linear(h["oq"], h["so"], "gate_up", gu, "C4 gate|up (all rows)")
+    hh = oracle.silu_mul(h["gate"], h["up"])
+    quant(hh, h["hq"], h["sh"], "C4 silu*up requant")
+    linear(h["hq"], h["sh"], "down", h["down"], "C4 down (all rows)")
+    # 8 tokens end to end from X
     rows = np.array([0, 1, 777, 1023, 1024, 1500, 2046, 2047])
     ref = OC.c4_expected_rows(inp, rows, packed_ref)
-    for k in ("qkv", "o", "gate", "up", "down"):
-        same_bits(host(out[k])[rows], ref[k], f"C4 {k}")
+    for k in ("qkv", "gate", "up", "down"):
+        same_bits(h[k][rows], ref[k], f"C4 {k} end to end")
+    so_ref = oracle.scales_per_token(ref["o"])
+    same_bits(h["so"][rows], so_ref, "C4 o scales end to end")
+    same_bits(h["oq"][rows], oracle.quantize_rows(ref["o"], so_ref), "C4 o codes end to end")
 
 
 def test_c5_gemv(mods, oracle):

@@ -109,3 +109,99 @@ def test_c2_with_fused_static_requant_equals_dynamic_c2(ops, oracle):
     Wq, sW = packed[2]
     y = ops.qlinear(hq, dev(np.array([scales[2]])), dev(Wq), dev(sW))
     same_bits(host(y), y_ref)
+
+
+# ------------------------------------------------------------ dynamic per-row requant
+DYN_SHAPES = [(2048, 4096, 4096),   # C4's O projection: 128 co-resident tiles, fused route
+              (300, 520, 1024),     # edge tiles in both dimensions, N % 4 == 0
+              (257, 131, 64),       # N not a multiple of 4 (scalar stores)
+              (12, 900, 4096),      # GEMV route (fp32 in the workspace, then quantize_rows)
+              (4096, 8192, 256),    # 512 tiles: more than fit the chip, fallback route
+              (64, 96, 40)]         # K not a multiple of 16
+
+
+@pytest.mark.parametrize("M,N,K", DYN_SHAPES)
+@pytest.mark.parametrize("bias,act", [(False, "none"), (True, "relu"), (True, "silu")])
+def test_requant_dynamic_matches_epilogue_then_quantize_rows(ops, oracle, M, N, K, bias, act):
+    if M * N * K > 2048 * 4096 * 4096 // 4 and (bias, act) != (False, "none"):
+        pytest.skip("the full-size shape runs once, without bias")
+    rng = np.random.default_rng(M + 3 * N + 7 * K + len(act))
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    sA = (rng.random(M) * 0.01 + 1e-4).astype(np.float64)
+    sB = (rng.random(N) * 1e-3 + 1e-5).astype(np.float64)
+    b = (rng.standard_normal(N) * 0.5).astype(np.float32) if bias else None
+    # a row of saturating accumulators (|acc| > 2^24: the f64 epilogue path)
+    A[1, :] = 127
+    B[3, :] = 127
+    q, s = ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB),
+                                       bias=dev(b) if bias else None, act=None if act == "none" else act)
+    if M * N * K > 1 << 30:
+        # exact: |acc| <= 4096 * 128 * 128 < 2^53
+        acc = (A.astype(np.float64) @ B.T.astype(np.float64)).astype(np.int32)
+    else:
+        acc = oracle.quantized_dot(A, B, b_layout=1)
+    y = oracle.epilogue(acc, "rowcol", sA, sB, bias=b, act=act)
+    s_ref = oracle.scales_per_token(y)
+    same_bits(host(s), s_ref)
+    same_bits(host(q), oracle.quantize_rows(y, s_ref))
+
+
+def test_requant_dynamic_routes_and_status(ops):
+    from mlfw_amd import _lib
+    import ctypes as C
+    nb, fused = ops.requant_dynamic_workspace(2048, 4096, 4096)
+    assert fused and nb < 64 * 1024, (nb, fused)
+    nb, fused = ops.requant_dynamic_workspace(4096, 8192, 256)
+    assert not fused and nb >= 4096 * 8192 * 4
+    nb, fused = ops.requant_dynamic_workspace(12, 900, 4096)
+    assert not fused
+    # the fused route's bounded wait did not run out
+    M, N, K = 1024, 2048, 512
+    rng = np.random.default_rng(5)
+    A = dev(rng.integers(-128, 128, (M, K)).astype(np.int8))
+    B = dev(rng.integers(-128, 128, (N, K)).astype(np.int8))
+    sA = dev(np.full(M, 1e-3))
+    sB = dev(np.full(N, 1e-3))
+    nb, fused = ops.requant_dynamic_workspace(M, N, K)
+    assert fused
+    ws = torch.empty(nb, dtype=torch.int8, device=DEV)
+    for _ in range(3):
+        ops.qlinear_requant_dynamic(A, sA, B, sB, workspace=ws)
+    flag = C.c_int(-1)
+    _lib.call("q8_gemm_requant_dynamic_status", C.c_void_p(ws.data_ptr()), M, C.byref(flag),
+              C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert flag.value == 0
+
+
+def test_requant_dynamic_reports_a_timed_out_wait(ops, monkeypatch):
+    """The host-forced timeout (an arrival target the grid never reaches,
+    a short bound): every workgroup's wait ends, the status word reports it,
+    and the next ordinary call clears it and is exact again."""
+    from mlfw_amd import _lib
+    import ctypes as C
+    M, N, K = 512, 1024, 256
+    rng = np.random.default_rng(9)
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    sA, sB = np.full(M, 1e-3), np.full(N, 2e-3)
+    nb, fused = ops.requant_dynamic_workspace(M, N, K)
+    assert fused
+    ws = torch.empty(nb, dtype=torch.int8, device=DEV)
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def status():
+        flag = C.c_int(-1)
+        _lib.call("q8_gemm_requant_dynamic_status", C.c_void_p(ws.data_ptr()), M, C.byref(flag), st)
+        return flag.value
+
+    monkeypatch.setenv("Q8_DQ_TEST_TIMEOUT", "1")
+    ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws)
+    assert status() == 1
+    monkeypatch.delenv("Q8_DQ_TEST_TIMEOUT")
+    q, s = ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws)
+    assert status() == 0
+    y = ops.qlinear(dev(A), dev(sA), dev(B), dev(sB))
+    q_ref, s_ref = ops.quantize_per_token(y)
+    same_bits(host(s), host(s_ref))
+    same_bits(host(q), host(q_ref))
