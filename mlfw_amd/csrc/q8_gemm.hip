@@ -201,6 +201,22 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = in / gm;
 }
 
+// Maximum over each half of the wave (lanes 0-31, 32-63), in the last lane
+// of the half (lanes 31 and 63; other lanes hold partial maxima).  DPP row
+// operations stay in the VALU: quad swaps, the half-row and row mirrors
+// reduce each 16-lane row, then row_bcast:15 feeds lane 15 of rows 0 and 2
+// into rows 1 and 3.  (A ds_bpermute butterfly takes an LDS round trip per
+// step.)
+__device__ __forceinline__ int half_wave_max(int v) {
+  auto mx = [](int a, int b) { return a > b ? a : b; };
+  v = mx(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  v = mx(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  v = mx(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = mx(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
+  v = mx(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));  // row_bcast:15 into rows 1, 3
+  return v;
+}
+
 // Compile-time epilogue variant of the MFMA kernel:
 //   bit 4 int32 output (raw accumulators), else fp32 output with
 //   bit 3 MODE (0: fround(acc * s_out), 1: fround(acc * fround(sA[m] * sB[n]))),
@@ -586,6 +602,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     // step a straight-line block over the U quads.
     constexpr int U = 8;
     static_assert(NQ % U == 0, "whole groups of quads");
+    static_assert(LPR == 32, "a strip row is one half of the wave (half_wave_max)");
     auto dq_values = [&](auto ic) {
       constexpr int i = decltype(ic)::value;
 #pragma unroll
@@ -654,13 +671,8 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
           }
         }
 #pragma unroll
-        for (int off = 1; off < LPR; off <<= 1)
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const int o = __shfl_xor(k[u], off, 64);
-            k[u] = o > k[u] ? o : k[u];
-          }
-        if (lane % LPR == 0) {
+        for (int u = 0; u < U; ++u) k[u] = half_wave_max(k[u]);
+        if (lane % LPR == LPR - 1) {
 #pragma unroll
           for (int u = 0; u < U; ++u) atomicMax(&tkey[trow0 + u * RPI], k[u]);
         }
