@@ -215,7 +215,9 @@ int q8_pack_weight(const float* W, int64_t rows, int64_t cols, int axis, int gra
  *                      Q8_PER_TOKEN / Q8_PER_CHANNEL index by m / n)
  *   bias (may be NULL): fround(y + bias[n]); act: Q8_ACT_*.
  * zpA / zpB must be 0 in this build (Q8_ERR_UNSUPPORTED otherwise).
- * Routes M <= 16 to the GEMV kernel. */
+ * Routes M <= 16 to the GEMV kernel.  K % 16 != 0 or A / B not 16-byte
+ * aligned take a generic one-thread-per-output kernel (exact, slow);
+ * q8_generic_gemm_launches counts those launches. */
 int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int32_t zpA, int32_t zpB,
             const double* sA, int sA_mode, const double* sB, int sB_mode,
@@ -223,11 +225,20 @@ int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int out_kind, void* out, void* stream);
 
 /* The skinny (decode) form of q8_gemm for 1 <= M <= 16: same contract,
- * HBM-bound kernel (packed int8 dot products, no matrix cores). */
+ * HBM-bound kernels that stream the weight once: packed int8 dot products
+ * (v_dot4_i32_i8) for M <= 4, one 16x16x64 int8 MFMA per 16 weight rows x
+ * 64 K-bytes for 4 < M <= 16. */
 int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             const double* sA, int sA_mode, const double* sB, int sB_mode,
             int epi, double s_out, const float* bias, int act,
             int out_kind, void* out, void* stream);
+
+/* Launches of the generic (non-MFMA) GEMM kernel since the library was
+ * loaded, over all devices and threads: q8_gemm / q8_quantized_dot calls
+ * whose K is not a multiple of 16 or whose operands are not 16-byte
+ * aligned.  No counterpart in the reference (its CPU kernels have one
+ * path); it makes the slow route visible to callers and tests. */
+int q8_generic_gemm_launches(int64_t* count);
 
 /* quantized_dot as the reference defines it (src/compiler/ir/graph/ops/
  * quantization.ts:103-155, lowering rules/quantization.ts:23-42): operands

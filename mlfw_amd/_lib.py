@@ -72,6 +72,7 @@ SIGNATURES = {
                 _int, _dbl, _vp, _int, _int, _vp, _vp],
     "q8_gemv": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                 _int, _vp, _vp],
+    "q8_generic_gemm_launches": [_vp],
     "q8_gemm_requant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                         _dbl, _vp, _vp],
     "q8_gemm_requant_dynamic_workspace": [_i64, _i64, _i64, _vp, _vp],

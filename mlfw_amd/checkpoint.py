@@ -129,6 +129,23 @@ def _js_number(x) -> str:
             ("+" if e >= 0 else "-") + str(abs(e)))
 
 
+def _is_array_index(k: str) -> bool:
+    """A canonical array index (ECMA-262 6.1.7): the decimal form of an
+    integer 0 <= n < 2^32 - 1 with no leading zeros."""
+    return (k.isascii() and k.isdigit() and (k == "0" or k[0] != "0")
+            and int(k) < 2 ** 32 - 1)
+
+
+def _js_items(d: dict):
+    """A plain object's own keys in the order JS enumerates them
+    (OrdinaryOwnPropertyKeys, ECMA-262 10.1.11.1; Object.keys and
+    JSON.stringify follow it): array-index keys ascending, then the other
+    string keys in insertion order."""
+    items = [(str(k), v) for k, v in d.items()]
+    index = sorted((int(k), k, v) for k, v in items if _is_array_index(k))
+    return [(k, v) for _, k, v in index] + [(k, v) for k, v in items if not _is_array_index(k)]
+
+
 def _js_json(v) -> str:
     if v is None:
         return "null"
@@ -139,8 +156,8 @@ def _js_json(v) -> str:
     if isinstance(v, list):
         return "[" + ",".join(_js_json(e) for e in v) + "]"
     if isinstance(v, dict):
-        return "{" + ",".join(json.dumps(str(k), ensure_ascii=False) + ":" + _js_json(e)
-                              for k, e in v.items()) + "}"
+        return "{" + ",".join(json.dumps(k, ensure_ascii=False) + ":" + _js_json(e)
+                              for k, e in _js_items(v)) + "}"
     raise TypeError(f"not JSON-encodable: {type(v)}")
 
 
@@ -162,7 +179,7 @@ def _encode(value, buffers):
     if isinstance(value, (list, tuple)):
         return [_encode(v, buffers) for v in value]
     if isinstance(value, dict):
-        return {str(k): _encode(v, buffers) for k, v in value.items()}
+        return {k: _encode(v, buffers) for k, v in _js_items(value)}
     return value
 
 

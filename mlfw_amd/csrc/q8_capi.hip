@@ -429,6 +429,12 @@ int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, i
   return launched(err, "q8_gemm launch");
 }
 
+int q8_generic_gemm_launches(int64_t* count) {
+  Q8_REQUIRE(count != nullptr, "q8_generic_gemm_launches: count is NULL");
+  *count = (int64_t)q8::g_generic_gemm_launches.load(std::memory_order_relaxed);
+  return Q8_OK;
+}
+
 int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, const double* sA,
             int sA_mode, const double* sB, int sB_mode, int epi, double s_out, const float* bias,
             int act, int out_kind, void* out, void* stream) {

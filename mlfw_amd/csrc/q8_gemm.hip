@@ -837,6 +837,8 @@ static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int
   return hipGetLastError();
 }
 
+std::atomic<long long> g_generic_gemm_launches{0};
+
 hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
@@ -847,6 +849,7 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                    ((reinterpret_cast<uintptr_t>(B) & 15) == 0);
   if (!vec) {
     const int64_t n = M * N;
+    g_generic_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     hipLaunchKernelGGL(k_gemm_i8_generic, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();

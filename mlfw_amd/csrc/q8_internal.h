@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/q8hip.h"
 
 namespace q8 {
@@ -60,6 +62,8 @@ hipError_t launch_pack_weight(const float* W, int64_t rows, int64_t cols, int ax
 hipError_t launch_silu_mul_quant_rows(const float* g, int64_t ldg, const float* u, int64_t ldu,
                                       int64_t M, int64_t K, float* h, int8_t* q, double* scales,
                                       hipStream_t st);
+// launches of the generic (non-MFMA) GEMM kernel, for q8_generic_gemm_launches
+extern std::atomic<long long> g_generic_gemm_launches;
 hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
 // GEMM with the dynamic per-row requant epilogue (e.out_dq fields filled by

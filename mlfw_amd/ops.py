@@ -375,6 +375,15 @@ def qlinear_requant(A: torch.Tensor, sA: torch.Tensor | None, B: torch.Tensor,
     return out
 
 
+def generic_gemm_launches() -> int:
+    """Launches of the generic (non-MFMA) GEMM kernel so far in this process:
+    GEMMs whose K is not a multiple of 16 or whose operands are not 16-byte
+    aligned take it."""
+    n = C.c_int64(0)
+    L.call("q8_generic_gemm_launches", C.byref(n))
+    return n.value
+
+
 def requant_dynamic_workspace(M: int, N: int, K: int):
     """(bytes, fused) of q8_gemm_requant_dynamic for this shape."""
     nb, fused = C.c_size_t(0), C.c_int(0)

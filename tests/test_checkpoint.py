@@ -85,6 +85,10 @@ def _rich_tree(tmp_path):
         "params": {"scheme": "per_group", "scale": f64, "zeroPoint": i32, "axis": None,
                    "groupSize": 128, "dtype": "i8", "numBits": 4},
         "byIndex": ck.JSMap([(0, {"step": 1}), (1, {"step": 2})]),
+        # integer-like keys: JS enumerates "0", "2", "10" first, ascending
+        # (which also fixes the $buf order), then the others as inserted
+        "layers": {"name": "mlp", "10": ck.Tensor("f32", [3, 5], files["h"][2]), "01": 1,
+                   "2": ck.Tensor("i8", [4, 6], files["w8"][2]), "0": {"b": 2, "1": 3}},
     }
     spec = {
         "epoch": 7, "note": "int8 é \"quoted\"\n", "flags": [True, False, None], "nums": nums,
@@ -94,6 +98,9 @@ def _rich_tree(tmp_path):
                    "zeroPoint": {"__array": {"type": "Int32Array", "file": "i32.bin"}}, "axis": None,
                    "groupSize": 128, "dtype": "i8", "numBits": 4},
         "byIndex": {"__map": [[0, {"step": 1}], [1, {"step": 2}]]},
+        "layers": {"name": "mlp", "10": {"__tensor": {"dtype": "f32", "shape": [3, 5], "file": "h.bin"}},
+                   "01": 1, "2": {"__tensor": {"dtype": "i8", "shape": [4, 6], "file": "w8.bin"}},
+                   "0": {"b": 2, "1": 3}},
     }
     return py, spec
 
@@ -116,6 +123,13 @@ def test_bytes_match_the_js_restatement(tmp_path):
     assert r.returncode == 0, r.stderr
     assert (tmp_path / "re.bin").read_bytes() == ours
     assert ck.serialize_checkpoint(ck.deserialize_checkpoint(theirs)) == theirs
+
+
+def test_plain_object_keys_follow_js_enumeration_order():
+    tree = {"z": 1, "10": 2, "2": 3, "01": 4, "4294967295": 5, "4294967294": 6, "-1": 7, "0": 8}
+    header = ck.serialize_checkpoint(tree)[8:].decode("utf-8")
+    order = json.loads(header, object_pairs_hook=lambda kv: [k for k, _ in kv] if "z" in dict(kv) else dict(kv))
+    assert order["tree"] == ["0", "2", "10", "4294967294", "z", "01", "4294967295", "-1"]
 
 
 def test_int4_packing_round_trip_and_layout():

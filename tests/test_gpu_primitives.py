@@ -347,6 +347,21 @@ def test_quantized_dot_small(ops, oracle, M, N, K):
     same_bits(host(acc), oracle.quantized_dot(A, B, b_layout=1))
 
 
+def test_generic_gemm_route_is_counted(ops, oracle):
+    """K % 16 != 0 takes the generic kernel (exact) and is counted; an
+    MFMA-shaped call is not."""
+    rng = np.random.default_rng(41)
+    before = ops.generic_gemm_launches()
+    A = rng.integers(-128, 128, (40, 40)).astype(np.int8)
+    B = rng.integers(-128, 128, (24, 40)).astype(np.int8)
+    same_bits(host(ops.quantized_dot(dev(A), dev(B))), oracle.quantized_dot(A, B, b_layout=1))
+    assert ops.generic_gemm_launches() == before + 1
+    A = rng.integers(-128, 128, (40, 64)).astype(np.int8)
+    B = rng.integers(-128, 128, (24, 64)).astype(np.int8)
+    same_bits(host(ops.quantized_dot(dev(A), dev(B))), oracle.quantized_dot(A, B, b_layout=1))
+    assert ops.generic_gemm_launches() == before + 1
+
+
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 4096), (2048, 4096, 4096), (768, 1280, 11008),
                                    (4096, 4096, 4096), (4001, 3100, 2048), (4001, 3099, 2064),
                                    (1000, 1001, 4112), (513, 4095, 272), (2048, 12288, 4096),
