@@ -9,28 +9,35 @@
 //     kept in AGPRs).  A lane feeds 16 K-bytes of one row of A and the same
 //     16 K-bytes of one row of B per instruction, so fragments are single
 //     128-bit LDS reads.
-//   * K is walked in BK = 64-byte stages held in a ring of four LDS
-//     buffers.  Global -> LDS copies use the buffer_load_dwordx4 ... lds
-//     form (no VGPR staging): each instruction moves 16 tile rows x 64 B,
-//     lane l landing at LDS byte 16*l of the wave's destination.
+//   * K is walked in BK = 128-byte stages held in a ring of two LDS
+//     buffers (2 x 64 KiB for the 256 x 256 tile).  Global -> LDS copies
+//     use the buffer_load_dwordx4 ... lds form (no VGPR staging): each
+//     instruction moves 8 tile rows x 128 B, lane l landing at LDS byte
+//     16*l of the wave's destination, so every row segment is one whole
+//     128-byte line.  Measured against 64-byte stages in a ring of four on
+//     the 4096^3 GEMM: the same cycles per tile, half the L1 -> L2 requests
+//     and barriers, and a part that holds a ~5% higher clock under the
+//     MFMA load (power-limited at ~1.7 GHz): 63-64 us instead of 67 us.
 //     Out-of-range rows and the K tail are fetched through offsets past
 //     the buffer resource's num_records, which the hardware returns as
 //     zero -- edge tiles need no separate code.
-//   * LDS layout: tile row r occupies 64 B; its logical 16-byte K chunk c
-//     is stored at chunk position c ^ swz(r), swz(r) = (r>>2) & 3: rows
-//     r, r+4, r+8, r+12 start on the same bank (64-byte rows over 256 bytes
-//     of banks) and the swizzle puts their chunks on four distinct 16-byte
-//     bank groups.  Measured on the 2048 x 4096 x 4096 int8 GEMM:
-//     SQ_LDS_BANK_CONFLICT 0 (the earlier ((r>>1) ^ (r>>3)) & 3 read 4.2M
-//     conflict cycles, with no difference in run time).  The swizzle is
-//     applied on the global side (each lane fetches the chunk its LDS slot
-//     must hold), so the DMA writes stay linear.
-//   * Pipeline: one barrier per stage, between its two 32-byte K sub-steps;
-//     a stage's refill is spread over the following two sub-steps, so each
-//     sub-step issues a quarter of a stage's copies between its MFMAs (a
-//     burst of copies backs up the address unit and stalls MFMA issue) and
-//     copies run more than two stages ahead of their use.  Fragments are
-//     double-buffered in registers: every sub-step reads the next one's.
+//   * LDS layout: tile row r occupies 128 B; its logical 16-byte K chunk c
+//     is stored at chunk position c ^ swz(r), swz(r) = (r>>1) & 7: rows
+//     r, r+2, ..., r+14 start on the same bank (128-byte rows over 256
+//     bytes of banks) and the swizzle puts their chunks on eight distinct
+//     16-byte bank groups.  (The 64-byte-row form of the same rule,
+//     (r>>2) & 3, measured SQ_LDS_BANK_CONFLICT 0 where ((r>>1) ^ (r>>3)) & 3
+//     read 4.2M conflict cycles.)  The swizzle is applied on the global side
+//     (each lane fetches the chunk its LDS slot must hold), so the DMA
+//     writes stay linear.
+//   * Pipeline: a stage is four 32-byte K sub-steps and one barrier, before
+//     its last sub-step: after it every wave is done with the stage's
+//     buffer and the next stage has landed.  The refill of that buffer with
+//     the stage after next goes out in two halves, in the last sub-step and
+//     in the next stage's first, spread between their MFMAs (a burst of
+//     copies backs up the address unit and stalls MFMA issue), and lands
+//     within the two sub-steps that follow.  Fragments are double-buffered
+//     in registers: every sub-step reads the next one's.
 //   * Workgroup -> tile order undoes the round-robin dispatch over the 8
 //     XCDs (consecutive workgroup ids land on different XCDs), then walks
 //     groups of 4 tile rows column by column, so the tiles resident on one
@@ -95,8 +102,8 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, int acc, int64
 }
 
 // ------------------------------------------------------------------ MFMA GEMM
-constexpr int BK = 64;                  // K bytes per LDS stage
-constexpr int NBUF = 4;                 // LDS stages in the ring
+constexpr int BK = 128;                 // K bytes per LDS stage
+constexpr int NBUF = 2;                 // LDS stages in the ring
 constexpr int GEMM_THREADS = 256;       // 4 waves, 2 x 2
 constexpr uint32_t OOB = 0x80000000u;   // voffset past every buffer's num_records
 
@@ -108,12 +115,12 @@ struct GemmCfg {
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int LDS = NBUF * STAGE;              // the stage ring
   static constexpr int LDS_TOTAL = LDS + 8 * (BM + BN);  // + the tile's f64 scales
-  static constexpr int A_LOADS = BM / 64;              // 16-row copies per wave per stage
-  static constexpr int B_LOADS = BN / 64;
+  static constexpr int A_LOADS = BM / 32;              // 8-row copies per wave per stage
+  static constexpr int B_LOADS = BN / 32;
   static_assert(TM >= 1 && TN >= 1 && BM % 64 == 0 && BN % 64 == 0, "tile shape");
 };
 
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
 // Buffer resource (V#) of a raw byte range: base, stride 0, num_records
 // bytes, gfx9 data-format word.
@@ -278,21 +285,21 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   }
 
   // Copy plan: wave w fills tile rows [w*BM/4, (w+1)*BM/4) of A and the
-  // same share of B, 16 rows per instruction.  Lane l lands in row
-  // 16j + l/4 at chunk position l%4 and so fetches logical chunk
-  // (l%4) ^ swz(row).
+  // same share of B, 8 rows per instruction.  Lane l lands in row
+  // 8j + l/8 at chunk position l%8 and so fetches logical chunk
+  // (l%8) ^ swz(row).
   uint32_t offa[C::A_LOADS], offb[C::B_LOADS];
   int kca[C::A_LOADS], kcb[C::B_LOADS];
 #pragma unroll
   for (int j = 0; j < C::A_LOADS; ++j) {
-    const int row = wave * (BM / 4) + 16 * j + (lane >> 2);
-    kca[j] = 16 * ((lane & 3) ^ swz(row));
+    const int row = wave * (BM / 4) + 8 * j + (lane >> 3);
+    kca[j] = 16 * ((lane & 7) ^ swz(row));
     offa[j] = row < rows_a ? (uint32_t)(row * K + kca[j]) : OOB;
   }
 #pragma unroll
   for (int j = 0; j < C::B_LOADS; ++j) {
-    const int row = wave * (BN / 4) + 16 * j + (lane >> 2);
-    kcb[j] = 16 * ((lane & 3) ^ swz(row));
+    const int row = wave * (BN / 4) + 8 * j + (lane >> 3);
+    kcb[j] = 16 * ((lane & 7) ^ swz(row));
     offb[j] = row < rows_b ? (uint32_t)(row * K + kcb[j]) : OOB;
   }
   const uint32_t bytes_a = (uint32_t)rows_a * (uint32_t)K;
@@ -307,11 +314,11 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
 #pragma unroll
   for (int j = 0; j < C::B_LOADS; ++j) offb_t[j] = kb_last + kcb[j] >= K ? OOB : offb[j];
 
-  // Copies of the A (resp. B) half of K stage kt into `stage`.  kt >= KT
-  // copies nothing: with num_records 0 every lane is out of range and
-  // writes zeros into a stage that is no longer read, which keeps the loop
-  // body branch-free.
-  auto issue_a = [&](int kt, int8_t* stage) {
+  // Copies j0 <= j < j1 of the A (resp. B) part of K stage kt into
+  // `stage`.  kt >= KT copies nothing: with num_records 0 every lane is out
+  // of range and writes zeros into a stage that is no longer read, which
+  // keeps the loop body branch-free.
+  auto issue_a = [&](int kt, int8_t* stage, int j0, int j1) {
     const bool live = kt < KT;
     const int kb = live ? kt * BK : 0;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab + kb, live ? bytes_a - (uint32_t)kb : 0u);
@@ -319,9 +326,9 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const bool tail = kb + BK > K;
 #pragma unroll
     for (int j = 0; j < C::A_LOADS; ++j)
-      copy16_to_lds(ra, sa + j * 16 * BK, tail ? offa_t[j] : offa[j]);
+      if (j >= j0 && j < j1) copy16_to_lds(ra, sa + j * 8 * BK, tail ? offa_t[j] : offa[j]);
   };
-  auto issue_b = [&](int kt, int8_t* stage) {
+  auto issue_b = [&](int kt, int8_t* stage, int j0, int j1) {
     const bool live = kt < KT;
     const int kb = live ? kt * BK : 0;
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
@@ -329,7 +336,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const bool tail = kb + BK > K;
 #pragma unroll
     for (int j = 0; j < C::B_LOADS; ++j)
-      copy16_to_lds(rb, sb + j * 16 * BK, tail ? offb_t[j] : offb[j]);
+      if (j >= j0 && j < j1) copy16_to_lds(rb, sb + j * 8 * BK, tail ? offb_t[j] : offb[j]);
   };
 
   // Fragment addresses: byte offset of the fragment row within a stage and
@@ -374,48 +381,57 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
   };
 
-  // Pipeline over a ring of NBUF = 4 stages (stage kt in buffer kt % 4).
-  // A stage is two 32-byte K sub-steps.  Barrier B_kt sits between the two
-  // sub-steps of stage kt: after it every wave has finished reading buffer
-  // kt % 4 and stage kt+1 has landed.  The refill of that buffer with
-  // stage kt+4 is spread over the next two sub-steps (A half after B_kt,
-  // B half in the first sub-step of stage kt+1) so that each sub-step
-  // issues only a quarter of a stage's copies between its MFMAs, and every
-  // copy is issued more than two stages ahead of its use.  Each sub-step
-  // also reads the next sub-step's fragments into the other register set.
+  // Pipeline over a ring of NBUF = 2 stages (stage kt in buffer kt % 2).
+  // A stage is four 32-byte K sub-steps.  The barrier of stage kt sits
+  // before its last sub-step: every fragment read of buffer kt % 2 has
+  // returned (the last sub-step's fragments were read one sub-step ahead)
+  // and stage kt+1 has landed.  The refill of buffer kt % 2 with stage
+  // kt+2 goes out in two halves: with the last sub-step of stage kt and the
+  // first of stage kt+1, so every copy has at least two sub-steps to land
+  // before the next barrier.
   int8_t* const ring = lds;
   auto buf = [&](int kt) { return ring + (kt & (NBUF - 1)) * C::STAGE; };
   constexpr int NV = C::A_LOADS + C::B_LOADS;    // copies per stage
-  issue_a(0, buf(0));
-  issue_b(0, buf(0));
-  issue_a(1, buf(1));
-  issue_b(1, buf(1));
-  issue_a(2, buf(2));
-  issue_b(2, buf(2));
-  issue_a(3, buf(3));
+  constexpr int HA = C::A_LOADS / 2, HB = C::B_LOADS / 2;
+  static_assert(C::A_LOADS % 2 == 0 && C::B_LOADS % 2 == 0, "copies split in halves");
+  issue_a(0, buf(0), 0, C::A_LOADS);
+  issue_b(0, buf(0), 0, C::B_LOADS);
+  issue_a(1, buf(1), 0, C::A_LOADS);
+  issue_b(1, buf(1), 0, C::B_LOADS);
   if (!OUT_I32 && MODE == 1) {
 #pragma unroll
     for (int u = 0; u < NSC; ++u)
       if (tid + u * GEMM_THREADS < BM + BN) s_rows[tid + u * GEMM_THREADS] = scv[u];
   }
-  stage_sync_keep<2 * NV + C::A_LOADS>();       // stage 0 landed
+  stage_sync_keep<NV>();                          // stage 0 landed
   v4i fa0[C::TM], fb0[C::TN], fa1[C::TM], fb1[C::TN];
   read_frags(buf(0), 0, fa0, fb0);
   for (int kt = 0; kt < KT; ++kt) {
     int8_t* cur = buf(kt);
-    // sub-step 0 of stage kt; B half of stage kt+3 into the buffer freed by B_{kt-1}
+    // sub-step 0; the second half of stage kt+1's copies (stage 1 went out
+    // whole in the prologue)
     read_frags(cur, 1, fa1, fb1);
-    issue_b(kt + 3, buf(kt + 3));
+    if (kt >= 1) {
+      issue_a(kt + 1, buf(kt + 1), HA, C::A_LOADS);
+      issue_b(kt + 1, buf(kt + 1), HB, C::B_LOADS);
+    }
     mfma_all(fa0, fb0);
-    sched_substep<C::TM + C::TN, C::TM * C::TN, C::B_LOADS>();
-    // B_kt: reads of `cur` returned everywhere; stage kt+1 landed (stages
-    // kt+2 and kt+3 may still be in flight)
-    stage_sync_keep<2 * NV>();
-    // sub-step 1 of stage kt; A half of stage kt+4 into `cur`
-    read_frags(buf(kt + 1), 0, fa0, fb0);
-    issue_a(kt + 4, cur);
+    sched_substep<C::TM + C::TN, C::TM * C::TN, NV / 2>();
+    // sub-steps 1 and 2
+    read_frags(cur, 2, fa0, fb0);
     mfma_all(fa1, fb1);
-    sched_substep<C::TM + C::TN, C::TM * C::TN, C::A_LOADS>();
+    sched_substep<C::TM + C::TN, C::TM * C::TN, 0>();
+    read_frags(cur, 3, fa1, fb1);
+    mfma_all(fa0, fb0);
+    sched_substep<C::TM + C::TN, C::TM * C::TN, 0>();
+    // every read of `cur` returned everywhere; stage kt+1 landed
+    stage_sync();
+    // sub-step 3; the first half of stage kt+2's copies into `cur`
+    read_frags(buf(kt + 1), 0, fa0, fb0);
+    issue_a(kt + 2, cur, 0, HA);
+    issue_b(kt + 2, cur, 0, HB);
+    mfma_all(fa1, fb1);
+    sched_substep<C::TM + C::TN, C::TM * C::TN, NV / 2>();
   }
   // The last iterations issued zero-filling copies for stages past KT into
   // the stage buffers the epilogue reuses: drain them first.
