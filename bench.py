@@ -279,17 +279,20 @@ def ceilings():
     import ctypes as C
     from mlfw_amd import build as B
     lib = C.CDLL(B.CEILING_LIB)
-    lib.q8c_mfma.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    lib.q8c_mfma.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                             C.POINTER(C.c_double)]
     lib.q8c_stream.argtypes = [C.c_size_t, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
-    us, mhz = C.c_double(), C.c_double()
+    us, mhz, cyc = C.c_double(), C.c_double(), C.c_double()
     out = {}
-    if lib.q8c_mfma(2048, 10, C.byref(us), C.byref(mhz)) == 0:
+    if lib.q8c_mfma(2048, 10, C.byref(us), C.byref(mhz), C.byref(cyc)) == 0:
         tops = GEMM_OPS / (us.value * 1e-6) / 1e12
         out["mfma_random_int8_4096cube"] = {
             "what": "256 workgroups x 4 waves x 2048 v_mfma_i32_32x32x32_i8 (the C3 GEMM's MFMA "
-                    "count), random operands, no loads or stores",
+                    "count), random operands cycled through 16 register fragments, no loads, "
+                    "stores or other instructions in the loop",
             "avg_us": us.value, "TOPS": tops, "frac_of_peak": tops / PEAK_INT8_TOPS,
-            "shader_clock_mhz": mhz.value}
+            "shader_clock_mhz": mhz.value,
+            "loop_mfma_busy": 2048 * 32 / cyc.value if cyc.value > 0 else None}
     for kind, name, nbytes in (("read", "gemv_N4096", 4096 * 4096 + 8 * 4096 + 4 * 4096),
                                ("read", "gemv_N11008", 11008 * 4096 + 8 * 11008 + 4 * 4096),
                                ("read", "quantize_16384x4096", 335675392),

@@ -7,7 +7,8 @@
 //     workgroups x 4 waves, each wave 2048 v_mfma_i32_32x32x32_i8 on a 4x4
 //     grid of accumulators (the GEMM's per-wave count at 4096^3) with
 //     random int8 operands (operand entropy sets the power draw, and so the
-//     clock MI355X holds).  Reports the kernel time and the shader clock
+//     clock MI355X holds), cycled through 16 fragments held in registers:
+//     nothing but MFMAs issues in the loop.  Reports the kernel time and the shader clock
 //     read in the kernel (s_memtime against the 100 MHz s_memrealtime).
 //   * q8c_stream: a streaming read or write of `bytes` (16-byte
 //     non-temporal accesses, 1 KiB per wave instruction), the HBM floor of a
@@ -35,11 +36,14 @@ __device__ __forceinline__ uint32_t mix(uint32_t x) {
 
 __global__ __launch_bounds__(256, 1) void k_mfma(int iters, uint32_t seed, int* out,
                                                  long long* clk) {
-  const int lane = threadIdx.x & 63;
+  // 16 random fragments, generated once; the loop cycles through them with
+  // compile-time indices, so no VGPR that feeds an in-flight MFMA is ever
+  // rewritten (such a write stalls issue until the MFMA has read it) and
+  // the only instructions in the loop are the MFMAs and the loop count.
   const uint32_t base = seed + (blockIdx.x * 256u + threadIdx.x) * 64u;
-  v4i f[8];
+  v4i f[16];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 16; ++i)
     f[i] = v4i{(int)mix(base + 4 * i), (int)mix(base + 4 * i + 1), (int)mix(base + 4 * i + 2),
                (int)mix(base + 4 * i + 3)};
   v16i acc[4][4];
@@ -54,17 +58,17 @@ __global__ __launch_bounds__(256, 1) void k_mfma(int iters, uint32_t seed, int* 
     t0 = __builtin_amdgcn_s_memtime();
     r0 = __builtin_amdgcn_s_memrealtime();
   }
-  for (int it = 0; it < iters; ++it) {
+  // each pass: 4 phases x 16 MFMAs; phase p pairs A fragment (i + 4p) % 16
+  // with B fragment (8 + j + 4p) % 16
+  for (int it = 0; it < iters; it += 4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[4 + j], acc[i][j], 0, 0, 0);
-    // rotate operands so consecutive iterations do not see identical inputs
-    const v4i t = f[0];
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 7; ++i) f[i] = f[i + 1];
-    f[7] = t ^ v4i{lane, it, lane, it};
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[(i + 4 * p) & 15], f[(8 + j + 4 * p) & 15],
+                                                            acc[i][j], 0, 0, 0);
   }
   int s = 0;
 #pragma unroll
@@ -108,8 +112,10 @@ __global__ __launch_bounds__(256) void k_write(v4i* __restrict__ p, int64_t nchu
 extern "C" {
 
 // MFMA ceiling: `reps` launches back to back; *us = average launch time,
-// *mhz = shader clock over block 0's run of the last launch.
-int q8c_mfma(int iters_per_wave, int reps, double* us, double* mhz) {
+// *mhz = shader clock over block 0's run of the last launch, *loop_cycles =
+// that run's shader cycles (2048 MFMAs x 32 cycles = 65,536 when the MFMA
+// pipe never idles).
+int q8c_mfma(int iters_per_wave, int reps, double* us, double* mhz, double* loop_cycles) {
   const int blocks = 256;
   if (iters_per_wave < 1 || reps < 1 || !us || !mhz) return 1;
   int* out = nullptr;
@@ -133,6 +139,7 @@ int q8c_mfma(int iters_per_wave, int reps, double* us, double* mhz) {
           hipMemcpy(h, clk, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess) {
         *us = 1e3 * ms / reps;
         *mhz = h[1] > 0 ? 100.0 * (double)h[0] / (double)h[1] : 0.0;
+        if (loop_cycles) *loop_cycles = (double)h[0];
         rc = 0;
       }
     }

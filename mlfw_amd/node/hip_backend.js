@@ -23,6 +23,12 @@
 
 const HIP_KIND = 'hip';
 const PROVIDER = 'hip_int8';
+// Target attribute (TargetFeatures.withAttr, support/target.ts:145-147) that
+// selects how a compiled plan quantizes activations: 'static' (the
+// calibrated scales of QuantizationPass, the reference's semantics),
+// 'per_token' or 'per_tensor' (absmax scales taken at run time).
+const ACTIVATIONS_ATTR = 'q8_activations';
+const ACTIVATION_MODES = new Set(['static', 'per_token', 'per_tensor']);
 
 let _q8 = null;
 function q8() {
@@ -287,7 +293,8 @@ function detectInt8Kernel(primFunc) {
 // derived form (the [N,K] transpose of a [K,N] weight, f64 widening of an
 // f32 scale vector) is cached beside it.  markHostDirty(array) drops the
 // copies of an array the host rewrote.
-const stats = { uploadBytes: 0, constUploadBytes: 0, downloadBytes: 0, launches: 0, fusedLinears: 0 };
+const stats = { uploadBytes: 0, constUploadBytes: 0, downloadBytes: 0, launches: 0, fusedLinears: 0,
+                dynamicLinears: 0 };
 const _resident = new WeakMap();
 
 function resetStats() { for (const k of Object.keys(stats)) stats[k] = 0; }
@@ -618,6 +625,15 @@ function runPlanOnDevice(plan, slots, steps, opts) {
   for (let k = 0; k < steps.length; k++) {
     const s = steps[k], inst = instOf(s.kernel), d = inst.desc;
     need(!s.shapeValues || s.shapeValues.length === 0, 'dynamic shapes are not supported by the int8 kernels');
+    const mode = (opts && opts.q8Activations) || d.activations || 'static';
+    if (d.op === 'quantize' && mode !== 'static' && k + 2 < steps.length) {
+      need(ACTIVATION_MODES.has(mode), `unknown q8 activation mode '${mode}'`);
+      if (tryDynamicLinear(mode, s, d, steps[k + 1], instOf(steps[k + 1].kernel), steps[k + 2],
+                           instOf(steps[k + 2].kernel), slots, readers, argSet, hostNeeds, slotBuf, dev, hostArgs)) {
+        k += 2;
+        continue;
+      }
+    }
     const fused = !(opts && opts.fuse === false) && k + 1 < steps.length &&
                   tryFusedLinear(s, inst, steps[k + 1], instOf(steps[k + 1].kernel), slots, readers, argSet, hostNeeds,
                                  slotBuf, dev, hostArgs);
@@ -631,6 +647,58 @@ function runPlanOnDevice(plan, slots, steps, opts) {
     execDevice(d, dv, dev, rhsNK);
   }
   for (const s of hostNeeds) if (slots[s] && slots[s].data) download(slots[s].data, slotBuf(s));
+}
+
+/**
+ * The per-token (or per-tensor) dynamic form of one linear, for plans
+ * compiled with q8 activations 'per_token' / 'per_tensor' (hipTarget's
+ * q8opts): QuantizationPass's quantize(x, s) -> quantized_dot(xq, W) ->
+ * convert * sv[n] (+ bias) (-> max 0) chain (quantization_pass.ts:390-459)
+ * runs as one q8_qlinear_dynamic call that quantizes x at run time instead
+ * of with the calibrated static scale s.  The weight's own scale is not in
+ * the plan, only sv[n] = fround(s * sW[n]); the call uses sv[n] / s (f64),
+ * so y = fround(acc * fround(sx[m] * (sv[n] / s))) -- the static result
+ * exactly when the dynamic scale equals s.  No counterpart in the reference
+ * (its activation scales are static); chains whose epilogue requantizes
+ * (max -> quantize fused) stay static.
+ */
+function tryDynamicLinear(mode, sq, dq, s0, i0, s1, i1, slots, readers, argSet, hostNeeds, slotBuf, dev, hostArgs) {
+  const d0 = i0.desc, e = i1.desc;
+  if (dq.targetDtype !== 'i8' || dq.zeroPoint !== 0 || !(dq.scale > 0)) return false;
+  if (d0.op !== 'quantized_dot' || e.op !== 'ewise' || !e.epilogue || e.epilogue.quant) return false;
+  if ((d0.aDtype || 'i8') !== 'i8' || (d0.bDtype || 'i8') !== 'i8' || d0.zpA || d0.zpB) return false;
+  const xSlot = sq.inputSlots[dq.inIdx], xqSlot = sq.outputSlots[dq.outIdx - sq.inputSlots.length];
+  if (d0.aIdx >= s0.inputSlots.length || s0.inputSlots[d0.aIdx] !== xqSlot) return false;
+  if ((readers.get(xqSlot) || []).length !== 1 || argSet.has(xqSlot) || hostNeeds.has(xqSlot)) return false;
+  const accSlot = s0.outputSlots[d0.outIdx - s0.inputSlots.length];
+  const ep = e.epilogue;
+  const args1 = s1.inputSlots.concat(s1.outputSlots);
+  if (args1[ep.accParam] !== accSlot || ep.M !== d0.M || ep.N !== d0.N || d0.M * d0.K !== dq.n) return false;
+  if ((readers.get(accSlot) || []).length !== 1 || argSet.has(accSlot) || hostNeeds.has(accSlot)) return false;
+  const h1 = hostArgs(s1, i1);
+  const sv = h1[ep.svParam];
+  if (!(sv instanceof Float32Array) || !i1.consts.has(sv) || sv.length !== d0.N) return false;
+  const bHost = hostArgs(s0, i0)[d0.bIdx];
+  if (!i0.consts.has(bHost)) return false;
+  const A = q8();
+  const wq = d0.rhsLayout === 'KN' ? residentConst(bHost, 'T', (w) => transposeI8(w, d0.K, d0.N))
+                                   : residentConst(bHost, 'plain');
+  const s = dq.scale;
+  const wEff = residentConst(sv, `dyn:${s}`, (x) => Float64Array.from(x, (v) => v / s));
+  let bias = null;
+  if (ep.biasParam >= 0) {
+    const bh = h1[ep.biasParam];
+    if (!(bh instanceof Float32Array) || bh.length !== d0.N) return false;
+    bias = i1.consts.has(bh) ? residentConst(bh, 'plain') : (ep.biasParam < s1.inputSlots.length ? slotBuf(s1.inputSlots[ep.biasParam]) : null);
+    if (!bias) return false;
+  }
+  const perTensor = mode === 'per_tensor';
+  stats.launches++;
+  stats.dynamicLinears++;
+  A.qlinearDynamic(slotBuf(xSlot), d0.M, d0.K, perTensor ? A.Q8_PER_TENSOR : A.Q8_PER_TOKEN, wq, wEff, A.Q8_PER_CHANNEL,
+                   d0.N, bias, ep.relu ? A.Q8_ACT_RELU : A.Q8_ACT_NONE, slotBuf(args1[e.outIdx]),
+                   dev.get('dyn_xq', d0.M * d0.K), dev.get('dyn_sx', 8 * (perTensor ? 1 : d0.M)));
+  return true;
 }
 
 function tryFusedLinear(s0, i0, s1, i1, slots, readers, argSet, hostNeeds, slotBuf, dev, hostArgs) {
@@ -724,6 +792,8 @@ function createHipExternalCodegen(CONST_BUFFERS_ATTR) {
     targetKind: HIP_KIND,
     runtimeKind: HIP_KIND,
     compile(primFunc, target, info) {
+      const mode = activationMode(target);
+      if (mode !== 'static' && info && info.op === 'quantize') info = Object.assign({}, info, { activations: mode });
       const metadata = { kind: HIP_KIND, q8: info, outputIndices: info.outputIndices };
       const cbs = primFunc && typeof primFunc.getAttr === 'function' ? primFunc.getAttr(cattr) : null;
       if (cbs && cbs.length > 0) {
@@ -808,10 +878,32 @@ function createHipCodegenEntry(getCodegenEntry, hostKind) {
  * one, a plain object with the fields the provider and QuantizationPass
  * read.
  */
-function hipTarget(CPUTarget, overrides) {
+function hipTarget(CPUTarget, overrides, q8opts) {
   const f = { kind: HIP_KIND, name: 'hip_mi355x', supportsInt8: true, supportsConstBuffers: true };
-  if (typeof CPUTarget === 'function') return CPUTarget(Object.assign(f, overrides || {}));
-  return Object.assign({ isGPU: () => false, isCPU: () => false, getAttr: () => null }, f, overrides || {});
+  const mode = (q8opts && q8opts.activations) || 'static';
+  need(ACTIVATION_MODES.has(mode), `q8 activations must be one of ${[...ACTIVATION_MODES].join(', ')} (got '${mode}')`);
+  let t;
+  if (typeof CPUTarget === 'function') {
+    t = CPUTarget(Object.assign(f, overrides || {}));
+  } else {
+    const attrs = new Map();
+    t = Object.assign({ isGPU: () => false, isCPU: () => false, attrs,
+                        getAttr: (k, fb = null) => (attrs.has(k) ? attrs.get(k) : fb),
+                        withAttr(k, v) { attrs.set(k, v); return this; } }, f, overrides || {});
+  }
+  if (mode !== 'static') {
+    need(typeof t.withAttr === 'function', 'the target factory gives no withAttr for the q8 activation mode');
+    t.withAttr(ACTIVATIONS_ATTR, mode);
+  }
+  return t;
+}
+
+/** The activation quantization a target asks for (ACTIVATIONS_ATTR). */
+function activationMode(target) {
+  const m = target && typeof target.getAttr === 'function' ? target.getAttr(ACTIVATIONS_ATTR) : null;
+  if (m === null || m === undefined) return 'static';
+  need(ACTIVATION_MODES.has(m), `unknown q8 activation mode '${m}'`);
+  return m;
 }
 
 // ---------------------------------------------------------------- eager library
@@ -889,7 +981,7 @@ function registerHip(r) {
 }
 
 module.exports = {
-  HIP_KIND, PROVIDER, registerHip, createHipRuntimeBackend, createHipExternalCodegen, createHipCodegenEntry,
+  HIP_KIND, PROVIDER, ACTIVATIONS_ATTR, activationMode, registerHip, createHipRuntimeBackend, createHipExternalCodegen, createHipCodegenEntry,
   createHipProvider, defineEagerLibrary, detectInt8Kernel, describe, runDescriptor, hipTarget, DeviceArgs,
   markHostDirty, stats, resetStats,
 };

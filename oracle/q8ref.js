@@ -75,6 +75,24 @@ function buildQuantizeRows(M, K) {
   return new Function('x', 'sc', 'q', src);
 }
 
+// Per-row dynamic scales: ValueObserver.update's min / max over the row
+// (calibration.ts:24-34: plain < / > compares, so NaN never moves them),
+// then fromRange symmetric (quantization_types.ts:249-253): absmax / 127,
+// 0 or NaN -> 1e-10; an empty row keeps defaultForActivation's 6 / 127.
+function scalesPerToken(x, M, K, out) {
+  for (let m = 0; m < M; m++) {
+    if (K === 0) { out[m] = 6 / 127; continue; }
+    let lo = Infinity, hi = -Infinity;
+    for (let k = 0; k < K; k++) {
+      const v = x[m * K + k];
+      if (v < lo) lo = v;
+      if (v > hi) hi = v;
+    }
+    out[m] = Math.max(Math.abs(lo), Math.abs(hi)) / 127 || 1e-10;
+  }
+  return out;
+}
+
 function buildDequantize(n, scale, zeroPoint) {
   let v = '(+q[i])';
   if (zeroPoint !== 0) v = `Math.fround(${v} - ${String(zeroPoint)})`;
@@ -174,6 +192,9 @@ function main(argv) {
     const q = new Int8Array(p.M * p.K);
     buildQuantizeRows(p.M, p.K)(x, sc, q);
     writeArr(outs[0], q);
+  } else if (cmd === 'scales_rows') {
+    const x = readArr(ins[0], 'f32');
+    writeArr(outs[0], scalesPerToken(x, p.M, p.K, new Float64Array(p.M)));
   } else if (cmd === 'dequantize') {
     const q = readArr(ins[0], p.src || 'i8');
     const y = new Float32Array(q.length);
@@ -249,6 +270,6 @@ function main(argv) {
 if (require.main === module) main(process.argv.slice(2));
 
 module.exports = {
-  makeRng, normalFill, uniformFill, buildQuantize, buildQuantizeRows, buildDequantize,
+  makeRng, normalFill, uniformFill, buildQuantize, buildQuantizeRows, scalesPerToken, buildDequantize,
   buildDequantizeRows, buildQuantizedDot, buildEpiloguePerChannel, buildSiluMul,
 };

@@ -182,12 +182,12 @@ function emulate(tr, args) {
 
 // ---------------------------------------------------------------- the cases
 const M = 37, N = 96, K = 256;
-function linearSet() {
+function linearSet(sX = 4.9 / 127) {
   const x = buf('x', [M, K], 'f32'), xq = buf('xq', [M, K], 'i8'), W = buf('w', [N, K], 'i8');
   const acc = buf('acc', [M, N], 'i32'), sv = buf('sv', [N], 'f32'), b = buf('b', [N], 'f32');
   const y = buf('y', [M, N], 'f32'), y2 = buf('y2', [M, N], 'f32'), y3 = buf('y3', [M, N], 'f32');
   const zero = buf('zero', [1, 1], 'f32'), q2 = buf('q2', [M, N], 'i8');
-  const sX = 4.9 / 127, sNext = 0.0371;
+  const sNext = 0.0371;
   const Wdata = randI8(5, N * K);
   const svData = new Float32Array(N);
   for (let i = 0; i < N; i++) svData[i] = Math.fround(sX * (0.001 + 0.0002 * ((i * 37) % 17)));
@@ -400,6 +400,30 @@ function cpuTests() {
     assert.strictEqual(rk.metadata.hipRoute, 'host');
   });
 
+  test('q8 activation mode travels on the target into the quantize descriptors', () => {
+    assert.strictEqual(hip.activationMode(hip.hipTarget()), 'static');
+    const t = hip.hipTarget(null, null, { activations: 'per_token' });
+    assert.strictEqual(t.getAttr(hip.ACTIVATIONS_ATTR), 'per_token');
+    assert.throws(() => hip.hipTarget(null, null, { activations: 'per_row' }), /q8 activations must be one of/);
+    // with the reference factory: TargetFeatures.withAttr (support/target.ts:145-147)
+    const made = hip.hipTarget((cfg) => {
+      const attrs = new Map();
+      return Object.assign({}, cfg, { getAttr: (k, f = null) => (attrs.has(k) ? attrs.get(k) : f),
+                                      withAttr(k, v) { attrs.set(k, v); return this; } });
+    }, null, { activations: 'per_tensor' });
+    assert.strictEqual(hip.activationMode(made), 'per_tensor');
+    const L = linearSet();
+    const cg = hip.createHipExternalCodegen('const_buffers');
+    const prov = hip.createHipProvider('external_codegen', 'const_buffers');
+    prov.annotate([L.pf.quantize, L.pf.qmatmul]);
+    const kq = cg.compile(L.pf.quantize, t, L.pf.quantize.getAttr('external_codegen').info);
+    const kd = cg.compile(L.pf.qmatmul, t, L.pf.qmatmul.getAttr('external_codegen').info);
+    assert.strictEqual(kq.metadata.q8.activations, 'per_token');
+    assert.strictEqual(kd.metadata.q8.activations, undefined);
+    const ks = cg.compile(L.pf.quantize, hip.hipTarget(), L.pf.quantize.getAttr('external_codegen').info);
+    assert.strictEqual(ks.metadata.q8.activations, undefined);
+  });
+
   test('hipTarget builds on the reference factory when given one', () => {
     const seen = [];
     const t = hip.hipTarget((cfg) => { seen.push(cfg); return { kind: cfg.kind, made: true }; });
@@ -525,6 +549,140 @@ function gpuTests() {
       assert.strictEqual(hip.stats.uploadBytes, 4 * M * K + 4 * N, 'second run uploads only x and b');
     });
   }
+
+  // per-token / per-tensor dynamic activations (hipTarget q8 activations)
+  const S = (pf, ins, outs, target) => ({ name: pf.name, inputSlots: ins, outputSlots: outs, shapeValues: null,
+                                           kernel: (() => { provider.annotate([pf]);
+                                             return codegen.compile(pf, target || hip.hipTarget(), pf.getAttr('external_codegen').info); })() });
+  const mkSlot = (data, shape, dtype) => ({ data, shape, dtype });
+  function dynamicWant(L, x, b, mode) {
+    // the oracle of the dynamic form: S-token (or S-abs over the tensor), R1,
+    // quantized_dot, then fround(acc * fround(sx[m] * (sv[n] / s))) + bias, ReLU
+    const sx = new Float64Array(M);
+    if (mode === 'per_tensor') { const t = q8ref.scalesPerToken(x, 1, M * K, new Float64Array(1)); sx.fill(t[0]); }
+    else q8ref.scalesPerToken(x, M, K, sx);
+    const xq = new Int8Array(M * K); q8ref.buildQuantizeRows(M, K)(x, sx, xq);
+    const acc = new Int32Array(M * N); q8ref.buildQuantizedDot(M, N, K, 1, 0, 0)(xq, L.consts.W.data, acc);
+    const sv = L.consts.sv.data, y = new Float32Array(M * N);
+    for (let m = 0; m < M; m++) for (let n = 0; n < N; n++) {
+      const v = Math.fround(Math.fround((+acc[m * N + n]) * Math.fround(sx[m] * (sv[n] / L.sX))) + b[n]);
+      y[m * N + n] = Math.max(v, 0);
+    }
+    return y;
+  }
+  for (const mode of ['per_token', 'per_tensor']) {
+    test(`GPU: runPlan with ${mode} dynamic activations: one q8_qlinear_dynamic launch, bit for bit`, () => {
+      const L = linearSet();
+      const x = normal(31, M * K, 1.5), b = normal(32, N, 0.05);
+      for (let k = 0; k < K; k++) x[3 * K + k] = 0;            // a row of zeros: scale 1e-10
+      const tq = hip.hipTarget(null, null, { activations: mode });
+      const steps = [S(L.pf.quantize, [0], [2], tq), S(L.pf.qmatmul, [2], [3]), S(L.pf.fused, [3, 1], [4])];
+      const plan = makePlan(steps, [0, 1, 4], 5);
+      const out = new Float32Array(M * N);
+      const slots = [mkSlot(x, [M, K], 'f32'), mkSlot(b, [N], 'f32'), mkSlot(new Int8Array(M * K), [M, K], 'i8'),
+                     mkSlot(new Int32Array(M * N), [M, N], 'i32'), mkSlot(out, [M, N], 'f32')];
+      hip.resetStats();
+      let err = null;
+      be.runPlan(plan, slots, steps).catch((e) => { err = e; });
+      assert.strictEqual(err, null);
+      assert.strictEqual(hip.stats.launches, 1, 'one launch for the linear');
+      assert.strictEqual(hip.stats.dynamicLinears, 1);
+      sameBits(out, dynamicWant(L, x, b, mode), `${mode} dynamic linear`);
+      // the run-time option overrides the compiled mode, and 'static' is the reference's result
+      const stat = new Float32Array(M * N);
+      slots[4] = mkSlot(stat, [M, N], 'f32');
+      be.runPlan(plan, slots, steps, { q8Activations: 'static' }).catch((e) => { err = e; });
+      assert.strictEqual(err, null);
+      const h = {};
+      h.xq = new Int8Array(M * K); ref.compilePrimFunc(L.pf.quantize).fn(x, h.xq);
+      h.acc = new Int32Array(M * N); q8ref.buildQuantizedDot(M, N, K, 1, 0, 0)(h.xq, L.consts.W.data, h.acc);
+      h.y = new Float32Array(M * N); ref.compilePrimFunc(L.pf.fused).fn(h.acc, b, h.y, L.consts.sv.data, L.consts.zero.data);
+      sameBits(stat, h.y, 'static plan');
+    });
+  }
+
+  test('GPU: a dynamic scale equal to the static one gives the static result', () => {
+    const sX = 4.5 / 127;                    // 4.5 is a float: the per-tensor absmax below
+    const L = linearSet(sX);
+    const x = normal(33, M * K, 1.0), b = normal(34, N, 0.05);
+    for (let i = 0; i < x.length; i++) x[i] = Math.max(-4.25, Math.min(4.25, x[i]));
+    x[17] = -4.5;
+    const run = (target) => {
+      const steps = [S(L.pf.quantize, [0], [2], target), S(L.pf.qmatmul, [2], [3]), S(L.pf.fused, [3, 1], [4])];
+      const out = new Float32Array(M * N);
+      const slots = [mkSlot(x, [M, K], 'f32'), mkSlot(b, [N], 'f32'), mkSlot(new Int8Array(M * K), [M, K], 'i8'),
+                     mkSlot(new Int32Array(M * N), [M, N], 'i32'), mkSlot(out, [M, N], 'f32')];
+      let err = null;
+      be.runPlan(makePlan(steps, [0, 1, 4], 5), slots, steps).catch((e) => { err = e; });
+      assert.strictEqual(err, null);
+      return out;
+    };
+    hip.resetStats();
+    const dyn = run(hip.hipTarget(null, null, { activations: 'per_tensor' }));
+    assert.strictEqual(hip.stats.dynamicLinears, 1);
+    sameBits(dyn, run(hip.hipTarget()), 'per-tensor dynamic vs static');
+  });
+
+  test('GPU: three linears, each layer requantized in its GEMM epilogue: one launch per linear', () => {
+    // x -> quantize -> [qmatmul, fused relu+requant] -> [qmatmul, fused relu+requant] -> [qmatmul, tail]
+    // (every layer [N,K] = [K,K] so the layers chain), against the oracle run step by step
+    const Kx = K;
+    // layer i reads the previous layer's int8 codes: the quantize scale of
+    // layer i+1 is the sNext the fused requant of layer i writes with
+    const layers = [];
+    for (let i = 0; i < 3; i++) {
+      const xq = buf(`xq${i}`, [M, Kx], 'i8'), W = buf(`w${i}`, [Kx, Kx], 'i8'), acc = buf(`acc${i}`, [M, Kx], 'i32');
+      const sv = buf(`sv${i}`, [Kx], 'f32'), b = buf(`b${i}`, [Kx], 'f32'), zero = buf(`zero${i}`, [1, 1], 'f32');
+      const out = buf(`o${i}`, [M, Kx], i < 2 ? 'i8' : 'f32');
+      const sIn = i === 0 ? 4.9 / 127 : 0.0371 * (1 + i);
+      const sOut = 0.0371 * (2 + i);
+      const Wd = randI8(50 + i, Kx * Kx), svd = new Float32Array(Kx);
+      for (let n = 0; n < Kx; n++) svd[n] = Math.fround(sIn * (0.001 + 0.0002 * ((n * 31 + i) % 13)));
+      const cW = { buffer: W, data: Wd }, cS = { buffer: sv, data: svd }, cZ = { buffer: zero, data: new Float32Array([0]) };
+      const body = (l) => ext('max', [math('+', math('*', cast(l[0], 'i32', 'f32'), l[1]), l[2]), l[3]]);
+      layers.push({
+        qmm: qmatmulPF(M, Kx, Kx, xq, W, acc, [cW]),
+        epi: i < 2 ? pointwise(`fused_rq${i}`, out, [acc, sv, b, zero], (l) => quantizeExpr(body(l), sOut), [cS, cZ])
+                   : pointwise(`fused_tail${i}`, out, [acc, sv, b, zero], body, [cS, cZ]),
+        W: Wd, sv: svd, sOut,
+      });
+    }
+    const x0 = buf('x0', [M, Kx], 'f32'), q0 = buf('q0', [M, Kx], 'i8');
+    const quant0 = pointwise('quantize0', q0, [x0], (l) => quantizeExpr(l[0], 4.9 / 127));
+    const x = withEdges(normal(40, M * Kx, 1.5));
+    const bs = [normal(41, Kx, 0.05), normal(42, Kx, 0.05), normal(43, Kx, 0.05)];
+    // slots: 0 x, 1..3 biases, 4 q0, 5 acc0, 6 q1, 7 acc1, 8 q2, 9 acc2, 10 y
+    const steps = [S(quant0, [0], [4])];
+    for (let i = 0; i < 3; i++) {
+      steps.push(S(layers[i].qmm, [4 + 2 * i], [5 + 2 * i]));
+      steps.push(S(layers[i].epi, [5 + 2 * i, 1 + i], [i < 2 ? 6 + 2 * i : 10]));
+    }
+    const y = new Float32Array(M * Kx);
+    const slots = [mkSlot(x, [M, Kx], 'f32'), mkSlot(bs[0], [Kx], 'f32'), mkSlot(bs[1], [Kx], 'f32'), mkSlot(bs[2], [Kx], 'f32')];
+    for (let i = 0; i < 3; i++) {
+      slots.push(mkSlot(new Int8Array(M * Kx), [M, Kx], 'i8'));
+      slots.push(mkSlot(new Int32Array(M * Kx), [M, Kx], 'i32'));
+    }
+    slots.push(mkSlot(y, [M, Kx], 'f32'));
+    // oracle, step by step on the host
+    let cur = new Int8Array(M * Kx);
+    ref.compilePrimFunc(quant0).fn(x, cur);
+    let want = null;
+    for (let i = 0; i < 3; i++) {
+      const acc = new Int32Array(M * Kx);
+      q8ref.buildQuantizedDot(M, Kx, Kx, 1, 0, 0)(cur, layers[i].W, acc);
+      const o = i < 2 ? new Int8Array(M * Kx) : new Float32Array(M * Kx);
+      ref.compilePrimFunc(layers[i].epi).fn(acc, bs[i], o, layers[i].sv, new Float32Array([0]));  // params: acc, b, out, sv, zero
+      if (i < 2) cur = o; else want = o;
+    }
+    hip.resetStats();
+    let err = null;
+    be.runPlan(makePlan(steps, [0, 1, 2, 3, 10], 11), slots, steps).catch((e) => { err = e; });
+    assert.strictEqual(err, null);
+    sameBits(y, want, 'three-layer output');
+    assert.strictEqual(hip.stats.fusedLinears, 3);
+    assert.strictEqual(hip.stats.launches, 4, 'the input quantize + one GEMM per linear');
+  });
 
   test('GPU: runSync of the linear set step by step, weights resident after the first call', () => {
     const t = linearRun('unfused', true);

@@ -409,6 +409,19 @@ def test_js_quantize_matches(oracle, tmp_path, scale, zp, unsigned):
 
 
 @needs_node
+def test_js_scales_per_token_matches(oracle, tmp_path):
+    x = edge_floats(oracle, 64 * 128, seed=6).reshape(64, 128)
+    x[5] = 0.0                       # all zeros: 1e-10
+    x[6] = np.nan                    # no value ever compares: +-inf range, absmax inf
+    x[7, :64] = np.nan
+    x[9] = -0.0
+    (s,) = run_js(tmp_path, "scales_rows", {"M": 64, "K": 128}, [x], [(np.float64, (64,))])
+    same_bits(oracle.scales_per_token(x), s, "S-token")
+    (s0,) = run_js(tmp_path, "scales_rows", {"M": 3, "K": 0}, [np.zeros(0, np.float32)], [(np.float64, (3,))])
+    same_bits(oracle.scales_per_token(np.zeros((3, 0), np.float32)), s0, "S-token, empty rows")
+
+
+@needs_node
 def test_js_quantize_rows_matches(oracle, tmp_path):
     x = edge_floats(oracle, 64 * 128, seed=4).reshape(64, 128)
     x[5] = 0.0
