@@ -246,7 +246,7 @@ def bench_c5_gemv():
     return res
 
 
-def bench_c4():
+def bench_c4(fused_requant=True):
     import torch
     from mlfw_amd import configs as C
     inp = C.c4_inputs("cuda")
@@ -256,16 +256,16 @@ def bench_c4():
     from mlfw_amd import ops as O
     us, how = graph_time_us(lambda i: C.c4_step(X, P), 1, replays=5)
     ms = us / 1e3
-    # the same step with the O projection's per-token requant fused into its
-    # GEMM epilogue (no fp32 intermediate; one cooperative launch)
-    nb, fused = O.requant_dynamic_workspace(X.shape[0], *C.C4_SHAPES["o"])
-    ws = torch.empty(nb, dtype=torch.int8, device="cuda")
-    us_f, _ = graph_time_us(lambda i: C.c4_step(X, P, fused_requant=True, ws=ws), 1, replays=5)
-    return {"c4_projection_set": {"avg_ms": ms, "ops": C.C4_OPS,
-                                  "TOPS": C.C4_OPS / (ms * 1e-3) / 1e12,
-                                  "frac_mfma": C.C4_OPS / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
-                                  "timing": how,
-                                  "fused_o_requant_ms": us_f / 1e3, "fused_o_route": fused}}
+    res = {"avg_ms": ms, "ops": C.C4_OPS, "TOPS": C.C4_OPS / (ms * 1e-3) / 1e12,
+           "frac_mfma": C.C4_OPS / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, "timing": how}
+    if fused_requant:
+        # the same step with the O projection's per-token requant fused into
+        # its GEMM epilogue (no fp32 intermediate; one cooperative launch)
+        nb, fused = O.requant_dynamic_workspace(X.shape[0], *C.C4_SHAPES["o"])
+        ws = torch.empty(nb, dtype=torch.int8, device="cuda")
+        us_f, _ = graph_time_us(lambda i: C.c4_step(X, P, fused_requant=True, ws=ws), 1, replays=5)
+        res.update({"fused_o_requant_ms": us_f / 1e3, "fused_o_route": fused})
+    return {"c4_projection_set": res}
 
 
 # ---------------------------------------------------------------- ceilings
@@ -371,6 +371,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fused-requant", action="store_true",
+                    help="skip the C4 step with the O projection's requant fused (its cooperative "
+                         "launch makes rocprofv3's CSV writer crash at exit)")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the MFMA / streaming-read ceiling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -422,7 +425,8 @@ def main():
 
     secondary = {}
     if not args.no_secondary:
-        for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", bench_c4)):
+        c4 = lambda: bench_c4(fused_requant=not args.no_fused_requant)
+        for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", c4)):
             log(f"[bench] secondary {name}")
             try:
                 secondary.update(fn())
