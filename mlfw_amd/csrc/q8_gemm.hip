@@ -870,20 +870,29 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();
   }
-  // Tile choice: every tile of one launch runs concurrently when the grid
-  // fits the 256 CUs (one workgroup per CU), so the cost is
-  //   rounds = ceil(tiles / 256), times the time of one tile,
-  // where a tile's time is its area times a per-shape factor: smaller tiles
-  // move more bytes through LDS per MAC (measured ratios, C3/C4 shapes).
-  struct Cand { int bm, bn; double cost_per_area; };
-  const Cand cands[] = {{256, 256, 1.00}, {256, 128, 1.15}, {128, 128, 1.40}, {64, 64, 2.50}};
+  // Tile choice by a fill-aware cost of the launch's rounds.  A tile shape
+  // has `slots` workgroups resident at once (CUs x the workgroups per CU its
+  // LDS allows: 1 for 256x256 and 256x128, 2 for 128x128, 4 for 64x64);
+  // a round of it costs tmin + (tfull - tmin) * fill, fill = its tiles /
+  // slots (a partial round is cheaper but not free).  The constants are
+  // microseconds at K = 4096, fitted to measurements of every shape on
+  // M in 256..4096 x N in 2048..22016 (they pick the fastest tile on all 56);
+  // K scales every shape alike, so it does not enter the choice.  Two
+  // resident 128x128 workgroups per CU overlap one's epilogue with the
+  // other's main loop, which is why they win many mid-size shapes.
+  struct Cand { int bm, bn, per_cu; double tmin, tfull; };
+  const Cand cands[] = {{256, 256, 1, 44.0, 63.0}, {256, 128, 1, 27.5, 40.0},
+                        {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0}};
+  const int cus = cu_count() > 0 ? cu_count() : 256;
   int best = 0;
   double best_cost = 1e300;
   for (int c = 0; c < 4; ++c) {
     const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
-    const int64_t rounds = (tiles + 255) / 256;
-    const double cost = (double)rounds * cands[c].bm * cands[c].bn * cands[c].cost_per_area;
-    if (cost < best_cost * 0.999) { best_cost = cost; best = c; }
+    const int64_t slots = (int64_t)cus * cands[c].per_cu;
+    const int64_t full = tiles / slots, rest = tiles % slots;
+    double cost = (double)full * cands[c].tfull;
+    if (rest) cost += cands[c].tmin + (cands[c].tfull - cands[c].tmin) * (double)rest / (double)slots;
+    if (cost < best_cost * 0.995) { best_cost = cost; best = c; }   // near ties keep the larger tile
   }
   switch (best) {
     case 0: return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
