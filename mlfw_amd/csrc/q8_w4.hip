@@ -337,7 +337,7 @@ __device__ __forceinline__ v4i w4_transpose4(v4i v) {
   return v4i{(int)t01[0], (int)t01[1], (int)t23[0], (int)t23[1]};
 }
 
-template <int NW, int RS, bool TR, bool ONE>
+template <int NW, int RS, bool TR, bool ONE, bool XH>
 __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restrict__ xq,
                                                           const double* __restrict__ sx,
                                                           int sx_stride,
@@ -357,7 +357,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
   const int G = K / group, KB = K >> 1;
   const int SL = min(PS, group);                        // segment length (codes)
   const int nseg = NW * segw;                           // segments per round
-  const int win = nseg * NO + 2 * 16 * ng;              // ints per LDS window: sums, then the
+  const int ngp = ng | 1;                               // scale row pitch (doubles): odd, so
+                                                        // the 16 rows' reads hit distinct banks
+  const int win = nseg * NO + 2 * 16 * ngp;             // ints per LDS window: sums, then the
                                                         // scales of the <= ng groups that end
   const int RC = NW * PS;                               // codes per round
   const int rounds = (K + RC - 1) / RC;
@@ -367,7 +369,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
   const __amdgpu_buffer_rsrc_t rx = w4_rsrc(xq + (int64_t)t0 * K, (uint32_t)MB * (uint32_t)K);
   const __amdgpu_buffer_rsrc_t rs = w4_rsrc(sw + (int64_t)n0 * G, rows * (uint32_t)G * 8u);
   const uint32_t wrow = (uint32_t)r16 < rows ? (uint32_t)r16 : rows;    // past the end: zero
-  const uint32_t xtok = r16 < MB ? (uint32_t)r16 : (uint32_t)MB;
+  // XH (at most 8 tokens): lane (t, q) loads half t >> 3 of token t & 7's
+  // 32-byte chunk, and lanes t < 8 take the other half from lane t + 8 of
+  // their row; B's columns 8..15 then hold data of no token and their
+  // outputs are never stored
+  const int xr = XH ? (r16 & 7) : r16;
+  const uint32_t xtok = xr < MB ? (uint32_t)xr : (uint32_t)MB;
 
   // this lane's output
   const int o = tid, otok = o >> 4, orow = o & 15;
@@ -377,11 +384,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
   // scale slots u = tid + NT * u2 of a window: row u / ng, group u % ng
   constexpr int NSC = (16 * 64 + NT - 1) / NT;          // ng <= 64
   uint32_t sc_off[NSC];
-  int sc_g[NSC];
+  int sc_g[NSC], sc_w[NSC];
 #pragma unroll
   for (int u2 = 0; u2 < NSC; ++u2) {
     const int u = tid + NT * u2, rr = u / ng;
     sc_g[u2] = u < 16 * ng ? u - rr * ng : G;          // G: past the end
+    sc_w[u2] = rr * ngp + (u - rr * ng);                // LDS slot
     sc_off[u2] = (uint32_t)(rr < 16 ? rr : 16) * (uint32_t)G;
   }
 
@@ -408,8 +416,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
       const uint32_t wr = ok ? wrow : rows, xt = ok ? xtok : (uint32_t)MB;
       wv[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wr * (uint32_t)KB + kk / 2, 0, 0));
       const uint32_t xo = xt * (uint32_t)K + kk;
-      xv[s][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
-      xv[s][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0));
+      if constexpr (XH) {
+        xv[s][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16u * (uint32_t)(r16 >> 3), 0, 0));
+      } else {
+        xv[s][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
+        xv[s][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0));
+      }
     }
 #pragma unroll
     for (int u2 = 0; u2 < NSC; ++u2) {
@@ -421,8 +433,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
     // otherwise sink a step's loads into the branch that consumes them,
     // behind all the others, and wait for every load before the first MFMA
 #pragma unroll
-    for (int s = 0; s < RS; ++s) asm volatile("" ::"v"(wv[s]), "v"(xv[s][0]), "v"(xv[s][1]));
+    for (int s = 0; s < RS; ++s) {
+      if constexpr (XH) asm volatile("" ::"v"(wv[s]), "v"(xv[s][0]));
+      else asm volatile("" ::"v"(wv[s]), "v"(xv[s][0]), "v"(xv[s][1]));
+    }
     __builtin_amdgcn_sched_barrier(0);
+    auto x_second_half = [&](int s) {                  // XH: row rotate by 8 lanes
+      if constexpr (XH) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) xv[s][1][d] = __builtin_amdgcn_update_dpp(0, xv[s][0][d], 0x128, 0xF, 0xF, false);
+      }
+    };
 
     // MFMAs over the span's chunks; segment sums to LDS [segment][token][row]
     const int nch = max(0, min(PS, K - k0)) >> 5;       // chunks of this span inside K
@@ -438,6 +459,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
 #pragma unroll
       for (int s = 0; s < RS; ++s) {
         if (4 * s < nch) {                              // uniform
+          x_second_half(s);
           if (left == 0) {                              // a segment starts
             acc = v4i{0, 0, 0, 0};
             left = SL >> 7;
@@ -452,6 +474,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
 #pragma unroll
     for (int s = 0; s < RS; ++s) {
       if (4 * s < nch) {                                // uniform
+        x_second_half(s);
         const v4i wt = w4_transpose4(wv[s]);
         // chunk j's codes 8q..8q+7 = dwords 2q, 2q+1 of lane (t, j)'s 32 bytes
         const v4i xe = w4_transpose4(v4i{xv[s][0][0], xv[s][0][2], xv[s][1][0], xv[s][1][2]});
@@ -473,12 +496,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
     double* scw = reinterpret_cast<double*>(wbuf + nseg * NO);
 #pragma unroll
     for (int u2 = 0; u2 < NSC; ++u2)
-      if (tid + NT * u2 < 16 * ng) scw[tid + NT * u2] = scv[u2];
+      if (tid + NT * u2 < 16 * ng) scw[sc_w[u2]] = scv[u2];
     w4_lds_barrier();
 
     // lane o adds the round's groups in order
     if (out_lane) {
-      const double* sco = scw + orow * ng;
+      const double* sco = scw + orow * ngp;
       const int kr = NW * r * PS;                       // the round's first code
       if (group <= PS) {                                // uniform: every segment is a group
         const int nv = min(nseg, (K - kr) / group);
@@ -552,7 +575,7 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int n
   // when there is more than one round)
   auto lds_of = [&](int64_t PS, int64_t segw, int64_t ng) {
     const int64_t nwin = K > NW * PS ? 2 : 1;
-    return nwin * (NW * segw * NO + 2 * 16 * ng) * 4;
+    return nwin * (NW * segw * NO + 2 * 16 * (ng | 1)) * 4;
   };
   int64_t PS = 0;
   if (group <= span) {
@@ -669,21 +692,25 @@ hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, con
   // not apply), the MFMA kernel from three tokens on
   if (mfma && (!dot4 || M >= 3)) {
     const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16)), block(64 * mp.nw);
+#define Q8_W4M1(NW, RS, TR, ONE, XH)                                                              \
+  hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR, ONE, XH>), grid, block, mp.lds, st, xq, sx,      \
+                     sx_stride, wq4, sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw,      \
+                     mp.ng, bias, act, y)
 #define Q8_W4M(NW, RS, TR)                                                                        \
   do {                                                                                            \
-    if (mp.one)                                                                                   \
-      hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR, true>), grid, block, mp.lds, st, xq, sx,     \
-                         sx_stride, wq4, sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw,  \
-                         mp.ng, bias, act, y);                                                    \
-    else                                                                                          \
-      hipLaunchKernelGGL((k_gemv_w4_mfma<NW, RS, TR, false>), grid, block, mp.lds, st, xq, sx,    \
-                         sx_stride, wq4, sw, (int)M, (int)N, (int)K, (int)group, mp.PS, mp.segw,  \
-                         mp.ng, bias, act, y);                                                    \
+    if (mp.one) {                                                                                 \
+      if (M <= 8) Q8_W4M1(NW, RS, TR, true, true);                                                \
+      else Q8_W4M1(NW, RS, TR, true, false);                                                      \
+    } else {                                                                                      \
+      if (M <= 8) Q8_W4M1(NW, RS, TR, false, true);                                               \
+      else Q8_W4M1(NW, RS, TR, false, false);                                                     \
+    }                                                                                             \
   } while (0)
     if (mp.nw == 4) Q8_W4M(4, 8, false);
     else if (mp.tr) Q8_W4M(8, 4, true);
     else Q8_W4M(8, 4, false);
 #undef Q8_W4M
+#undef Q8_W4M1
     return hipGetLastError();
   }
   if (!dot4) {
