@@ -505,18 +505,21 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
       const int kr = NW * r * PS;                       // the round's first code
       if (group <= PS) {                                // uniform: every segment is a group
         const int nv = min(nseg, (K - kr) / group);
-        for (int i = 0; i < nv; i += 8) {
-          int a8[8];
-          double t8[8];
+        // 16 segments per batch: one LDS round trip per 16 products (the
+        // registers of the loads above are free by now; 32 per batch would
+        // raise the kernel's VGPR count and cost a workgroup per CU)
+        for (int i = 0; i < nv; i += 16) {
+          int a16[16];
+          double t16[16];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {                 // reads stay inside the window
+          for (int u = 0; u < 16; ++u) {                // reads stay inside the window
             const int iu = min(i + u, nseg - 1);
-            a8[u] = wbuf[iu * NO + o];
-            t8[u] = sco[iu];
+            a16[u] = wbuf[iu * NO + o];
+            t16[u] = sco[iu];
           }
 #pragma unroll
-          for (int u = 0; u < 8; ++u)
-            if (i + u < nv) S = S + (double)a8[u] * t8[u];
+          for (int u = 0; u < 16; ++u)
+            if (i + u < nv) S = S + (double)a16[u] * t16[u];
         }
       } else {                                          // a group spans P wave spans
         for (int w = 0; w < NW; ++w) {
