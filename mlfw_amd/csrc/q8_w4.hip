@@ -262,12 +262,12 @@ __global__ __launch_bounds__(256) void k_gemv_w4(const int8_t* __restrict__ xq,
         const double* t = t0 + tid;
         double S = -0.0;
         int g = 0;
-        for (; g + 8 <= G; g += 8) {
-          double v[8];
+        for (; g + 16 <= G; g += 16) {                  // 16 products per LDS round trip
+          double v[16];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = t[(g + j) * pitch];
+          for (int j = 0; j < 16; ++j) v[j] = t[(g + j) * pitch];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) S = S + v[j];
+          for (int j = 0; j < 16; ++j) S = S + v[j];
         }
         for (; g < G; ++g) S = S + t[g * pitch];
         float v = (float)(S * sxm);
