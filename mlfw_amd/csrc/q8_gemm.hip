@@ -1260,24 +1260,29 @@ void k_qlinear_dot4(const float* __restrict__ x, int M, int K, int per_tensor,
 // all the weight-row blocks it visits (grid-stride over blocks of 16 rows),
 // and the 4 partial 16x16 results meet in LDS (double-buffered: one
 // barrier per block).  Output element (row n0 + 4*(l/16) + r, token l%16)
-// is accumulator r of lane l.  At most 168 VGPRs (3 waves per SIMD), so
-// 3 workgroups per CU are resident and the C5 shapes run in one round.
-template <int KB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+// is accumulator r of lane l.  NW = 4: at most 168 VGPRs (3 waves per
+// SIMD), so 3 workgroups per CU are resident and the C5 shapes run in one
+// round.  NW = 16 (KB = 4): one 1024-lane workgroup per CU walks several
+// row blocks, each wave a sixteenth of K with 32 VGPRs of operands -- for
+// 16 tokens and more row blocks than two per CU, where it keeps more
+// loads in flight per CU than three 4-wave workgroups (N = 11008, M = 16:
+// 14.8 -> 13.3 us).
+template <int KB, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 3 : 4)))
 void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
                  GemmEpi e, void* __restrict__ out) {
-  __shared__ int red[2][4][256];
+  __shared__ int red[2][NW][256];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
   const int nblk = (N + 15) >> 4;
-  const int passes = (K + 256 * KB - 1) / (256 * KB);  // K bytes per pass: 4 waves x KB x 64
+  const int passes = (K + 64 * NW * KB - 1) / (64 * NW * KB);  // K bytes per pass: NW x KB x 64
   // Buffer loads: offsets past num_records return zeros.  Activation
   // chunks past K are masked explicitly (zeros); weight chunks past K then
   // only ever meet zero activations, so they need no mask.
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
   v4i xf[KB];
   auto load_x = [&](int pass) {
-    const int kw = pass * 256 * KB + wave * 64 * KB + 16 * g;
+    const int kw = pass * 64 * NW * KB + wave * 64 * KB + 16 * g;
     const uint32_t xrow = r16 < M ? (uint32_t)(r16 * K) : OOB;
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
@@ -1295,7 +1300,7 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
     v4i acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};     // two chains of dependent MFMAs
     for (int pass = 0; pass < passes; ++pass) {
       if (passes > 1) load_x(pass);
-      const uint32_t wo = (uint32_t)(r16 * K + pass * 256 * KB + wave * 64 * KB + 16 * g);
+      const uint32_t wo = (uint32_t)(r16 * K + pass * 64 * NW * KB + wave * 64 * KB + 16 * g);
       v4i w[KB];
 #pragma unroll
       for (int j = 0; j < KB; ++j)
@@ -1314,10 +1319,11 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
     for (int r = 0; r < 4; ++r) red[rb][wave][r16 * 16 + 4 * g + r] = acc[r];
     __syncthreads();
     const int t = tid >> 4, i = tid & 15, n = n0 + i;
-    if (t < M && n < N) {
-      const int s = (int)((uint32_t)red[rb][0][tid] + (uint32_t)red[rb][1][tid] +
-                          (uint32_t)red[rb][2][tid] + (uint32_t)red[rb][3][tid]);
-      store_out(out, (int64_t)t * N + n, s, t, n, e);
+    if (tid < 256 && t < M && n < N) {
+      uint32_t su = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) su += (uint32_t)red[rb][w][tid];
+      store_out(out, (int64_t)t * N + n, (int)su, t, n, e);
     }
   }
 }
@@ -1339,14 +1345,20 @@ static hipError_t launch_gemv_mfma(const int8_t* A, const int8_t* B, int M, int 
   // every workgroup resident at once (3 per CU): weight loads of all row
   // blocks are in flight together
   const int nblk = (N + 15) / 16;
+  if (M > 8 && K >= 4096 && nblk > 2 * cu_count()) {
+    const int cap = cu_count();
+    hipLaunchKernelGGL((k_gemv_mfma<4, 16>), dim3((unsigned)(nblk < cap ? nblk : cap)), dim3(1024), 0,
+                       st, A, B, M, N, K, e, out);
+    return hipGetLastError();
+  }
   const int cap = 3 * cu_count();
   const dim3 grid((unsigned)(nblk < cap ? nblk : cap)), block(256);
   if (K <= 1024)
-    hipLaunchKernelGGL((k_gemv_mfma<4>), grid, block, 0, st, A, B, M, N, K, e, out);
+    hipLaunchKernelGGL((k_gemv_mfma<4, 4>), grid, block, 0, st, A, B, M, N, K, e, out);
   else if (K <= 2048)
-    hipLaunchKernelGGL((k_gemv_mfma<8>), grid, block, 0, st, A, B, M, N, K, e, out);
+    hipLaunchKernelGGL((k_gemv_mfma<8, 4>), grid, block, 0, st, A, B, M, N, K, e, out);
   else
-    hipLaunchKernelGGL((k_gemv_mfma<16>), grid, block, 0, st, A, B, M, N, K, e, out);
+    hipLaunchKernelGGL((k_gemv_mfma<16, 4>), grid, block, 0, st, A, B, M, N, K, e, out);
   return hipGetLastError();
 }
 

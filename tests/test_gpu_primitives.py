@@ -489,6 +489,26 @@ def test_gemv(ops, oracle, M, N, K):
     same_bits(host(acc_gpu), acc)
 
 
+@pytest.mark.parametrize("M", [9, 16])
+def test_gemv_sixteen_wave_route(ops, oracle, M):
+    """More row blocks than two per CU and more than 8 tokens: one 16-wave
+    workgroup per CU walks the row blocks; N not a multiple of 16, K = 11008
+    in three passes of 4096 (the last one partial), bias and SiLU."""
+    N, K = 9001, 11008
+    rng = oracle.Rng(M * 7 + 11)
+    x = rng.normal((M, K))
+    W = rng.normal((N, K), 0.0, 0.02)
+    bias = rng.uniform((N,), -0.1, 0.1)
+    sx = oracle.scales_per_token(x)
+    xq = oracle.quantize_rows(x, sx)
+    sw = oracle.scales_per_channel(W, 0)
+    Wq = oracle.weight_quantize_per_channel(W, 0, sw)
+    acc = oracle.quantized_dot(xq, Wq, b_layout=1)
+    y = ops.qlinear(dev(xq), dev(sx), dev(Wq), dev(sw), bias=dev(bias), act="silu")
+    same_bits(host(y), oracle.epilogue(acc, "rowcol", sx, sw, bias=bias, act="silu"))
+    same_bits(host(ops.quantized_dot(dev(xq), dev(Wq))), acc)
+
+
 # ------------------------------------------------------------------ fused / inputs
 @pytest.mark.parametrize("M,K", [(4, 11008), (3, 1000), (2, 64), (2, 8192), (3, 6000), (2, 12288)])
 def test_silu_mul_quantize(ops, oracle, M, K):
