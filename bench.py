@@ -298,10 +298,17 @@ def ceilings():
                                ("read", "quantize_16384x4096", 335675392),
                                ("write", "dequantize_out_16384x4096", 268435456)):
         bufs = max(5, math.ceil((1 << 30) / nbytes))
-        if lib.q8c_stream(nbytes, bufs, 5, 1 if kind == "write" else 0, C.byref(us)) == 0:
-            gbs = nbytes / (us.value * 1e-6) / 1e9
-            out[f"{kind}_{name}"] = {"bytes": nbytes, "avg_us": us.value, "GB/s": gbs,
-                                     "frac_of_peak": gbs / PEAK_HBM_GBS}
+        # best of three timed batches: a ceiling is the fastest the box
+        # reaches, and one batch now and then runs several times slower
+        best = None
+        for _ in range(3):
+            if lib.q8c_stream(nbytes, bufs, 5, 1 if kind == "write" else 0, C.byref(us)) == 0:
+                best = us.value if best is None else min(best, us.value)
+        if best is not None:
+            gbs = nbytes / (best * 1e-6) / 1e9
+            out[f"{kind}_{name}"] = {"bytes": nbytes, "avg_us": best, "GB/s": gbs,
+                                     "frac_of_peak": gbs / PEAK_HBM_GBS,
+                                     "of": "best of 3 batches of 5 graph replays"}
     return out
 
 

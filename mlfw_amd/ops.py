@@ -309,7 +309,8 @@ def qlinear_dynamic(x: torch.Tensor, Wq: torch.Tensor, sW: torch.Tensor,
     """Dynamic int8 linear in one call: quantize x (fp32 [M,K]) per token (or
     per tensor), then the int8 GEMM with the qlinear epilogue.  Equal bit
     for bit to quantize_per_token / quantize_per_tensor followed by qlinear;
-    decode shapes (M <= 4, K <= 4096) run as one kernel.
+    one-token decode (M = 1, K <= 4096) runs as one kernel, larger M as the
+    quantize and the GEMM / GEMV back to back.
     Returns (y fp32 [M,N], int8 codes [M,K], f64 scales [M] or [1])."""
     _need(x, torch.float32, "x")
     M, K = _rows(x)
