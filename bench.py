@@ -141,17 +141,32 @@ def bench_c3(steps, warmup):
 
 
 # ---------------------------------------------------------------- secondary
+_CAPTURE = []
+
+
+def _capture_stream():
+    """One side stream for every graph capture of the run."""
+    import torch
+    if not _CAPTURE:
+        _CAPTURE.append(torch.cuda.Stream())
+    return _CAPTURE[0]
+
+
 def graph_time_us(body, copies, replays=5):
     """Average microseconds per launch of body(i), i < copies, captured in one
     HIP graph and replayed `replays` times between two events.  Falls back
     to eager launches if capture is not possible."""
     import torch
     try:
-        for i in range(copies):        # warm up outside the capture
-            body(i)
+        # warm up on the stream the graph is captured on: per-stream state
+        # (the GEMM's stream-K workspace) is made there, outside the capture
+        s = _capture_stream()
+        with torch.cuda.stream(s):
+            for i in range(copies):
+                body(i)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=s):
             for i in range(copies):
                 body(i)
         g.replay()
