@@ -511,3 +511,32 @@ def test_gemv_w4_matches_independent_evaluation(oracle):
                     S = S + float(parts[m, n, gi]) * sw[n * G + gi]
                 want[m, n] = np.float32(S * sx[m])
         same_bits(got, want)
+
+
+# The oracle's SiLU (glibc exp) against V8's on whole chunks of 2^24 inputs:
+# the chunks where 1 / (1 + exp(-x)) is neither 0, 1/2 nor 1 in f32 (|x|
+# from ~1e-4 to ~100, both signs), the zero / subnormal chunks and the
+# chunks holding the infinities and NaNs.  The hashes are those of
+# tests/golden/silu_v8_hashes.json (see silu_v8_hashes.js).
+SILU_CHUNKS = [0, 1] + list(range(56, 68)) + [127, 128, 129] + list(range(184, 196)) + [255]
+
+
+def test_oracle_silu_equals_v8_on_whole_chunks(oracle):
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "silu_v8_hashes.json")) as f:
+        golden = json.load(f)["hashes"]
+    n = 1 << 24
+    w = 2 * np.arange(n, dtype=np.uint64) + 1
+    ones = np.ones(n, np.float32)
+    for c in SILU_CHUNKS:
+        x = (np.arange(n, dtype=np.uint64) + np.uint64(c * n)).astype(np.uint32).view(np.float32)
+        h = oracle.silu_mul(x, ones)
+        v = h.view(np.uint32).astype(np.uint64)
+        v[np.isnan(h)] = 0x7FC00000
+        v ^= v >> np.uint64(16)
+        v = (v * np.uint64(0x7FEB352D)) & np.uint64(0xFFFFFFFF)
+        v ^= v >> np.uint64(15)
+        s1 = int(((v * w) & np.uint64(0xFFFFFFFF)).sum()) & 0xFFFFFFFF
+        s2 = int(v.sum()) & 0xFFFFFFFF
+        assert [s1, s2] == golden[c], f"chunk {c}"
