@@ -37,6 +37,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+/* The declarations below are the library's whole export list (it is built
+ * with hidden visibility by default). */
+#pragma GCC visibility push(default)
 
 #define Q8HIP_VERSION 1
 
@@ -568,6 +571,7 @@ int q8_hist_entropy(const double* summary, const double* bins, int num_quant_bin
 int q8_calib_params(const double* summary, const double* bins, int mode, int scheme,
                     int unsigned_, double* scale, double* zero_point, int* has_params);
 
+#pragma GCC visibility pop
 #ifdef __cplusplus
 }
 #endif

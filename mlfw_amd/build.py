@@ -39,6 +39,14 @@ HIP_FLAGS = [
     "-ffp-contract=off",
     "-fno-fast-math",
     "-fno-gpu-rdc",
+    # only the C ABI is exported (q8hip.h marks it visible): the kernels'
+    # host stubs and every C++ symbol stay inside the library, so another
+    # library with a same-named template instantiation can neither take
+    # over nor be taken over by these launches when loaded RTLD_GLOBAL
+    "-fvisibility=hidden",
+    # and the library's own references (kernel handles included) bind to its
+    # own definitions, whatever was loaded before it
+    "-Wl,-Bsymbolic",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-command-line-argument",
@@ -67,7 +75,7 @@ def build_hip(verbose: bool = False) -> str:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(compile_one, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -115,6 +115,7 @@ extern "C" {
 // *mhz = shader clock over block 0's run of the last launch, *loop_cycles =
 // that run's shader cycles (2048 MFMAs x 32 cycles = 65,536 when the MFMA
 // pipe never idles).
+__attribute__((visibility("default")))
 int q8c_mfma(int iters_per_wave, int reps, double* us, double* mhz, double* loop_cycles) {
   const int blocks = 256;
   if (iters_per_wave < 1 || reps < 1 || !us || !mhz) return 1;
@@ -154,6 +155,7 @@ int q8c_mfma(int iters_per_wave, int reps, double* us, double* mhz, double* loop
 // Streaming-read (write = 0) or streaming-write (write = 1) floor: a graph
 // of `buffers` launches, each on its own buffer of `bytes`, replayed `reps`
 // times; *us = average per launch.
+__attribute__((visibility("default")))
 int q8c_stream(size_t bytes, int buffers, int reps, int write, double* us) {
   if (bytes < 16 || buffers < 1 || reps < 1 || !us) return 1;
   std::vector<v4i*> bufs(buffers, nullptr);
