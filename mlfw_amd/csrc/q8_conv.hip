@@ -9,13 +9,18 @@
 //
 // Two paths, both exact:
 //   * implicit-GEMM form for contractions of 64 or more (Cg * prod(K)):
-//     per image and group, an im2col pass writes the [P, Kc16] int8 matrix
-//     of that group's receptive fields (contraction padded with zeros to a
-//     multiple of 16) into the caller's workspace, and the int8 MFMA GEMM
-//     computes out[n, g*Og : (g+1)*Og, :] = W_g [Og, Kc16] x col^T -- the
-//     weight is the A operand, so the [Og, P] result is already the
-//     NC(spatial) output block and the dequant epilogue is fused as in
-//     q8_gemm.  An OI(spatial) weight is [O, Kc] row-major, i.e. the GEMM's
+//     an im2col pass writes the [P, Kc16] int8 matrix of a group's receptive
+//     fields (contraction padded with zeros to a multiple of 16) into the
+//     caller's workspace, and the int8 MFMA GEMM computes
+//     out[n, g*Og : (g+1)*Og, :] = W_g [Og, Kc16] x col^T -- the weight is
+//     the A operand, so the [Og, P] result is already the NC(spatial)
+//     output block and the dequant epilogue is fused as in q8_gemm.  With
+//     more than 16 output channels per group the images go in batches: one
+//     im2col launch fills [nb * P, Kc16] and one GEMM computes [Og, nb * P],
+//     its epilogue storing column n * P + p of the product at image n,
+//     position p (column-blocked output), so a batch of images is one
+//     launch of a GEMM large enough to fill the chip instead of nb small
+//     ones.  An OI(spatial) weight is [O, Kc] row-major, i.e. the GEMM's
 //     A layout; it is copied to a 16-byte-aligned row pitch only when Kc is
 //     not a multiple of 16.
 //   * a direct kernel (one thread per output element) for short
@@ -32,7 +37,10 @@ namespace q8 {
 // position p, contraction indices 16c .. 16c+15 (ic-major, then kernel
 // positions in row-major order -- the OI(spatial) weight's own order).
 __global__ __launch_bounds__(256) void k_im2col(const int8_t* __restrict__ x, ConvGeom G,
-                                                int64_t n, int64_t g, int8_t* __restrict__ col) {
+                                                int64_t n0, int64_t g, int8_t* __restrict__ col) {
+  // blockIdx.y: image n0 + y of a batch, written at matrix rows y * P ..
+  const int64_t n = n0 + blockIdx.y;
+  col += (int64_t)blockIdx.y * G.Pn * G.Kc16;
   const int64_t nch = G.Kc16 >> 4;
   const int64_t idx = blockIdx.x * 256LL + threadIdx.x;
   if (idx >= G.Pn * nch) return;
@@ -140,9 +148,24 @@ bool conv_direct(const ConvGeom& G) {
   return !conv_uses_gemm(G) || G.zpx != 0 || G.zpw != 0 || G.x_u8 || G.w_u8;
 }
 
+// Images per im2col batch: all of them, up to CONV_BATCH_BYTES of im2col
+// matrix; 1 with 16 or fewer output channels per group, which go through
+// the GEMV kernel one image at a time.
+constexpr size_t CONV_BATCH_BYTES = (size_t)128 << 20;
+static int64_t conv_batch(const ConvGeom& G) {
+  if (G.Og <= 16) return 1;
+  const size_t per = (size_t)G.Pn * (size_t)G.Kc16;
+  int64_t nb = per ? (int64_t)(CONV_BATCH_BYTES / per) : 1;
+  nb = nb > G.N ? G.N : nb;
+  nb = nb > 65535 ? 65535 : nb;                                 // grid.y of the im2col launch
+  const int64_t cap = ((int64_t)1 << 31) / (G.Pn > 0 ? G.Pn : 1) - 1;   // GEMM N = nb * P in an int
+  nb = nb > cap ? cap : nb;
+  return nb < 1 ? 1 : nb;
+}
+
 size_t conv_workspace_bytes(const ConvGeom& G) {
   if (!conv_uses_gemm(G)) return 0;
-  size_t b = (size_t)G.Pn * (size_t)G.Kc16;              // one im2col matrix
+  size_t b = (size_t)conv_batch(G) * (size_t)G.Pn * (size_t)G.Kc16;   // im2col matrices
   b = (b + 255) & ~(size_t)255;
   if (G.Kc16 != G.Kc) b += (size_t)G.O * (size_t)G.Kc16;  // padded weight rows
   return b;
@@ -158,7 +181,8 @@ hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, cons
     return hipGetLastError();
   }
   int8_t* col = static_cast<int8_t*>(workspace);
-  const size_t col_bytes = ((size_t)G.Pn * (size_t)G.Kc16 + 255) & ~(size_t)255;
+  const int64_t NB = conv_batch(G);
+  const size_t col_bytes = ((size_t)NB * (size_t)G.Pn * (size_t)G.Kc16 + 255) & ~(size_t)255;
   const int8_t* wmat = w;
   if (G.Kc16 != G.Kc) {
     int8_t* wp = col + col_bytes;
@@ -171,6 +195,29 @@ hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, cons
   }
   const int64_t cells = G.Pn * (G.Kc16 >> 4);
   const size_t osz = e.out_i32 ? sizeof(int32_t) : sizeof(float);
+  // batched form: the GEMM's MFMA path needs 16-byte-aligned operands (the
+  // weight rows and the workspace); otherwise one image at a time
+  const bool aligned = ((reinterpret_cast<uintptr_t>(wmat) | reinterpret_cast<uintptr_t>(col)) & 15) == 0;
+  if (NB > 1 && aligned && (int64_t)G.Kc16 * 256 < ((int64_t)1 << 31)) {
+    GemmEpi eb = e;
+    eb.col_blk = G.Pn;
+    eb.blk_stride = G.O * G.Pn;
+    eb.ld_out = G.Pn;
+    for (int64_t n0 = 0; n0 < G.N; n0 += NB) {
+      const int64_t nb = G.N - n0 < NB ? G.N - n0 : NB;
+      for (int64_t g = 0; g < G.groups; ++g) {
+        hipLaunchKernelGGL(k_im2col, dim3((unsigned)((cells + 255) / 256), (unsigned)nb), dim3(256), 0, st,
+                           x, G, n0, g, col);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        const int8_t* A = wmat + g * G.Og * G.Kc16;
+        void* o = static_cast<char*>(out) + (size_t)((n0 * G.O + g * G.Og) * G.Pn) * osz;
+        err = launch_gemm(A, col, G.Og, nb * G.Pn, G.Kc16, eb, o, st);
+        if (err != hipSuccess) return err;
+      }
+    }
+    return hipSuccess;
+  }
   for (int64_t n = 0; n < G.N; ++n)
     for (int64_t g = 0; g < G.groups; ++g) {
       hipLaunchKernelGGL(k_im2col, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, st, x, G,

@@ -96,6 +96,7 @@ __device__ __forceinline__ int requant(float y, const GemmEpi& e) {
 // Final store of one output element of the GEMV / generic kernels.
 __device__ __forceinline__ void store_out(void* out, int64_t idx, int acc, int64_t m, int64_t n,
                                           const GemmEpi& e) {
+  if (e.col_blk > 0) idx = (n / e.col_blk) * e.blk_stride + m * e.ld_out + n % e.col_blk;
   if (e.out_i32) static_cast<int32_t*>(out)[idx] = acc;
   else if (e.out_q8) static_cast<int8_t*>(out)[idx] = (int8_t)requant(epi_value(acc, m, n, e), e);
   else static_cast<float*>(out)[idx] = epi_value(acc, m, n, e);
@@ -237,6 +238,7 @@ struct Epi {
   static constexpr bool OUT_I32 = (EPI & 16) != 0;
   static constexpr bool OUT_Q8 = (EPI & 32) != 0;
   static constexpr bool OUT_DQ = (EPI & 64) != 0;
+  static constexpr bool COLBLK = (EPI & 128) != 0;   // GemmEpi::col_blk addressing
   static constexpr int MODE = (EPI >> 3) & 1;
   static constexpr bool BIAS = (EPI & 4) != 0;
   static constexpr int ACT = EPI & 3;
@@ -244,9 +246,10 @@ struct Epi {
 
 inline int epi_code(const GemmEpi& e) {
   if (e.out_dq) return 64 | (e.mode << 3);
-  if (e.out_i32) return 16;
+  const int cb = e.col_blk > 0 ? 128 : 0;
+  if (e.out_i32) return 16 | cb;
   if (e.out_q8) return 32 | (e.mode << 3);
-  return (e.mode << 3) | (e.bias ? 4 : 0) | e.act;
+  return (e.mode << 3) | (e.bias ? 4 : 0) | e.act | cb;
 }
 
 template <int BM, int BN, int EPI>
@@ -454,8 +457,14 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   int32_t* strip = reinterpret_cast<int32_t*>(lds) + wave * 32 * PITCH;
   const int qcol = 4 * (lane % LPR), qrow = lane / LPR;
   const int gcol = n0 + wn + qcol;
+  // COLBLK: 16-byte quads need column blocks, and so the rows of every
+  // block, that start on multiples of 4 elements
   const bool interior = m0 + BM <= M && n0 + BN <= N && (N % 4 == 0) &&
-                        (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+                        (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                        (!P::COLBLK || ((e.col_blk | e.blk_stride | e.ld_out) & 3) == 0);
+  // COLBLK: the column part of this lane's output offset (fixed for the lane)
+  const int64_t colblk_base =
+      P::COLBLK ? ((int64_t)gcol / e.col_blk) * e.blk_stride + (int64_t)gcol % e.col_blk : 0;
   double sbj[C::TN];
   float bj[C::TN];
 #pragma unroll
@@ -555,7 +564,9 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
 #pragma unroll
       for (int it = 0; it < NQ; ++it) {
         const int64_t row = m0 + wm + 32 * i + it * RPI + qrow;
-        __builtin_nontemporal_store(q[it], reinterpret_cast<v4i*>(o + row * N + gcol));
+        // COLBLK: a quad never straddles two column blocks (col_blk % 4 == 0)
+        const int64_t at = P::COLBLK ? colblk_base + row * e.ld_out : row * N + gcol;
+        __builtin_nontemporal_store(q[it], reinterpret_cast<v4i*>(o + at));
       }
     } else {
 #pragma unroll
@@ -564,7 +575,15 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
         if (row < M) {
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            if (gcol + c < N) o[(int64_t)row * N + gcol + c] = q[it][c];
+            if (gcol + c < N) {
+              int64_t at = (int64_t)row * N + gcol + c;
+              if constexpr (P::COLBLK) {   // N < 2^31: 32-bit division
+                const unsigned j = (unsigned)(gcol + c), cb = (unsigned)e.col_blk;
+                const unsigned blk = j / cb;
+                at = (int64_t)blk * e.blk_stride + (int64_t)row * e.ld_out + (j - blk * cb);
+              }
+              o[at] = q[it][c];
+            }
         }
       }
     }
@@ -831,7 +850,7 @@ __global__ __launch_bounds__(256) void k_gemm_i8_generic(const int8_t* __restric
 }
 
 #define Q8_EPI_CODES(X) \
-  X(16) X(0) X(1) X(2) X(4) X(5) X(6) X(8) X(9) X(10) X(12) X(13) X(14) X(32) X(40)
+  X(16) X(0) X(1) X(2) X(4) X(5) X(6) X(8) X(9) X(10) X(12) X(13) X(14) X(32) X(40) X(128) X(144)
 
 template <int BM, int BN>
 static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int N, int K,

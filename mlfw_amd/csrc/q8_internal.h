@@ -38,6 +38,13 @@ struct GemmEpi {
   double* q_scales;     // [M] row scales, written by the tiles of column 0
   int nwg;              // workgroups of the launch
   int spin_limit;       // bound of the wait (polls)
+  // column-blocked output (quantized_conv over a batch of images): GEMM
+  // column j is position j % col_blk of image j / col_blk, and element
+  // (row, j) is stored at (j / col_blk) * blk_stride + row * ld_out +
+  // j % col_blk.  col_blk = 0: plain row-major [M, N].
+  int64_t col_blk;
+  int64_t blk_stride;
+  int64_t ld_out;
 };
 
 hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,

@@ -5,7 +5,10 @@ The cases cover both device paths (direct kernel for contractions shorter
 than 64, im2col + MFMA GEMM otherwise, with and without a contraction that
 is a multiple of 16), the GEMV and the GEMM kernels behind the latter
 (<= 16 and > 16 output channels per group), groups / depthwise, strides,
-asymmetric padding, dilation, batch > 1 and spatial ranks 1 to 3; zero
+asymmetric padding, dilation, batch > 1 (batches of images in one GEMM
+whose epilogue scatters columns to images, with 16-byte and with
+per-element stores; one image at a time for the GEMV) and spatial ranks
+1 to 3; zero
 points and ui8 operands; then the whole pipeline QuantizationPass builds
 for a conv (quantize input, quantize kernel, quantized_conv, dequantize).
 """
@@ -62,6 +65,12 @@ CASES = [
     ((3, 16, 7, 9), (8, 16, 2, 3), [1, 1], [[1, 0], [0, 0]], [2, 1], 1),     # GEMV (Og 8), Kc 96
     ((1, 8, 6, 5, 7), (24, 8, 2, 3, 2), [1, 2, 1], [[1, 0], [0, 1], [1, 1]], [1, 1, 2], 1),  # 3-D
     ((1, 256, 14, 14), (300, 256, 1, 1), [1, 1], [[0, 0], [0, 0]], [1, 1], 1),  # 1x1, tile edges
+    # batched im2col + column-blocked GEMM (N > 1, Og > 16)
+    ((3, 20, 12, 12), (48, 10, 3, 3), [1, 1], [[1, 1], [1, 1]], [1, 1], 2),  # groups, Kc 90 -> 96
+    ((5, 256, 14, 14), (300, 256, 1, 1), [1, 1], [[0, 0], [0, 0]], [1, 1], 1),  # P 196, edges
+    ((4, 32, 6, 10), (40, 32, 3, 3), [1, 1], [[1, 1], [1, 1]], [1, 1], 1),   # P 60, tile straddles
+    ((2, 64, 11, 11), (32, 64, 3, 3), [1, 1], [[0, 0], [0, 0]], [1, 1], 1),  # P 81: element stores
+    ((3, 512, 7, 7), (64, 512, 3, 3), [1, 1], [[1, 1], [1, 1]], [1, 1], 1),  # P 49, Kc 4608
 ]
 
 
@@ -76,7 +85,7 @@ def test_quantized_conv_int32(ops, oracle, case):
     same_bits(host(got), oracle.quantized_conv(x, w, st, pd, dl, g))
 
 
-@pytest.mark.parametrize("case", CASES[:2] + CASES[4:6])
+@pytest.mark.parametrize("case", CASES[:2] + CASES[4:6] + CASES[9:14])
 def test_quantized_conv_dequant_epilogue(ops, oracle, case):
     xs, ws, st, pd, dl, g = case
     rng = np.random.default_rng(sum(ws))
