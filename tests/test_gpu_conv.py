@@ -7,8 +7,10 @@ is a multiple of 16), the GEMV and the GEMM kernels behind the latter
 (<= 16 and > 16 output channels per group), groups / depthwise, strides,
 asymmetric padding, dilation, batch > 1 (batches of images in one GEMM
 whose epilogue scatters columns to images, with 16-byte and with
-per-element stores; one image at a time for the GEMV) and spatial ranks
-1 to 3; zero
+per-element stores; one image at a time for the GEMV), spatial ranks 1 to
+3, and both im2col forms: the byte gather (channels per group not a
+multiple of 16) and the channel-last frame with a tap-major contraction,
+including 1 x 1 kernels whose frame is the GEMM operand itself; zero
 points and ui8 operands; then the whole pipeline QuantizationPass builds
 for a conv (quantize input, quantize kernel, quantized_conv, dequantize).
 """
@@ -71,6 +73,11 @@ CASES = [
     ((4, 32, 6, 10), (40, 32, 3, 3), [1, 1], [[1, 1], [1, 1]], [1, 1], 1),   # P 60, tile straddles
     ((2, 64, 11, 11), (32, 64, 3, 3), [1, 1], [[0, 0], [0, 0]], [1, 1], 1),  # P 81: element stores
     ((3, 512, 7, 7), (64, 512, 3, 3), [1, 1], [[1, 1], [1, 1]], [1, 1], 1),  # P 49, Kc 4608
+    # channel-last frame (Cg % 16 == 0) beyond the cases above
+    ((2, 32, 9, 11), (48, 16, 3, 2), [2, 1], [[1, 2], [0, 1]], [1, 2], 2),   # groups, stride, dilation
+    ((2, 16, 5, 6, 7), (32, 16, 2, 3, 2), [1, 2, 1], [[1, 0], [0, 1], [1, 1]], [1, 1, 2], 1),  # 3-D
+    ((3, 64, 9, 9), (40, 64, 1, 1), [2, 2], [[0, 0], [0, 0]], [1, 1], 1),    # 1x1 at stride 2
+    ((2, 48, 6, 6), (24, 48, 1, 1), [1, 1], [[1, 1], [0, 2]], [1, 1], 1),    # 1x1 padded: frame is B
 ]
 
 
@@ -85,7 +92,7 @@ def test_quantized_conv_int32(ops, oracle, case):
     same_bits(host(got), oracle.quantized_conv(x, w, st, pd, dl, g))
 
 
-@pytest.mark.parametrize("case", CASES[:2] + CASES[4:6] + CASES[9:14])
+@pytest.mark.parametrize("case", CASES[:2] + CASES[4:6] + CASES[9:])
 def test_quantized_conv_dequant_epilogue(ops, oracle, case):
     xs, ws, st, pd, dl, g = case
     rng = np.random.default_rng(sum(ws))
