@@ -399,7 +399,15 @@ static bool conv_pointwise(const ConvGeom& G) {
   return G.Kn == 1 && G.st[0] == 1 && G.st[1] == 1 && G.st[2] == 1;
 }
 
-// channel-last workspace: [col: nb * Pn * Kc, unless pointwise] [frame:
+// Implicit GEMM (launch_gemm_conv: the GEMM reads the frame itself, no
+// im2col matrix): channels per group a multiple of 64, a contraction of at
+// most 16384, more than 16 output channels per group (the GEMM, not the
+// GEMV); a pointwise conv needs no im2col in any case.
+static bool conv_implicit(const ConvGeom& G) {
+  return !conv_pointwise(G) && G.Cg % 64 == 0 && G.Kc <= 16384 && G.Og > 16;
+}
+
+// channel-last workspace: [col: nb * Pn * Kc, unless pointwise or implicit] [frame:
 // nb * Ep * Cg] [tap-major weight: O * Kc, unless 1 x 1], each rounded up
 // to 256 bytes
 struct ClLayout {
@@ -407,8 +415,8 @@ struct ClLayout {
   size_t col, frame, wt;
 };
 static ClLayout cl_layout(const ConvGeom& G, const ConvFrame& F) {
-  const bool pw = conv_pointwise(G);
-  const size_t col1 = pw ? 0 : (size_t)G.Pn * (size_t)G.Kc;
+  const bool no_col = conv_pointwise(G) || conv_implicit(G);
+  const size_t col1 = no_col ? 0 : (size_t)G.Pn * (size_t)G.Kc;
   const size_t fr1 = (size_t)F.Ep * (size_t)G.Cg;
   ClLayout L;
   L.nb = conv_batch_of(G, col1 + fr1);
@@ -464,6 +472,26 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
   eb.col_blk = G.Pn;
   eb.blk_stride = G.O * G.Pn;
   eb.ld_out = G.Pn;
+  const bool impl = conv_implicit(G);
+  if (impl) {
+    GemmEpi::ConvB& c = eb.cb;
+    c.Pn = (uint32_t)G.Pn;
+    c.P1 = (uint32_t)G.P[1];
+    c.P2 = (uint32_t)G.P[2];
+    c.st0 = (uint32_t)G.st[0];
+    c.st1 = (uint32_t)G.st[1];
+    c.st2 = (uint32_t)G.st[2];
+    c.E1 = (uint32_t)F.E[1];
+    c.E2 = (uint32_t)F.E[2];
+    c.Ep = (uint32_t)F.Ep;
+    c.Cg = (uint32_t)G.Cg;
+    c.K1 = (uint32_t)G.K[1];
+    c.K2 = (uint32_t)G.K[2];
+    c.Kn = (uint32_t)G.Kn;
+    c.dl0 = (uint32_t)G.dl[0];
+    c.dl1 = (uint32_t)G.dl[1];
+    c.dl2 = (uint32_t)G.dl[2];
+  }
   for (int64_t n0 = 0; n0 < G.N; n0 += L.nb) {
     const int64_t nb = G.N - n0 < L.nb ? G.N - n0 : L.nb;
     for (int64_t g = 0; g < G.groups; ++g) {
@@ -471,6 +499,15 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
                          dim3(256), 0, st, x, G, F, n0, g, xp);
       err = hipGetLastError();
       if (err != hipSuccess) return err;
+      const int8_t* A = wt + g * G.Og * G.Kc;
+      void* o = static_cast<char*>(out) + (size_t)((n0 * G.O + g * G.Og) * G.Pn) * osz;
+      if (impl) {
+        GemmEpi ei = eb;
+        ei.cb.frame_bytes = (uint32_t)(nb * F.Ep * G.Cg);
+        err = launch_gemm_conv(A, xp, G.Og, nb * G.Pn, G.Kc, ei, o, st);
+        if (err != hipSuccess) return err;
+        continue;
+      }
       const int8_t* B = xp;
       if (!pw) {
         hipLaunchKernelGGL(k_im2col_taps, dim3((unsigned)((xch + 255) / 256), (unsigned)nb, tz),
@@ -479,8 +516,6 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
         if (err != hipSuccess) return err;
         B = col;
       }
-      const int8_t* A = wt + g * G.Og * G.Kc;
-      void* o = static_cast<char*>(out) + (size_t)((n0 * G.O + g * G.Og) * G.Pn) * osz;
       if (nb > 1) err = launch_gemm(A, B, G.Og, nb * G.Pn, G.Kc, eb, o, st);
       else if (G.Og <= 16) err = launch_gemv(A, B, G.Og, G.Pn, G.Kc, e, o, st);
       else err = launch_gemm(A, B, G.Og, G.Pn, G.Kc, e, o, st);

@@ -239,6 +239,7 @@ struct Epi {
   static constexpr bool OUT_Q8 = (EPI & 32) != 0;
   static constexpr bool OUT_DQ = (EPI & 64) != 0;
   static constexpr bool COLBLK = (EPI & 128) != 0;   // GemmEpi::col_blk addressing
+  static constexpr bool IMPL = (EPI & 256) != 0;     // B is a conv frame (GemmEpi::cb)
   static constexpr int MODE = (EPI >> 3) & 1;
   static constexpr bool BIAS = (EPI & 4) != 0;
   static constexpr int ACT = EPI & 3;
@@ -252,6 +253,29 @@ inline int epi_code(const GemmEpi& e) {
   return (e.mode << 3) | (e.bias ? 4 : 0) | e.act | cb;
 }
 
+// Implicit conv B operand (GemmEpi::ConvB): frame offset of tap t relative
+// to tap 0, in positions.
+__device__ __forceinline__ uint32_t convb_tap(const GemmEpi::ConvB& c, uint32_t t) {
+  const uint32_t k2 = t % c.K2, r = t / c.K2, k1 = r % c.K1, k0 = r / c.K1;
+  return (k0 * c.dl0 * c.E1 + k1 * c.dl1) * c.E2 + k2 * c.dl2;
+}
+// frame byte offset of GEMM column n's contraction byte 0 (tap 0, channel 0)
+__device__ __forceinline__ uint32_t convb_row(const GemmEpi::ConvB& c, uint32_t n) {
+  const uint32_t y = n / c.Pn, p = n - y * c.Pn;
+  const uint32_t o2 = p % c.P2, q = p / c.P2, o1 = q % c.P1, o0 = q / c.P1;
+  return (y * c.Ep + (o0 * c.st0 * c.E1 + o1 * c.st1) * c.E2 + o2 * c.st2) * c.Cg;
+}
+// byte offsets, relative to a column's convb_row, of the two 64-byte halves
+// of K stage s (contraction bytes 128 s .. 128 s + 127): Cg is a multiple of
+// 64, so a half never straddles two taps.  A half past the last tap
+// repeats the first (its lanes read out of range there).
+__device__ __forceinline__ void convb_stage(const GemmEpi::ConvB& c, uint32_t s, uint32_t& lo,
+                                            uint32_t& hi) {
+  const uint32_t k = 128u * s, t = k / c.Cg, ch = k - t * c.Cg;
+  lo = convb_tap(c, t) * c.Cg + ch;
+  hi = ch + 64 < c.Cg ? lo + 64 : (t + 1 < c.Kn ? convb_tap(c, t + 1) * c.Cg : lo);
+}
+
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(GEMM_THREADS, 1)
 void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
@@ -259,6 +283,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   using C = GemmCfg<BM, BN>;
   constexpr bool OUT_I32 = Epi<EPI>::OUT_I32;
   constexpr int MODE = Epi<EPI>::MODE;
+  constexpr bool IMPL = Epi<EPI>::IMPL;
   extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
   // the wave index is uniform: kept in an SGPR, the LDS destinations of the
   // copies (M0) follow without a VGPR round trip
@@ -303,7 +328,16 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   for (int j = 0; j < C::B_LOADS; ++j) {
     const int row = wave * (BN / 4) + 8 * j + (lane >> 3);
     kcb[j] = 16 * ((lane & 7) ^ swz(row));
-    offb[j] = row < rows_b ? (uint32_t)(row * K + kcb[j]) : OOB;
+    if constexpr (IMPL)   // the column's frame row; the stage adds its tap offset
+      offb[j] = row < rows_b ? convb_row(e.cb, (uint32_t)(n0 + row)) + (uint32_t)(kcb[j] & 63) : OOB;
+    else
+      offb[j] = row < rows_b ? (uint32_t)(row * K + kcb[j]) : OOB;
+  }
+  // IMPL: lane l holds the half offsets of K stages l and l + 64
+  uint32_t stg_lo[2] = {0u, 0u}, stg_hi[2] = {0u, 0u};
+  if constexpr (IMPL) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) convb_stage(e.cb, (uint32_t)(lane + 64 * r), stg_lo[r], stg_hi[r]);
   }
   const uint32_t bytes_a = (uint32_t)rows_a * (uint32_t)K;
   const uint32_t bytes_b = (uint32_t)rows_b * (uint32_t)K;
@@ -332,14 +366,37 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
       if (j >= j0 && j < j1) copy16_to_lds(ra, sa + j * 8 * BK, tail ? offa_t[j] : offa[j]);
   };
   auto issue_b = [&](int kt, int8_t* stage, int j0, int j1) {
-    const bool live = kt < KT;
-    const int kb = live ? kt * BK : 0;
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
-    int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
-    const bool tail = kb + BK > K;
+    if constexpr (IMPL) {
+      // the stage's two halves sit at frame offsets lo and hi from each
+      // column's row; the resource starts at the lower one
+      // (both lanes read, then a bit select: no branch in the loop)
+      const bool live = kt < KT;
+      const int s = live ? kt : 0;
+      const uint32_t up = 0u - (uint32_t)(s >> 6);   // all ones for stages 64 .. 127
+      const uint32_t lo0 = __builtin_amdgcn_readlane(stg_lo[0], s & 63);
+      const uint32_t lo1 = __builtin_amdgcn_readlane(stg_lo[1], s & 63);
+      const uint32_t hi0 = __builtin_amdgcn_readlane(stg_hi[0], s & 63);
+      const uint32_t hi1 = __builtin_amdgcn_readlane(stg_hi[1], s & 63);
+      const uint32_t lo = lo0 ^ ((lo0 ^ lo1) & up), hi = hi0 ^ ((hi0 ^ hi1) & up);
+      const uint32_t base = lo < hi ? lo : hi;
+      const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + base, live ? e.cb.frame_bytes - base : 0u);
+      const uint32_t dlo = lo - base, dhi = hi - base;
+      int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
+      const bool tail = s * BK + BK > K;
 #pragma unroll
-    for (int j = 0; j < C::B_LOADS; ++j)
-      if (j >= j0 && j < j1) copy16_to_lds(rb, sb + j * 8 * BK, tail ? offb_t[j] : offb[j]);
+      for (int j = 0; j < C::B_LOADS; ++j)
+        if (j >= j0 && j < j1)
+          copy16_to_lds(rb, sb + j * 8 * BK, (tail ? offb_t[j] : offb[j]) + (kcb[j] >= 64 ? dhi : dlo));
+    } else {
+      const bool live = kt < KT;
+      const int kb = live ? kt * BK : 0;
+      const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
+      int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
+      const bool tail = kb + BK > K;
+#pragma unroll
+      for (int j = 0; j < C::B_LOADS; ++j)
+        if (j >= j0 && j < j1) copy16_to_lds(rb, sb + j * 8 * BK, tail ? offb_t[j] : offb[j]);
+    }
   };
 
   // Fragment addresses: byte offset of the fragment row within a stage and
@@ -872,7 +929,72 @@ static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int
   return hipGetLastError();
 }
 
+// Implicit conv GEMM (B a conv frame, column-blocked output): i32 and the
+// per-tensor f32 dequant, on the tiles whose register budget has room for
+// the per-column frame offsets.
+#define Q8_EPI_CODES_CONV(X) X(384) X(400)
+
+template <int BM, int BN>
+static hipError_t launch_qgemm_conv_tile(const int8_t* A, const int8_t* B, int M, int N, int K,
+                                         const GemmEpi& e, void* out, hipStream_t st) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const dim3 grid((unsigned)(tm * tn)), block(GEMM_THREADS);
+  constexpr int lds = qgemm_lds<BM, BN>();
+  switch (epi_code(e) | 256) {
+#define Q8_LAUNCH_EPI(code)                                                                  \
+  case code:                                                                                 \
+    hipLaunchKernelGGL((k_qgemm<BM, BN, code>), grid, block, lds, st, A, B, M, N, K, tm, tn, \
+                       e, out);                                                              \
+    break;
+    Q8_EPI_CODES_CONV(Q8_LAUNCH_EPI)
+#undef Q8_LAUNCH_EPI
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 std::atomic<long long> g_generic_gemm_launches{0};
+
+// Tile choice by a fill-aware cost of the launch's rounds.  A tile shape
+// has `slots` workgroups resident at once (CUs x the workgroups per CU its
+// LDS allows: 1 for 256x256 and 256x128, 2 for 128x128, 4 for 64x64); a
+// round of it costs tmin + (tfull - tmin) * fill, fill = its tiles / slots
+// (a partial round is cheaper but not free).  The constants are
+// microseconds at K = 4096, fitted to measurements of every shape on M in
+// 256..4096 x N in 2048..22016 (they pick the fastest tile on all 56); K
+// scales every shape alike, so it does not enter the choice.  Two resident
+// 128x128 workgroups per CU overlap one's epilogue with the other's main
+// loop, which is why they win many mid-size shapes.  Candidates from
+// `first` on (0: all four; 2: 128x128 and 64x64).  Returns 0 .. 3.
+static int gemm_tile_choice(int64_t M, int64_t N, int first) {
+  struct Cand { int bm, bn, per_cu; double tmin, tfull; };
+  const Cand cands[] = {{256, 256, 1, 44.0, 63.0}, {256, 128, 1, 27.5, 40.0},
+                        {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0}};
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  int best = first;
+  double best_cost = 1e300;
+  for (int c = first; c < 4; ++c) {
+    const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
+    const int64_t slots = (int64_t)cus * cands[c].per_cu;
+    const int64_t full = tiles / slots, rest = tiles % slots;
+    double cost = (double)full * cands[c].tfull;
+    if (rest) cost += cands[c].tmin + (cands[c].tfull - cands[c].tmin) * (double)rest / (double)slots;
+    if (cost < best_cost * 0.995) { best_cost = cost; best = c; }   // near ties keep the larger tile
+  }
+  return best;
+}
+
+hipError_t launch_gemm_conv(const int8_t* A, const int8_t* frame, int64_t M, int64_t N, int64_t K,
+                            const GemmEpi& e, void* out, hipStream_t st) {
+  if (M == 0 || N == 0) return hipSuccess;
+  if (K % 64 != 0 || K <= 0 || K > 16384 || (e.cb.Cg % 64) != 0 || e.col_blk <= 0 || M > INT32_MAX ||
+      N > INT32_MAX || ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(frame)) & 15) != 0)
+    return hipErrorInvalidValue;
+  if (gemm_tile_choice(M, N, 2) == 2)
+    return launch_qgemm_conv_tile<128, 128>(A, frame, (int)M, (int)N, (int)K, e, out, st);
+  return launch_qgemm_conv_tile<64, 64>(A, frame, (int)M, (int)N, (int)K, e, out, st);
+}
 
 hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st) {
@@ -889,31 +1011,7 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();
   }
-  // Tile choice by a fill-aware cost of the launch's rounds.  A tile shape
-  // has `slots` workgroups resident at once (CUs x the workgroups per CU its
-  // LDS allows: 1 for 256x256 and 256x128, 2 for 128x128, 4 for 64x64);
-  // a round of it costs tmin + (tfull - tmin) * fill, fill = its tiles /
-  // slots (a partial round is cheaper but not free).  The constants are
-  // microseconds at K = 4096, fitted to measurements of every shape on
-  // M in 256..4096 x N in 2048..22016 (they pick the fastest tile on all 56);
-  // K scales every shape alike, so it does not enter the choice.  Two
-  // resident 128x128 workgroups per CU overlap one's epilogue with the
-  // other's main loop, which is why they win many mid-size shapes.
-  struct Cand { int bm, bn, per_cu; double tmin, tfull; };
-  const Cand cands[] = {{256, 256, 1, 44.0, 63.0}, {256, 128, 1, 27.5, 40.0},
-                        {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0}};
-  const int cus = cu_count() > 0 ? cu_count() : 256;
-  int best = 0;
-  double best_cost = 1e300;
-  for (int c = 0; c < 4; ++c) {
-    const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
-    const int64_t slots = (int64_t)cus * cands[c].per_cu;
-    const int64_t full = tiles / slots, rest = tiles % slots;
-    double cost = (double)full * cands[c].tfull;
-    if (rest) cost += cands[c].tmin + (cands[c].tfull - cands[c].tmin) * (double)rest / (double)slots;
-    if (cost < best_cost * 0.995) { best_cost = cost; best = c; }   // near ties keep the larger tile
-  }
-  switch (best) {
+  switch (gemm_tile_choice(M, N, 0)) {
     case 0: return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
     case 1: return launch_qgemm_tile<256, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
     case 2: return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
@@ -1440,6 +1538,8 @@ hipError_t setup_kernel_attributes() {
   Q8_EPI_CODES(Q8_SET_64)
   Q8_SET_256(64)
   Q8_SET_256(72)
+  Q8_EPI_CODES_CONV(Q8_SET_128)
+  Q8_EPI_CODES_CONV(Q8_SET_64)
 #undef Q8_SET_256
 #undef Q8_SET_256x128
 #undef Q8_SET_128

@@ -45,7 +45,28 @@ struct GemmEpi {
   int64_t col_blk;
   int64_t blk_stride;
   int64_t ld_out;
+  // implicit-GEMM B operand of quantized_conv (EPI bit 256): B is the
+  // channel-last frame of a batch of images.  GEMM column j is output
+  // position p = j % Pn of image y = j / Pn, and its contraction byte
+  // k = t * Cg + c (tap t, channel c) is frame byte
+  // (y * Ep + e(p) + off(t)) * Cg + c, e(p) the frame position of p's tap 0
+  // and off(t) that of tap t relative to it.  All offsets fit 31 bits.
+  struct ConvB {
+    uint32_t Pn, P1, P2;       // positions per image; output sizes of dims 1, 2
+    uint32_t st0, st1, st2;    // strides
+    uint32_t E1, E2;           // frame sizes of dims 1, 2
+    uint32_t Ep, Cg;           // frame positions per image; channels, a multiple of 64
+    uint32_t K1, K2, Kn;       // kernel sizes of dims 1, 2; kernel positions
+    uint32_t dl0, dl1, dl2;    // dilations
+    uint32_t frame_bytes;      // bytes of the batch's frames
+  } cb;
 };
+
+// GEMM of quantized_conv's implicit form: A [M, K] (tap-major weight rows),
+// B the frames described by e.cb (N = images x Pn columns), column-blocked
+// output as set in e.  K a multiple of 64, at most 16384.
+hipError_t launch_gemm_conv(const int8_t* A, const int8_t* frame, int64_t M, int64_t N, int64_t K,
+                            const GemmEpi& e, void* out, hipStream_t st);
 
 hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
                               double mean, double std, hipStream_t st);
