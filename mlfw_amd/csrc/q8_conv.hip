@@ -408,11 +408,11 @@ static bool conv_implicit(const ConvGeom& G) {
 }
 
 // channel-last workspace: [col: nb * Pn * Kc, unless pointwise or implicit] [frame:
-// nb * Ep * Cg] [tap-major weight: O * Kc, unless 1 x 1], each rounded up
-// to 256 bytes
+// nb * Ep * Cg] [tap-major weight: O * Kc, unless 1 x 1] [split-K partial
+// sums of the implicit GEMM], each rounded up to 256 bytes
 struct ClLayout {
   int64_t nb;
-  size_t col, frame, wt;
+  size_t col, frame, wt, part;   // part: split-K partial sums of the implicit GEMM
 };
 static ClLayout cl_layout(const ConvGeom& G, const ConvFrame& F) {
   const bool no_col = conv_pointwise(G) || conv_implicit(G);
@@ -423,6 +423,11 @@ static ClLayout cl_layout(const ConvGeom& G, const ConvFrame& F) {
   L.col = round256((size_t)L.nb * col1);
   L.frame = round256((size_t)L.nb * fr1);
   L.wt = G.Kn == 1 ? 0 : round256((size_t)G.O * (size_t)G.Kc);   // 1 x 1: the weight as given
+  L.part = 0;
+  if (conv_implicit(G)) {
+    const ConvGemmPlan pl = conv_gemm_plan(G.Og, L.nb * G.Pn, G.Kc, (size_t)1 << 30);
+    if (pl.splits > 1) L.part = round256((size_t)pl.splits * (size_t)G.Og * (size_t)(L.nb * G.Pn) * 4);
+  }
   return L;
 }
 
@@ -435,7 +440,7 @@ size_t conv_workspace_bytes(const ConvGeom& G) {
   ConvFrame F;
   if (conv_frame_of(G, &F)) {   // also enough for the im2col form it falls back to
     const ClLayout L = cl_layout(G, F);
-    const size_t cl = L.col + L.frame + L.wt;
+    const size_t cl = L.col + L.frame + L.wt + L.part;
     b = cl > b ? cl : b;
   }
   return b;
@@ -450,6 +455,7 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
   int8_t* xp = col + L.col;
   // a 1 x 1 kernel's weight is its own tap-major form
   int8_t* wt = G.Kn == 1 ? const_cast<int8_t*>(w) : xp + L.frame;
+  int32_t* part = reinterpret_cast<int32_t*>(xp + L.frame + L.wt);
   const int64_t nsl = G.O * (G.Cg >> 4);                   // weight slices
   const int wns = G.Kn >= 256 ? WT_CHUNKS / G.Kn : 256 / G.Kn;   // slices per workgroup
   const int64_t wblk = (nsl + wns - 1) / wns;
@@ -504,7 +510,8 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
       if (impl) {
         GemmEpi ei = eb;
         ei.cb.frame_bytes = (uint32_t)(nb * F.Ep * G.Cg);
-        err = launch_gemm_conv(A, xp, G.Og, nb * G.Pn, G.Kc, ei, o, st);
+        const ConvGemmPlan pl = conv_gemm_plan(G.Og, nb * G.Pn, G.Kc, L.part);
+        err = launch_gemm_conv(A, xp, G.Og, nb * G.Pn, G.Kc, ei, pl, part, o, st);
         if (err != hipSuccess) return err;
         continue;
       }

@@ -289,7 +289,12 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   // copies (M0) follow without a VGPR round trip
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  // IMPL: blockIdx.x = split * tiles + tile; split s takes K stages
+  // [s * kps, (s + 1) * kps) and, with more than one split, writes its raw
+  // partial sums to out + s * M * N (row-major int32)
+  const int split = IMPL ? (int)(blockIdx.x / (unsigned)(tiles_m * tiles_n)) : 0;
+  tile_of(IMPL ? (int)blockIdx.x - split * tiles_m * tiles_n : (int)blockIdx.x, tiles_m, tiles_n, tm, tn);
+  if constexpr (IMPL) out = static_cast<int32_t*>(out) + (int64_t)split * M * N;
   const int m0 = tm * BM, n0 = tn * BN;
   const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
   const int8_t* Ab = A + (int64_t)m0 * K;
@@ -342,6 +347,8 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   const uint32_t bytes_a = (uint32_t)rows_a * (uint32_t)K;
   const uint32_t bytes_b = (uint32_t)rows_b * (uint32_t)K;
   const int KT = (K + BK - 1) / BK;
+  const int kt0 = IMPL ? split * (int)e.cb.kps : 0;                    // this split's stages
+  const int KTe = IMPL ? min(KT, kt0 + (int)e.cb.kps) : KT;
   // offsets for the last stage when K is not a multiple of BK: the lane's
   // chunk past K reads past the buffer's end (zero) instead of the next row
   const int kb_last = (KT - 1) * BK;
@@ -356,7 +363,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   // of range and writes zeros into a stage that is no longer read, which
   // keeps the loop body branch-free.
   auto issue_a = [&](int kt, int8_t* stage, int j0, int j1) {
-    const bool live = kt < KT;
+    const bool live = kt < KTe;
     const int kb = live ? kt * BK : 0;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab + kb, live ? bytes_a - (uint32_t)kb : 0u);
     int8_t* sa = stage + wave * (BM / 4) * BK;
@@ -370,7 +377,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
       // the stage's two halves sit at frame offsets lo and hi from each
       // column's row; the resource starts at the lower one
       // (both lanes read, then a bit select: no branch in the loop)
-      const bool live = kt < KT;
+      const bool live = kt < KTe;
       const int s = live ? kt : 0;
       const uint32_t up = 0u - (uint32_t)(s >> 6);   // all ones for stages 64 .. 127
       const uint32_t lo0 = __builtin_amdgcn_readlane(stg_lo[0], s & 63);
@@ -388,7 +395,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
         if (j >= j0 && j < j1)
           copy16_to_lds(rb, sb + j * 8 * BK, (tail ? offb_t[j] : offb[j]) + (kcb[j] >= 64 ? dhi : dlo));
     } else {
-      const bool live = kt < KT;
+      const bool live = kt < KTe;
       const int kb = live ? kt * BK : 0;
       const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb + kb, live ? bytes_b - (uint32_t)kb : 0u);
       int8_t* sb = stage + C::A_BYTES + wave * (BN / 4) * BK;
@@ -454,10 +461,10 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   constexpr int NV = C::A_LOADS + C::B_LOADS;    // copies per stage
   constexpr int HA = C::A_LOADS / 2, HB = C::B_LOADS / 2;
   static_assert(C::A_LOADS % 2 == 0 && C::B_LOADS % 2 == 0, "copies split in halves");
-  issue_a(0, buf(0), 0, C::A_LOADS);
-  issue_b(0, buf(0), 0, C::B_LOADS);
-  issue_a(1, buf(1), 0, C::A_LOADS);
-  issue_b(1, buf(1), 0, C::B_LOADS);
+  issue_a(kt0, buf(kt0), 0, C::A_LOADS);
+  issue_b(kt0, buf(kt0), 0, C::B_LOADS);
+  issue_a(kt0 + 1, buf(kt0 + 1), 0, C::A_LOADS);
+  issue_b(kt0 + 1, buf(kt0 + 1), 0, C::B_LOADS);
   if (!OUT_I32 && MODE == 1) {
 #pragma unroll
     for (int u = 0; u < NSC; ++u)
@@ -465,13 +472,13 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   }
   stage_sync_keep<NV>();                          // stage 0 landed
   v4i fa0[C::TM], fb0[C::TN], fa1[C::TM], fb1[C::TN];
-  read_frags(buf(0), 0, fa0, fb0);
-  for (int kt = 0; kt < KT; ++kt) {
+  read_frags(buf(kt0), 0, fa0, fb0);
+  for (int kt = kt0; kt < KTe; ++kt) {
     int8_t* cur = buf(kt);
     // sub-step 0; the second half of stage kt+1's copies (stage 1 went out
     // whole in the prologue)
     read_frags(cur, 1, fa1, fb1);
-    if (kt >= 1) {
+    if (kt >= kt0 + 1) {
       issue_a(kt + 1, buf(kt + 1), HA, C::A_LOADS);
       issue_b(kt + 1, buf(kt + 1), HB, C::B_LOADS);
     }
@@ -929,30 +936,10 @@ static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int
   return hipGetLastError();
 }
 
-// Implicit conv GEMM (B a conv frame, column-blocked output): i32 and the
-// per-tensor f32 dequant, on the tiles whose register budget has room for
-// the per-column frame offsets.
-#define Q8_EPI_CODES_CONV(X) X(384) X(400)
-
-template <int BM, int BN>
-static hipError_t launch_qgemm_conv_tile(const int8_t* A, const int8_t* B, int M, int N, int K,
-                                         const GemmEpi& e, void* out, hipStream_t st) {
-  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  const dim3 grid((unsigned)(tm * tn)), block(GEMM_THREADS);
-  constexpr int lds = qgemm_lds<BM, BN>();
-  switch (epi_code(e) | 256) {
-#define Q8_LAUNCH_EPI(code)                                                                  \
-  case code:                                                                                 \
-    hipLaunchKernelGGL((k_qgemm<BM, BN, code>), grid, block, lds, st, A, B, M, N, K, tm, tn, \
-                       e, out);                                                              \
-    break;
-    Q8_EPI_CODES_CONV(Q8_LAUNCH_EPI)
-#undef Q8_LAUNCH_EPI
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
+// Implicit conv GEMM (B a conv frame): column-blocked i32 and per-tensor f32
+// dequant outputs, and the raw row-major partial sums of a K split, on the
+// tiles whose register budget has room for the per-column frame offsets.
+#define Q8_EPI_CODES_CONV(X) X(272) X(384) X(400)   // 272: a split's raw partial sums
 
 std::atomic<long long> g_generic_gemm_launches{0};
 
@@ -965,16 +952,16 @@ std::atomic<long long> g_generic_gemm_launches{0};
 // 256..4096 x N in 2048..22016 (they pick the fastest tile on all 56); K
 // scales every shape alike, so it does not enter the choice.  Two resident
 // 128x128 workgroups per CU overlap one's epilogue with the other's main
-// loop, which is why they win many mid-size shapes.  Candidates from
-// `first` on (0: all four; 2: 128x128 and 64x64).  Returns 0 .. 3.
-static int gemm_tile_choice(int64_t M, int64_t N, int first) {
+// loop, which is why they win many mid-size shapes.  Returns the index of
+// the chosen tile in cands.
+static int gemm_tile_choice(int64_t M, int64_t N) {
   struct Cand { int bm, bn, per_cu; double tmin, tfull; };
   const Cand cands[] = {{256, 256, 1, 44.0, 63.0}, {256, 128, 1, 27.5, 40.0},
                         {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0}};
   const int cus = cu_count() > 0 ? cu_count() : 256;
-  int best = first;
+  int best = 0;
   double best_cost = 1e300;
-  for (int c = first; c < 4; ++c) {
+  for (int c = 0; c < 4; ++c) {
     const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
     const int64_t slots = (int64_t)cus * cands[c].per_cu;
     const int64_t full = tiles / slots, rest = tiles % slots;
@@ -985,15 +972,125 @@ static int gemm_tile_choice(int64_t M, int64_t N, int first) {
   return best;
 }
 
+ConvGemmPlan conv_gemm_plan(int64_t M, int64_t N, int64_t K, size_t part_cap_bytes) {
+  // Measured on ResNet-style layers at batch 32: with few tiles per CU the
+  // K loop is bound by load latency, which four resident 64x64 workgroups
+  // per CU hide better than two 128x128 ones; with two or more 64x64 tiles
+  // per CU the 64x64 tile is bound by its L2 traffic (64 operations per
+  // staged byte) and 128x128 (128 per byte) is faster.
+  const int64_t cus = cu_count() > 0 ? cu_count() : 256;
+  const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+  ConvGemmPlan p;
+  p.bm = M >= 128 && tiles64 >= 2 * cus ? 128 : 64;
+  const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bm - 1) / p.bm);
+  const int64_t KT = (K + BK - 1) / BK;
+  // Split only when the tiles leave CUs idle and K is long: the partial
+  // sums cost 8 * splits bytes of traffic per output element, against
+  // 2 * K operations.  Aim at two workgroups per CU, 8 stages per split.
+  int64_t splits = 1;
+  if (tiles < cus && K >= 4096) {
+    splits = (2 * cus + tiles - 1) / tiles;
+    splits = splits < 8 ? splits : 8;
+    splits = splits < KT / 8 ? splits : KT / 8;
+    splits = splits > 1 ? splits : 1;
+  }
+  while (splits > 1 && (size_t)splits * (size_t)M * (size_t)N * 4 > part_cap_bytes) --splits;
+  p.kps = (int)((KT + splits - 1) / splits);
+  p.splits = (int)((KT + p.kps - 1) / p.kps);   // no empty split
+  return p;
+}
+
+// Sum of the splits' partial sums, stored with the column-blocked mapping
+// and output kind of e (int32, or fround(acc * s_out) as the GEMM epilogue).
+// Row m = blockIdx.y (+ multiples of gridDim.y); a thread takes 4
+// consecutive columns.  M * N < 2^31 (split plans only go to small outputs).
+__global__ __launch_bounds__(256) void k_conv_splitk_finish(const int32_t* __restrict__ part, int splits,
+                                                            int M, int N, GemmEpi e,
+                                                            void* __restrict__ out) {
+  const int j0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (j0 >= N) return;
+  const int cb = (int)e.col_blk;
+  const int nj = N - j0 < 4 ? N - j0 : 4;
+  const bool vec = (N & 3) == 0;   // 16-byte rows of partial sums
+  const int blk0 = j0 / cb, p0 = j0 - blk0 * cb;
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    uint32_t acc[4] = {0u, 0u, 0u, 0u};
+    const int32_t* src = part + (int64_t)m * N + j0;
+    // at most 8 splits: unrolled, so that their loads are in flight together
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s < splits) {
+        const int32_t* ps = src + (int64_t)s * M * N;
+        if (vec) {
+          const v4i v = *reinterpret_cast<const v4i*>(ps);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[c] += (uint32_t)v[c];
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (c < nj) acc[c] += (uint32_t)ps[c];
+        }
+      }
+    }
+    int blk = blk0, p = p0;
+    int64_t at = (int64_t)blk * e.blk_stride + (int64_t)m * e.ld_out + p;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c < nj) {
+        if (e.out_i32) static_cast<int32_t*>(out)[at] = (int32_t)acc[c];
+        else static_cast<float*>(out)[at] = (float)((double)(int32_t)acc[c] * e.s_out);
+      }
+      ++at;
+      if (++p == cb) {   // next image's block
+        p = 0;
+        ++blk;
+        at = (int64_t)blk * e.blk_stride + (int64_t)m * e.ld_out;
+      }
+    }
+  }
+}
+
 hipError_t launch_gemm_conv(const int8_t* A, const int8_t* frame, int64_t M, int64_t N, int64_t K,
-                            const GemmEpi& e, void* out, hipStream_t st) {
+                            const GemmEpi& e, const ConvGemmPlan& plan, int32_t* part, void* out,
+                            hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
+  const int64_t KT = (K + BK - 1) / BK;
   if (K % 64 != 0 || K <= 0 || K > 16384 || (e.cb.Cg % 64) != 0 || e.col_blk <= 0 || M > INT32_MAX ||
-      N > INT32_MAX || ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(frame)) & 15) != 0)
+      N > INT32_MAX || ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(frame)) & 15) != 0 ||
+      plan.splits < 1 || plan.splits > 8 || plan.kps < 1 || (int64_t)plan.splits * plan.kps < KT ||
+      (plan.splits > 1 && (part == nullptr || (reinterpret_cast<uintptr_t>(part) & 15) != 0 ||
+                           M * N >= ((int64_t)1 << 31))) ||
+      (plan.bm != 64 && plan.bm != 128))
     return hipErrorInvalidValue;
-  if (gemm_tile_choice(M, N, 2) == 2)
-    return launch_qgemm_conv_tile<128, 128>(A, frame, (int)M, (int)N, (int)K, e, out, st);
-  return launch_qgemm_conv_tile<64, 64>(A, frame, (int)M, (int)N, (int)K, e, out, st);
+  GemmEpi eg = e;
+  eg.cb.kps = (uint32_t)(plan.splits > 1 ? plan.kps : KT);
+  void* dst = out;
+  if (plan.splits > 1) {   // raw partial sums, row-major [M, N] per split
+    eg.col_blk = 0;
+    eg.out_i32 = 1;
+    dst = part;
+  }
+  const int tm = (int)((M + plan.bm - 1) / plan.bm), tn = (int)((N + plan.bm - 1) / plan.bm);
+  if ((int64_t)tm * tn * plan.splits >= ((int64_t)1 << 31) / GEMM_THREADS) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(tm * tn * plan.splits)), block(GEMM_THREADS);
+  const int code = epi_code(eg) | 256;
+  hipError_t err = hipErrorInvalidValue;
+  constexpr int lds128 = qgemm_lds<128, 128>(), lds64 = qgemm_lds<64, 64>();
+#define Q8_CONV_LAUNCH(BMV, codev)                                                                \
+  if (plan.bm == BMV && code == codev) {                                                          \
+    hipLaunchKernelGGL((k_qgemm<BMV, BMV, codev>), grid, block, BMV == 128 ? lds128 : lds64, st, A, \
+                       frame, (int)M, (int)N, (int)K, tm, tn, eg, dst);                           \
+    err = hipGetLastError();                                                                      \
+  }
+#define Q8_CONV_LAUNCH_BOTH(codev) Q8_CONV_LAUNCH(128, codev) Q8_CONV_LAUNCH(64, codev)
+  Q8_EPI_CODES_CONV(Q8_CONV_LAUNCH_BOTH)
+#undef Q8_CONV_LAUNCH_BOTH
+#undef Q8_CONV_LAUNCH
+  if (err != hipSuccess || plan.splits == 1) return err;
+  const unsigned gy = (unsigned)(M < 65535 ? M : 65535);
+  hipLaunchKernelGGL(k_conv_splitk_finish, dim3((unsigned)((N + 1023) / 1024), gy), dim3(256), 0, st,
+                     part, plan.splits, (int)M, (int)N, e, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
@@ -1011,7 +1108,7 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();
   }
-  switch (gemm_tile_choice(M, N, 0)) {
+  switch (gemm_tile_choice(M, N)) {
     case 0: return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
     case 1: return launch_qgemm_tile<256, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
     case 2: return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);

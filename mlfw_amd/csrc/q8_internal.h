@@ -59,14 +59,26 @@ struct GemmEpi {
     uint32_t K1, K2, Kn;       // kernel sizes of dims 1, 2; kernel positions
     uint32_t dl0, dl1, dl2;    // dilations
     uint32_t frame_bytes;      // bytes of the batch's frames
+    uint32_t kps;              // K stages per split (split-K), >= all stages for one split
   } cb;
 };
 
 // GEMM of quantized_conv's implicit form: A [M, K] (tap-major weight rows),
 // B the frames described by e.cb (N = images x Pn columns), column-blocked
-// output as set in e.  K a multiple of 64, at most 16384.
+// output as set in e.  K a multiple of 64, at most 16384.  The plan picks
+// the tile and a split of K when the tiles alone would leave most of the
+// chip idle; the splits' int32 partial sums go to `part` (splits * M * N
+// words) and a finishing pass adds them (int32 addition does not depend on
+// the order) and applies the output mapping and dequant.
+struct ConvGemmPlan {
+  int bm;       // square tile edge, 128 or 64
+  int splits;   // K splits, >= 1
+  int kps;      // K stages (of 128) per split
+};
+ConvGemmPlan conv_gemm_plan(int64_t M, int64_t N, int64_t K, size_t part_cap_bytes);
 hipError_t launch_gemm_conv(const int8_t* A, const int8_t* frame, int64_t M, int64_t N, int64_t K,
-                            const GemmEpi& e, void* out, hipStream_t st);
+                            const GemmEpi& e, const ConvGemmPlan& plan, int32_t* part, void* out,
+                            hipStream_t st);
 
 hipError_t launch_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset,
                               double mean, double std, hipStream_t st);

@@ -8,9 +8,11 @@ is a multiple of 16), the GEMV and the GEMM kernels behind the latter
 asymmetric padding, dilation, batch > 1 (batches of images in one GEMM
 whose epilogue scatters columns to images, with 16-byte and with
 per-element stores; one image at a time for the GEMV), spatial ranks 1 to
-3, and both im2col forms: the byte gather (channels per group not a
-multiple of 16) and the channel-last frame with a tap-major contraction,
-including 1 x 1 kernels whose frame is the GEMM operand itself; zero
+3, and the three GEMM forms of the contraction: the byte-gather im2col
+(channels per group not a multiple of 16), the channel-last frame with a
+tap-major im2col (1 x 1 kernels use the frame itself), and the implicit
+GEMM reading the frame (channels per group a multiple of 64), with and
+without a split of K; zero
 points and ui8 operands; then the whole pipeline QuantizationPass builds
 for a conv (quantize input, quantize kernel, quantized_conv, dequantize).
 """
@@ -78,6 +80,9 @@ CASES = [
     ((2, 16, 5, 6, 7), (32, 16, 2, 3, 2), [1, 2, 1], [[1, 0], [0, 1], [1, 1]], [1, 1, 2], 1),  # 3-D
     ((3, 64, 9, 9), (40, 64, 1, 1), [2, 2], [[0, 0], [0, 0]], [1, 1], 1),    # 1x1 at stride 2
     ((2, 48, 6, 6), (24, 48, 1, 1), [1, 1], [[1, 1], [0, 2]], [1, 1], 1),    # 1x1 padded: frame is B
+    # implicit GEMM split over K (few tiles, long contraction)
+    ((2, 64, 9, 9), (48, 64, 5, 5), [1, 1], [[2, 2], [2, 2]], [1, 1], 1),    # 3 splits, K % 128 = 64
+    ((2, 256, 6, 6), (96, 128, 3, 3), [1, 1], [[1, 1], [1, 1]], [1, 1], 2),  # 2 splits, groups
 ]
 
 
