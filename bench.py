@@ -25,9 +25,11 @@ calibration), or null when that file is absent.
 secondary: the HBM-bound kernels of C5 (per-token quantize and dequantize
 of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}, and the same
 GEMVs for M <= 4 with 4-bit per-group weights, and the one-call dynamic
-qlinear) and the C4 projection set.  Each is captured R times in a HIP graph (rotating input
-buffers so the 256 MB Infinity Cache cannot serve repeats) and the graph
-is replayed between two events: per-launch host overhead would otherwise
+qlinear), the C4 projection set, and quantized_conv on ResNet-style
+layers at batch 32 (synthetic int8 data).  Each is captured R times in a
+HIP graph (rotating input buffers so the 256 MB Infinity Cache cannot
+serve repeats, except conv, whose inputs are a few MB) and the graph is
+replayed between two events: per-launch host overhead would otherwise
 dominate kernels of a few microseconds.
 
 cpu_baseline: the reference's generated single-thread CPU kernels, mirrored
@@ -283,6 +285,38 @@ def bench_c4(fused_requant=True):
     return {"c4_projection_set": res}
 
 
+# ResNet-50-style conv layers at batch 32: N, C, H, W, O, kernel, padding
+# (stride 1, one group)
+CONV_LAYERS = [(32, 64, 56, 56, 64, 3, 1), (32, 128, 28, 28, 128, 3, 1), (32, 256, 14, 14, 256, 3, 1),
+               (32, 512, 7, 7, 512, 3, 1), (32, 1024, 14, 14, 256, 1, 0)]
+
+
+def bench_conv():
+    """quantized_conv with the fused per-tensor dequant (fp32 out), int8
+    operands: the whole call (frame transpose, weight permutation, implicit
+    GEMM, split-K finish where planned) per launch, 8 calls per graph."""
+    import torch
+    from mlfw_amd import ops as O
+    res = {}
+    ws = torch.empty(1 << 28, dtype=torch.int8, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    for (N, C, H, W, Oc, k, p) in CONV_LAYERS:
+        x = torch.randint(-128, 128, (N, C, H, W), dtype=torch.int8, device="cuda", generator=gen)
+        w = torch.randint(-128, 128, (Oc, C, k, k), dtype=torch.int8, device="cuda", generator=gen)
+        pad = [[p, p], [p, p]]
+        s_out = 1e-4
+        out = O.quantized_conv(x, w, [1, 1], pad, s_out=s_out, workspace=ws)
+        us, how = graph_time_us(
+            lambda i: O.quantized_conv(x, w, [1, 1], pad, s_out=s_out, out=out, workspace=ws), 8)
+        Ho, Wo = H + 2 * p - k + 1, W + 2 * p - k + 1
+        ops = 2 * N * Oc * Ho * Wo * C * k * k
+        tops = ops / (us * 1e-6) / 1e12
+        res[f"conv_N{N}_C{C}_{H}x{W}_O{Oc}_k{k}"] = {
+            "avg_us": us, "ops": ops, "TOPS": tops, "frac_mfma": tops / PEAK_INT8_TOPS, "timing": how}
+        del x, w, out
+    return res
+
+
 # ---------------------------------------------------------------- ceilings
 def ceilings():
     """Practical ceilings measured on this box (mlfw_amd/libq8ceiling.so):
@@ -448,7 +482,8 @@ def main():
     secondary = {}
     if not args.no_secondary:
         c4 = lambda: bench_c4(fused_requant=not args.no_fused_requant)
-        for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", c4)):
+        for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", c4),
+                         ("conv", bench_conv)):
             log(f"[bench] secondary {name}")
             try:
                 secondary.update(fn())
