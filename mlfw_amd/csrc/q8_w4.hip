@@ -571,7 +571,7 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int n
   // whole 128-code steps; other groups work in 32-code chunks
   pl->tr = group % 128 != 0;
   pl->nw = nw;
-  pl->rs = nw == 8 ? 4 : 8;
+  pl->rs = nw == 16 ? 2 : nw == 8 ? 4 : 8;
   const int64_t NW = pl->nw, span = 128 * pl->rs;
   const int64_t unit = pl->tr ? 32 : 128;
   // LDS: one window of segment sums and scales per round in flight (two
@@ -600,11 +600,20 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int n
   pl->lds = (size_t)lds_of(PS, pl->segw, pl->ng);
   pl->one = K <= NW * PS;
   if (!(pl->ng <= 64 && pl->lds <= 65536)) return false;
+  // Waves per workgroup by the number of (row, token) blocks: 16 while
+  // every block has a CU to itself, 4 when they outnumber the resident
+  // 8-wave workgroups.  Measured with groups of 128 at K = 4096, M 3..16:
+  // N = 4096 (256 blocks) 5.5 / 6.7 us at M = 4 / 16 with 16 waves against
+  // 6.0 / 7.1 with 8; N = 11008 (688 blocks) 8 waves, 16 being 3-5% slower.
   if (nw == 8 && !pl->tr) {
     const int64_t blocks = ((N + 15) / 16) * ((M + 15) / 16);
-    if (blocks > (pl->one ? 3 : 2) * (int64_t)cu_count()) {
+    const int64_t cus = cu_count() > 0 ? cu_count() : 256;
+    if (blocks > (pl->one ? 3 : 2) * cus) {
       W4MPlan p4;
       if (w4m_plan(M, N, K, group, &p4, 4)) *pl = p4;
+    } else if (blocks <= cus) {
+      W4MPlan p16;
+      if (w4m_plan(M, N, K, group, &p16, 16)) *pl = p16;
     }
   }
   return true;
@@ -710,6 +719,7 @@ hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, con
     }                                                                                             \
   } while (0)
     if (mp.nw == 4) Q8_W4M(4, 8, false);
+    else if (mp.nw == 16) Q8_W4M(16, 2, false);
     else if (mp.tr) Q8_W4M(8, 4, true);
     else Q8_W4M(8, 4, false);
 #undef Q8_W4M
