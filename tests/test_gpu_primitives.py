@@ -298,6 +298,24 @@ def test_dequantize_per_tensor(ops, oracle, dt, zp):
         same_bits(host(y), oracle.dequantize(q, s, zp))
 
 
+@pytest.mark.parametrize("dt,zp", [(np.int8, 0.0), (np.uint8, 128.0), (np.int32, -7.0)])
+@pytest.mark.parametrize("K", [4096, 4100, 11008])
+def test_dequantize_long_rows(ops, oracle, dt, zp, K):
+    """Rows of 4096 elements and more take the 512-thread form (two
+    4-element groups per lane); 4100 and 11008 leave a partial last pass."""
+    rng = np.random.default_rng(K)
+    if dt == np.int32:
+        q = rng.integers(-2 ** 31, 2 ** 31, size=(3, K), dtype=np.int64).astype(np.int32)
+    else:
+        info = np.iinfo(dt)
+        q = rng.integers(info.min, info.max + 1, size=(3, K)).astype(dt)
+    s = 0.0012345678901234
+    same_bits(host(ops.dequantize(dev(q), s, zp)), oracle.dequantize(q, s, zp))
+    if dt == np.int8:
+        rows = oracle.Rng(K).uniform((3,), 0.001, 0.1).astype(np.float64)
+        same_bits(host(ops.dequantize(dev(q), dev(rows))), oracle.dequantize_rows(q, rows))
+
+
 def test_dequantize_scalar_path(ops, oracle):
     q = np.random.default_rng(1).integers(-128, 128, size=(5, 13)).astype(np.int8)
     s = oracle.Rng(9).uniform((5,), 0.001, 0.1).astype(np.float64)
