@@ -79,7 +79,13 @@ def load_traffic():
 
 
 # ---------------------------------------------------------------- headline
-def bench_c3(steps, warmup):
+# Untimed load before the warm-up steps: the part raises its clocks over the
+# first tens of milliseconds of load, so the C3 step runs for at least this
+# long (wall time, synchronized) before the W warm-up steps and the timed K.
+SETTLE_MS = 150.0
+
+
+def bench_c3(steps, warmup, settle_ms=SETTLE_MS):
     import torch
     from mlfw_amd import configs as C
     from mlfw_amd import ops as O
@@ -99,6 +105,17 @@ def bench_c3(steps, warmup):
         sA = torch.empty(4096, dtype=torch.float64, device="cuda")
         quants.append(O.prepare(O.quantize_per_token, A, Aq, sA))
         gemms.append(O.prepare(O.qlinear, Aq, sA, Bq, sB, out=out))
+    # clock settling: chunks of 50 steps until settle_ms of wall time
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    settle_steps = 0
+    while settle_ms > 0 and (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for w in range(50):
+            quants[w % C3_SETS]()
+            gemms[w % C3_SETS]()
+        torch.cuda.synchronize()
+        settle_steps += 50
+    settled_ms = (time.perf_counter() - t0) * 1e3
     for w in range(warmup):
         quants[w % C3_SETS]()
         gemms[w % C3_SETS]()
@@ -136,6 +153,8 @@ def bench_c3(steps, warmup):
     gemm_ms = step_ms - quant_ms
     return {
         "step_ms": step_ms,
+        "settle_steps": settle_steps,
+        "settle_ms": settled_ms,
         "wall_ms_per_step": 1e3 * wall / steps,
         "gemm_avg_ms": gemm_ms,
         "quant_avg_ms": quant_ms,
@@ -277,7 +296,7 @@ def bench_c4(fused_requant=True):
            "frac_mfma": C.C4_OPS / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, "timing": how}
     if fused_requant:
         # the same step with the O projection's per-token requant fused into
-        # its GEMM epilogue (no fp32 intermediate; one cooperative launch)
+        # its GEMM epilogue (no fp32 intermediate; the tiles meet once grid-wide)
         nb, fused = O.requant_dynamic_workspace(X.shape[0], *C.C4_SHAPES["o"])
         ws = torch.empty(nb, dtype=torch.int8, device="cuda")
         us_f, _ = graph_time_us(lambda i: C.c4_step(X, P, fused_requant=True, ws=ws), 1, replays=5)
@@ -421,15 +440,17 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     # the part ramps its clocks over the first few tens of milliseconds of
-    # load: 400 warm steps (~40 ms) reach the steady state, 5 leave the
-    # timed steps on the ramp (up to ~15% slower, varying run to run)
+    # load; an untimed settling phase (--settle-ms of the same step) comes
+    # before the W warm-up steps, so a small W does not leave the timed
+    # steps on the ramp
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed wall time of C3 steps before the warm-up steps (0: none)")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-requant", action="store_true",
-                    help="skip the C4 step with the O projection's requant fused (its cooperative "
-                         "launch makes rocprofv3's CSV writer crash at exit)")
+                    help="skip the C4 step with the O projection's requant fused into its GEMM")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the MFMA / streaming-read ceiling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -453,7 +474,10 @@ def main():
     _lib.call("q8_init", 0)
 
     log(f"[bench] C3 4096^3: warmup {args.warmup}, steps {args.steps}")
-    r = bench_c3(args.steps, args.warmup)
+    if args.settle_ms < 0:
+        print("bench.py: --settle-ms must be >= 0", file=sys.stderr)
+        return 2
+    r = bench_c3(args.steps, args.warmup, args.settle_ms)
     tops = GEMM_OPS / (r["step_ms"] * 1e-3) / 1e12
     gemm_tops = GEMM_OPS / (r["gemm_avg_ms"] * 1e-3) / 1e12
     log(f"[bench] step {r['step_ms']:.4f} ms -> {tops:.1f} TOPS; gemm {r['gemm_avg_ms'] * 1e3:.1f} us "
@@ -533,6 +557,8 @@ def main():
                    "residency": (f"A fp32, Aq, sA and out rotate over {C3_SETS} sets (1.1 GiB > the "
                                  "256 MB Infinity Cache); B (16 MiB int8) is shared by every step"),
                    "quantize_avg_us": r["quant_avg_ms"] * 1e3,
+                   "clock_settle": {"ms": r["settle_ms"], "steps": r["settle_steps"],
+                                    "what": "untimed C3 steps before the W warm-up steps"},
                    "wall_ms_per_step": r["wall_ms_per_step"]},
         "roofline": roofline,
         "cpu_baseline": cpu,

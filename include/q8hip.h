@@ -236,6 +236,32 @@ int q8_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
             int epi, double s_out, const float* bias, int act,
             int out_kind, void* out, void* stream);
 
+/* Gate and up projections with the SwiGLU product fused: the reference's
+ * silu(gate) * up (decomposition_pass.ts:197-230: SiLU as
+ * fround(x * fround(1 / fround(1 + fround(exp(-x))))), then
+ * fround(silu * up)) applied to two per-channel linears of the same input
+ * (quantization_pass.ts:390-459 each), without g or u reaching memory:
+ *   g[m,f] = fround(accg * fround(sA[m] * sg[f])) (+ bg[f], fround)
+ *   u[m,f] = fround(accu * fround(sA[m] * su[f])) (+ bu[f], fround)
+ *   h[m,f] = fround(silu(g[m,f]) * u[m,f])        h: fp32 [M, F]
+ * bit for bit two q8_gemm calls and the elementwise chain.  The weights
+ * come interleaved by q8_glu_interleave from two q8_pack_weight results
+ * (per channel, [F,K] each): B [2F,K], packed row 64 j + c is gate row
+ * 32 j + c and 64 j + 32 + c is up row 32 j + c, with the f64 scales
+ * (and optional biases) in the same order; F must be a multiple of 32.
+ * sB_mode must be Q8_PER_CHANNEL (2F scales) or Q8_PER_TENSOR.  M <= 16
+ * runs the GEMV into a workspace of q8_gemm_glu_workspace bytes and forms
+ * h from it; larger M needs none (0 bytes, workspace may be NULL).  No
+ * single counterpart in the reference, whose graph runs the two linears,
+ * the SiLU decomposition and the product as separate ops. */
+int q8_glu_interleave(const int8_t* Wg, const double* sg, const float* bg, const int8_t* Wu,
+                      const double* su, const float* bu, int64_t F, int64_t K, int8_t* W, double* s,
+                      float* b, void* stream);
+int q8_gemm_glu_workspace(int64_t M, int64_t F, int64_t K, size_t* bytes);
+int q8_gemm_glu(const int8_t* A, const int8_t* B, int64_t M, int64_t F, int64_t K, const double* sA,
+                int sA_mode, const double* sB, int sB_mode, const float* bias, float* h, void* workspace,
+                size_t workspace_bytes, void* stream);
+
 /* Launches of the generic (non-MFMA) GEMM kernel since the library was
  * loaded, over all devices and threads: q8_gemm / q8_quantized_dot calls
  * whose K is not a multiple of 16 or whose operands are not 16-byte
@@ -319,10 +345,10 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
  *   out[m,n] = the compiled quantize of y[m,n] with scale[m]
  * bit for bit equal to q8_gemm followed by q8_quantize_rows, without the
  * fp32 tensor reaching memory when the fused route applies: every 256x256
- * tile of the MFMA GEMM is resident at once (cooperative launch), the tiles
- * of a row block publish their rows' absmax through atomics in the
- * workspace, meet once grid-wide (a bounded wait) and quantize the values
- * they hold.  Otherwise (M <= 16, more tiles than fit the chip, K not a
+ * tile of the MFMA GEMM is resident at once (one workgroup per CU; the route
+ * is taken only when every tile has a CU), the tiles of a row block publish
+ * their rows' absmax through atomics in the workspace, meet once grid-wide
+ * (a bounded wait) and quantize the values they hold.  Otherwise (M <= 16, more tiles than fit the chip, K not a
  * multiple of 16) the GEMM writes y into the workspace and q8_quantize_rows
  * follows.  No counterpart in the reference, whose scales are static (it
  * composes quantization_pass.ts:390-459 with a per-token scale); the
@@ -330,10 +356,12 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
  * q8_gemm_requant_dynamic_workspace gives the workspace bytes and whether
  * the fused route applies (it then needs 16-byte aligned A and B); calls that
  * share a workspace must be ordered.  q8_gemm_requant_dynamic_status reads
- * (synchronously) whether the fused route's bounded wait ran out -- never
- * expected, since co-residency is guaranteed; out is then unreliable.  The
- * environment variable Q8_DQ_TEST_TIMEOUT=1 (read at each call; tests only)
- * makes every wait run out, to exercise that report. */
+ * (synchronously) whether the fused route's bounded wait ran out; out and
+ * out_scales of that call are then unreliable.  On a device that runs
+ * nothing else every tile is dispatched at once and the wait cannot run out;
+ * a caller that shares the device with other streams or processes (which
+ * can hold CUs while the tiles wait) must check the status and, on a
+ * timeout, call again or take q8_gemm + q8_quantize_rows. */
 int q8_gemm_requant_dynamic_workspace(int64_t M, int64_t N, int64_t K, size_t* bytes, int* fused);
 int q8_gemm_requant_dynamic(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                             const double* sA, int sA_mode, const double* sB, int sB_mode, int epi,
@@ -341,6 +369,12 @@ int q8_gemm_requant_dynamic(const int8_t* A, const int8_t* B, int64_t M, int64_t
                             double* out_scales, void* workspace, size_t workspace_bytes,
                             void* stream);
 int q8_gemm_requant_dynamic_status(const void* workspace, int64_t M, int* timed_out, void* stream);
+
+/* Test hook, no counterpart in the reference: while `on` is non-zero every
+ * fused q8_gemm_requant_dynamic launch waits for one workgroup more than it
+ * has, so its bounded wait runs out and the status word reports it (the
+ * kernel still ends normally).  For tests of the timeout report only. */
+int q8_debug_dq_force_timeout(int on);
 
 /* ---------------------------------------------------------------- 4-bit weights */
 

@@ -73,12 +73,16 @@ SIGNATURES = {
     "q8_gemv": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                 _int, _vp, _vp],
     "q8_generic_gemm_launches": [_vp],
+    "q8_glu_interleave": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp],
+    "q8_gemm_glu_workspace": [_i64, _i64, _i64, _vp],
+    "q8_gemm_glu": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _vp, _vp, C.c_size_t, _vp],
     "q8_gemm_requant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp, _int,
                         _dbl, _vp, _vp],
     "q8_gemm_requant_dynamic_workspace": [_i64, _i64, _i64, _vp, _vp],
     "q8_gemm_requant_dynamic": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _dbl, _vp,
                                 _int, _vp, _vp, _vp, C.c_size_t, _vp],
     "q8_gemm_requant_dynamic_status": [_vp, _i64, _vp, _vp],
+    "q8_debug_dq_force_timeout": [_int],
     "q8_quantized_dot_workspace": [_i64, _i64, _i64, _int, _int, C.c_int32, C.c_int32, _vp],
     "q8_quantized_dot": [_vp, _int, _vp, _int, _i64, _i64, _i64, C.c_int32, C.c_int32, _vp, C.c_size_t,
                          _vp, _vp],

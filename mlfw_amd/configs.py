@@ -121,21 +121,28 @@ def c4_inputs(device="cuda", tokens=2048):
 
 
 def c4_prepare(W):
-    """Per-channel int8 weights of the projection set.  Gate and up are packed
-    as one [2 * 11008, 4096] weight (codes and scales are per row, so each
-    row is what packing them apart gives): one GEMM computes both."""
-    P = {k: ops.pack_weight(w, axis=0) for k, w in W.items() if k not in ("gate", "up")}
-    P["gate_up"] = ops.pack_weight(torch.cat([W["gate"], W["up"]], 0), axis=0)
+    """Per-channel int8 weights of the projection set.  Gate and up are
+    packed apart (codes and scales are per row) and interleaved into one
+    [2 * 11008, 4096] weight in groups of 32 rows ("gate_up_glu"), so one
+    GEMM computes both and applies SiLU(gate) * up in its epilogue; the
+    plain concatenation [gate; up] ("gate_up") serves the unfused route."""
+    P = {k: ops.pack_weight(w, axis=0) for k, w in W.items()}
+    P["gate_up_glu"] = ops.glu_interleave(P["gate"], P["up"])
+    P["gate_up"] = tuple(torch.cat([P["gate"][i], P["up"][i]], 0) for i in (0, 1))
+    del P["gate"], P["up"]
     return P
 
 
-def c4_step(X, P, fused_requant=False, ws=None):
+def c4_step(X, P, fused_requant=False, ws=None, glu=False):
     """One pass of the projection set.  With fused_requant the O projection
     writes its per-token int8 codes and scales directly from the GEMM
-    epilogue (q8_gemm_requant_dynamic: 128 co-resident tiles, one
-    cooperative launch), so its fp32 output never reaches memory; otherwise
-    (the default, faster on MI355X at this shape: the cooperative launch
-    alone costs ~20 us) it is written and quantized by a second kernel.
+    epilogue (q8_gemm_requant_dynamic: 128 co-resident 256 x 256 tiles that
+    meet once grid-wide), so its fp32 output never reaches memory; otherwise
+    (the default, faster on MI355X at this shape: the fused kernel runs on
+    128 of the 256 CUs) it is written and quantized by a second kernel.
+    With glu, gate|up runs as q8_gemm_glu (SiLU(gate) * up in the GEMM
+    epilogue) followed by the per-token quantize of h; the default runs the
+    [gate; up] GEMM and the fused SiLU*up requant kernel.
     Returns every stage's tensors."""
     xq, sx = ops.quantize_per_token(X)
     qkv = ops.qlinear(xq, sx, *P["qkv"])
@@ -147,12 +154,23 @@ def c4_step(X, P, fused_requant=False, ws=None):
         o = ops.qlinear(vq, sv, *P["o"])
         oq, so = ops.quantize_per_token(o)
         out["o"] = o
-    gu = ops.qlinear(oq, so, *P["gate_up"])               # [tokens, gate | up]
-    nf = gu.shape[1] // 2
-    g, u = gu[:, :nf], gu[:, nf:]                          # row-strided halves
-    hq, sh = ops.silu_mul_quantize(g, u)
+    if glu:
+        # gate and up in one GEMM with h = SiLU(gate) * up in its epilogue
+        # (gate and up never reach memory), then the per-token quantize of h.
+        # Not the default: on MI355X the epilogue's f64-exp SiLU runs at one
+        # wave per SIMD with nothing to hide it (GEMM 219-228 us against 182
+        # us without it), more than the 86 MiB of g|u traffic it saves.
+        h = ops.qlinear_glu(oq, so, *P["gate_up_glu"])
+        hq, sh = ops.quantize_per_token(h)
+        out["h"] = h
+    else:
+        gu = ops.qlinear(oq, so, *P["gate_up"])           # [tokens, gate | up]
+        nf = gu.shape[1] // 2
+        g, u = gu[:, :nf], gu[:, nf:]                      # row-strided halves
+        hq, sh = ops.silu_mul_quantize(g, u)
+        out.update({"gate": g, "up": u})
     d = ops.qlinear(hq, sh, *P["down"])
-    out.update({"oq": oq, "so": so, "gate": g, "up": u, "hq": hq, "sh": sh, "down": d})
+    out.update({"oq": oq, "so": so, "hq": hq, "sh": sh, "down": d})
     return out
 
 

@@ -429,6 +429,45 @@ int q8_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, i
   return launched(err, "q8_gemm launch");
 }
 
+int q8_glu_interleave(const int8_t* Wg, const double* sg, const float* bg, const int8_t* Wu,
+                      const double* su, const float* bu, int64_t F, int64_t K, int8_t* W, double* s,
+                      float* b, void* stream) {
+  Q8_REQUIRE(F >= 0 && K >= 0 && mul_ok(2 * F, K), "q8_glu_interleave: bad shape F=%lld K=%lld",
+             (long long)F, (long long)K);
+  Q8_REQUIRE(F % 32 == 0, "q8_glu_interleave: F (%lld) must be a multiple of 32", (long long)F);
+  Q8_REQUIRE(F == 0 || (sg && su && s && (K == 0 || (Wg && Wu && W))), "q8_glu_interleave: NULL pointer");
+  Q8_REQUIRE((bg == nullptr) == (bu == nullptr) && (bg == nullptr) == (b == nullptr),
+             "q8_glu_interleave: give both biases and the output bias, or none");
+  int rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_glu_interleave(Wg, Wu, sg, su, bg, bu, F, K, W, s, b, as_stream(stream)),
+                  "q8_glu_interleave launch");
+}
+
+int q8_gemm_glu_workspace(int64_t M, int64_t F, int64_t K, size_t* bytes) {
+  Q8_REQUIRE(M >= 0 && F >= 0 && K >= 0 && mul_ok(M, 8 * F), "q8_gemm_glu_workspace: bad shape");
+  Q8_REQUIRE(bytes != nullptr, "q8_gemm_glu_workspace: bytes is NULL");
+  *bytes = q8::gemm_glu_ws_bytes(M, F, K);
+  return Q8_OK;
+}
+
+int q8_gemm_glu(const int8_t* A, const int8_t* B, int64_t M, int64_t F, int64_t K, const double* sA,
+                int sA_mode, const double* sB, int sB_mode, const float* bias, float* h, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  Q8_REQUIRE(F >= 0 && F % 32 == 0, "q8_gemm_glu: F (%lld) must be a multiple of 32", (long long)F);
+  Q8_REQUIRE(mul_ok(M, 2 * F), "q8_gemm_glu: bad shape");
+  q8::GemmEpi e{};
+  int rc = gemm_common("q8_gemm_glu", A, B, M, 2 * F, K, 0, 0, sA, sA_mode, sB, sB_mode, Q8_EPI_ROWCOL, 0.0,
+                       bias, Q8_ACT_NONE, Q8_F32, h, &e);
+  if (rc != Q8_OK) return rc;
+  const size_t need = q8::gemm_glu_ws_bytes(M, F, K);
+  Q8_REQUIRE(need == 0 || (workspace && workspace_bytes >= need),
+             "q8_gemm_glu: needs a workspace of %zu bytes (got %zu)", need, workspace_bytes);
+  rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_gemm_glu(A, B, M, F, K, e, h, workspace, as_stream(stream)), "q8_gemm_glu launch");
+}
+
 int q8_generic_gemm_launches(int64_t* count) {
   Q8_REQUIRE(count != nullptr, "q8_generic_gemm_launches: count is NULL");
   *count = (int64_t)q8::g_generic_gemm_launches.load(std::memory_order_relaxed);
@@ -624,7 +663,7 @@ int q8_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int6
   return launched(err, "q8_gemm_requant launch");
 }
 
-// Route of q8_gemm_requant_dynamic: the fused cooperative kernel needs the
+// Route of q8_gemm_requant_dynamic: the fused kernel needs the
 // MFMA GEMM (M > 16, K a multiple of 16, 256-row tile offsets in 32 bits)
 // and every 256 x 256 tile resident at once.
 static bool dq_fused_route(int64_t M, int64_t N, int64_t K) {
@@ -690,6 +729,11 @@ int q8_gemm_requant_dynamic_status(const void* workspace, int64_t M, int* timed_
   e = hipMemcpy(&v, static_cast<const char*>(workspace) + off, sizeof(int), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
   *timed_out = v;
+  return Q8_OK;
+}
+
+int q8_debug_dq_force_timeout(int on) {
+  q8::g_dq_force_timeout.store(on ? 1 : 0, std::memory_order_relaxed);
   return Q8_OK;
 }
 

@@ -50,6 +50,7 @@
 // (v_dot4_i32_i8), no MFMA; 4 < M <= 16: one 16x16x64 MFMA per 16 weight
 // rows x 64 K-bytes (dot4 would make it VALU-bound); see the kernels' own
 // comments.
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 #include <type_traits>
@@ -232,7 +233,8 @@ __device__ __forceinline__ int half_wave_max(int v) {
 //   bit 5 int8 output: the fp32 value (MODE as above, bias and activation
 //   taken from the runtime epilogue) requantized with a static scale;
 //   bit 6 int8 output requantized per row with the row's dynamic absmax
-//   scale (cooperative launch; the OUT_DQ branch of k_qgemm's epilogue).
+//   scale (every tile resident at once; the OUT_DQ branch of k_qgemm's
+//   epilogue).
 template <int EPI>
 struct Epi {
   static constexpr bool OUT_I32 = (EPI & 16) != 0;
@@ -240,6 +242,7 @@ struct Epi {
   static constexpr bool OUT_DQ = (EPI & 64) != 0;
   static constexpr bool COLBLK = (EPI & 128) != 0;   // GemmEpi::col_blk addressing
   static constexpr bool IMPL = (EPI & 256) != 0;     // B is a conv frame (GemmEpi::cb)
+  static constexpr bool GLU = (EPI & 512) != 0;      // gate|up interleaved, h = silu(g) * u out
   static constexpr int MODE = (EPI >> 3) & 1;
   static constexpr bool BIAS = (EPI & 4) != 0;
   static constexpr int ACT = EPI & 3;
@@ -536,7 +539,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     const int lc = wn + 32 * j + r32;
     sbj[j] = (!OUT_I32 && MODE == 1) ? s_cols[lc] : 0.0;
     if constexpr (P::BIAS) bj[j] = e.bias[n0 + lc < N ? n0 + lc : N - 1];
-    else if constexpr (P::OUT_Q8 || P::OUT_DQ) bj[j] = e.bias ? e.bias[n0 + lc < N ? n0 + lc : N - 1] : 0.0f;
+    else if constexpr (P::OUT_Q8 || P::OUT_DQ || P::GLU) bj[j] = e.bias ? e.bias[n0 + lc < N ? n0 + lc : N - 1] : 0.0f;
     else bj[j] = 0.0f;
   }
   auto strip_out = [&](auto ic) {
@@ -653,7 +656,98 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     }
     }
   };
-  if constexpr (P::OUT_DQ) {
+  if constexpr (P::GLU) {
+    // Gate|up with SiLU(gate) * up (decomposition_pass.ts:197-230): B holds
+    // the gate and up weights interleaved in groups of 32 rows (packed
+    // column 64 g + c is gate feature 32 g + c, 64 g + 32 + c is up feature
+    // 32 g + c), and BN is a multiple of 128, so the wave's 32x32 blocks 2p
+    // and 2p + 1 hold the gate and up accumulators of the same 32 features.
+    // Per strip of 32 rows the accumulators go to the wave's LDS strip
+    // (accumulator layout, static register indices), then a rolled loop over
+    // the lane's 4-feature quads reads each quad's gate and up accumulators,
+    // takes both epilogues (E-rowcol, bias), h = fround(silu(g) * u) (a
+    // binary32 product of binary32 values is the rounded exact product) and
+    // stores the 16-byte quad of h ([M, N/2] fp32).  Rolled, so the code
+    // the wave runs stays small: the f64 exp of every SiLU inlined over the
+    // 256 values a lane holds would overflow the instruction cache.
+    static_assert(C::TN % 2 == 0 && MODE == 1, "GLU needs pairs of column blocks and the row x column scales");
+    constexpr int WH = C::WN / 2;                  // h columns of the wave
+    constexpr int LPRH = WH / 4, RPIH = 64 / LPRH, NQH = 32 / RPIH;
+    static_assert(NQH % 2 == 0, "quads in pairs");
+    const int64_t F = N / 2;
+    const int qcolh = 4 * (lane % LPRH), qrowh = lane / LPRH;
+    // the lane's four h columns are features qcolh .. qcolh + 3 of the wave:
+    // pair p = qcolh / 32, gate strip columns 64 p + qcolh % 32 + c, up 32 after
+    const int gcs = 64 * (qcolh / 32) + (qcolh % 32);
+    const int64_t hcol = (int64_t)(n0 + wn) / 2 + qcolh;
+    double sg4[4], su4[4];
+    float bg4[4], bu4[4];
+    const bool has_bias = e.bias != nullptr;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int lg = wn + gcs + c, lu = lg + 32;
+      sg4[c] = s_cols[lg];
+      su4[c] = s_cols[lu];
+      bg4[c] = has_bias ? e.bias[n0 + lg < N ? n0 + lg : N - 1] : 0.0f;
+      bu4[c] = has_bias ? e.bias[n0 + lu < N ? n0 + lu : N - 1] : 0.0f;
+    }
+    float* hout = static_cast<float*>(out);
+    const bool interior_h = m0 + BM <= M && n0 + BN <= N && (F % 4 == 0) &&
+                            (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    auto glu_strip = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) strip[((r >> 2) * 8 + kh * 4 + (r & 3)) * PITCH + 32 * j + r32] = acc[i][j][r];
+#pragma unroll 1
+      for (int it0 = 0; it0 < NQH; it0 += 2) {
+        float h[2][4];
+        int64_t rowg[2];
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2) {
+          const int srow = (it0 + u2) * RPIH + qrowh;           // strip row
+          rowg[u2] = m0 + wm + 32 * i + srow;
+          const v4i ag = *reinterpret_cast<const v4i*>(strip + srow * PITCH + gcs);
+          const v4i au = *reinterpret_cast<const v4i*>(strip + srow * PITCH + gcs + 32);
+          const double sr = s_rows[wm + 32 * i + srow];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float g = mul_acc_f32scale(ag[c], (float)(sr * sg4[c]));
+            float u = mul_acc_f32scale(au[c], (float)(sr * su4[c]));
+            if (has_bias) {
+              g = g + bg4[c];
+              u = u + bu4[c];
+            }
+            h[u2][c] = silu_js(g) * u;
+          }
+        }
+        if (interior_h) {
+#pragma unroll
+          for (int u2 = 0; u2 < 2; ++u2) {
+            const v4i hv{__float_as_int(h[u2][0]), __float_as_int(h[u2][1]), __float_as_int(h[u2][2]),
+                         __float_as_int(h[u2][3])};
+            v4i* dst = reinterpret_cast<v4i*>(hout + rowg[u2] * F + hcol);
+            if (e.h_plain) *dst = hv;
+            else __builtin_nontemporal_store(hv, dst);
+          }
+        } else {
+#pragma unroll
+          for (int u2 = 0; u2 < 2; ++u2)
+            if (rowg[u2] < M) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                if (hcol + c < F) hout[rowg[u2] * F + hcol + c] = h[u2][c];
+            }
+        }
+      }
+    };
+    glu_strip(std::integral_constant<int, 0>{});
+    if constexpr (C::TM > 1) glu_strip(std::integral_constant<int, 1>{});
+    if constexpr (C::TM > 2) glu_strip(std::integral_constant<int, 2>{});
+    if constexpr (C::TM > 3) glu_strip(std::integral_constant<int, 3>{});
+    static_assert(C::TM <= 4, "glu_strip calls cover TM <= 4");
+  } else if constexpr (P::OUT_DQ) {
     // Dynamic per-row requant: the row's scale is S-abs over all N columns,
     // so every tile of a row block must have seen its values first.
     //  A. per strip: the accumulators go to the wave's LDS strip; a rolled
@@ -663,8 +757,8 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     //     keys (LDS); the fp32 values go back to the accumulator registers
     //     in quad order;
     //  B. the tile's row keys are max-ed into the caller's workspace (one
-    //     32-bit atomic per row) and all workgroups (co-resident by the
-    //     cooperative launch) meet once: an arrival counter, polled with a
+    //     32-bit atomic per row) and all workgroups (co-resident: one per
+    //     CU, no more than the chip holds) meet once: an arrival counter, polled with a
     //     bound (a timed-out wait sets the status word and carries on with
     //     the keys it sees);
     //  C. each row's scale, and its binary32 reciprocal (NaN where the f32
@@ -793,12 +887,23 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     if constexpr (C::TM > 3) dq_values(std::integral_constant<int, 3>{});
     static_assert(C::TM <= 4 && C::TN * 16 == 4 * NQ, "dq_values covers TM <= 4; a strip is NQ quads per lane");
     __syncthreads();
-    // Agent-scope atomics; the workgroup barrier orders them before thread
-    // 0's release increment of the arrival counter.  The counter is polled
-    // relaxed (an acquire per poll would invalidate this XCD's L2 each
-    // time) and a single acquire fence follows the wait.
+    // Publication of the tile's row keys, then the grid-wide meeting.
+    // Ordering argument:
+    //  1. each publishing lane's agent-scope fetch_max is followed by that
+    //     lane's own agent-scope release fence, which waits until the
+    //     wave's atomics are performed at the device-coherent level
+    //     (vmcnt(0)) -- a workgroup barrier alone does not: its release is
+    //     workgroup-scoped and waits only for LDS traffic, so waves 1-3
+    //     could still have their atomics in flight;
+    //  2. the workgroup barrier then orders every wave's fence before
+    //     thread 0's release increment of the arrival counter;
+    //  3. a workgroup that sees the counter reach nwg (relaxed polls: an
+    //     acquire per poll would invalidate this XCD's L2 each time) runs
+    //     one agent-scope acquire fence before reading any key, so it sees
+    //     every key published before every increment it counted.
     if (tid < rows_a && tkey[tid] >= 0)
       __hip_atomic_fetch_max(&e.row_keys[m0 + tid], tkey[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (tid == 0) {
       __hip_atomic_fetch_add(e.sync, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -954,7 +1059,7 @@ std::atomic<long long> g_generic_gemm_launches{0};
 // 128x128 workgroups per CU overlap one's epilogue with the other's main
 // loop, which is why they win many mid-size shapes.  Returns the index of
 // the chosen tile in cands.
-static int gemm_tile_choice(int64_t M, int64_t N) {
+static int gemm_tile_choice(int64_t M, int64_t N, unsigned allowed = 0xF) {
   struct Cand { int bm, bn, per_cu; double tmin, tfull; };
   const Cand cands[] = {{256, 256, 1, 44.0, 63.0}, {256, 128, 1, 27.5, 40.0},
                         {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0}};
@@ -962,6 +1067,7 @@ static int gemm_tile_choice(int64_t M, int64_t N) {
   int best = 0;
   double best_cost = 1e300;
   for (int c = 0; c < 4; ++c) {
+    if (!((allowed >> c) & 1u)) continue;
     const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
     const int64_t slots = (int64_t)cus * cands[c].per_cu;
     const int64_t full = tiles / slots, rest = tiles % slots;
@@ -1116,6 +1222,159 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
   }
 }
 
+// ------------------------------------------------------------------ gate|up GEMM (GLU)
+// One output element h[m, f] per thread for the shapes the MFMA kernel does
+// not take (K % 16 != 0, unaligned operands): the gate and up dot products of
+// feature f over the interleaved weight, then the same arithmetic as the
+// MFMA epilogue.
+__global__ __launch_bounds__(256) void k_glu_generic(const int8_t* __restrict__ A,
+                                                     const int8_t* __restrict__ B, int M, int F, int K,
+                                                     GemmEpi e, float* __restrict__ h) {
+  const int64_t idx = blockIdx.x * 256LL + threadIdx.x;
+  if (idx >= (int64_t)M * F) return;
+  const int64_t m = idx / F, f = idx % F;
+  const int64_t pg = 64 * (f / 32) + f % 32, pu = pg + 32;
+  uint32_t sg = 0, su = 0;
+  for (int k = 0; k < K; ++k) {
+    sg += (uint32_t)((int)A[m * K + k] * (int)B[pg * K + k]);
+    su += (uint32_t)((int)A[m * K + k] * (int)B[pu * K + k]);
+  }
+  GemmEpi en = e;
+  en.act = 0;
+  const float g = epi_value((int)sg, m, pg, en), u = epi_value((int)su, m, pu, en);
+  h[idx] = silu_js(g) * u;
+}
+
+// h from the epilogue values of the interleaved columns ([M, 2F], bias
+// already added): h[m, f] = fround(silu(y[m, pg]) * y[m, pg + 32]).
+__global__ __launch_bounds__(256) void k_glu_combine(const float* __restrict__ y, int64_t M, int64_t F,
+                                                     float* __restrict__ h) {
+  const int64_t idx = blockIdx.x * 256LL + threadIdx.x;
+  if (idx >= M * F) return;
+  const int64_t m = idx / F, f = idx % F;
+  const int64_t pg = 64 * (f / 32) + f % 32;
+  const float* row = y + m * 2 * F;
+  h[idx] = silu_js(row[pg]) * row[pg + 32];
+}
+
+// Interleave per-channel packed gate and up weights (and their scales, and
+// optionally biases) into the layout of the GLU GEMM: packed row 64 g + c is
+// gate row 32 g + c, 64 g + 32 + c is up row 32 g + c.  F % 32 == 0.
+__global__ __launch_bounds__(256) void k_glu_interleave(const int8_t* __restrict__ Wg,
+                                                        const int8_t* __restrict__ Wu, int64_t F,
+                                                        int64_t K, int8_t* __restrict__ W) {
+  // one 16-byte chunk per thread (K % 16 == 0, 16-byte aligned rows)
+  const int64_t per_row = K / 16;
+  const int64_t total = 2 * F * per_row;
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t pr = i / per_row, c = i % per_row;
+    const int64_t g = pr / 64, w = pr % 64;
+    const int8_t* src = (w < 32 ? Wg : Wu) + (32 * g + (w & 31)) * K;
+    *reinterpret_cast<v4i*>(W + pr * K + 16 * c) = *reinterpret_cast<const v4i*>(src + 16 * c);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_glu_interleave_bytes(const int8_t* __restrict__ Wg,
+                                                              const int8_t* __restrict__ Wu, int64_t F,
+                                                              int64_t K, int8_t* __restrict__ W) {
+  const int64_t total = 2 * F * K;
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t pr = i / K, c = i % K;
+    const int64_t g = pr / 64, w = pr % 64;
+    W[i] = ((w < 32 ? Wg : Wu) + (32 * g + (w & 31)) * K)[c];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_glu_interleave_vec(const double* __restrict__ sg,
+                                                            const double* __restrict__ su,
+                                                            const float* __restrict__ bg,
+                                                            const float* __restrict__ bu, int64_t F,
+                                                            double* __restrict__ s, float* __restrict__ b) {
+  const int64_t pr = blockIdx.x * 256LL + threadIdx.x;
+  if (pr >= 2 * F) return;
+  const int64_t g = pr / 64, w = pr % 64, f = 32 * g + (w & 31);
+  s[pr] = w < 32 ? sg[f] : su[f];
+  if (b) b[pr] = w < 32 ? bg[f] : bu[f];
+}
+
+hipError_t launch_glu_interleave(const int8_t* Wg, const int8_t* Wu, const double* sg, const double* su,
+                                 const float* bg, const float* bu, int64_t F, int64_t K, int8_t* W,
+                                 double* s, float* b, hipStream_t st) {
+  if (F == 0) return hipSuccess;
+  const bool vec = (K % 16) == 0 && ((reinterpret_cast<uintptr_t>(Wg) | reinterpret_cast<uintptr_t>(Wu) |
+                                      reinterpret_cast<uintptr_t>(W)) & 15) == 0;
+  if (K > 0) {
+    if (vec) {
+      const int64_t total = 2 * F * (K / 16);
+      const unsigned g = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+      hipLaunchKernelGGL(k_glu_interleave, dim3(g), dim3(256), 0, st, Wg, Wu, F, K, W);
+    } else {
+      // byte copies: the same kernel with K seen as not a multiple of 16
+      const int64_t total = 2 * F * K;
+      const unsigned g = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+      hipLaunchKernelGGL(k_glu_interleave_bytes, dim3(g), dim3(256), 0, st, Wg, Wu, F, K, W);
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL(k_glu_interleave_vec, dim3((unsigned)((2 * F + 255) / 256)), dim3(256), 0, st, sg, su,
+                     bg, bu, F, s, b);
+  return hipGetLastError();
+}
+
+size_t gemm_glu_ws_bytes(int64_t M, int64_t F, int64_t K) {
+  (void)K;
+  return M <= 16 ? (size_t)((M * 2 * F * 4 + 255) / 256 * 256) : 0;
+}
+
+hipError_t launch_gemm_glu(const int8_t* A, const int8_t* B, int64_t M, int64_t F, int64_t K,
+                           const GemmEpi& e, float* h, void* ws, hipStream_t st) {
+  if (M == 0 || F == 0) return hipSuccess;
+  const int64_t N = 2 * F;
+  if (M <= 16) {
+    // decode: the GEMV's epilogue values of the interleaved columns into the
+    // workspace, then h from pairs of them
+    float* y = static_cast<float*>(ws);
+    hipError_t err = launch_gemv(A, B, M, N, K, e, y, st);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_glu_combine, dim3((unsigned)((M * F + 255) / 256)), dim3(256), 0, st, y, M, F, h);
+    return hipGetLastError();
+  }
+  GemmEpi eg = e;
+  eg.act = 0;
+  const bool vec = (K % 16 == 0) && K > 0 && (256 * K < (int64_t)OOB) &&
+                   ((reinterpret_cast<uintptr_t>(A) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(B) & 15) == 0);
+  if (!vec) {
+    g_generic_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    hipLaunchKernelGGL(k_glu_generic, dim3((unsigned)((M * F + 255) / 256)), dim3(256), 0, st, A, B, (int)M,
+                       (int)F, (int)K, eg, h);
+    return hipGetLastError();
+  }
+  // 256 x 256 or 128 x 128: the 64 x 64 tile has one 32-column block per
+  // wave (no gate/up pairs), and the cost model picks 256 x 128 for no
+  // shape of interest
+  const int c = gemm_tile_choice(M, N, 0x5u);
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+  switch (c) {
+    case 0: {
+      const int tm = (Mi + 255) / 256, tn = (Ni + 255) / 256;
+      constexpr unsigned lds = (unsigned)qgemm_lds<256, 256>();
+      hipLaunchKernelGGL((k_qgemm<256, 256, 520>), dim3((unsigned)(tm * tn)), dim3(GEMM_THREADS), lds, st, A,
+                         B, Mi, Ni, Ki, tm, tn, eg, (void*)h);
+      break;
+    }
+    default: {
+      const int tm = (Mi + 127) / 128, tn = (Ni + 127) / 128;
+      constexpr unsigned lds = (unsigned)qgemm_lds<128, 128>();
+      hipLaunchKernelGGL((k_qgemm<128, 128, 520>), dim3((unsigned)(tm * tn)), dim3(GEMM_THREADS), lds, st, A,
+                         B, Mi, Ni, Ki, tm, tn, eg, (void*)h);
+      break;
+    }
+  }
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ dynamic requant GEMM
 // Workspace: [M] int32 row keys (rounded up to 256 bytes), then the arrival
 // counter and the status word.
@@ -1152,6 +1411,12 @@ bool gemm_dq_fits(int64_t M, int64_t N) {
   return tiles <= dq_capacity();
 }
 
+// Test hook (q8_debug_dq_force_timeout): while set, the arrival count a
+// launch waits for is one more than its workgroups, so every wait runs out
+// after a few polls and the status word reports it (the kernel still ends
+// normally; its output is then unreliable).
+std::atomic<int> g_dq_force_timeout{0};
+
 hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                           GemmEpi e, int8_t* out, double* scales, void* ws, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
@@ -1167,11 +1432,7 @@ hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N
   e.q_scales = scales;
   e.nwg = nwg;
   e.spin_limit = 1 << 18;      // a poll is a device-coherent load (~1 us) and a short sleep: < 1 s in all
-  // Test hook for the timeout report: the arrival count can never reach
-  // nwg + 1, so every workgroup's wait runs out after a few polls (the
-  // kernel still ends normally; its output is then unreliable).
-  const char* t = getenv("Q8_DQ_TEST_TIMEOUT");
-  if (t && t[0] == '1') {
+  if (g_dq_force_timeout.load(std::memory_order_relaxed)) {
     e.nwg = nwg + 1;
     e.spin_limit = 64;
   }
@@ -1179,11 +1440,25 @@ hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N
   hipLaunchKernelGGL(k_dq_init, dim3(ig), dim3(256), 0, st, e.row_keys, M, e.sync, e.status);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  int Mi = (int)M, Ni = (int)N, Ki = (int)K;
-  void* args[] = {(void*)&A, (void*)&B, &Mi, &Ni, &Ki, (void*)&tm, (void*)&tn, &e, (void*)&out};
-  const void* kern = e.mode == 1 ? (const void*)k_qgemm<256, 256, 72> : (const void*)k_qgemm<256, 256, 64>;
-  return hipLaunchCooperativeKernel(kern, dim3((unsigned)nwg), dim3(GEMM_THREADS), args,
-                                    (unsigned)qgemm_lds<256, 256>(), st);
+  // An ordinary launch.  Every workgroup needs a CU of its own (LDS) and
+  // nwg <= dq_capacity(), so on a device that runs nothing else all of them
+  // are dispatched at once: the kernels of one stream run one after another,
+  // and the kernel before this one has ended before its first workgroup
+  // starts.  Work on other streams or processes can hold CUs for a while;
+  // the bounded wait then runs out instead of hanging, and the status word
+  // (q8_gemm_requant_dynamic_status) reports it.  A cooperative launch
+  // would guarantee co-residency instead, at ~20 us per call on MI355X (the
+  // fused O projection of C4: 121 vs 101 us), which is more than the
+  // fusion saves.
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+  constexpr unsigned lds = (unsigned)qgemm_lds<256, 256>();
+  if (e.mode == 1)
+    hipLaunchKernelGGL((k_qgemm<256, 256, 72>), dim3((unsigned)nwg), dim3(GEMM_THREADS), lds, st, A, B, Mi,
+                       Ni, Ki, tm, tn, e, (void*)out);
+  else
+    hipLaunchKernelGGL((k_qgemm<256, 256, 64>), dim3((unsigned)nwg), dim3(GEMM_THREADS), lds, st, A, B, Mi,
+                       Ni, Ki, tm, tn, e, (void*)out);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
@@ -1645,6 +1920,8 @@ hipError_t setup_kernel_attributes() {
   Q8_EPI_CODES(Q8_SET_64)
   Q8_SET_256(64)
   Q8_SET_256(72)
+  Q8_SET_256(520)
+  Q8_SET_128(520)
   Q8_EPI_CODES_CONV(Q8_SET_128)
   Q8_EPI_CODES_CONV(Q8_SET_64)
 #undef Q8_SET_256

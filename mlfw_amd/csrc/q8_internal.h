@@ -29,8 +29,9 @@ struct GemmEpi {
   int q_fast;           // s_q admits the fast path (normal, in [2^-100, 2^100])
   // out_dq: the fp32 value is requantized per row with the row's own
   // absmax scale (q8_gemm_requant_dynamic).  All workgroups are co-resident
-  // (cooperative launch): each publishes its rows' absmax keys, they meet
-  // once grid-wide, then quantize the values they still hold.
+  // (one per CU, no more than the chip holds): each publishes its rows'
+  // absmax keys, they meet once grid-wide (a bounded wait), then quantize
+  // the values they still hold.
   int out_dq;
   int* row_keys;        // [M] absmax keys, -1 at launch
   unsigned* sync;       // arrival counter, 0 at launch
@@ -42,6 +43,9 @@ struct GemmEpi {
   // column j is position j % col_blk of image j / col_blk, and element
   // (row, j) is stored at (j / col_blk) * blk_stride + row * ld_out +
   // j % col_blk.  col_blk = 0: plain row-major [M, N].
+  // GLU output (q8_gemm_glu): 1 stores h with plain stores (kept in the
+  // caches for the quantize that reads it next), 0 non-temporal
+  int h_plain;
   int64_t col_blk;
   int64_t blk_stride;
   int64_t ld_out;
@@ -109,13 +113,25 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 // GEMM with the dynamic per-row requant epilogue (e.out_dq fields filled by
 // the caller except the meeting point, which comes from `ws`).  Returns
 // hipErrorCooperativeLaunchTooLarge when the tiles do not fit the chip at
-// once; gemm_dq_fits tells beforehand.
+// once; gemm_dq_fits tells beforehand.  g_dq_force_timeout (test hook) makes
+// every launch's grid-wide wait run out.
+extern std::atomic<int> g_dq_force_timeout;
 bool gemm_dq_fits(int64_t M, int64_t N);
 size_t gemm_dq_ws_bytes(int64_t M);
 hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                           GemmEpi e, int8_t* out, double* scales, void* ws, hipStream_t st);
 hipError_t launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                        const GemmEpi& e, void* out, hipStream_t st);
+// Gate|up GEMM with h = fround(silu(g) * u) fused (B interleaved by
+// launch_glu_interleave; e in MODE 1, bias in the interleaved order or null).
+// M <= 16 needs gemm_glu_ws_bytes of workspace (the GEMV's values of the
+// 2F interleaved columns), other shapes none.
+hipError_t launch_glu_interleave(const int8_t* Wg, const int8_t* Wu, const double* sg, const double* su,
+                                 const float* bg, const float* bu, int64_t F, int64_t K, int8_t* W,
+                                 double* s, float* b, hipStream_t st);
+size_t gemm_glu_ws_bytes(int64_t M, int64_t F, int64_t K);
+hipError_t launch_gemm_glu(const int8_t* A, const int8_t* B, int64_t M, int64_t F, int64_t K,
+                           const GemmEpi& e, float* h, void* ws, hipStream_t st);
 
 // 4-bit per-group weights (q8_w4.hip).
 hipError_t launch_pack_w4(const float* W, int64_t N, int64_t K, int64_t group, uint8_t* wq4,

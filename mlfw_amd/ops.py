@@ -279,6 +279,69 @@ def qlinear(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor
     return out
 
 
+def glu_interleave(gate, up, gate_bias: torch.Tensor | None = None, up_bias: torch.Tensor | None = None):
+    """The weight of qlinear_glu from two per-channel packed weights
+    (pack_weight results (int8 [F,K], f64 [F]) for gate and up, F a multiple
+    of 32): rows interleaved in groups of 32 (packed row 64 j + c is gate row
+    32 j + c, 64 j + 32 + c is up row 32 j + c), scales and optional biases
+    alike.  Returns (int8 [2F,K], f64 [2F]) or, with biases, (..., f32 [2F])."""
+    (Wg, sg), (Wu, su) = gate, up
+    for t, dt, what in ((Wg, torch.int8, "gate codes"), (Wu, torch.int8, "up codes")):
+        _need(t, dt, what, ndim=2)
+    F, K = Wg.shape
+    if tuple(Wu.shape) != (F, K):
+        raise ValueError("glu_interleave: gate and up weights must have the same shape")
+    for t, what in ((sg, "gate scales"), (su, "up scales")):
+        _need(t, torch.float64, what)
+        if t.numel() != F:
+            raise ValueError(f"glu_interleave: {what} must be per channel ({F} values)")
+    if (gate_bias is None) != (up_bias is None):
+        raise ValueError("glu_interleave: give both biases or none")
+    W = torch.empty((2 * F, K), dtype=torch.int8, device=Wg.device)
+    s = torch.empty(2 * F, dtype=torch.float64, device=Wg.device)
+    b = None
+    if gate_bias is not None:
+        for t, what in ((gate_bias, "gate bias"), (up_bias, "up bias")):
+            _need(t, torch.float32, what)
+            if t.numel() != F:
+                raise ValueError(f"glu_interleave: {what} must have {F} elements")
+        b = torch.empty(2 * F, dtype=torch.float32, device=Wg.device)
+    _call("q8_glu_interleave", _ptr(Wg), _ptr(sg), _ptr(gate_bias), _ptr(Wu), _ptr(su), _ptr(up_bias), F, K,
+          _ptr(W), _ptr(s), _ptr(b), _stream())
+    return (W, s) if b is None else (W, s, b)
+
+
+def qlinear_glu(A: torch.Tensor, sA: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
+                bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Gate and up linears with h = fround(silu(g) * u) fused into one GEMM
+    (q8_gemm_glu): W, sW (and bias) from glu_interleave; returns h fp32
+    [M, F], bit for bit qlinear of each half followed by silu_mul."""
+    M, N, K = _mk(A, W)
+    _need(sA, torch.float64, "sA")
+    _need(sW, torch.float64, "sW")
+    if N % 64 != 0:
+        raise ValueError("qlinear_glu: the interleaved weight must have 2F rows, F a multiple of 32")
+    F = N // 2
+    if sA.numel() not in (1, M) or sW.numel() not in (1, N):
+        raise ValueError("qlinear_glu: scale sizes must be 1 or M (sA) and 1 or 2F (sW)")
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.numel() != N:
+            raise ValueError("qlinear_glu: bias must have 2F elements (interleaved)")
+    out = _out(out, (M, F), torch.float32, A, "out")
+    nb = C.c_size_t(0)
+    L.call("q8_gemm_glu_workspace", M, F, K, C.byref(nb))
+    if nb.value and (workspace is None or workspace.numel() < nb.value):
+        workspace = torch.empty(nb.value, dtype=torch.int8, device=A.device)
+    _call("q8_gemm_glu", _ptr(A), _ptr(W), M, F, K,
+          _ptr(sA), L.Q8_PER_TOKEN if sA.numel() == M and M != 1 else L.Q8_PER_TENSOR,
+          _ptr(sW), L.Q8_PER_CHANNEL if sW.numel() == N else L.Q8_PER_TENSOR,
+          _ptr(bias), _ptr(out), _ptr(workspace), workspace.numel() if workspace is not None else 0, _stream(),
+          keep=(workspace,) if workspace is not None else ())
+    return out
+
+
 def quantized_dot(A: torch.Tensor, B: torch.Tensor, zpA: int = 0, zpB: int = 0,
                   out: torch.Tensor | None = None) -> torch.Tensor:
     """The reference's quantized_dot: int32 [M,N] = sum_k (A[m,k] - zpA) *
@@ -395,14 +458,21 @@ def requant_dynamic_workspace(M: int, N: int, K: int):
 def qlinear_requant_dynamic(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, sB: torch.Tensor,
                             bias: torch.Tensor | None = None, act: str | None = None,
                             out: torch.Tensor | None = None, scales: torch.Tensor | None = None,
-                            workspace: torch.Tensor | None = None):
+                            workspace: torch.Tensor | None = None, check: bool = False):
     """int8 linear whose fp32 result (the qlinear epilogue) is requantized per
     row with the row's own dynamic absmax scale, as the next layer's
     per-token quantize takes it: returns (int8 codes [M, N], f64 scales [M]),
     bit for bit qlinear followed by quantize_per_token.  When every tile of
-    the MFMA GEMM fits the chip at once the fp32 tensor never reaches memory
-    (one cooperative launch); the workspace holds the row keys then, or the
-    fp32 result on the fallback route."""
+    the MFMA GEMM has a CU of its own the fp32 tensor never reaches memory
+    (one launch whose tiles meet once grid-wide); the workspace holds the
+    row keys then, or the fp32 result on the fallback route.
+
+    The grid-wide wait is bounded: if other streams or processes hold CUs
+    long enough for it to run out, the result is unreliable and the status
+    word says so.  check=True reads that word (a stream synchronization) and
+    raises RuntimeError on a timeout; callers that share the device should
+    check, callers that cannot synchronize (graph capture) read it later
+    with requant_dynamic_timed_out."""
     M, N, K = _mk(A, B)
     _need(sA, torch.float64, "sA")
     _need(sB, torch.float64, "sB")
@@ -414,7 +484,7 @@ def qlinear_requant_dynamic(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, 
             raise ValueError("qlinear_requant_dynamic: bias must have N elements")
     out = _out(out, (M, N), torch.int8, A, "out")
     scales = _out(scales, M, torch.float64, A, "scales")
-    nb, _ = requant_dynamic_workspace(M, N, K)
+    nb, fused = requant_dynamic_workspace(M, N, K)
     if workspace is None or workspace.numel() < nb:
         workspace = torch.empty(max(nb, 1), dtype=torch.int8, device=A.device)
     _call("q8_gemm_requant_dynamic", _ptr(A), _ptr(B), M, N, K,
@@ -422,7 +492,20 @@ def qlinear_requant_dynamic(A: torch.Tensor, sA: torch.Tensor, B: torch.Tensor, 
           _ptr(sB), L.Q8_PER_CHANNEL if sB.numel() == N and N != 1 else L.Q8_PER_TENSOR,
           L.Q8_EPI_ROWCOL, 0.0, _ptr(bias), _ACT[act], _ptr(out), _ptr(scales), _ptr(workspace),
           workspace.numel(), _stream(), keep=(workspace,))
+    if check and fused and requant_dynamic_timed_out(workspace, M):
+        raise RuntimeError("qlinear_requant_dynamic: the grid-wide wait ran out (other work held CUs); "
+                           "the codes and scales of this call are unreliable")
     return out, scales
+
+
+def requant_dynamic_timed_out(workspace: torch.Tensor, M: int) -> bool:
+    """Whether the last qlinear_requant_dynamic call on this workspace (M
+    rows) ran out of its grid-wide wait; meaningful after a call that took
+    the fused route (requant_dynamic_workspace).  Synchronizes the current
+    stream."""
+    flag = C.c_int(0)
+    L.call("q8_gemm_requant_dynamic_status", _ptr(workspace), M, C.byref(flag), _stream())
+    return flag.value != 0
 
 
 def pack_weight_int4(W: torch.Tensor, group_size: int):

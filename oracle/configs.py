@@ -91,7 +91,7 @@ def c4_expected_rows(inp, rows, packed=None):
     u = qlinear_rows(ob, *P["up"])
     h = o.silu_mul(g, u)
     d = qlinear_rows(h, *P["down"])
-    return {"qkv": qkv, "o": ob, "gate": g, "up": u, "down": d}
+    return {"qkv": qkv, "o": ob, "gate": g, "up": u, "h": h, "down": d}
 
 
 def c5_inputs(with_quant_tensor=True):

@@ -96,23 +96,37 @@ def exact_acc(Aq, Bq):
     return (Aq.astype(np.float64) @ Bq.astype(np.float64).T).astype(np.int32)
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_c4_decoder_projections(mods, oracle, fused):
+def interleave_rows(g, u):
+    """numpy form of the GLU weight layout (groups of 32 gate rows, then the
+    same 32 up rows)."""
+    F = g.shape[0]
+    out = np.empty((2 * F,) + g.shape[1:], g.dtype)
+    for j in range(F // 32):
+        out[64 * j:64 * j + 32] = g[32 * j:32 * j + 32]
+        out[64 * j + 32:64 * j + 64] = u[32 * j:32 * j + 32]
+    return out
+
+
+@pytest.mark.parametrize("fused,glu", [(False, True), (True, True), (False, False)])
+def test_c4_decoder_projections(mods, oracle, fused, glu):
     """Every stage of the projection set on all 2048 tokens, each fed the
     device's own inputs: int32 accumulators against an exact f64 matmul, the
     per-channel epilogue, the per-token quantizes (the O projection's fused
-    into its GEMM when `fused`) and SiLU*up requant against the oracle; plus
-    8 tokens end to end from X."""
+    into its GEMM when `fused`), SiLU*up (in the gate|up GEMM's epilogue
+    when `glu`) and its requant against the oracle; plus 8 tokens end to end
+    from X."""
     C, O, OC = mods
     inp = OC.c4_inputs()
     packed_ref = {k: OC.pack_pc(w, 0) for k, w in inp["W"].items()}
     P = C.c4_prepare({k: dev(w) for k, w in inp["W"].items()})
-    # gate and up run as one GEMM over the concatenated weight
+    # gate and up run as one GEMM: over the concatenated weight, or the
+    # interleaved one with SiLU*up fused
     packed_ref["gate_up"] = tuple(np.concatenate([packed_ref["gate"][i], packed_ref["up"][i]]) for i in (0, 1))
+    packed_ref["gate_up_glu"] = tuple(interleave_rows(packed_ref["gate"][i], packed_ref["up"][i]) for i in (0, 1))
     for k in P:
         same_bits(host(P[k][1]), packed_ref[k][1], f"C4 {k} scales")
         same_bits(host(P[k][0]), packed_ref[k][0], f"C4 {k} codes")
-    out = C.c4_step(dev(inp["X"]), P, fused_requant=fused)
+    out = C.c4_step(dev(inp["X"]), P, fused_requant=fused, glu=glu)
     h = {k: host(v) for k, v in out.items()}
 
     def quant(x, q, s, what):
@@ -131,15 +145,21 @@ def test_c4_decoder_projections(mods, oracle, fused):
     if not fused:
         same_bits(h["o"], o_ref, "C4 o (all rows)")
     quant(o_ref, h["oq"], h["so"], "C4 o requant" + (" (fused in the GEMM)" if fused else ""))
-    gu = np.concatenate([h["gate"], h["up"]], 1)
-    linear(h["oq"], h["so"], "gate_up", gu, "C4 gate|up (all rows)")
-    hh = oracle.silu_mul(h["gate"], h["up"])
+    if glu:
+        g_ref = oracle.epilogue(exact_acc(h["oq"], packed_ref["gate"][0]), "rowcol", h["so"], packed_ref["gate"][1])
+        u_ref = oracle.epilogue(exact_acc(h["oq"], packed_ref["up"][0]), "rowcol", h["so"], packed_ref["up"][1])
+        hh = oracle.silu_mul(g_ref, u_ref)
+        same_bits(h["h"], hh, "C4 silu(gate)*up in the gate|up epilogue (all rows)")
+    else:
+        gu = np.concatenate([h["gate"], h["up"]], 1)
+        linear(h["oq"], h["so"], "gate_up", gu, "C4 gate|up (all rows)")
+        hh = oracle.silu_mul(h["gate"], h["up"])
     quant(hh, h["hq"], h["sh"], "C4 silu*up requant")
     linear(h["hq"], h["sh"], "down", h["down"], "C4 down (all rows)")
     # 8 tokens end to end from X
     rows = np.array([0, 1, 777, 1023, 1024, 1500, 2046, 2047])
     ref = OC.c4_expected_rows(inp, rows, packed_ref)
-    for k in ("qkv", "gate", "up", "down"):
+    for k in ("qkv", "down") + (("h",) if glu else ("gate", "up")):
         same_bits(h[k][rows], ref[k], f"C4 {k} end to end")
     so_ref = oracle.scales_per_token(ref["o"])
     same_bits(h["so"][rows], so_ref, "C4 o scales end to end")

@@ -174,7 +174,7 @@ def test_requant_dynamic_routes_and_status(ops):
     assert flag.value == 0
 
 
-def test_requant_dynamic_reports_a_timed_out_wait(ops, monkeypatch):
+def test_requant_dynamic_reports_a_timed_out_wait(ops):
     """The host-forced timeout (an arrival target the grid never reaches,
     a short bound): every workgroup's wait ends, the status word reports it,
     and the next ordinary call clears it and is exact again."""
@@ -195,11 +195,15 @@ def test_requant_dynamic_reports_a_timed_out_wait(ops, monkeypatch):
         _lib.call("q8_gemm_requant_dynamic_status", C.c_void_p(ws.data_ptr()), M, C.byref(flag), st)
         return flag.value
 
-    monkeypatch.setenv("Q8_DQ_TEST_TIMEOUT", "1")
-    ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws)
-    assert status() == 1
-    monkeypatch.delenv("Q8_DQ_TEST_TIMEOUT")
-    q, s = ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws)
+    _lib.call("q8_debug_dq_force_timeout", 1)
+    try:
+        ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws)
+        assert status() == 1
+        with pytest.raises(RuntimeError, match="wait ran out"):
+            ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws, check=True)
+    finally:
+        _lib.call("q8_debug_dq_force_timeout", 0)
+    q, s = ops.qlinear_requant_dynamic(dev(A), dev(sA), dev(B), dev(sB), workspace=ws, check=True)
     assert status() == 0
     y = ops.qlinear(dev(A), dev(sA), dev(B), dev(sB))
     q_ref, s_ref = ops.quantize_per_token(y)
