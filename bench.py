@@ -336,6 +336,22 @@ def bench_conv():
     return res
 
 
+def bench_napi_plans(calls=200):
+    """Whole plans through the Node drop-in (mlfw_amd/node/plan_bench.js):
+    the 'hip' runtime backend's runPlan over the N-API addon, per-call host
+    time for C2 (batch 256) and a four-linear one-token decode chain, eager
+    and as replayed HIP graphs, with inputs uploaded every call and pinned
+    resident.  Runs in a child process (its own HIP context)."""
+    node = shutil.which("node")
+    if node is None:
+        return {"napi_plans": {"error": "node is not installed"}}
+    script = os.path.join(ROOT, "mlfw_amd", "node", "plan_bench.js")
+    r = subprocess.run([node, script, str(calls)], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"napi_plans": {"error": f"plan_bench.js exited {r.returncode}: {r.stderr[-400:]}"}}
+    return {"napi_plans": json.loads(r.stdout.strip().splitlines()[-1])}
+
+
 # ---------------------------------------------------------------- ceilings
 def ceilings():
     """Practical ceilings measured on this box (mlfw_amd/libq8ceiling.so):
@@ -507,7 +523,7 @@ def main():
     if not args.no_secondary:
         c4 = lambda: bench_c4(fused_requant=not args.no_fused_requant)
         for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", c4),
-                         ("conv", bench_conv)):
+                         ("conv", bench_conv), ("napi_plans", bench_napi_plans)):
             log(f"[bench] secondary {name}")
             try:
                 secondary.update(fn())

@@ -111,6 +111,26 @@ int q8_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int q8_memset(void* dst, int value, size_t bytes, void* stream);
 int q8_stream_sync(void* stream);
 
+/* One stream for a host runtime's launches, and whole launch sequences
+ * captured on it and replayed: the reference's device stream and eager
+ * graphs (src/runtime/node/cuda/device.ts:14-35; cuStreamBeginCapture /
+ * cuStreamEndCapture / cuGraphInstantiateWithFlags / cuGraphLaunch /
+ * cuGraphExecDestroy through koffi, src/runtime/node/cuda/ffi.ts:80-84,
+ * used by eager_graph.ts and the plan runner, device_plan.ts:178-218).
+ * The stream has the default priority.  Capture is thread-local; while a
+ * stream captures, entry points that block (q8_h2d, q8_d2h,
+ * q8_stream_sync) fail on it, and launches are recorded, not run.
+ * q8_graph_capture_end instantiates the captured sequence; q8_graph_launch
+ * replays it on a stream (the device buffers it names must stay allocated
+ * while the graph exists).  No library call records a memset node: buffers
+ * that must start at zero are cleared by fill kernels. */
+int q8_stream_create(void** stream);
+int q8_stream_destroy(void* stream);
+int q8_graph_capture_begin(void* stream);
+int q8_graph_capture_end(void* stream, void** graph_exec);
+int q8_graph_launch(void* graph_exec, void* stream);
+int q8_graph_destroy(void* graph_exec);
+
 /* ---------------------------------------------------------------- inputs */
 
 /* Seeded synthetic inputs, counter-based form of mulberry32

@@ -61,6 +61,12 @@ SIGNATURES = {
     "q8_d2h": [_vp, _vp, C.c_size_t, _vp],
     "q8_memset": [_vp, _int, C.c_size_t, _vp],
     "q8_stream_sync": [_vp],
+    "q8_stream_create": [_vp],
+    "q8_stream_destroy": [_vp],
+    "q8_graph_capture_begin": [_vp],
+    "q8_graph_capture_end": [_vp, _vp],
+    "q8_graph_launch": [_vp, _vp],
+    "q8_graph_destroy": [_vp],
     "q8_fill_normal": [_vp, _i64, C.c_uint32, C.c_uint64, _dbl, _dbl, _vp],
     "q8_fill_uniform": [_vp, _i64, C.c_uint32, C.c_uint64, _dbl, _dbl, _vp],
     "q8_apply_outliers": [_vp, _i64, C.c_uint32, _dbl, _dbl, _vp],

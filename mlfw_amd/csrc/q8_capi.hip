@@ -264,6 +264,57 @@ int q8_stream_sync(void* stream) {
   return launched(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
 }
 
+int q8_stream_create(void** stream) {
+  Q8_REQUIRE(stream != nullptr, "q8_stream_create: stream is NULL");
+  *stream = nullptr;
+  int rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  hipStream_t s = nullptr;
+  // default priority; non-blocking so the legacy null stream never joins it
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
+  *stream = s;
+  return launched(hipSuccess, "q8_stream_create");
+}
+
+int q8_stream_destroy(void* stream) {
+  if (stream == nullptr) return Q8_OK;
+  return launched(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+}
+
+int q8_graph_capture_begin(void* stream) {
+  Q8_REQUIRE(stream != nullptr, "q8_graph_capture_begin: capture needs a created stream, not the null stream");
+  return launched(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
+                  "hipStreamBeginCapture");
+}
+
+int q8_graph_capture_end(void* stream, void** graph_exec) {
+  Q8_REQUIRE(stream != nullptr && graph_exec != nullptr, "q8_graph_capture_end: NULL argument");
+  *graph_exec = nullptr;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(as_stream(stream), &g);
+  if (e != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return hip_fail(e, "hipStreamEndCapture");
+  }
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph_exec = x;
+  return launched(hipSuccess, "q8_graph_capture_end");
+}
+
+int q8_graph_launch(void* graph_exec, void* stream) {
+  Q8_REQUIRE(graph_exec != nullptr, "q8_graph_launch: graph_exec is NULL");
+  return launched(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)), "hipGraphLaunch");
+}
+
+int q8_graph_destroy(void* graph_exec) {
+  if (graph_exec == nullptr) return Q8_OK;
+  return launched(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+}
+
 int q8_fill_normal(float* out, int64_t n, uint32_t seed, uint64_t offset, double mean,
                    double std, void* stream) {
   Q8_REQUIRE(n >= 0, "q8_fill_normal: n < 0");

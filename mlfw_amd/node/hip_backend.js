@@ -294,7 +294,7 @@ function detectInt8Kernel(primFunc) {
 // f32 scale vector) is cached beside it.  markHostDirty(array) drops the
 // copies of an array the host rewrote.
 const stats = { uploadBytes: 0, constUploadBytes: 0, downloadBytes: 0, launches: 0, fusedLinears: 0,
-                dynamicLinears: 0 };
+                dynamicLinears: 0, residentSkips: 0, graphCaptures: 0, graphReplays: 0 };
 const _resident = new WeakMap();
 
 function resetStats() { for (const k of Object.keys(stats)) stats[k] = 0; }
@@ -320,10 +320,14 @@ function residentConst(arr, variant, derive) {
     upload(b, host, true);
     m.set(variant, b);
   }
+  if (_recordConsts) _recordConsts.push(b);
   return b;
 }
 
-function markHostDirty(arr) { _resident.delete(arr); }
+function markHostDirty(arr) {
+  _resident.delete(arr);
+  _constEpoch++;
+}
 
 // ---------------------------------------------------------------- runtime backend
 const SRC_CODE = { i8: 'Q8_I8', ui8: 'Q8_U8', i32: 'Q8_I32' };
@@ -331,25 +335,42 @@ const ACT_CODE = { none: 'Q8_ACT_NONE', relu: 'Q8_ACT_RELU', silu: 'Q8_ACT_SILU'
 
 /** Device buffers of one kernel instance (or plan), reused across runs. */
 class DeviceArgs {
-  constructor() { this.bufs = new Map(); }
+  // graphed: the owner captures graphs that may name these buffers
+  constructor(graphed = false) { this.bufs = new Map(); this.epoch = 0; this.retired = []; this.graphed = graphed; }
   get(key, bytes) {
     let b = this.bufs.get(key);
     if (!b || q8().bytes(b) < bytes) {
-      if (b) q8().free(b);
+      // a replaced buffer may still be named by a captured graph: it is
+      // retired, not freed, until the owner drops that graph
+      if (b && this.graphed) this.retired.push(b);
+      else if (b) q8().free(b);
       b = q8().alloc(Math.max(bytes, 1));
       this.bufs.set(key, b);
+      this.epoch++;
     }
     return b;
   }
   f64(key, values) {                    // a small constant f64 array, uploaded once
     const k = `${key}:${values.join(',')}`;
     let b = this.bufs.get(k);
-    if (!b) { b = q8().alloc(8 * values.length); upload(b, new Float64Array(values), true); this.bufs.set(k, b); }
+    if (!b) {
+      b = q8().alloc(8 * values.length);
+      upload(b, new Float64Array(values), true);
+      this.bufs.set(k, b);
+      this.epoch++;
+    }
     return b;
+  }
+  live() { return [...this.bufs.values()]; }
+  freeRetired() {
+    for (const b of this.retired) q8().free(b);
+    this.retired = [];
   }
   release() {
     for (const b of this.bufs.values()) q8().free(b);
+    for (const b of this.retired) q8().free(b);
     this.bufs.clear();
+    this.retired = [];
   }
 }
 
@@ -570,22 +591,92 @@ function constSet(kernel) {
 // ---------------------------------------------------------------- plan execution
 /**
  * runPlan (backend_registry.ts:14-20, RuntimeModule.runPlanAsync,
- * runtime.ts:290-329): every step is a hip kernel, so the whole plan runs
- * with its slots resident on the device.  Plan inputs are uploaded once,
- * intermediates never leave the device, and the slots the caller reads back
- * (plan outputs and the sources of return fix-ups) are downloaded at the
- * end.  A quantized_dot whose int32 result feeds only the per-channel
- * epilogue group of the next step (matchEpilogue: convert -> mul(sv)
- * [-> add(b)] [-> max(0)] [-> quantize]) runs as one fused GEMM launch
- * (q8_gemm / q8_gemm_requant), and the int32 tensor is never written.
+ * runtime.ts:290-329), the hip form of the reference's CUDA plan runner
+ * (src/runtime/node/cuda/device_plan.ts:178-297): every step is a hip
+ * kernel, so the whole plan runs with its slots on the device.
+ *  - Every step's arguments (plan slots and the kernel's constant buffers)
+ *    are checked against its descriptor before anything is uploaded or
+ *    launched, as runSync checks them.
+ *  - Slots share device memory by the plan's buffer assignment
+ *    (plan.buffers.slotBuffer / bufferBytes, the compiler's lifetime-based
+ *    groups, _groupsOf in device_plan.ts:44-60); without one every slot has
+ *    its own buffer.  Buffers stay with the plan across calls.
+ *  - Plan inputs (slots read before any step writes them) are uploaded;
+ *    with opts.resident (tracing/compile.ts:115) an input whose
+ *    RuntimeTensor.resident {key, version} (runtime.ts:128) is what the last
+ *    call uploaded into the same buffer is not uploaded again
+ *    (device_plan.ts:220-262).  Intermediates never leave the device, and
+ *    only the slots the caller reads back are downloaded.
+ *  - A quantized_dot whose int32 result feeds only the per-channel epilogue
+ *    group of the next step (matchEpilogue: convert -> mul(sv) [-> add(b)]
+ *    [-> max(0)] [-> quantize]) runs as one fused GEMM launch (q8_gemm /
+ *    q8_gemm_requant), and the int32 tensor is never written.
+ *  - With HIP graphs on (setHipGraphEnabled, the reference's
+ *    setCudaGraphEnabled; or opts.graph), the first call runs eagerly, the
+ *    second captures the plan's launches on the addon's stream and every
+ *    later call replays the graph (device_plan.ts:178-218).  The graph is
+ *    dropped and re-captured when a buffer it names changes (a slot group
+ *    grows, a constant buffer is marked dirty).
  */
 const _planState = new WeakMap();
+let _useHipGraph = false;
+/** The reference's setCudaGraphEnabled / isCudaGraphEnabled (device_plan.ts:40-42). */
+function setHipGraphEnabled(on) { _useHipGraph = !!on; }
+function isHipGraphEnabled() { return _useHipGraph; }
 
 function slotBytes(t) { return t && t.data ? t.data.byteLength : 0; }
 
-function runPlanOnDevice(plan, slots, steps, opts) {
+/** Slot -> buffer group (device_plan.ts _groupsOf). */
+function groupsOf(plan) {
+  const b = plan.buffers;
+  const count = b ? b.bufferBytes.length : plan.numSlots;
+  const of = new Array(plan.numSlots);
+  for (let s = 0; s < plan.numSlots; s++) of[s] = b ? b.slotBuffer[s] : s;
+  return { of, count };
+}
+
+function planStateOf(plan) {
   let st = _planState.get(plan);
-  if (!st) { st = { dev: new DeviceArgs(), inst: new Map() }; _planState.set(plan, st); }
+  if (!st) {
+    st = { dev: new DeviceArgs(true), inst: new Map(), gbuf: [], pin: new Map(), graph: null, graphKeep: null,
+           warm: false, noGraph: false, epoch: -1, devEpoch: -1 };
+    _planState.set(plan, st);
+  }
+  return st;
+}
+
+/** Frees a plan's device buffers and graph (releaseAllPlanBuffers for one plan). */
+function releasePlan(plan) {
+  const st = _planState.get(plan);
+  if (!st) return;
+  dropGraph(st);
+  for (const b of st.gbuf) if (b) q8().free(b);
+  st.dev.release();
+  _planState.delete(plan);
+}
+
+function dropGraph(st) {
+  if (st.graph) q8().graphDestroy(st.graph);
+  st.graph = null;
+  st.graphKeep = null;
+  st.warm = false;
+  st.dev.freeRetired();
+}
+
+// constant buffers marked dirty since a graph was captured invalidate it
+let _constEpoch = 0;
+let _recordConsts = null;
+
+function checkStepArgs(s, inst, slots) {
+  const d = inst.desc;
+  const io = s.inputSlots.concat(s.outputSlots);
+  const argAt = (i) => (i < io.length ? (slots[io[i]] ? slots[io[i]].data : undefined) : inst.constData[i - io.length]);
+  for (const [i, spec] of inputSpecs(d)) checkArg(argAt(i), spec);
+  for (const [i, spec] of outputSpecs(d)) checkArg(argAt(i), spec);
+}
+
+function runPlanOnDevice(plan, slots, steps, opts) {
+  const st = planStateOf(plan);
   const dev = st.dev;
   const instOf = (kernel) => {
     let i = st.inst.get(kernel);
@@ -597,6 +688,11 @@ function runPlanOnDevice(plan, slots, steps, opts) {
     }
     return i;
   };
+  // every argument of every step is checked before the first device call
+  steps.forEach((s) => {
+    need(!s.shapeValues || s.shapeValues.length === 0, 'dynamic shapes are not supported by the int8 kernels');
+    checkStepArgs(s, instOf(s.kernel), slots);
+  });
   const produced = new Map(), readers = new Map();
   steps.forEach((s, k) => {
     for (const o of s.outputSlots) if (!produced.has(o)) produced.set(o, k);
@@ -606,13 +702,53 @@ function runPlanOnDevice(plan, slots, steps, opts) {
   const hostNeeds = new Set();
   for (const a of plan.argSlots) if (produced.has(a)) hostNeeds.add(a);
   for (const fx of plan.returnFixups || []) if (fx.kind === 'copy') hostNeeds.add(fx.srcSlot);
-  const slotBuf = (s) => dev.get(`slot${s}`, slotBytes(slots[s]));
-  // plan inputs: argument slots read before any step writes them
-  for (const a of plan.argSlots) {
-    const first = produced.has(a) ? produced.get(a) : Infinity;
-    const rd = readers.get(a) || [];
-    if (rd.some((k) => k <= first) && slots[a] && slots[a].data) upload(slotBuf(a), slots[a].data, false);
+
+  // device memory: one buffer per slot group, sized for its largest slot
+  const groups = groupsOf(plan);
+  const wanted = new Array(groups.count).fill(0);
+  const members = new Array(groups.count).fill(0);
+  for (let s = 0; s < plan.numSlots; s++) {
+    if (!slots[s] || !slots[s].data) continue;
+    const g = groups.of[s];
+    wanted[g] = Math.max(wanted[g], slotBytes(slots[s]), 1);
+    members[g]++;
   }
+  for (let g = 0; g < groups.count; g++) {
+    if (!wanted[g] || (st.gbuf[g] && q8().bytes(st.gbuf[g]) >= wanted[g])) continue;
+    dropGraph(st);                                   // the graph names the old buffer
+    if (st.gbuf[g]) q8().free(st.gbuf[g]);
+    st.gbuf[g] = q8().alloc(wanted[g]);
+    for (let s = 0; s < plan.numSlots; s++) if (groups.of[s] === g) st.pin.delete(s);
+  }
+  const slotBuf = (s) => {
+    const b = st.gbuf[groups.of[s]];
+    need(b, `plan slot ${s} has no device buffer`);
+    return b;
+  };
+
+  // plan inputs: slots read before any step writes them (resident pins
+  // only for slots alone in their buffer, which no step overwrites)
+  const resident = !!(opts && opts.resident);
+  for (let s = 0; s < plan.numSlots; s++) {
+    const t = slots[s];
+    if (!t || !t.data) continue;
+    const first = produced.has(s) ? produced.get(s) : Infinity;
+    const rd = readers.get(s) || [];
+    if (!rd.some((k) => k <= first)) continue;
+    const res = t.resident;
+    if (resident && res && first === Infinity && members[groups.of[s]] === 1) {
+      const prev = st.pin.get(s);
+      if (prev && prev.key === res.key && prev.version === res.version && prev.data === t.data) {
+        stats.residentSkips++;
+        continue;
+      }
+      st.pin.set(s, { key: res.key, version: res.version, data: t.data });
+    } else {
+      st.pin.delete(s);
+    }
+    upload(slotBuf(s), t.data, false);
+  }
+
   const devArgs = (s, inst) => {
     const dv = [];
     const all = s.inputSlots.concat(s.outputSlots);
@@ -622,30 +758,67 @@ function runPlanOnDevice(plan, slots, steps, opts) {
   };
   const hostArgs = (s, inst) => s.inputSlots.concat(s.outputSlots).map((slot) => slots[slot] && slots[slot].data)
     .concat(inst.constData);
-  for (let k = 0; k < steps.length; k++) {
-    const s = steps[k], inst = instOf(s.kernel), d = inst.desc;
-    need(!s.shapeValues || s.shapeValues.length === 0, 'dynamic shapes are not supported by the int8 kernels');
-    const mode = (opts && opts.q8Activations) || d.activations || 'static';
-    if (d.op === 'quantize' && mode !== 'static' && k + 2 < steps.length) {
-      need(ACTIVATION_MODES.has(mode), `unknown q8 activation mode '${mode}'`);
-      if (tryDynamicLinear(mode, s, d, steps[k + 1], instOf(steps[k + 1].kernel), steps[k + 2],
-                           instOf(steps[k + 2].kernel), slots, readers, argSet, hostNeeds, slotBuf, dev, hostArgs)) {
-        k += 2;
-        continue;
+  const launchAll = () => {
+    for (let k = 0; k < steps.length; k++) {
+      const s = steps[k], inst = instOf(s.kernel), d = inst.desc;
+      const mode = (opts && opts.q8Activations) || d.activations || 'static';
+      if (d.op === 'quantize' && mode !== 'static' && k + 2 < steps.length) {
+        need(ACTIVATION_MODES.has(mode), `unknown q8 activation mode '${mode}'`);
+        if (tryDynamicLinear(mode, s, d, steps[k + 1], instOf(steps[k + 1].kernel), steps[k + 2],
+                             instOf(steps[k + 2].kernel), slots, readers, argSet, hostNeeds, slotBuf, dev, hostArgs)) {
+          k += 2;
+          continue;
+        }
       }
+      const fused = !(opts && opts.fuse === false) && k + 1 < steps.length &&
+                    tryFusedLinear(s, inst, steps[k + 1], instOf(steps[k + 1].kernel), slots, readers, argSet,
+                                   hostNeeds, slotBuf, dev, hostArgs);
+      if (fused) { k++; continue; }
+      const dv = devArgs(s, inst);
+      let rhsNK = null;
+      if (d.op === 'quantized_dot' && d.rhsLayout === 'KN') {
+        const b = hostArgs(s, inst)[d.bIdx];
+        if (inst.consts.has(b)) rhsNK = residentConst(b, 'T', (w) => transposeI8(w, d.K, d.N));
+      }
+      execDevice(d, dv, dev, rhsNK);
     }
-    const fused = !(opts && opts.fuse === false) && k + 1 < steps.length &&
-                  tryFusedLinear(s, inst, steps[k + 1], instOf(steps[k + 1].kernel), slots, readers, argSet, hostNeeds,
-                                 slotBuf, dev, hostArgs);
-    if (fused) { k++; continue; }
-    const dv = devArgs(s, inst);
-    let rhsNK = null;
-    if (d.op === 'quantized_dot' && d.rhsLayout === 'KN') {
-      const b = hostArgs(s, inst)[d.bIdx];
-      if (inst.consts.has(b)) rhsNK = residentConst(b, 'T', (w) => transposeI8(w, d.K, d.N));
+  };
+
+  const graphOn = opts && opts.graph !== undefined ? !!opts.graph : _useHipGraph;
+  if (st.graph && (st.epoch !== _constEpoch || st.devEpoch !== dev.epoch)) dropGraph(st);
+  if (!graphOn || st.noGraph) {
+    launchAll();
+  } else if (st.graph) {
+    q8().graphLaunch(st.graph);
+    stats.graphReplays++;
+  } else if (!st.warm) {
+    launchAll();                     // fills every cache the launches read, so a capture allocates nothing
+    st.warm = true;
+  } else {
+    const A = q8();
+    const keep = [];
+    A.captureBegin();
+    _recordConsts = keep;
+    let g = null;
+    try {
+      launchAll();
+    } catch (e) {
+      _recordConsts = null;
+      try { A.graphDestroy(A.captureEnd()); } catch (e2) { /* the capture is void either way */ }
+      st.noGraph = true;             // this plan runs eagerly from now on
+      throw e;
     }
-    execDevice(d, dv, dev, rhsNK);
+    _recordConsts = null;
+    g = A.captureEnd();
+    st.graph = g;
+    st.graphKeep = keep.concat(st.dev.live());      // every buffer the graph names stays alive with it
+    st.epoch = _constEpoch;
+    st.devEpoch = dev.epoch;
+    stats.graphCaptures++;
+    A.graphLaunch(g);
+    stats.graphReplays++;
   }
+  q8().sync();
   for (const s of hostNeeds) if (slots[s] && slots[s].data) download(slots[s].data, slotBuf(s));
 }
 
@@ -983,5 +1156,7 @@ function registerHip(r) {
 module.exports = {
   HIP_KIND, PROVIDER, ACTIVATIONS_ATTR, activationMode, registerHip, createHipRuntimeBackend, createHipExternalCodegen, createHipCodegenEntry,
   createHipProvider, defineEagerLibrary, detectInt8Kernel, describe, runDescriptor, hipTarget, DeviceArgs,
-  markHostDirty, stats, resetStats,
+  markHostDirty, stats, resetStats, setHipGraphEnabled, isHipGraphEnabled, releasePlan,
+  // runPlan's body without the promise: it throws where runPlan rejects
+  runPlanSync: runPlanOnDevice,
 };

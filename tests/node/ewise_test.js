@@ -26,78 +26,18 @@ let failures = 0;
 function test(name, fn) {
   try { fn(); console.log(`ok   ${name}`); } catch (e) { failures++; console.log(`FAIL ${name}\n     ${e.stack}`); }
 }
+// tests of a promise: settled before the process reports and exits
+const pending = [];
+function testAsync(name, promiseFn) {
+  let p;
+  try { p = Promise.resolve(promiseFn()); } catch (e) { p = Promise.reject(e); }
+  pending.push(p.then(() => console.log(`ok   ${name}`),
+                      (e) => { failures++; console.log(`FAIL ${name}\n     ${e && e.stack}`); }));
+}
 
 // ---------------------------------------------------------------- TIR builders
-const V = (name, dtype = 'index') => ({ type: 'VariableNode', name, dtype });
-const I = (value) => ({ type: 'IntImmNode', value });
-const F = (value) => ({ type: 'FloatImmNode', value });
-const buf = (name, shape, dtype) => ({ name, shape, dtype });
-const load = (b, indices) => ({ type: 'BufferLoadNode', buffer: b, indices });
-const math = (op, a, b = null) => ({ type: 'MathOpNode', op, a, b });
-const ext = (externName, args, dtype = 'f32') => ({ type: 'CallExternNode', externName, args, dtype });
-const cast = (expr, fromDtype, toDtype) => ({ type: 'CastNode', expr, fromDtype, toDtype });
-const cmp = (direction, a, b) => ({ type: 'CompareNode', direction, a, b });
-const sel = (condition, thenBody, elseBody) => ({ type: 'IfThenElseNode', condition, thenBody, elseBody });
-
-let uid = 0;
-function primFunc(name, params, body, consts) {
-  const attrs = new Map();
-  const bufferMap = new Map();
-  params.forEach((b) => bufferMap.set(V(`p${uid++}`, 'handle'), b));
-  if (consts && consts.length) attrs.set('const_buffers', consts);
-  return {
-    name, params: [...bufferMap.keys()], body, bufferMap, attrs,
-    getAttr(k) { return attrs.has(k) ? attrs.get(k) : null; },
-    setAttr(k, v) { attrs.set(k, v); return this; },
-  };
-}
-
-/** lowerPointwise: loops over out's shape, loads through broadcast indices. */
-function pointwise(name, out, inputs, exprBuilder, consts) {
-  const n = out.shape.length, tag = uid++;
-  const loopVars = [], ivs = [], indices = [];
-  for (let d = 0; d < n; d++) {
-    loopVars.push(V(`i${d}_${tag}`));
-    const iv = V(`v${d}_${tag}`);
-    ivs.push({ type: 'BlockRealizeNode', iterVar: iv, binding: loopVars[d], kind: 0 });
-    indices.push(iv);
-  }
-  const loads = inputs.map((b) => {
-    const off = n - b.shape.length;
-    return load(b, b.shape.map((s, j) => (s === 1 ? I(0) : indices[off + j])));
-  });
-  const store = { type: 'BufferStoreNode', buffer: out, indices, value: exprBuilder(loads, indices) };
-  let body = { type: 'BlockNode', name: `${name}_block`, iterVars: ivs, reads: inputs.map((b) => ({ buffer: b })),
-               writes: [{ buffer: out }], body: store, initBody: null };
-  for (let d = n - 1; d >= 0; d--) {
-    body = { type: 'ForNode', loopVar: loopVars[d], min: I(0), extent: I(out.shape[d]), kind: 'serial', body };
-  }
-  const constBufs = (consts || []).map((c) => c.buffer);
-  const params = inputs.filter((b) => !constBufs.includes(b)).concat([out], constBufs);
-  return primFunc(name, params, body, consts);
-}
-
-/** quantize_block (quant_math.ts:16-27) around an inner expression. */
-function quantizeExpr(e, scale, zp = 0, tgt = 'i8') {
-  let s = math('/', e, F(scale));
-  if (zp !== 0) s = math('+', s, F(zp));
-  const lo = tgt === 'ui8' ? 0 : -128, hi = tgt === 'ui8' ? 255 : 127;
-  return cast(ext('min', [ext('max', [ext('round', [s]), F(lo)]), F(hi)]), 'f32', tgt);
-}
-
-/** qmatmul_init / qmatmul_acc (rules/quantization.ts:23-42) with W [N,K]. */
-function qmatmulPF(M, N, K, a, w, out, consts) {
-  const tag = uid++;
-  const m = V(`vm_${tag}`), n = V(`vn_${tag}`), k = V(`vk_${tag}`);
-  const init = { type: 'BlockNode', name: 'qmatmul_init', iterVars: [], reads: [], writes: [{ buffer: out }],
-                 body: { type: 'BufferStoreNode', buffer: out, indices: [m, n], value: I(0) } };
-  const acc = { type: 'BlockNode', name: 'qmatmul_acc_1', iterVars: [], reads: [{ buffer: a }, { buffer: w }],
-                writes: [{ buffer: out }],
-                body: { type: 'BufferStoreNode', buffer: out, indices: [m, n],
-                        value: math('+', load(out, [m, n]), math('*', cast(load(a, [m, k]), 'i8', 'i32'),
-                                                               cast(load(w, [n, k]), 'i8', 'i32'))) } };
-  return primFunc('qmatmul', [a, out, w], { type: 'ForNode', body: { type: 'SeqNode', stmts: [init, acc] } }, consts);
-}
+const { V, I, F, buf, load, math, ext, cast, cmp, sel, primFunc, pointwise, quantizeExpr, qmatmulPF } =
+  require(path.join(ROOT, 'mlfw_amd', 'node', 'tir_build.js'));
 
 // ---------------------------------------------------------------- data
 function rng(seed) { return q8ref.makeRng(seed); }
@@ -285,6 +225,40 @@ function cpuTests() {
     assert.strictEqual(fi(buf('m', [3, 4], 'f32'), [I(0), idx('j')]), 'j');
     assert.strictEqual(fi(buf('m', [3, 4], 'f32'), [I(0), I(0)]), '0');
   });
+
+  // runPlan checks every step's arguments before it touches the device: an
+  // undersized or mistyped slot is a JS error here, where no device exists
+  {
+    const L = linearSet();
+    const provider = hip.createHipProvider('external_codegen', 'const_buffers');
+    const codegen = hip.createHipExternalCodegen('const_buffers');
+    const kernelOf = (pf) => { provider.annotate([pf]); return codegen.compile(pf, hip.hipTarget(), pf.getAttr('external_codegen').info); };
+    const S = (pf, ins, outs) => ({ name: pf.name, inputSlots: ins, outputSlots: outs, kernel: kernelOf(pf), shapeValues: null });
+    const steps = [S(L.pf.quantize, [0], [2]), S(L.pf.qmatmul, [2], [3]), S(L.pf.fused, [3, 1], [4])];
+    const plan = { numSlots: 5, argSlots: [0, 1, 4], intermediates: [],
+                   steps: steps.map((x) => ({ name: x.name, inputSlots: x.inputSlots, outputSlots: x.outputSlots })) };
+    const mk = (data) => ({ data, shape: [data.length], dtype: 'f32' });
+    const good = () => [mk(new Float32Array(M * K)), mk(new Float32Array(N)), mk(new Int8Array(M * K)),
+                        mk(new Int32Array(M * N)), mk(new Float32Array(M * N))];
+    const be = hip.createHipRuntimeBackend();
+    test('runPlan rejects an undersized plan argument before any device call', () => {
+      const sl = good();
+      sl[0] = mk(new Float32Array(M * K - 1));
+      assert.throws(() => hip.runPlanSync(plan, sl, steps), /quantize input has \d+ elements, expected \d+/);
+      const s2 = good();
+      s2[4] = mk(new Float32Array(M * N - 3));
+      assert.throws(() => hip.runPlanSync(plan, s2, steps), /out has \d+ elements, expected/);
+      const s3 = good();
+      s3[3] = mk(new Float32Array(M * N));                  // the int32 accumulator slot as f32
+      assert.throws(() => hip.runPlanSync(plan, s3, steps), /must be a Int32Array/);
+    });
+    testAsync('runPlan (the promise form) rejects an undersized plan argument', () => {
+      const sl = good();
+      sl[1] = mk(new Float32Array(N - 1));
+      return be.runPlan(plan, sl, steps).then(() => { throw new Error('runPlan resolved'); },
+                                              (e) => assert.ok(/has \d+ elements, expected/.test(e.message), e.message));
+    });
+  }
 
   test('the oracle per-channel tail agrees with q8ref.js (two restatements, one engine)', () => {
     const L = linearSet();
@@ -524,8 +498,106 @@ function gpuTests() {
     const slots = [mk(xD, [M, K], 'f32'), mk(bD, [N], 'f32'), mk(new Int8Array(M * K), [M, K], 'i8'),
                    mk(new Int32Array(M * N), [M, N], 'i32'), mk(new Float32Array(M * N), [M, N], 'f32'),
                    mk(new Float32Array(M * N), [M, N], 'f32'), mk(out, [M, N], which === 'requant' ? 'i8' : 'f32')];
-    return { plan, slots, steps, out, want, h, fuse };
+    return { plan, slots, steps, out, want, h, fuse, L, xD, bD };
   }
+
+  // the oracle of linearRun's plans for any input x (host, step by step)
+  function oracleLinear(L, which, xD, bD) {
+    const run = (pf, args) => ref.compilePrimFunc(pf).fn(...args);
+    const xq = new Int8Array(M * K); run(L.pf.quantize, [xD, xq]);
+    const acc = new Int32Array(M * N); q8ref.buildQuantizedDot(M, N, K, 1, 0, 0)(xq, L.consts.W.data, acc);
+    const y = new Float32Array(M * N); run(L.pf.tail, [acc, y, L.consts.sv.data]);
+    const y2 = new Float32Array(M * N); run(L.pf.add, [y, bD, y2]);
+    if (which === 'requant') { const q2 = new Int8Array(M * N); run(L.pf.reluQuant, [y2, q2, L.consts.zero.data]); return q2; }
+    const y3 = new Float32Array(M * N); run(L.pf.max, [y2, y3, L.consts.zero.data]);
+    return y3;
+  }
+
+  test('GPU: resident plan inputs are not uploaded again while their key and version are unchanged', () => {
+    const t = linearRun('fused', true);
+    t.slots[0].resident = { key: t.slots[0].data, version: 1 };
+    t.slots[1].resident = { key: t.slots[1].data, version: 1 };
+    hip.resetStats();
+    hip.runPlanSync(t.plan, t.slots, t.steps, { resident: true });
+    sameBits(t.out, t.want, 'first call');
+    assert.strictEqual(hip.stats.uploadBytes - hip.stats.constUploadBytes, 4 * M * K + 4 * N, 'first call uploads x and b');
+    hip.resetStats();
+    t.out.fill(0);
+    hip.runPlanSync(t.plan, t.slots, t.steps, { resident: true });
+    sameBits(t.out, t.want, 'second call');
+    assert.strictEqual(hip.stats.uploadBytes, 0, 'second call with unchanged arguments uploads 0 bytes');
+    assert.strictEqual(hip.stats.residentSkips, 2);
+    // a new version of x is uploaded, b stays
+    const x2 = normal(77, M * K, 1.5);
+    t.slots[0].data.set(x2);
+    t.slots[0].resident.version = 2;
+    hip.resetStats();
+    hip.runPlanSync(t.plan, t.slots, t.steps, { resident: true });
+    assert.strictEqual(hip.stats.uploadBytes, 4 * M * K, 'only the new version of x');
+    sameBits(t.out, oracleLinear(t.L, 'fused', x2, t.bD), 'new x');
+    // without {resident: true} every input is uploaded
+    hip.resetStats();
+    hip.runPlanSync(t.plan, t.slots, t.steps);
+    assert.strictEqual(hip.stats.uploadBytes, 4 * M * K + 4 * N);
+  });
+
+  test('GPU: slots share device buffers by the plan buffer assignment', () => {
+    const t = linearRun('unfused', false);
+    // slots: 0 x, 1 b, 2 xq, 3 acc, 4 y, 5 y2, 6 y3: xq / y and acc / y2 do not overlap in time
+    t.plan.buffers = { slotBuffer: [0, 1, 2, 3, 2, 3, 4], bufferBytes: [4 * M * K, 4 * N, 4 * M * N, 4 * M * N, 4 * M * N] };
+    for (let c = 0; c < 2; c++) {
+      t.out.fill(0);
+      hip.runPlanSync(t.plan, t.slots, t.steps, { fuse: false });
+      sameBits(t.out, t.want, `grouped slots, call ${c}`);
+    }
+    hip.releasePlan(t.plan);
+  });
+
+  for (const [which, fuse] of [['fused', true], ['unfused', false], ['requant', true]]) {
+    test(`GPU: runPlan in graph mode (${which}, fusion ${fuse ? 'on' : 'off'}): eager, captured, replayed, fresh x every call`, () => {
+      const t = linearRun(which, fuse);
+      const A = require(path.join(ROOT, 'mlfw_amd', 'node', 'index.js'));
+      hip.resetStats();
+      for (let c = 0; c < 5; c++) {
+        const x = normal(90 + c, M * K, 1.5);
+        t.slots[0].data.set(x);
+        t.out.fill(0);
+        hip.runPlanSync(t.plan, t.slots, t.steps, { graph: true, fuse });
+        sameBits(t.out, oracleLinear(t.L, which, x, t.bD), `${which} call ${c}`);
+        // eager device work and a synchronization between replays
+        const junk = A.alloc(4096);
+        A.fillUniform(junk, 1024, 5, 0, 0, 1);
+        A.sync();
+        A.free(junk);
+      }
+      assert.strictEqual(hip.stats.graphCaptures, 1, 'captured once (on the second call)');
+      assert.strictEqual(hip.stats.graphReplays, 4, 'calls 2-5 replay');
+      // a constant marked dirty drops the graph: one eager call, then a new capture
+      hip.markHostDirty(t.L.consts.W.data);
+      for (let c = 0; c < 3; c++) {
+        t.out.fill(0);
+        hip.runPlanSync(t.plan, t.slots, t.steps, { graph: true, fuse });
+        sameBits(t.out, oracleLinear(t.L, which, t.slots[0].data, t.bD), `${which} after markHostDirty, call ${c}`);
+      }
+      assert.strictEqual(hip.stats.graphCaptures, 2);
+      hip.releasePlan(t.plan);
+    });
+  }
+
+  test('GPU: the addon rejects device buffers smaller than the call needs', () => {
+    const A = require(path.join(ROOT, 'mlfw_amd', 'node', 'index.js'));
+    const small = A.alloc(16), big = A.alloc(64 * 64 * 4);
+    assert.throws(() => A.gemm(small, big, 64, 64, 64, 0, 0, null, 0, null, 0, A.Q8_EPI_PT, 1.0, null, 0, A.Q8_I32, big),
+                  /gemm A device buffer holds 16 bytes, the call needs 4096/);
+    assert.throws(() => A.gemm(big, big, 64, 64, 64, 0, 0, null, 0, null, 0, A.Q8_EPI_PT, 1.0, null, 0, A.Q8_I32, small),
+                  /gemm out device buffer holds 16 bytes, the call needs 16384/);
+    assert.throws(() => A.quantizeRows(big, 64, 64, A.Q8_PER_TOKEN, big, small), /quantizeRows scales/);
+    assert.throws(() => A.dequantize(small, A.Q8_I32, 2, 4, big, A.Q8_PER_TENSOR, 0, big), /dequantize q/);
+    assert.throws(() => A.fillNormal(small, 5, 1, 0, 0, 1), /fill output/);
+    A.free(small);
+    A.free(big);
+  });
+
 
   for (const [which, fuse, fusedCount] of [['unfused', true, 1], ['unfused', false, 0], ['fused', true, 1],
                                             ['fused', false, 0], ['requant', true, 1], ['requant', false, 0]]) {
@@ -533,7 +605,7 @@ function gpuTests() {
       const t = linearRun(which, fuse);
       hip.resetStats();
       let err = null;
-      be.runPlan(t.plan, t.slots, t.steps, { fuse }).catch((e) => { err = e; });
+      try { hip.runPlanSync(t.plan, t.slots, t.steps, { fuse }); } catch (e) { err = e; }
       const first = Object.assign({}, hip.stats);
       sameBits(t.out, t.want, `${which} plan output`);
       assert.strictEqual(first.fusedLinears, fusedCount);
@@ -542,7 +614,7 @@ function gpuTests() {
       // a second run uploads no constant bytes and only the plan inputs
       hip.resetStats();
       t.out.fill(0);
-      be.runPlan(t.plan, t.slots, t.steps, { fuse }).catch((e) => { err = e; });
+      try { hip.runPlanSync(t.plan, t.slots, t.steps, { fuse }); } catch (e) { err = e; }
       assert.strictEqual(err, null);
       sameBits(t.out, t.want, `${which} plan output, second run`);
       assert.strictEqual(hip.stats.constUploadBytes, 0, 'weights uploaded again');
@@ -583,7 +655,7 @@ function gpuTests() {
                      mkSlot(new Int32Array(M * N), [M, N], 'i32'), mkSlot(out, [M, N], 'f32')];
       hip.resetStats();
       let err = null;
-      be.runPlan(plan, slots, steps).catch((e) => { err = e; });
+      try { hip.runPlanSync(plan, slots, steps); } catch (e) { err = e; }
       assert.strictEqual(err, null);
       assert.strictEqual(hip.stats.launches, 1, 'one launch for the linear');
       assert.strictEqual(hip.stats.dynamicLinears, 1);
@@ -591,7 +663,7 @@ function gpuTests() {
       // the run-time option overrides the compiled mode, and 'static' is the reference's result
       const stat = new Float32Array(M * N);
       slots[4] = mkSlot(stat, [M, N], 'f32');
-      be.runPlan(plan, slots, steps, { q8Activations: 'static' }).catch((e) => { err = e; });
+      try { hip.runPlanSync(plan, slots, steps, { q8Activations: 'static' }); } catch (e) { err = e; }
       assert.strictEqual(err, null);
       const h = {};
       h.xq = new Int8Array(M * K); ref.compilePrimFunc(L.pf.quantize).fn(x, h.xq);
@@ -613,7 +685,7 @@ function gpuTests() {
       const slots = [mkSlot(x, [M, K], 'f32'), mkSlot(b, [N], 'f32'), mkSlot(new Int8Array(M * K), [M, K], 'i8'),
                      mkSlot(new Int32Array(M * N), [M, N], 'i32'), mkSlot(out, [M, N], 'f32')];
       let err = null;
-      be.runPlan(makePlan(steps, [0, 1, 4], 5), slots, steps).catch((e) => { err = e; });
+      try { hip.runPlanSync(makePlan(steps, [0, 1, 4], 5), slots, steps); } catch (e) { err = e; }
       assert.strictEqual(err, null);
       return out;
     };
@@ -677,7 +749,7 @@ function gpuTests() {
     }
     hip.resetStats();
     let err = null;
-    be.runPlan(makePlan(steps, [0, 1, 2, 3, 10], 11), slots, steps).catch((e) => { err = e; });
+    try { hip.runPlanSync(makePlan(steps, [0, 1, 2, 3, 10], 11), slots, steps); } catch (e) { err = e; }
     assert.strictEqual(err, null);
     sameBits(y, want, 'three-layer output');
     assert.strictEqual(hip.stats.fusedLinears, 3);
@@ -704,5 +776,7 @@ function gpuTests() {
 const mode = process.argv[2] || 'cpu';
 if (mode === 'cpu') cpuTests();
 else gpuTests();
-console.log(failures ? `${failures} failed` : 'all passed');
-process.exit(failures ? 1 : 0);
+Promise.all(pending).then(() => {
+  console.log(failures ? `${failures} failed` : 'all passed');
+  process.exit(failures ? 1 : 0);
+});
