@@ -312,8 +312,10 @@ CONV_LAYERS = [(32, 64, 56, 56, 64, 3, 1), (32, 128, 28, 28, 128, 3, 1), (32, 25
 
 def bench_conv():
     """quantized_conv with the fused per-tensor dequant (fp32 out), int8
-    operands: the whole call (frame transpose, weight permutation, implicit
-    GEMM, split-K finish where planned) per launch, 8 calls per graph."""
+    operands: the whole call per launch (frame transpose, implicit GEMM,
+    split-K finish where planned), 8 calls per graph.  The constant weight
+    is prepacked once (conv_weight_taps); avg_us_unpacked_weight is the call
+    that permutes the weight itself."""
     import torch
     from mlfw_amd import ops as O
     res = {}
@@ -324,15 +326,19 @@ def bench_conv():
         w = torch.randint(-128, 128, (Oc, C, k, k), dtype=torch.int8, device="cuda", generator=gen)
         pad = [[p, p], [p, p]]
         s_out = 1e-4
-        out = O.quantized_conv(x, w, [1, 1], pad, s_out=s_out, workspace=ws)
+        wt = O.conv_weight_taps(w)
+        out = O.quantized_conv(x, w, [1, 1], pad, s_out=s_out, workspace=ws, w_taps=wt)
         us, how = graph_time_us(
+            lambda i: O.quantized_conv(x, w, [1, 1], pad, s_out=s_out, out=out, workspace=ws, w_taps=wt), 8)
+        us_raw, _ = graph_time_us(
             lambda i: O.quantized_conv(x, w, [1, 1], pad, s_out=s_out, out=out, workspace=ws), 8)
         Ho, Wo = H + 2 * p - k + 1, W + 2 * p - k + 1
         ops = 2 * N * Oc * Ho * Wo * C * k * k
         tops = ops / (us * 1e-6) / 1e12
         res[f"conv_N{N}_C{C}_{H}x{W}_O{Oc}_k{k}"] = {
-            "avg_us": us, "ops": ops, "TOPS": tops, "frac_mfma": tops / PEAK_INT8_TOPS, "timing": how}
-        del x, w, out
+            "avg_us": us, "ops": ops, "TOPS": tops, "frac_mfma": tops / PEAK_INT8_TOPS, "timing": how,
+            "weight": "prepacked" if wt is not None else "as given (1 x 1)", "avg_us_unpacked_weight": us_raw}
+        del x, w, out, wt
     return res
 
 

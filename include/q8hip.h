@@ -468,6 +468,26 @@ int q8_quantized_conv_ex(const void* x, int x_dtype, const void* w, int w_dtype,
                          int64_t groups, int32_t zp_x, int32_t zp_w, int out_kind, double s_out,
                          void* workspace, size_t workspace_bytes, void* out, void* stream);
 
+/* A conv weight prepacked once: the GEMM paths read the kernel tap-major,
+ * w_taps[o][t * Cg + c] = w[o][c][t] (t the kernel position in row-major
+ * order, Cg = C/groups), which q8_quantized_conv otherwise permutes on every
+ * call.  The reference keeps its conv kernel as a constant buffer of the
+ * compiled function (QuantizationPass quantizes it once,
+ * quantization_pass.ts:286-360; ops/quantization.ts:156-190), so a weight
+ * is constant across calls.  q8_conv_weight_taps writes the O * Cg *
+ * prod(K) bytes for weights whose Cg is a multiple of 16 with 2..1024
+ * kernel positions (Q8_ERR_UNSUPPORTED otherwise: those weights are used as
+ * given); q8_quantized_conv_prepacked is q8_quantized_conv with that copy
+ * (w stays an argument: paths that do not read the tap-major form use it),
+ * bit for bit the same output.  16-byte aligned w and w_taps. */
+int q8_conv_weight_taps(const int8_t* w, int spatial_dims, const int64_t* w_shape, int64_t groups,
+                        int8_t* w_taps, void* stream);
+int q8_quantized_conv_prepacked(const int8_t* x, const int8_t* w, const int8_t* w_taps, int spatial_dims,
+                                const int64_t* x_shape, const int64_t* w_shape, const int64_t* strides,
+                                const int64_t* pad_lo, const int64_t* pad_hi, const int64_t* dilation,
+                                int64_t groups, int32_t zp_x, int32_t zp_w, int out_kind, double s_out,
+                                void* workspace, size_t workspace_bytes, void* out, void* stream);
+
 /* ---------------------------------------------------------------- fused */
 
 /* h = fround(silu(g) * u) for the gated MLP (SiLU decomposition

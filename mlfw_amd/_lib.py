@@ -99,6 +99,9 @@ SIGNATURES = {
     "q8_pack_weight_int4": [_vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "q8_gemv_w4": [_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _int, _vp, _vp],
     "q8_quantized_conv_workspace": [_int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp],
+    "q8_conv_weight_taps": [_vp, _int, _vp, _i64, _vp, _vp],
+    "q8_quantized_conv_prepacked": [_vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, C.c_int32,
+                                    C.c_int32, _int, _dbl, _vp, C.c_size_t, _vp, _vp],
     "q8_quantized_conv": [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, C.c_int32,
                           C.c_int32, _int, _dbl, _vp, C.c_size_t, _vp, _vp],
     "q8_quantized_conv_ex": [_vp, _int, _vp, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64,

@@ -901,7 +901,7 @@ int q8_quantized_conv_workspace(int spatial_dims, const int64_t* x_shape, const 
 }
 
 static int conv_impl(const char* who, const void* x, int x_dtype, const void* w, int w_dtype,
-                     int spatial_dims, const int64_t* x_shape, const int64_t* w_shape,
+                     const int8_t* w_taps, int spatial_dims, const int64_t* x_shape, const int64_t* w_shape,
                      const int64_t* strides, const int64_t* pad_lo, const int64_t* pad_hi,
                      const int64_t* dilation, int64_t groups, int32_t zp_x, int32_t zp_w,
                      int out_kind, double s_out, void* workspace, size_t workspace_bytes, void* out,
@@ -930,9 +930,36 @@ static int conv_impl(const char* who, const void* x, int x_dtype, const void* w,
   e.out_i32 = out_kind == Q8_I32;
   rc = ensure_current();
   if (rc != Q8_OK) return rc;
-  return launched(q8::launch_conv(static_cast<const int8_t*>(x), static_cast<const int8_t*>(w), G,
+  if (w_taps) {
+    Q8_REQUIRE(q8::conv_taps_used(G), "%s: this weight shape has no tap-major form (q8_conv_weight_taps)", who);
+    Q8_REQUIRE((reinterpret_cast<uintptr_t>(w_taps) & 15) == 0, "%s: w_taps must be 16-byte aligned", who);
+  }
+  return launched(q8::launch_conv(static_cast<const int8_t*>(x), static_cast<const int8_t*>(w), w_taps, G,
                                   e, workspace, out, as_stream(stream)),
                   "quantized_conv launch");
+}
+
+int q8_conv_weight_taps(const int8_t* w, int spatial_dims, const int64_t* w_shape, int64_t groups,
+                        int8_t* w_taps, void* stream) {
+  Q8_REQUIRE(w_shape != nullptr && spatial_dims >= 1 && spatial_dims <= 3,
+             "q8_conv_weight_taps: spatial_dims must be 1, 2 or 3 (got %d)", spatial_dims);
+  Q8_REQUIRE(groups >= 1 && w_shape[0] > 0 && w_shape[0] % groups == 0 && w_shape[1] > 0,
+             "q8_conv_weight_taps: bad weight shape or groups");
+  // the geometry of a 1-image input that the kernel fits exactly (only the
+  // weight's dimensions matter for the permutation)
+  int64_t xs[5] = {1, w_shape[1] * groups, 1, 1, 1}, st[3] = {1, 1, 1}, lo[3] = {0, 0, 0}, dl[3] = {1, 1, 1};
+  for (int i = 0; i < spatial_dims; ++i) xs[2 + i] = w_shape[2 + i];
+  q8::ConvGeom G;
+  int rc = conv_geom("q8_conv_weight_taps", spatial_dims, xs, w_shape, st, lo, lo, dl, groups, &G);
+  if (rc != Q8_OK) return rc;
+  if (!q8::conv_taps_used(G))
+    return fail(Q8_ERR_UNSUPPORTED, "q8_conv_weight_taps: weights of this shape are used as given "
+                "(the tap-major form needs channels per group a multiple of 16 and 2..1024 kernel positions)");
+  Q8_REQUIRE(w && w_taps && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(w_taps)) & 15) == 0,
+             "q8_conv_weight_taps: w and w_taps must be 16-byte aligned device pointers");
+  rc = ensure_current();
+  if (rc != Q8_OK) return rc;
+  return launched(q8::launch_conv_weight_taps(w, G, w_taps, as_stream(stream)), "q8_conv_weight_taps launch");
 }
 
 int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const int64_t* x_shape,
@@ -940,8 +967,19 @@ int q8_quantized_conv(const int8_t* x, const int8_t* w, int spatial_dims, const 
                       const int64_t* pad_hi, const int64_t* dilation, int64_t groups,
                       int32_t zp_x, int32_t zp_w, int out_kind, double s_out, void* workspace,
                       size_t workspace_bytes, void* out, void* stream) {
-  return conv_impl("q8_quantized_conv", x, Q8_I8, w, Q8_I8, spatial_dims, x_shape, w_shape, strides,
+  return conv_impl("q8_quantized_conv", x, Q8_I8, w, Q8_I8, nullptr, spatial_dims, x_shape, w_shape, strides,
                    pad_lo, pad_hi, dilation, groups, zp_x, zp_w, out_kind, s_out, workspace,
+                   workspace_bytes, out, stream);
+}
+
+int q8_quantized_conv_prepacked(const int8_t* x, const int8_t* w, const int8_t* w_taps, int spatial_dims,
+                                const int64_t* x_shape, const int64_t* w_shape, const int64_t* strides,
+                                const int64_t* pad_lo, const int64_t* pad_hi, const int64_t* dilation,
+                                int64_t groups, int32_t zp_x, int32_t zp_w, int out_kind, double s_out,
+                                void* workspace, size_t workspace_bytes, void* out, void* stream) {
+  Q8_REQUIRE(w_taps != nullptr, "q8_quantized_conv_prepacked: w_taps is NULL (use q8_quantized_conv)");
+  return conv_impl("q8_quantized_conv_prepacked", x, Q8_I8, w, Q8_I8, w_taps, spatial_dims, x_shape, w_shape,
+                   strides, pad_lo, pad_hi, dilation, groups, zp_x, zp_w, out_kind, s_out, workspace,
                    workspace_bytes, out, stream);
 }
 
@@ -950,7 +988,7 @@ int q8_quantized_conv_ex(const void* x, int x_dtype, const void* w, int w_dtype,
                          const int64_t* pad_lo, const int64_t* pad_hi, const int64_t* dilation,
                          int64_t groups, int32_t zp_x, int32_t zp_w, int out_kind, double s_out,
                          void* workspace, size_t workspace_bytes, void* out, void* stream) {
-  return conv_impl("q8_quantized_conv_ex", x, x_dtype, w, w_dtype, spatial_dims, x_shape, w_shape,
+  return conv_impl("q8_quantized_conv_ex", x, x_dtype, w, w_dtype, nullptr, spatial_dims, x_shape, w_shape,
                    strides, pad_lo, pad_hi, dilation, groups, zp_x, zp_w, out_kind, s_out, workspace,
                    workspace_bytes, out, stream);
 }

@@ -446,15 +446,16 @@ size_t conv_workspace_bytes(const ConvGeom& G) {
   return b;
 }
 
-static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, const ConvGeom& G,
-                                           const ConvFrame& F, const GemmEpi& e, void* workspace,
-                                           void* out, hipStream_t st) {
+static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, const int8_t* w_taps,
+                                           const ConvGeom& G, const ConvFrame& F, const GemmEpi& e,
+                                           void* workspace, void* out, hipStream_t st) {
   const ClLayout L = cl_layout(G, F);
   const bool pw = conv_pointwise(G);
   int8_t* col = static_cast<int8_t*>(workspace);
   int8_t* xp = col + L.col;
-  // a 1 x 1 kernel's weight is its own tap-major form
-  int8_t* wt = G.Kn == 1 ? const_cast<int8_t*>(w) : xp + L.frame;
+  // a 1 x 1 kernel's weight is its own tap-major form; a prepacked one
+  // (q8_conv_weight_taps) is used as given
+  int8_t* wt = G.Kn == 1 ? const_cast<int8_t*>(w) : w_taps ? const_cast<int8_t*>(w_taps) : xp + L.frame;
   int32_t* part = reinterpret_cast<int32_t*>(xp + L.frame + L.wt);
   const int64_t nsl = G.O * (G.Cg >> 4);                   // weight slices
   const int wns = G.Kn >= 256 ? WT_CHUNKS / G.Kn : 256 / G.Kn;   // slices per workgroup
@@ -467,7 +468,7 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
   const unsigned fz = (unsigned)(ctiles < 65535 ? ctiles : 65535);   // strided loops cover the rest
   const unsigned tz = (unsigned)(tgroups < 65535 ? tgroups : 65535);
   hipError_t err = hipSuccess;
-  if (G.Kn > 1) {
+  if (G.Kn > 1 && !w_taps) {
     hipLaunchKernelGGL(k_conv_weight_taps, dim3((unsigned)wblk), dim3(256), 0, st, w, nsl, G.Cg, G.Kn,
                        wns, wt);
     err = hipGetLastError();
@@ -532,8 +533,20 @@ static hipError_t launch_conv_channel_last(const int8_t* x, const int8_t* w, con
   return hipSuccess;
 }
 
-hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, const GemmEpi& e,
-                       void* workspace, void* out, hipStream_t st) {
+bool conv_taps_used(const ConvGeom& G) { return G.Cg % 16 == 0 && G.Kn > 1 && G.Kn <= WT_CHUNKS; }
+
+hipError_t launch_conv_weight_taps(const int8_t* w, const ConvGeom& G, int8_t* w_taps, hipStream_t st) {
+  if (!conv_taps_used(G) || G.O == 0) return hipErrorInvalidValue;
+  const int64_t nsl = G.O * (G.Cg >> 4);
+  const int wns = G.Kn >= 256 ? WT_CHUNKS / G.Kn : 256 / G.Kn;
+  const int64_t wblk = (nsl + wns - 1) / wns;
+  if (wblk >= ((int64_t)1 << 24)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_conv_weight_taps, dim3((unsigned)wblk), dim3(256), 0, st, w, nsl, G.Cg, G.Kn, wns, w_taps);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv(const int8_t* x, const int8_t* w, const int8_t* w_taps, const ConvGeom& G,
+                       const GemmEpi& e, void* workspace, void* out, hipStream_t st) {
   if (G.N * G.O * G.Pn == 0) return hipSuccess;
   if (conv_direct(G)) {
     const int64_t total = G.N * G.O * G.Pn;
@@ -543,7 +556,7 @@ hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, cons
   }
   ConvFrame F;
   if (conv_frame_of(G, &F) && ((reinterpret_cast<uintptr_t>(workspace) | reinterpret_cast<uintptr_t>(w)) & 15) == 0)
-    return launch_conv_channel_last(x, w, G, F, e, workspace, out, st);
+    return launch_conv_channel_last(x, w, w_taps, G, F, e, workspace, out, st);
   int8_t* col = static_cast<int8_t*>(workspace);
   const int64_t NB = conv_batch_of(G, (size_t)G.Pn * (size_t)G.Kc16);
   const size_t col_bytes = ((size_t)NB * (size_t)G.Pn * (size_t)G.Kc16 + 255) & ~(size_t)255;

@@ -177,8 +177,15 @@ struct ConvGeom {
 bool conv_direct(const ConvGeom& G);
 bool conv_uses_gemm(const ConvGeom& G);
 size_t conv_workspace_bytes(const ConvGeom& G);
-hipError_t launch_conv(const int8_t* x, const int8_t* w, const ConvGeom& G, const GemmEpi& e,
-                       void* workspace, void* out, hipStream_t st);
+// w_taps (may be null): the weight already in the channel-last path's
+// tap-major form (launch_conv_weight_taps), which then is not permuted per call.
+hipError_t launch_conv(const int8_t* x, const int8_t* w, const int8_t* w_taps, const ConvGeom& G,
+                       const GemmEpi& e, void* workspace, void* out, hipStream_t st);
+// Whether the tap-major weight form is used for weights of G's shape (Cg a
+// multiple of 16, 2 <= prod(K) <= 1024), and the permutation that makes it:
+// w_taps[o][t * Cg + c] = w[o][c][t], O * Cg * prod(K) bytes.
+bool conv_taps_used(const ConvGeom& G);
+hipError_t launch_conv_weight_taps(const int8_t* w, const ConvGeom& G, int8_t* w_taps, hipStream_t st);
 
 // Calibration observer state in device memory: this header, then
 // num_bins 64-bit bin counts, then num_bins words of re-bucketing scratch.

@@ -324,6 +324,29 @@ function residentConst(arr, variant, derive) {
   return b;
 }
 
+/**
+ * The tap-major device copy of a constant int8 conv weight (convWeightTaps,
+ * made from its resident plain copy on the first use), or null for weights
+ * the conv uses as given: ui8 operands or zero points (the direct kernel),
+ * channels per group not a multiple of 16, one kernel position.
+ */
+function residentConvTaps(arr, d) {
+  const kn = numel(d.wShape.slice(2));
+  if ((d.xDtype || 'i8') !== 'i8' || (d.wDtype || 'i8') !== 'i8' || d.zpX || d.zpW) return null;
+  if (d.wShape[1] % 16 !== 0 || kn < 2 || kn > 1024) return null;
+  let m = _resident.get(arr);
+  if (!m) { m = new Map(); _resident.set(arr, m); }
+  let t = m.get('taps');
+  if (!t) {
+    const plain = residentConst(arr, 'plain');
+    t = q8().alloc(Math.max(arr.byteLength, 1));
+    q8().convWeightTaps(plain, d.d, d.wShape, d.groups, t);
+    m.set('taps', t);
+  }
+  if (_recordConsts) _recordConsts.push(t);
+  return t;
+}
+
 function markHostDirty(arr) {
   _resident.delete(arr);
   _constEpoch++;
@@ -457,7 +480,7 @@ function checkArg(a, spec) {
  * tensor argument i; `rhsNK` (quantized_dot) is the weight already in the
  * [N,K] layout when the caller has it.
  */
-function execDevice(d, dv, dev, rhsNK) {
+function execDevice(d, dv, dev, rhsNK, wTaps) {
   const A = q8();
   stats.launches++;
   switch (d.op) {
@@ -487,6 +510,12 @@ function execDevice(d, dv, dev, rhsNK) {
     case 'quantized_conv': {
       const xD = (d.xDtype || 'i8') === 'ui8' ? A.Q8_U8 : A.Q8_I8, wD = (d.wDtype || 'i8') === 'ui8' ? A.Q8_U8 : A.Q8_I8;
       const ws = A.convWorkspace(d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi, d.dilation, d.groups);
+      if (wTaps) {            // a constant weight, prepacked once
+        A.quantizedConvPrepacked(dv[d.xIdx], dv[d.wIdx], wTaps, d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi,
+                                 d.dilation, d.groups, d.zpX, d.zpW, A.Q8_I32, 0, ws > 0 ? dev.get('ws', ws) : null,
+                                 dv[d.outIdx]);
+        return;
+      }
       A.quantizedConvEx(dv[d.xIdx], xD, dv[d.wIdx], wD, d.d, d.xShape, d.wShape, d.strides, d.padLo, d.padHi,
                         d.dilation, d.groups, d.zpX, d.zpW, A.Q8_I32, 0, ws > 0 ? dev.get('ws', ws) : null,
                         dv[d.outIdx]);
@@ -575,7 +604,8 @@ function runDescriptor(d, args, dev, consts) {
     upload(dv[i], a, false);
   }
   for (const [i] of outs) dv[i] = dev.get(`out${i}`, args[i].byteLength);
-  execDevice(d, dv, dev, rhsNK);
+  const wTaps = d.op === 'quantized_conv' && consts && consts.has(args[d.wIdx]) ? residentConvTaps(args[d.wIdx], d) : null;
+  execDevice(d, dv, dev, rhsNK, wTaps);
   for (const [i] of outs) download(args[i], dv[i]);
   return args[d.outIdx];
 }
@@ -780,7 +810,12 @@ function runPlanOnDevice(plan, slots, steps, opts) {
         const b = hostArgs(s, inst)[d.bIdx];
         if (inst.consts.has(b)) rhsNK = residentConst(b, 'T', (w) => transposeI8(w, d.K, d.N));
       }
-      execDevice(d, dv, dev, rhsNK);
+      let wTaps = null;
+      if (d.op === 'quantized_conv') {
+        const w = hostArgs(s, inst)[d.wIdx];
+        if (inst.consts.has(w)) wTaps = residentConvTaps(w, d);
+      }
+      execDevice(d, dv, dev, rhsNK, wTaps);
     }
   };
 
@@ -1137,10 +1172,60 @@ function defineEagerLibrary(Library, DispatchKey, tensors) {
  * the provider leaves untagged compile for the host instead of throwing
  * 'Unsupported target kind: hip' (backend/pipeline.ts:46-47).
  */
+/**
+ * Kernel measurer of backend kind 'hip' (registerMeasurer('hip', ...), as
+ * the reference registers one per runtime: measurer_registry.ts:5-15,
+ * 'cuda' at cuda_runtime.ts:46-76,452; read by the autotuner,
+ * autotuner.ts:80-88).  Same contract as measureCudaKernel: device buffers
+ * of bufferByteSizes (the kernel's tensor arguments, then its constant
+ * buffers) hold the arguments, `warmup` launches (and at least minWarmupMs
+ * of them) run first, then `repeat` samples in milliseconds.  Each sample
+ * is one launch of the descriptor's kernels and a synchronization of the
+ * addon's stream, timed on the host: the device time of the launch plus
+ * the host round trip (CUDA's samples time the asynchronous launch only).
+ * Sizes below what the descriptor reads or writes are rejected.
+ */
+function measureHipKernel(kernel, bufferByteSizes, shapeValues, opts) {
+  const d = kernel && kernel.metadata && kernel.metadata.q8;
+  need(kernel && kernel.metadata && kernel.metadata.kind === HIP_KIND && d, 'measureHipKernel: not a hip kernel');
+  need(!shapeValues || shapeValues.length === 0, 'dynamic shapes are not supported by the int8 kernels');
+  const o = opts || {};
+  const warmup = o.warmup !== undefined ? o.warmup : 5;
+  const repeat = o.repeat !== undefined ? o.repeat : 30;
+  const minWarmupMs = o.minWarmupMs !== undefined ? o.minWarmupMs : 25;
+  const maxWarmup = o.maxWarmup !== undefined ? o.maxWarmup : 100000;
+  const specs = new Map([...inputSpecs(d), ...outputSpecs(d)]);
+  for (const [i, spec] of specs) {
+    const have = bufferByteSizes[i] || 0, want = spec.n * spec.ctor.BYTES_PER_ELEMENT;
+    need(have >= want, `measureHipKernel: buffer ${i} (${spec.what}) has ${have} bytes, the kernel needs ${want}`);
+  }
+  const A = q8();
+  const dev = new DeviceArgs();
+  const dv = bufferByteSizes.map((bytes, i) => dev.get(`m${i}`, Math.max(bytes, 1)));
+  const now = () => Number(process.hrtime.bigint()) / 1e6;
+  try {
+    const once = () => execDevice(d, dv, dev, null);
+    const t0 = now();
+    for (let w = 0; w < maxWarmup && (w < warmup || now() - t0 < minWarmupMs); w++) once();
+    A.sync();
+    const samples = [];
+    for (let i = 0; i < repeat; i++) {
+      const a = now();
+      once();
+      A.sync();
+      samples.push(now() - a);
+    }
+    return samples;
+  } finally {
+    dev.release();
+  }
+}
+
 function registerHip(r) {
   need(r && typeof r.registerBackend === 'function', 'registerBackend is required');
   const fa = r.FuncAttr || {};
   r.registerBackend(HIP_KIND, createHipRuntimeBackend());
+  if (r.registerMeasurer) r.registerMeasurer(HIP_KIND, measureHipKernel);
   if (r.registerExternalCodegen) r.registerExternalCodegen(PROVIDER, createHipExternalCodegen(fa.CONST_BUFFERS));
   if (r.registerExternalCodegenProvider) {
     r.registerExternalCodegenProvider(createHipProvider(fa.EXTERNAL_CODEGEN, fa.CONST_BUFFERS));
@@ -1156,7 +1241,7 @@ function registerHip(r) {
 module.exports = {
   HIP_KIND, PROVIDER, ACTIVATIONS_ATTR, activationMode, registerHip, createHipRuntimeBackend, createHipExternalCodegen, createHipCodegenEntry,
   createHipProvider, defineEagerLibrary, detectInt8Kernel, describe, runDescriptor, hipTarget, DeviceArgs,
-  markHostDirty, stats, resetStats, setHipGraphEnabled, isHipGraphEnabled, releasePlan,
+  markHostDirty, stats, resetStats, setHipGraphEnabled, isHipGraphEnabled, releasePlan, measureHipKernel,
   // runPlan's body without the promise: it throws where runPlan rejects
   runPlanSync: runPlanOnDevice,
 };

@@ -702,6 +702,56 @@ static napi_value js_quantized_conv(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+/* convWeightTaps(w, d, wShape, groups, wTaps): the tap-major copy of a conv
+ * weight (q8_conv_weight_taps) */
+static napi_value js_conv_weight_taps(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  void *w, *wt;
+  int64_t d, groups, ws[5];
+  uint32_t n = 0;
+  if (!get_args(env, info, 5, argv) || !arg_i64(env, argv[1], &d) || !arg_i64_array(env, argv[2], ws, 5, &n) ||
+      !arg_i64(env, argv[3], &groups))
+    return NULL;
+  if (n != (uint32_t)(2 + d)) {
+    napi_throw_range_error(env, NULL, "q8hip.convWeightTaps: wShape does not match the spatial rank");
+    return NULL;
+  }
+  int64_t wb = 1;
+  for (uint32_t i = 0; i < n; ++i) wb = nbytes(wb, ws[i], 1);
+  if (!arg_buf_n(env, argv[0], 1, wb, "convWeightTaps w", &w) || !arg_buf_n(env, argv[4], 1, wb, "convWeightTaps wTaps", &wt))
+    return NULL;
+  Q8_CHECK(env, q8_conv_weight_taps((const int8_t*)w, (int)d, ws, groups, (int8_t*)wt, g_stream));
+  return undefined(env);
+}
+
+/* quantizedConvPrepacked(x, w, wTaps, d, xShape, wShape, strides, padLo, padHi,
+ *                        dilation, groups, zpX, zpW, outKind, sOut, workspace, out) */
+static napi_value js_quantized_conv_prepacked(napi_env env, napi_callback_info info) {
+  napi_value argv[17];
+  void *x, *w, *wt, *ws, *out;
+  int64_t d, groups, zpx, zpw, ok;
+  double sOut;
+  ConvArgs c;
+  DevBuf* wsb = NULL;
+  int64_t xb, wb, ob;
+  if (!get_args(env, info, 17, argv) || !arg_i64(env, argv[3], &d) || !conv_args(env, argv + 4, d, &c) ||
+      !arg_i64(env, argv[10], &groups) || !arg_i64(env, argv[11], &zpx) || !arg_i64(env, argv[12], &zpw) ||
+      !arg_i64(env, argv[13], &ok) || !arg_f64(env, argv[14], &sOut) || !arg_buf(env, argv[15], 1, &ws))
+    return NULL;
+  conv_bytes(&c, d, 1, 1, &xb, &wb, &ob);
+  if (!arg_buf_n(env, argv[0], 1, xb, "quantizedConvPrepacked x", &x) ||
+      !arg_buf_n(env, argv[1], 1, wb, "quantizedConvPrepacked w", &w) ||
+      !arg_buf_n(env, argv[2], 1, wb, "quantizedConvPrepacked wTaps", &wt) ||
+      !arg_buf_n(env, argv[16], 1, ob, "quantizedConvPrepacked out", &out))
+    return NULL;
+  size_t ws_bytes = 0;
+  if (ws != NULL && arg_devbuf(env, argv[15], &wsb)) ws_bytes = wsb->bytes;
+  Q8_CHECK(env, q8_quantized_conv_prepacked((const int8_t*)x, (const int8_t*)w, (const int8_t*)wt, (int)d, c.xs,
+                                            c.ws, c.st, c.lo, c.hi, c.dl, groups, (int32_t)zpx, (int32_t)zpw,
+                                            (int)ok, sOut, ws, ws_bytes, out, g_stream));
+  return undefined(env);
+}
+
 /* siluMulQuantizeRows(g, u, M, K, h, q, scales) */
 /* quantizedConvEx(x, xDtype, w, wDtype, d, xShape, wShape, strides, padLo, padHi, dilation,
  *                 groups, zpX, zpW, outKind, sOut, workspace, out) */
@@ -870,6 +920,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"convWorkspace", js_conv_workspace},
       {"quantizedConv", js_quantized_conv},
       {"quantizedConvEx", js_quantized_conv_ex},
+      {"convWeightTaps", js_conv_weight_taps},
+      {"quantizedConvPrepacked", js_quantized_conv_prepacked},
       {"quantizedDotWorkspace", js_quantized_dot_workspace},
       {"quantizedDot", js_quantized_dot},
       {"ewise", js_ewise},

@@ -557,17 +557,37 @@ def conv_out_shape(x_shape, w_shape, strides, padding, dilation=None):
     return out
 
 
+def conv_weight_taps(w: torch.Tensor, groups: int = 1):
+    """The tap-major copy of a constant int8 conv weight [O, C/groups, K..]
+    that quantized_conv(..., w_taps=) uses instead of permuting w on every
+    call (q8_conv_weight_taps); None for weight shapes that are used as
+    given (channels per group not a multiple of 16, one kernel position)."""
+    _need(w, torch.int8, "conv_weight_taps w")
+    d = w.dim() - 2
+    if d < 1 or d > 3:
+        raise ValueError("conv_weight_taps: w must be [O, C/groups, K..] with 1-3 spatial dims")
+    kn = math.prod(w.shape[2:])
+    if w.shape[1] % 16 != 0 or kn < 2 or kn > 1024:
+        return None
+    wt = torch.empty(w.numel(), dtype=torch.int8, device=w.device)
+    ws = _i64_array(w.shape)
+    _call("q8_conv_weight_taps", _ptr(w), d, ws, groups, _ptr(wt), _stream(), keep=(ws,))
+    return wt
+
+
 def quantized_conv(x: torch.Tensor, w: torch.Tensor, strides, padding, dilation=None,
                    groups: int = 1, s_out: float | None = None, out: torch.Tensor | None = None,
                    workspace: torch.Tensor | None = None, zpx: int = 0,
-                   zpw: int = 0) -> torch.Tensor:
+                   zpw: int = 0, w_taps: torch.Tensor | None = None) -> torch.Tensor:
     """quantized_conv (src/compiler/ir/graph/ops/quantization.ts:156-190):
     x [N, C, S..] (NCHW and its 1-D / 3-D forms) and w [O, C/groups, K..]
     (OIHW), each int8 (read as i8) or uint8 (read as ui8), padding as
     [[lo, hi], ...] per spatial dim, zero points zpx / zpw.  s_out None: the
     int32 accumulator; otherwise the fused per-tensor dequantize
     fround(acc * s_out) as fp32 (the `dequantize` QuantizationPass appends,
-    output_scale = input_scale * kernel_scale)."""
+    output_scale = input_scale * kernel_scale).  w_taps: conv_weight_taps(w)
+    of a constant weight, so the call does not permute it (int8 operands,
+    same output bits)."""
     codes = {torch.int8: L.Q8_I8, torch.uint8: L.Q8_U8}
     for t, name in ((x, "x"), (w, "w")):
         if t.dtype not in codes:
@@ -592,6 +612,17 @@ def quantized_conv(x: torch.Tensor, w: torch.Tensor, strides, padding, dilation=
             raise ValueError(f"quantized_conv: out must have shape {shape}")
     if need.value and (workspace is None or workspace.numel() < need.value):
         workspace = torch.empty(need.value, dtype=torch.int8, device=x.device)
+    if w_taps is not None:
+        if x.dtype != torch.int8 or w.dtype != torch.int8:
+            raise ValueError("quantized_conv: w_taps is for int8 operands")
+        _need(w_taps, torch.int8, "quantized_conv w_taps")
+        if w_taps.numel() != w.numel():
+            raise ValueError("quantized_conv: w_taps must be conv_weight_taps(w)")
+        _call("q8_quantized_conv_prepacked", _ptr(x), _ptr(w), _ptr(w_taps), d, xs, ws, st, lo, hi, dl, groups,
+              int(zpx), int(zpw), L.Q8_I32 if s_out is None else L.Q8_F32, 0.0 if s_out is None else float(s_out),
+              _ptr(workspace if need.value else None), need.value, _ptr(out), _stream(),
+              keep=(xs, ws, st, lo, hi, dl, workspace, w_taps))
+        return out
     _call("q8_quantized_conv_ex", _ptr(x), codes[x.dtype], _ptr(w), codes[w.dtype], d, xs, ws, st, lo,
           hi, dl, groups, int(zpx), int(zpw),
           L.Q8_I32 if s_out is None else L.Q8_F32, 0.0 if s_out is None else float(s_out),

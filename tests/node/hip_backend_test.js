@@ -29,9 +29,11 @@ function makeRegistries() {
     def(schema) { ops.push(`${this.ns}::${schema}`); return this; }
     impl(name, key, fn) { impls.set(`${this.ns}::${name}`, { key, fn }); return this; }
   }
+  const measurers = new Map();
   return {
-    backends, codegens, providers, ops, impls,
+    backends, codegens, providers, ops, impls, measurers,
     registerBackend: (k, b) => backends.set(k, b),
+    registerMeasurer: (k, fn) => measurers.set(k, fn),
     registerExternalCodegen: (n, e) => codegens.set(n, e),
     registerExternalCodegenProvider: (p) => providers.set(p.name, p),
     FuncAttr: { EXTERNAL_CODEGEN: 'external_codegen' },
@@ -167,6 +169,11 @@ function cpuTests() {
     assert.strictEqual(out.metadata.kind, 'hip');
     assert.ok(r.ops.some((s) => s.startsWith('q8::quantize_per_token(')));
     assert.strictEqual(r.impls.get('q8::qlinear').key, 1);
+    // the autotuner's measurer for kind 'hip' (measurer_registry.ts:5-15)
+    assert.strictEqual(r.measurers.get('hip'), hip.measureHipKernel);
+    const k = cg.compile({ params: [] }, hip.hipTarget(), { op: 'quantize', n: 64, scale: 0.1, zeroPoint: 0,
+                                                            targetDtype: 'i8', inIdx: 0, outIdx: 1, outputIndices: [1] });
+    assert.throws(() => hip.measureHipKernel(k, [4 * 64, 63], [], { repeat: 1 }), /buffer 1 .* has 63 bytes, the kernel needs 64/);
   });
 
   test('provider is enabled only for the hip target with quantization on', () => {
@@ -287,6 +294,14 @@ function gpuTests(dir) {
   const be = r.backends.get('hip');
   const cg = r.codegens.get('hip_int8');
 
+  test('measurer for kind hip: per-launch samples in milliseconds', () => {
+    const kern = cg.compile({}, hip.hipTarget(), { op: 'quantized_dot', M: 64, N: 256, K: 512, aIdx: 0, bIdx: 1,
+                                                   outIdx: 2, rhsLayout: 'NK', zpA: 0, zpB: 0, outputIndices: [2] });
+    const samples = r.measurers.get('hip')(kern, [64 * 512, 256 * 512, 4 * 64 * 256], [], { warmup: 2, repeat: 7, minWarmupMs: 1 });
+    assert.strictEqual(samples.length, 7);
+    for (const t of samples) assert.ok(t > 0 && t < 1000, `sample ${t} ms`);
+  });
+
   test('runtime backend: compiled quantize (static scale) on the GPU', () => {
     const kern = cg.compile({}, hip.hipTarget(), { op: 'quantize', n: M * K, scale: sX, zeroPoint: 0,
                                                    targetDtype: 'i8', inIdx: 0, outIdx: 1, outputIndices: [1] });
@@ -355,6 +370,31 @@ function gpuTests(dir) {
     const y = new Int32Array(info.outShape.reduce((a, b) => a * b, 1));
     be.runSync(be.instantiate(kern), [xc, wc, y], null);
     writeArr(dir, 'out_conv.bin', y);
+  });
+
+  test('runtime backend: a constant conv weight is prepacked once and gives the same bits', () => {
+    // 32 channels per group, 3 x 3: the channel-last path reads the tap-major form
+    const xs = [2, 64, 9, 9], ws = [48, 32, 3, 3];
+    const pf = qconvPF(xs, ws, [1, 1], [[1, 1], [1, 1]], [1, 1], 2);
+    const info = hip.detectInt8Kernel(pf);
+    const xc = new Int8Array(xs.reduce((a, b) => a * b, 1)), wc = new Int8Array(ws.reduce((a, b) => a * b, 1));
+    for (let i = 0; i < xc.length; i++) xc[i] = ((i * 2654435761) >>> 24) - 128;
+    for (let i = 0; i < wc.length; i++) wc[i] = ((i * 40503 + 17) >>> 8 & 255) - 128;
+    const n = info.outShape.reduce((a, b) => a * b, 1);
+    const plain = new Int32Array(n);
+    be.runSync(be.instantiate(cg.compile(pf, hip.hipTarget(), info)), [xc, wc, plain], null);
+    // the same op with the weight as the kernel's constant buffer (appended
+    // after the tensor arguments, runtime.ts:246-258)
+    const dConst = Object.assign({}, info, { xIdx: 0, outIdx: 1, wIdx: 2, outputIndices: [1] });
+    const kConst = { metadata: { kind: 'hip', q8: dConst, constBuffers: [{ name: 'w', dtype: 'i8', data: wc }] } };
+    const inst = be.instantiate(kConst);
+    hip.resetStats();
+    for (let call = 0; call < 2; call++) {
+      const y = new Int32Array(n);
+      be.runSync(inst, [xc, y, wc], null);
+      assert.ok(Buffer.compare(Buffer.from(y.buffer), Buffer.from(plain.buffer)) === 0, `prepacked conv, call ${call}`);
+    }
+    assert.strictEqual(hip.stats.constUploadBytes, wc.byteLength, 'the weight is uploaded (and prepacked) once');
   });
 
   test('runtime backend: one-token dynamic qlinear (quantize + GEMV in one kernel)', () => {

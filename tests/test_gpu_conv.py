@@ -97,6 +97,30 @@ def test_quantized_conv_int32(ops, oracle, case):
     same_bits(host(got), oracle.quantized_conv(x, w, st, pd, dl, g))
 
 
+@pytest.mark.parametrize("case", CASES)
+def test_quantized_conv_prepacked_weight(ops, oracle, case):
+    """A constant weight prepacked once (q8_conv_weight_taps: tap-major,
+    w_taps[o][t * Cg + c] = w[o][c][t]) gives the same bits as the per-call
+    permutation, on every path that reads it; weights without a tap-major
+    form (Cg % 16 != 0, one kernel position) report None."""
+    xs, ws, st, pd, dl, g = case
+    rng = np.random.default_rng(sum(xs) + 17 * g)
+    x = rng.integers(-128, 128, xs).astype(np.int8)
+    w = rng.integers(-128, 128, ws).astype(np.int8)
+    wt = ops.conv_weight_taps(dev(w), g)
+    kn = int(np.prod(ws[2:]))
+    if ws[1] % 16 != 0 or kn < 2:
+        assert wt is None
+        return
+    O, Cg = ws[0], ws[1]
+    same_bits(host(wt), w.reshape(O, Cg, kn).transpose(0, 2, 1).reshape(-1))
+    for s_out in (None, 1e-4):
+        got = ops.quantized_conv(dev(x), dev(w), st, pd, dl, g, s_out=s_out, w_taps=wt)
+        acc = oracle.quantized_conv(x, w, st, pd, dl, g)
+        want = acc if s_out is None else oracle.dequantize(acc.reshape(-1), s_out).reshape(acc.shape)
+        same_bits(host(got), want)
+
+
 @pytest.mark.parametrize("case", CASES[:2] + CASES[4:6] + CASES[9:])
 def test_quantized_conv_dequant_epilogue(ops, oracle, case):
     xs, ws, st, pd, dl, g = case
