@@ -173,10 +173,11 @@ def _capture_stream():
     return _CAPTURE[0]
 
 
-def graph_time_us(body, copies, replays=5):
-    """Average microseconds per launch of body(i), i < copies, captured in one
-    HIP graph and replayed `replays` times between two events.  Falls back
-    to eager launches if capture is not possible."""
+def graph_time_us(body, copies, replays=5, batches=3):
+    """Microseconds per launch of body(i), i < copies, captured in one HIP
+    graph: the median over `batches` batches of `replays` replays, each
+    batch between two events.  Falls back to eager launches if capture is
+    not possible."""
     import torch
     try:
         # warm up on the stream the graph is captured on: per-stream state
@@ -192,13 +193,16 @@ def graph_time_us(body, copies, replays=5):
                 body(i)
         g.replay()
         torch.cuda.synchronize()
-        a, b = ev(), ev()
-        a.record()
-        for _ in range(replays):
-            g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        return 1e3 * a.elapsed_time(b) / (replays * copies), "graph"
+        per = []
+        for _ in range(batches):
+            a, b = ev(), ev()
+            a.record()
+            for _ in range(replays):
+                g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            per.append(1e3 * a.elapsed_time(b) / (replays * copies))
+        return sorted(per)[len(per) // 2], "graph"
     except Exception as exc:            # eager fallback, reported
         log(f"[bench] graph capture failed ({exc!r}); timing eager launches")
         a, b = ev(), ev()

@@ -540,3 +540,37 @@ def test_oracle_silu_equals_v8_on_whole_chunks(oracle):
         s1 = int(((v * w) & np.uint64(0xFFFFFFFF)).sum()) & 0xFFFFFFFF
         s2 = int(v.sum()) & 0xFFFFFFFF
         assert [s1, s2] == golden[c], f"chunk {c}"
+
+
+def _chunk_hash_np(h, w):
+    v = h.view(np.uint32).astype(np.uint64)
+    v[np.isnan(h)] = 0x7FC00000
+    v ^= v >> np.uint64(16)
+    v = (v * np.uint64(0x7FEB352D)) & np.uint64(0xFFFFFFFF)
+    v ^= v >> np.uint64(15)
+    return [int(((v * w) & np.uint64(0xFFFFFFFF)).sum()) & 0xFFFFFFFF, int(v.sum()) & 0xFFFFFFFF]
+
+
+def test_ewise_v8_hashes_on_chunks_with_closed_forms():
+    """tests/golden/ewise_v8_hashes.json (V8's Math.fround(Math.exp / log /
+    tanh (x)) per chunk of 2^24 bit patterns) against results fixed by the
+    mathematics, so the file and its hash definition are pinned without an
+    engine.  Chunk 0 (+0, the subnormals and normals below 2^-103): exp(x)
+    rounds to 1 and tanh(x) to x.  Chunk 255 (bits 0xff000000..): the
+    negative finite values of exponent 254 and -Inf give exp = +0,
+    tanh = -1 and log = NaN, the patterns after -Inf are NaN for all three."""
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "ewise_v8_hashes.json")) as f:
+        golden = json.load(f)
+    n = 1 << 24
+    w = 2 * np.arange(n, dtype=np.uint64) + 1
+    x0 = np.arange(n, dtype=np.uint32).view(np.float32)
+    assert _chunk_hash_np(np.ones(n, np.float32), w) == golden["exp"][0]
+    assert _chunk_hash_np(x0.copy(), w) == golden["tanh"][0]
+    finite_and_inf = 0x800001                       # 0xff000000 .. 0xff800000 (-Inf)
+    want = {"exp": 0.0, "log": np.nan, "tanh": -1.0}
+    for fn, v in want.items():
+        h = np.full(n, np.nan, np.float32)
+        h[:finite_and_inf] = v
+        assert _chunk_hash_np(h, w) == golden[fn][255], fn
