@@ -173,11 +173,17 @@ def _capture_stream():
     return _CAPTURE[0]
 
 
-def graph_time_us(body, copies, replays=5, batches=3):
+GRAPH_SETTLE_MS = 20.0
+
+
+def graph_time_us(body, copies, replays=5, batches=3, settle_ms=GRAPH_SETTLE_MS):
     """Microseconds per launch of body(i), i < copies, captured in one HIP
     graph: the median over `batches` batches of `replays` replays, each
-    batch between two events.  Falls back to eager launches if capture is
-    not possible."""
+    batch between two events, after at least settle_ms of untimed replays
+    (freshly allocated and written buffers run unevenly for the first few
+    milliseconds: the C5 quantize swings between 53 and 66 us over its first
+    ~200 launches, then holds 53-54 us).  Falls back to eager launches if
+    capture is not possible."""
     import torch
     try:
         # warm up on the stream the graph is captured on: per-stream state
@@ -193,6 +199,10 @@ def graph_time_us(body, copies, replays=5, batches=3):
                 body(i)
         g.replay()
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < settle_ms:
+            g.replay()
+            torch.cuda.synchronize()
         per = []
         for _ in range(batches):
             a, b = ev(), ev()
@@ -477,6 +487,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-requant", action="store_true",
                     help="skip the C4 step with the O projection's requant fused into its GEMM")
+    ap.add_argument("--skip", action="append", default=[], metavar="NAME",
+                    help="leave out one secondary workload (c5_quant, c5_gemv, c4, conv, napi_plans); repeatable")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the MFMA / streaming-read ceiling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -534,6 +546,8 @@ def main():
         c4 = lambda: bench_c4(fused_requant=not args.no_fused_requant)
         for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", c4),
                          ("conv", bench_conv), ("napi_plans", bench_napi_plans)):
+            if name in args.skip:
+                continue
             log(f"[bench] secondary {name}")
             try:
                 secondary.update(fn())
