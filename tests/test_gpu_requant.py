@@ -80,6 +80,32 @@ def test_requant_matches_epilogue_then_quantize(ops, oracle, M, N, K, mode, bias
         same_bits(host(got), want)
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 260, 4096), (1030, 520, 4096)])
+@pytest.mark.parametrize("bias,act", [(False, "none"), (True, "relu"), (True, "silu")])
+def test_requant_large_accumulators(ops, oracle, M, N, K, bias, act):
+    """Saturated rows and columns (|acc| up to 2^26, past 2^24 where the
+    binary32 multiply of the epilogue stops being exact): the f64 path of the
+    static-requant epilogue, in quads that also hold small accumulators, on
+    the 128 x 128 and 256 x 256 tiles."""
+    rng = np.random.default_rng(M + N + len(act))
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    A[0, :] = 127
+    A[M - 1, :] = -128
+    B[:5, :] = 127
+    B[N - 1, : K // 2] = -128
+    sA = rng.random(M) * 1e-4 + 1e-6
+    sB = rng.random(N) * 1e-3 + 1e-5
+    b = (rng.random(N).astype(np.float32) - 0.5) if bias else None
+    acc = (A.astype(np.float64) @ B.T.astype(np.float64)).astype(np.int32)
+    assert np.abs(acc).max() > (1 << 24)
+    y = oracle.epilogue(acc, "rowcol", sA, sB, bias=b, act=act)
+    s_next = float(np.max(np.abs(y))) / 127
+    got = ops.qlinear_requant(dev(A), dev(sA), dev(B), dev(sB), s_next, bias=None if b is None else dev(b),
+                              act=None if act == "none" else act)
+    same_bits(host(got), oracle.quantize(y.reshape(-1), s_next).reshape(M, N))
+
+
 def test_c2_with_fused_static_requant_equals_dynamic_c2(ops, oracle):
     """C2 (784 -> 256 -> 128 -> 10, ReLU, per-tensor requant between layers)
     run with the requant of layers 1 and 2 fused into the GEMM epilogue.
