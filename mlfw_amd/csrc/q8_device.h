@@ -47,16 +47,20 @@ __device__ __forceinline__ int quant_exact(float x, double s, double zp, int lo,
 // Callers guarantee s is a normal double in [2^-100, 2^100] (else they use
 // quant_exact for every element).
 // quant_sym_try is that decision without branches: floor(t) clamped to
-// [-256, 256] (so |t| >= 256, infinities included, saturate through the
-// integer clamp), plus the rounding step; `bad` flags the inputs the fast
-// path cannot decide -- near-ties and NaN -- which take the exact f64 path.
+// [-256, 256] (so |t| >= 256 saturates through the integer clamp), plus the
+// rounding step; `bad` flags the inputs the fast path may not decide, which
+// take the exact f64 path: every t whose fraction is within 2^-13 of 0.5,
+// and NaN and infinite t (their fraction t - floor(t) is NaN).  Near-ties
+// with |t| >= 256 are flagged too although the clamp decides them; the exact
+// path gives the same code, and a single comparison is cheaper than
+// excluding them (this test runs once per quantized value).
 __device__ __forceinline__ int quant_sym_try(float x, float r32, bool& bad) {
   const float t = x * r32;
   const float fl = __builtin_floorf(t);
   const float fr = t - fl;
   int r = (int)__builtin_amdgcn_fmed3f(fl, -256.0f, 256.0f) + (fr > 0.5f ? 1 : 0);
   r = r < -128 ? -128 : (r > 127 ? 127 : r);
-  bad = (__builtin_fabsf(t) < 256.0f && !(__builtin_fabsf(fr - 0.5f) > 0x1p-13f)) || t != t;
+  bad = !(__builtin_fabsf(fr - 0.5f) > 0x1p-13f);
   return r;
 }
 
