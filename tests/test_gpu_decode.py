@@ -5,7 +5,7 @@ S-abs scales and R1 codes of x, exact int32 quantized_dot, the E-rowcol
 epilogue with bias and activation -- compared bit for bit, together with
 the codes and scales the call writes.  Shapes cover the fused one-token
 kernel (M = 1, K <= 4096, K % 16 == 0: partial row blocks, K = 16, K = 48)
-and the two-kernel route (M > 1, K % 16 != 0, K > 4096);
+and the two-kernel route (M > 1 up to 16 tokens, K % 16 != 0, K > 4096);
 rows carry NaN, +-inf, all-zero rows and exact half-way ties.  Each case is
 also compared with the two separate calls (quantize_per_token +
 qlinear) on the device.
@@ -89,7 +89,11 @@ def edge_rows(x):
 CASES = [(1, 4096, 4096), (2, 4096, 4096), (3, 4096, 4096), (4, 4096, 4096), (1, 1000, 4096),
          (4, 1001, 4096), (2, 77, 16), (1, 77, 16), (1, 33, 48), (3, 33, 48), (4, 11008, 4096),
          (1, 11008, 4096), (1, 19, 4000), (2, 19, 4000), (1, 64, 8192), (4, 64, 8192),
-         (6, 300, 512), (1, 5, 4096), (1, 1001, 1024)]
+         (6, 300, 512), (1, 5, 4096), (1, 1001, 1024),
+         # up to 16 tokens: the MFMA GEMV routes (balanced row ranges with
+         # partial blocks at K = 4096, K < 4096, K > 4096)
+         (8, 4096, 4096), (16, 4096, 4096), (16, 11008, 4096), (13, 1001, 1024), (16, 19, 4000),
+         (5, 77, 16), (9, 33, 48), (16, 64, 8192)]
 
 
 @pytest.mark.parametrize("M,N,K", CASES)
@@ -148,7 +152,8 @@ def test_qlinear_dynamic_one_token_edge_rows(ops, oracle, K):
         same_bits(host(y), want, f"{name} y")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (1, 513, 1024), (4, 513, 1024), (3, 40, 4000)])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (1, 513, 1024), (4, 513, 1024), (3, 40, 4000),
+                                   (16, 11008, 4096), (11, 300, 2048)])
 def test_qlinear_dynamic_per_tensor(ops, oracle, M, N, K):
     r = oracle.Rng(M + N + K + 7)
     x = r.normal((M, K))
