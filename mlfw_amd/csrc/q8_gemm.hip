@@ -523,6 +523,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
   static_assert(4 * 32 * PITCH * 4 <= C::LDS, "epilogue strips fit in the stage buffers");
   int32_t* strip = reinterpret_cast<int32_t*>(lds) + wave * 32 * PITCH;
   const int qcol = 4 * (lane % LPR), qrow = lane / LPR;
+  const bool qlane = 64 % LPR == 0 || lane < LPR * RPI;   // lanes that own quads of the strip
   const int gcol = n0 + wn + qcol;
   // COLBLK: 16-byte quads need column blocks, and so the rows of every
   // block, that start on multiples of 4 elements
@@ -594,6 +595,9 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
           }
       }
     }
+    // a strip row of WN = 96 columns is 24 lanes' quads: 48 lanes read two
+    // rows at a time and lanes 48-63 sit out
+    if (!qlane) return;
     v4i q[NQ];
 #pragma unroll
     for (int it = 0; it < NQ; ++it)
@@ -644,6 +648,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
     static_assert(C::TN % 2 == 0 && MODE == 1, "GLU needs pairs of column blocks and the row x column scales");
     constexpr int WH = C::WN / 2;                  // h columns of the wave
     constexpr int LPRH = WH / 4, RPIH = 64 / LPRH, NQH = 32 / RPIH;
+    static_assert(64 % LPRH == 0, "whole strip rows per lane set");
     static_assert(NQH % 2 == 0, "quads in pairs");
     const int64_t F = N / 2;
     const int qcolh = 4 * (lane % LPRH), qrowh = lane / LPRH;
@@ -983,6 +988,7 @@ void k_qgemm(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, 
       sc4[c] = MODE == 1 ? s_cols[lc] : 0.0;
       b4[c] = e.bias ? e.bias[n0 + lc < N ? n0 + lc : N - 1] : 0.0f;
     }
+    static_assert(64 % LPR == 0, "whole strip rows per lane set");
     auto quad_ptr = [&](int it) { return reinterpret_cast<const v4i*>(strip + (it * RPI + qrow) * PITCH + qcol); };
     int8_t* o8 = static_cast<int8_t*>(out);
     constexpr int U = 4;
@@ -1140,23 +1146,47 @@ __global__ __launch_bounds__(256) void k_gemm_i8_generic(const int8_t* __restric
 #define Q8_EPI_CODES(X) \
   X(16) X(0) X(1) X(2) X(4) X(5) X(6) X(8) X(9) X(10) X(12) X(13) X(14) X(32) X(40) X(128) X(144)
 
+// The 256 x 192 tile (three 32-column blocks per wave; a strip row of 96
+// columns): the plain fp32 and int32 epilogues only -- the rolled epilogues
+// (int8 out, SiLU, dynamic requant, GLU) assume whole strip rows per 64 lanes.
+#define Q8_EPI_CODES_192(X) X(16) X(0) X(1) X(4) X(5) X(8) X(9) X(12) X(13)
+
+static bool epi_192_ok(const GemmEpi& e) {
+  switch (epi_code(e)) {
+#define Q8_CASE(code) case code:
+    Q8_EPI_CODES_192(Q8_CASE)
+#undef Q8_CASE
+    return true;
+    default:
+      return false;
+  }
+}
+
 template <int BM, int BN>
 static hipError_t launch_qgemm_tile(const int8_t* A, const int8_t* B, int M, int N, int K,
                                     const GemmEpi& e, void* out, hipStream_t st) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const dim3 grid((unsigned)(tm * tn)), block(GEMM_THREADS);
   constexpr int lds = qgemm_lds<BM, BN>();
-  switch (epi_code(e)) {
 #define Q8_LAUNCH_EPI(code)                                                                  \
   case code:                                                                                 \
     hipLaunchKernelGGL((k_qgemm<BM, BN, code>), grid, block, lds, st, A, B, M, N, K, tm, tn, \
                        e, out);                                                              \
     break;
-    Q8_EPI_CODES(Q8_LAUNCH_EPI)
-#undef Q8_LAUNCH_EPI
-    default:
-      return hipErrorInvalidValue;
+  if constexpr (BN == 192) {
+    switch (epi_code(e)) {
+      Q8_EPI_CODES_192(Q8_LAUNCH_EPI)
+      default:
+        return hipErrorInvalidValue;
+    }
+  } else {
+    switch (epi_code(e)) {
+      Q8_EPI_CODES(Q8_LAUNCH_EPI)
+      default:
+        return hipErrorInvalidValue;
+    }
   }
+#undef Q8_LAUNCH_EPI
   return hipGetLastError();
 }
 
@@ -1176,16 +1206,22 @@ std::atomic<long long> g_generic_gemm_launches{0};
 // 256..4096 x N in 2048..22016 (they pick the fastest tile on all 56); K
 // scales every shape alike, so it does not enter the choice.  Two resident
 // 128x128 workgroups per CU overlap one's epilogue with the other's main
-// loop, which is why they win many mid-size shapes.  Returns the index of
-// the chosen tile in cands.
+// loop, which is why they win many mid-size shapes.  256x192 (the plain
+// epilogues only; allowed bit 4) fits N = 6144 / 12288 in whole rounds
+// where 256x256 leaves half a round: 9% less work per second than 256x256
+// but no idle half round (fitted on eleven shapes, M 1024..4096 x N
+// 4096..22016: C4's QKV 110.6 -> 103.5 us, 4096 x 6144 110.5 -> 102.3 us;
+// the rule keeps the fastest tile on all eleven).  Returns the index of the
+// chosen tile in cands.
 static int gemm_tile_choice(int64_t M, int64_t N, unsigned allowed = 0xF) {
   struct Cand { int bm, bn, per_cu; double tmin, tfull; };
   const Cand cands[] = {{256, 256, 1, 44.0, 63.0}, {256, 128, 1, 27.5, 40.0},
-                        {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0}};
+                        {128, 128, 2, 19.0, 36.0}, {64, 64, 4, 9.0, 28.0},
+                        {256, 192, 1, 44.0, 51.5}};
   const int cus = cu_count() > 0 ? cu_count() : 256;
   int best = 0;
   double best_cost = 1e300;
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < 5; ++c) {
     if (!((allowed >> c) & 1u)) continue;
     const int64_t tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn);
     const int64_t slots = (int64_t)cus * cands[c].per_cu;
@@ -1333,10 +1369,11 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
                        A, B, (int)M, (int)N, (int)K, e, out);
     return hipGetLastError();
   }
-  switch (gemm_tile_choice(M, N)) {
+  switch (gemm_tile_choice(M, N, epi_192_ok(e) ? 0x1Fu : 0xFu)) {
     case 0: return launch_qgemm_tile<256, 256>(A, B, (int)M, (int)N, (int)K, e, out, st);
     case 1: return launch_qgemm_tile<256, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
     case 2: return launch_qgemm_tile<128, 128>(A, B, (int)M, (int)N, (int)K, e, out, st);
+    case 4: return launch_qgemm_tile<256, 192>(A, B, (int)M, (int)N, (int)K, e, out, st);
     default: return launch_qgemm_tile<64, 64>(A, B, (int)M, (int)N, (int)K, e, out, st);
   }
 }
@@ -2033,6 +2070,8 @@ hipError_t setup_kernel_attributes() {
 #define Q8_SET_256x128(code) Q8_SET_LDS((k_qgemm<256, 128, code>), (qgemm_lds<256, 128>()));
 #define Q8_SET_128(code) Q8_SET_LDS((k_qgemm<128, 128, code>), (qgemm_lds<128, 128>()));
 #define Q8_SET_64(code) Q8_SET_LDS((k_qgemm<64, 64, code>), (qgemm_lds<64, 64>()));
+#define Q8_SET_256x192(code) Q8_SET_LDS((k_qgemm<256, 192, code>), (qgemm_lds<256, 192>()));
+  Q8_EPI_CODES_192(Q8_SET_256x192)
   Q8_EPI_CODES(Q8_SET_256)
   Q8_EPI_CODES(Q8_SET_256x128)
   Q8_EPI_CODES(Q8_SET_128)
@@ -2045,6 +2084,7 @@ hipError_t setup_kernel_attributes() {
   Q8_EPI_CODES_CONV(Q8_SET_64)
 #undef Q8_SET_256
 #undef Q8_SET_256x128
+#undef Q8_SET_256x192
 #undef Q8_SET_128
 #undef Q8_SET_64
 #undef Q8_SET_LDS

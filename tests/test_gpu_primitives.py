@@ -383,7 +383,9 @@ def test_generic_gemm_route_is_counted(ops, oracle):
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 4096), (2048, 4096, 4096), (768, 1280, 11008),
                                    (4096, 4096, 4096), (4001, 3100, 2048), (4001, 3099, 2064),
                                    (1000, 1001, 4112), (513, 4095, 272), (2048, 12288, 4096),
-                                   (100, 3000, 16), (3000, 100, 32)])
+                                   (100, 3000, 16), (3000, 100, 32),
+                                   # 256 x 192 tiles (whole rounds at N = 6144 / 12288), partial in M and N
+                                   (1000, 12100, 4096), (2048, 6144, 4096)])
 def test_quantized_dot_large_exact(ops, M, N, K):
     """Large shapes: integer products and sums are exact in f64 (|acc| < 2^53),
     so an f64 matmul of the same int8 values is an exact closed-form check."""
@@ -438,7 +440,8 @@ def test_qlinear_pertensor_scales(ops, oracle):
     same_bits(host(y), oracle.epilogue(acc, "rowcol", sx[0], sw))
 
 
-@pytest.mark.parametrize("M,N,K", [(2000, 3000, 1024), (4096, 4096, 4096), (515, 517, 528)])
+@pytest.mark.parametrize("M,N,K", [(2000, 3000, 1024), (4096, 4096, 4096), (515, 517, 528),
+                                   (1000, 12100, 1024), (2048, 6144, 4096)])   # the last two: 256 x 192 tiles
 def test_qlinear_large_rowcol_exact(ops, oracle, M, N, K):
     """Full-size epilogue check: accumulators from an exact f64 matmul of the
     same int8 values, then the oracle epilogue on every element."""
@@ -454,7 +457,7 @@ def test_qlinear_large_rowcol_exact(ops, oracle, M, N, K):
     same_bits(host(y), ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 260, 4096), (8, 300, 4096), (2, 77, 8192)])
+@pytest.mark.parametrize("M,N,K", [(300, 260, 4096), (8, 300, 4096), (2, 77, 8192), (1024, 6144, 4096)])
 def test_qlinear_large_accumulators(ops, oracle, M, N, K):
     """Saturated rows and columns (|acc| up to K * 128 * 128 = 2^26 at
     K = 4096, beyond 2^24 where an int32 stops being exactly a binary32):
