@@ -248,6 +248,36 @@ def bench_c5_quant():
     return res
 
 
+def bench_ewise():
+    """q8_ewise, the device interpreter of the elementwise PrimFuncs the
+    GEMM chain fusion does not absorb, on [4096, 4096]: graph replays over
+    3 rotating input sets (> the MALL)."""
+    import torch
+    from mlfw_amd import ops as O
+    M = N = 4096
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(11)
+    from mlfw_amd import configs as C
+    for name, (prog, ins, odt, nbytes) in C.ewise_programs(M, N).items():
+        n = 3
+        sets = []
+        for _ in range(n):
+            ts = []
+            for dt, shape in ins:
+                if dt == torch.float32:
+                    ts.append(torch.randn(shape, device="cuda", generator=g))
+                else:
+                    ts.append(torch.randint(-1000 if dt == torch.int32 else -128, 1000 if dt == torch.int32 else 128,
+                                            shape, dtype=dt, device="cuda", generator=g))
+            sets.append((ts, torch.empty((M, N), dtype=odt, device="cuda")))
+        us, how = graph_time_us(lambda i: O.ewise(prog, sets[i][0], sets[i][1]), n)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"ewise_{name}_4096x4096"] = {"avg_us": us, "bytes": nbytes, "GB/s": gbs,
+                                           "frac_hbm": gbs / PEAK_HBM_GBS, "timing": how}
+        del sets
+    return res
+
+
 def bench_c5_gemv():
     import torch
     from mlfw_amd import configs as C
@@ -488,7 +518,7 @@ def main():
     ap.add_argument("--no-fused-requant", action="store_true",
                     help="skip the C4 step with the O projection's requant fused into its GEMM")
     ap.add_argument("--skip", action="append", default=[], metavar="NAME",
-                    help="leave out one secondary workload (c5_quant, c5_gemv, c4, conv, napi_plans); repeatable")
+                    help="leave out one secondary workload (c5_quant, c5_gemv, c4, conv, ewise, napi_plans); repeatable")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the MFMA / streaming-read ceiling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -545,7 +575,7 @@ def main():
     if not args.no_secondary:
         c4 = lambda: bench_c4(fused_requant=not args.no_fused_requant)
         for name, fn in (("c5_quant", bench_c5_quant), ("c5_gemv", bench_c5_gemv), ("c4", c4),
-                         ("conv", bench_conv), ("napi_plans", bench_napi_plans)):
+                         ("conv", bench_conv), ("ewise", bench_ewise), ("napi_plans", bench_napi_plans)):
             if name in args.skip:
                 continue
             log(f"[bench] secondary {name}")

@@ -198,3 +198,32 @@ def c5_gemv(x, Wq, sW, out=None):
 def c5_quant_dequant(X):
     q, s = ops.quantize_per_token(X)
     return q, s, ops.dequantize(q, s)
+
+
+# ------------------------------------------------------------------ elementwise programs
+def ewise_programs(M, N, s_q=0.05, s_dq=0.01):
+    """Three elementwise PrimFuncs as q8_ewise runs them on [M, N] (the forms
+    QuantizationPass and the fusion rules leave when the chain fusion does
+    not take them, quantization_pass.ts:431-456, rules/fusion.ts:66-79):
+    (program, input dtypes and shapes, output dtype, bytes per launch)."""
+    f32, i32, i8 = torch.float32, torch.int32, torch.int8
+    row, col = (N, 1), (0, 1)
+    progs = {}
+    # fround(fround(acc * sv[n]) + b[n]): the per-channel dequant and bias
+    progs["dequant_bias"] = (ops.ew_program((M, N), [(i32, row), (f32, col), (f32, col)], [
+        ("load", 0, 0, 0, 0, 0, 0), ("load", 1, 0, 0, 0, 1, 0), ("mul", 2, 0, 1, 0, 0, 1),
+        ("load", 3, 0, 0, 0, 2, 0), ("add", 4, 2, 3, 0, 0, 1)], 4, f32),
+        [(i32, (M, N)), (f32, (N,)), (f32, (N,))], f32, M * N * 8 + N * 8)
+    # (min(max(Math.round(Math.fround(max(x, 0) / s)), -128), 127) | 0): ReLU fused with quantize
+    progs["relu_quantize"] = (ops.ew_program((M, N), [(f32, row)], [
+        ("load", 0, 0, 0, 0, 0, 0), ("const", 1, 0, 0, 0, 0, 0), ("max", 2, 0, 1, 0, 0, 0),
+        ("const", 3, 0, 0, 0, 1, 0), ("div", 4, 2, 3, 0, 0, 1), ("round", 5, 4, 0, 0, 0, 0),
+        ("const", 6, 0, 0, 0, 2, 0), ("max", 7, 5, 6, 0, 0, 0), ("const", 8, 0, 0, 0, 3, 0),
+        ("min", 9, 7, 8, 0, 0, 0), ("toint32", 10, 9, 0, 0, 0, 0)], 10, i8, konst=(0.0, s_q, -128.0, 127.0)),
+        [(f32, (M, N))], i8, M * N * 5)
+    # fround(fround(q * s) + y): a dequantize feeding an add
+    progs["dequant_add"] = (ops.ew_program((M, N), [(i8, row), (f32, row)], [
+        ("load", 0, 0, 0, 0, 0, 0), ("const", 1, 0, 0, 0, 0, 0), ("mul", 2, 0, 1, 0, 0, 1),
+        ("load", 3, 0, 0, 0, 1, 0), ("add", 4, 2, 3, 0, 0, 1)], 4, f32, konst=(s_dq,)),
+        [(i8, (M, N)), (f32, (M, N))], f32, M * N * 9)
+    return progs

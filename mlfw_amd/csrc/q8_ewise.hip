@@ -10,10 +10,26 @@
 // register numbers come from the kernel arguments and stay in SGPRs), so the
 // interpreter never diverges.
 //
-// Registers live in LDS, register r of lane t at R[r * NT + t]: a
-// run-time register index into a private array would otherwise go to
-// scratch memory, and this layout keeps a wave's 64 accesses to one
-// register contiguous (no bank conflicts).
+// Registers live in LDS, register r of lane t at R[r * NT + t]: a wave's
+// 64 accesses to one register are contiguous (no bank conflicts).  When
+// every offset the nest forms fits in 31 bits (NARROW, checked on the host)
+// the loop indices come from 32-bit multiply-high divisions by precomputed
+// magic numbers and the offsets from 32-bit multiply-adds, else from int64
+// division.  The externs with long f64 code paths are out of line.
+//
+// Measured on [4096, 4096] (bench.py's `ewise_*` lines: a per-channel
+// dequant with bias, ReLU fused with quantize, a dequantize feeding an add):
+// 187 / 272 / 181 us, 6-10% of HBM -- the interpreter is instruction-bound,
+// not memory-bound.  Counters on the dequant-add program (5 instructions)
+// show ~145 VALU and ~170 SALU instructions per element per lane: operand
+// fetch and dispatch per program instruction, not the arithmetic.  Keeping
+// the registers in VGPRs instead (uniform register numbers, GPR index mode,
+// 2-4 elements per lane) measured slower (294 / 342 / 306 us): each indexed
+// access costs a mode switch, and the register files cut occupancy.
+// 32-bit indexing and the out-of-line externs gave 5-8% over int64
+// indexing with every extern inlined (201 / 286 / 195 us).  These are the
+// elementwise PrimFuncs the GEMM chain fusion does not absorb; a program
+// that matters for speed belongs in a fused epilogue.
 //
 // Value semantics (all f64, like JS numbers):
 //   * f32-typed arithmetic and non-exact externs round once to binary32
@@ -24,13 +40,14 @@
 //   * `| 0` is ECMA-262 ToInt32; typed-array stores convert as
 //     Float32Array (RNE), Float64Array, Int32Array (ToInt32), Int8Array and
 //     Uint8Array (low 8 bits of ToInt32).
-// exp / log / tanh / pow come from the device's f64 libm, not V8's: their
-// results can differ from the reference in the last bit of the f64, which
-// one binary32 rounding almost always absorbs (the same unpinned boundary as
-// SiLU's exp).
+// exp / log / tanh come from the device's f64 libm; rounded to binary32 (the
+// f32-typed externs) they equal V8's Math.fround(Math.exp / log / tanh(x))
+// for every binary32 x (tests/test_gpu_ewise_exhaustive.py).  pow is not
+// pinned: the f64 results of two libms can differ in the last bit.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "../../include/q8hip.h"
 #include "q8_internal.h"
@@ -107,21 +124,54 @@ __device__ __forceinline__ void store_elem(void* p, int dtype, int64_t off, doub
   }
 }
 
-__global__ __launch_bounds__(EW_NT) void k_ewise(q8_ew_prog p, EwPtrs ptr, int64_t n) {
+// x / d for 0 <= x < 2^31 by a multiply-high: m = ceil(2^(31+l) / d),
+// l = ceil(log2 d), q = (x * m) >> (31 + l) (the round-up method: the error
+// of m is below d / 2^(31+l), too small to change floor(x / d) for
+// x < 2^31).  d = 1: m = 0, q = x.
+struct EwDiv {
+  uint32_t m[Q8_EW_MAX_DIMS];
+  uint32_t sh[Q8_EW_MAX_DIMS];   // l - 1 (the multiply-high already shifts by 32)
+};
+
+__device__ __forceinline__ uint32_t ew_udiv(uint32_t x, uint32_t m, uint32_t sh) {
+  return m == 0 ? x : (__umulhi(x, m) >> sh);
+}
+
+// The externs with long f64 code paths, out of line: inlined once per
+// register file they would multiply the kernel's code and registers for
+// instructions most programs never run.
+__device__ __noinline__ double ew_slow(int op, double a, double b) {
+  switch (op) {
+    case Q8_EW_MOD: return js_rem(js_rem(a, b) + b, b);
+    case Q8_EW_TMOD: return js_rem(a, b);
+    case Q8_EW_FMOD: return js_rem(js_rem(a, b) + b, b);
+    case Q8_EW_EXP: return exp(a);
+    case Q8_EW_LOG: return log(a);
+    case Q8_EW_TANH: return tanh(a);
+    case Q8_EW_RSQRT: return 1.0 / sqrt(a);
+    default: return pow(a, b);
+  }
+}
+
+template <bool NARROW>
+__global__ __launch_bounds__(EW_NT) void k_ewise(q8_ew_prog p, EwPtrs ptr, EwDiv dv, int64_t n) {
+  using I = typename std::conditional<NARROW, uint32_t, int64_t>::type;
   __shared__ double R[Q8_EW_MAX_REGS * EW_NT];
   const int t = threadIdx.x;
   auto reg = [&](int r) -> double& { return R[r * EW_NT + t]; };
   const int nd = p.ndims;
   for (int64_t e = blockIdx.x * (int64_t)EW_NT + t; e < n; e += (int64_t)gridDim.x * EW_NT) {
     // loop indices of element e (row-major, last fastest)
-    int64_t idx[Q8_EW_MAX_DIMS];
-    int64_t rem = e;
+    I idx[Q8_EW_MAX_DIMS];
+    I rem = (I)e;
 #pragma unroll
     for (int d = Q8_EW_MAX_DIMS - 1; d >= 0; --d) {
       if (d < nd) {
-        const int64_t ext = p.extent[d];
-        idx[d] = rem % ext;
-        rem /= ext;
+        I q;
+        if constexpr (NARROW) q = ew_udiv(rem, dv.m[d], dv.sh[d]);
+        else q = rem / p.extent[d];
+        idx[d] = rem - q * (I)p.extent[d];
+        rem = q;
       } else {
         idx[d] = 0;
       }
@@ -131,10 +181,11 @@ __global__ __launch_bounds__(EW_NT) void k_ewise(q8_ew_prog p, EwPtrs ptr, int64
       double v = 0.0;
       if (in.op == Q8_EW_LOAD) {
         const int j = in.aux;
-        int64_t off = p.in_coef[j][Q8_EW_MAX_DIMS];
+        I off = (I)p.in_coef[j][Q8_EW_MAX_DIMS];
 #pragma unroll
-        for (int d = 0; d < Q8_EW_MAX_DIMS; ++d) off += p.in_coef[j][d] * idx[d];
-        v = load_elem(ptr.in[j], p.in_dtype[j], off);
+        for (int d = 0; d < Q8_EW_MAX_DIMS; ++d)
+          if (d < nd) off += (I)p.in_coef[j][d] * idx[d];
+        v = load_elem(ptr.in[j], p.in_dtype[j], (int64_t)off);
       } else if (in.op == Q8_EW_CONST) {
         v = p.konst[in.aux];
       } else if (in.op == Q8_EW_INDEX) {
@@ -147,9 +198,9 @@ __global__ __launch_bounds__(EW_NT) void k_ewise(q8_ew_prog p, EwPtrs ptr, int64
           case Q8_EW_MUL: v = a * b; break;
           case Q8_EW_DIV: v = a / b; break;
           case Q8_EW_IDIV: v = trunc(a / b); break;
-          case Q8_EW_MOD: v = js_rem(js_rem(a, b) + b, b); break;
+          case Q8_EW_MOD: v = ew_slow(Q8_EW_MOD, a, b); break;
           case Q8_EW_FLOORDIV: v = floor(a / b); break;
-          case Q8_EW_TMOD: v = js_rem(a, b); break;
+          case Q8_EW_TMOD: v = ew_slow(Q8_EW_TMOD, a, b); break;
           case Q8_EW_TDIV: v = (double)js_to_int32(a / b); break;
           case Q8_EW_NEG: v = -a; break;
           case Q8_EW_CMP:
@@ -173,12 +224,12 @@ __global__ __launch_bounds__(EW_NT) void k_ewise(q8_ew_prog p, EwPtrs ptr, int64
           case Q8_EW_ROUND: v = js_round_full(a); break;
           case Q8_EW_SIGN: v = js_sign(a); break;
           case Q8_EW_SQRT: v = sqrt(a); break;
-          case Q8_EW_FMOD: v = js_rem(js_rem(a, b) + b, b); break;
-          case Q8_EW_EXP: v = exp(a); break;
-          case Q8_EW_LOG: v = log(a); break;
-          case Q8_EW_TANH: v = tanh(a); break;
-          case Q8_EW_RSQRT: v = 1.0 / sqrt(a); break;
-          case Q8_EW_POW: v = pow(a, b); break;
+          case Q8_EW_FMOD: v = ew_slow(Q8_EW_FMOD, a, b); break;
+          case Q8_EW_EXP: v = ew_slow(Q8_EW_EXP, a, b); break;
+          case Q8_EW_LOG: v = ew_slow(Q8_EW_LOG, a, b); break;
+          case Q8_EW_TANH: v = ew_slow(Q8_EW_TANH, a, b); break;
+          case Q8_EW_RSQRT: v = ew_slow(Q8_EW_RSQRT, a, b); break;
+          case Q8_EW_POW: v = ew_slow(Q8_EW_POW, a, b); break;
           default: v = a; break;
         }
       }
@@ -249,9 +300,32 @@ hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* ou
   EwPtrs ptr{};
   for (int j = 0; j < p.ninputs; ++j) ptr.in[j] = inputs[j];
   ptr.out = out;
+  // 31-bit offsets: every extent, coefficient, offset and n
+  bool narrow = n < ((int64_t)1 << 31);
+  for (int d = 0; d < p.ndims; ++d) narrow = narrow && p.extent[d] < ((int64_t)1 << 31);
+  for (int j = 0; j < p.ninputs; ++j) {
+    int64_t hi = p.in_coef[j][Q8_EW_MAX_DIMS];
+    narrow = narrow && hi >= 0 && hi < ((int64_t)1 << 31);
+    for (int d = 0; d < p.ndims; ++d) {
+      const int64_t c = p.in_coef[j][d];
+      narrow = narrow && c > -((int64_t)1 << 31) && c < ((int64_t)1 << 31);
+      if (c > 0) hi += c * (p.extent[d] - 1);   // ewise_check bounds it by in_numel
+    }
+    narrow = narrow && hi < ((int64_t)1 << 31);
+  }
+  EwDiv dv{};
+  for (int d = 0; d < p.ndims; ++d) {
+    const uint64_t x = (uint64_t)p.extent[d];
+    if (!narrow || x <= 1) continue;     // extent 1 (or 0: no elements): q = x
+    int l = 0;
+    while (((uint64_t)1 << l) < x) ++l;
+    dv.m[d] = (uint32_t)((((uint64_t)1 << (31 + l)) + x - 1) / x);
+    dv.sh[d] = (uint32_t)(l - 1);
+  }
   const int64_t blocks = (n + EW_NT - 1) / EW_NT;
   const int grid = (int)(blocks < 16384 ? blocks : 16384);
-  hipLaunchKernelGGL(k_ewise, dim3(grid), dim3(EW_NT), 0, st, p, ptr, n);
+  if (narrow) hipLaunchKernelGGL((k_ewise<true>), dim3(grid), dim3(EW_NT), 0, st, p, ptr, dv, n);
+  else hipLaunchKernelGGL((k_ewise<false>), dim3(grid), dim3(EW_NT), 0, st, p, ptr, dv, n);
   return hipGetLastError();
 }
 

@@ -657,3 +657,67 @@ def silu_mul_quantize(g: torch.Tensor, u: torch.Tensor, h_out: torch.Tensor | No
     _call("q8_silu_mul_quantize_rows_ld", _ptr(g), ldg, _ptr(u), ldu, M, K, _ptr(h_out), _ptr(q),
           _ptr(scales), _stream())
     return q, scales
+
+
+# ------------------------------------------------------------------ elementwise programs
+# Python form of q8_ew_prog (include/q8hip.h): a loop nest of up to 6 loops,
+# inputs read at affine offsets of the loop indices, and straight-line code
+# over 16 f64 registers with the reference CPU codegen's rounding
+# (src/backend/cpu/codegen.ts:428-552).  The Node host builds these from
+# PrimFuncs (mlfw_amd/node/ewise.js); this form serves the tests and bench.
+EW_MAX_DIMS, EW_MAX_INPUTS, EW_MAX_CODE, EW_MAX_CONST = 6, 8, 96, 32
+EW_OPS = {name: i for i, name in enumerate(
+    ["load", "const", "index", "add", "sub", "mul", "div", "idiv", "mod", "floordiv", "tmod", "tdiv", "neg",
+     "cmp", "select", "toint32", "tobool", "max", "min", "abs", "floor", "ceil", "round", "sign", "sqrt",
+     "fmod", "exp", "log", "tanh", "rsqrt", "pow"])}
+_EW_DTYPES = {torch.int8: L.Q8_I8, torch.uint8: L.Q8_U8, torch.int32: L.Q8_I32, torch.float32: L.Q8_F32,
+              torch.float64: 4}
+
+
+class EwInstr(C.Structure):
+    _fields_ = [(n, C.c_uint8) for n in ("op", "dst", "a", "b", "c", "aux", "rnd", "pad")]
+
+
+class EwProg(C.Structure):
+    _fields_ = [("ndims", C.c_int32), ("ninputs", C.c_int32), ("extent", C.c_int64 * EW_MAX_DIMS),
+                ("in_dtype", C.c_int32 * EW_MAX_INPUTS),
+                ("in_coef", (C.c_int64 * (EW_MAX_DIMS + 1)) * EW_MAX_INPUTS),
+                ("out_dtype", C.c_int32), ("ncode", C.c_int32), ("result", C.c_int32), ("nconst", C.c_int32),
+                ("code", EwInstr * EW_MAX_CODE), ("konst", C.c_double * EW_MAX_CONST)]
+
+
+def ew_program(extents, inputs, code, result, out_dtype, konst=()):
+    """An EwProg.  inputs: [(dtype, coefs)] with coefs the per-loop element
+    strides (len(extents) of them, 0 for a broadcast loop) plus an optional
+    constant offset; code: [(op, dst, a, b, c, aux, rnd)] with op a name of
+    EW_OPS; result: the register stored; out_dtype a torch dtype."""
+    p = EwProg()
+    p.ndims, p.ninputs = len(extents), len(inputs)
+    if not 1 <= p.ndims <= EW_MAX_DIMS or p.ninputs > EW_MAX_INPUTS or len(code) > EW_MAX_CODE:
+        raise ValueError("ew_program: too many loops, inputs or instructions")
+    for d, x in enumerate(extents):
+        p.extent[d] = int(x)
+    for j, (dt, coefs) in enumerate(inputs):
+        p.in_dtype[j] = _EW_DTYPES[dt]
+        coefs = list(coefs)
+        for d in range(p.ndims):
+            p.in_coef[j][d] = int(coefs[d])
+        p.in_coef[j][EW_MAX_DIMS] = int(coefs[p.ndims]) if len(coefs) > p.ndims else 0
+    for i, (op, dst, a, b, c, aux, rnd) in enumerate(code):
+        p.code[i] = EwInstr(EW_OPS[op], dst, a, b, c, aux, rnd, 0)
+    p.ncode, p.result, p.out_dtype = len(code), int(result), _EW_DTYPES[out_dtype]
+    for i, k in enumerate(konst):
+        p.konst[i] = float(k)
+    p.nconst = len(konst)
+    return p
+
+
+def ewise(prog: EwProg, inputs, out: torch.Tensor) -> torch.Tensor:
+    """Runs an elementwise program over device tensors (contiguous, the
+    program's dtypes); out holds the product of the extents."""
+    n = len(inputs)
+    ins = (C.c_void_p * max(n, 1))(*[t.data_ptr() for t in inputs])
+    nums = (C.c_int64 * max(n, 1))(*[t.numel() for t in inputs])
+    _call("q8_ewise", C.c_void_p(C.addressof(prog)), C.cast(ins, C.c_void_p), C.cast(nums, C.c_void_p),
+          _ptr(out), out.numel(), _stream(), keep=(prog, ins, nums))
+    return out
