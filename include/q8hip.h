@@ -596,6 +596,17 @@ typedef struct {
 int q8_ewise(const q8_ew_prog* prog, const void* const* inputs, const int64_t* in_numel,
              void* out, int64_t out_numel, void* stream);
 
+/* How q8_ewise runs a program, no counterpart in the reference (its CUDA
+ * backend compiles every elementwise kernel with NVRTC, cuda_runtime.ts):
+ * a call over at least 2^20 elements compiles the program with hiprtc once
+ * per program and device (the same JS helper functions, the library's IEEE
+ * flags) and launches the cached kernel; smaller calls, and any program
+ * hiprtc cannot take, run on the interpreter.  mode >= 0 sets the choice
+ * (0 by size, 1 always the interpreter, 2 always compiled); the call
+ * returns the number of programs compiled and of compiled launches so far
+ * (either pointer may be NULL).  For tests and diagnosis. */
+int q8_debug_ewise_jit(int mode, int64_t* compiled, int64_t* launches);
+
 /* ------------------------------------------------------------ calibration */
 
 /* An observer is a device buffer of q8_observer_state_bytes(num_bins) bytes

@@ -783,6 +783,14 @@ int q8_gemm_requant_dynamic_status(const void* workspace, int64_t M, int* timed_
   return Q8_OK;
 }
 
+int q8_debug_ewise_jit(int mode, int64_t* compiled, int64_t* launches) {
+  Q8_REQUIRE(mode <= 2, "q8_debug_ewise_jit: mode must be 0, 1 or 2 (or negative to read only)");
+  if (mode >= 0) q8::g_ewise_jit_mode.store(mode, std::memory_order_relaxed);
+  if (compiled) *compiled = (int64_t)q8::g_ewise_jit_compiled.load(std::memory_order_relaxed);
+  if (launches) *launches = (int64_t)q8::g_ewise_jit_launches.load(std::memory_order_relaxed);
+  return Q8_OK;
+}
+
 int q8_debug_dq_force_timeout(int on) {
   q8::g_dq_force_timeout.store(on ? 1 : 0, std::memory_order_relaxed);
   return Q8_OK;

@@ -45,9 +45,17 @@
 // for every binary32 x (tests/test_gpu_ewise_exhaustive.py).  pow is not
 // pinned: the f64 results of two libms can differ in the last bit.
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
+#include <atomic>
+#include <cinttypes>
 #include <cmath>
+#include <cstdio>
+#include <mutex>
+#include <string>
 #include <type_traits>
+#include <unordered_map>
+#include <vector>
 
 #include "../../include/q8hip.h"
 #include "q8_internal.h"
@@ -63,46 +71,13 @@ struct EwPtrs {
   void* out;
 };
 
-// ECMA-262 ToInt32: NaN and infinities -> 0, otherwise trunc(x) mod 2^32.
-__device__ __forceinline__ int32_t js_to_int32(double x) {
-  if (!(x == x) || __builtin_isinf(x)) return 0;
-  double t = trunc(x);
-  if (t >= -2147483648.0 && t <= 2147483647.0) return (int32_t)t;
-  double m = fmod(t, 4294967296.0);       // exact
-  if (m < 0.0) m += 4294967296.0;          // exact: |m| < 2^32
-  return (int32_t)(uint32_t)m;
-}
-
-// Math.round: nearest integer, ties toward +inf, -0 for y in [-0.5, -0].
-__device__ __forceinline__ double js_round_full(double y) {
-  if (!(y == y) || __builtin_isinf(y)) return y;
-  const double f = floor(y);
-  double r = (y - f >= 0.5) ? f + 1.0 : f;   // y - f is exact
-  if (r == 0.0 && (y < 0.0 || __builtin_signbit(y))) r = -0.0;
-  return r;
-}
-
-// Math.max / Math.min: NaN wins; +0 is larger than -0.
-__device__ __forceinline__ double js_max(double a, double b) {
-  if (!(a == a) || !(b == b)) return __builtin_nan("");
-  if (a == b) return __builtin_signbit(a) ? b : a;
-  return a > b ? a : b;
-}
-__device__ __forceinline__ double js_min(double a, double b) {
-  if (!(a == a) || !(b == b)) return __builtin_nan("");
-  if (a == b) return __builtin_signbit(a) ? a : b;
-  return a < b ? a : b;
-}
-
-// JS `%` on numbers: the sign of the dividend, exact (C fmod).
-__device__ __forceinline__ double js_rem(double a, double b) { return fmod(a, b); }
-
-__device__ __forceinline__ double js_sign(double x) {
-  if (!(x == x) || x == 0.0) return x;     // NaN, +0, -0
-  return x > 0.0 ? 1.0 : -1.0;
-}
-
-__device__ __forceinline__ bool truthy(double x) { return x == x && x != 0.0; }
+// The JS helpers (q8_js_math.h): ECMA-262 ToInt32 (NaN and infinities ->
+// 0, else trunc(x) mod 2^32); Math.round (nearest, ties toward +inf, -0 for
+// y in [-0.5, -0]); Math.max / Math.min (NaN wins, +0 above -0); JS `%`
+// (C fmod: the sign of the dividend, exact); Math.sign; JS truthiness.
+#define Q8_JS_MATH_BODY(...) __VA_ARGS__
+#include "q8_js_math.h"
+#undef Q8_JS_MATH_BODY
 
 __device__ __forceinline__ double load_elem(const void* p, int dtype, int64_t off) {
   switch (dtype) {
@@ -294,6 +269,247 @@ const char* ewise_check(const q8_ew_prog& p, const int64_t* in_numel, int64_t ou
   return nullptr;
 }
 
+// ---------------------------------------------------------------- compiled programs
+// A program run over many elements is compiled instead: its HIP source (the
+// loop nest with its extents, offsets and dtypes as constants, one statement
+// per instruction over the same JS helpers, q8_js_math.h) goes through
+// hiprtc once per program and device, and later calls launch the cached
+// kernel.  The interpreter stays for small calls, where a compile (a few
+// hundred ms) would not pay, and as the fallback when hiprtc fails.
+std::atomic<int> g_ewise_jit_mode{0};              // 0 auto, 1 never, 2 always
+std::atomic<long long> g_ewise_jit_compiled{0}, g_ewise_jit_launches{0};
+
+namespace {
+
+const char kJsMathSrc[] =
+#define Q8_JS_MATH_BODY(...) #__VA_ARGS__
+#include "q8_js_math.h"
+#undef Q8_JS_MATH_BODY
+    ;
+
+constexpr int64_t EW_JIT_MIN_ELEMS = (int64_t)1 << 20;   // auto mode: compile from 2^20 elements
+constexpr size_t EW_JIT_MAX_PROGRAMS = 256;               // then every further program is interpreted
+
+// An exact C literal of v (hexadecimal significand).
+std::string ew_lit(double v) {
+  if (v != v) return "__builtin_nan(\"\")";
+  if (__builtin_isinf(v)) return v > 0 ? "__builtin_inf()" : "(-__builtin_inf())";
+  char buf[64];
+  snprintf(buf, sizeof buf, "(%a)", v);
+  return buf;
+}
+
+const char* ew_ctype(int dt) {
+  switch (dt) {
+    case Q8_I8: return "signed char";
+    case Q8_U8: return "unsigned char";
+    case Q8_I32: return "int";
+    case Q8_F32: return "float";
+    default: return "double";
+  }
+}
+
+const char* ew_ctype4(int dt) {
+  switch (dt) {
+    case Q8_I8: return "char4";
+    case Q8_U8: return "uchar4";
+    case Q8_I32: return "int4";
+    default: return "float4";
+  }
+}
+
+int ew_size(int dt) {
+  switch (dt) {
+    case Q8_I8: case Q8_U8: return 1;
+    case Q8_I32: case Q8_F32: return 4;
+    default: return 8;
+  }
+}
+
+// Load kinds of an input in the 4-element form
+enum { EW_LD_EACH = 0, EW_LD_VEC = 1, EW_LD_BCAST = 2 };
+
+// The kernel source of program p over V = 1 or 4 consecutive elements per
+// lane (V = 4: the last loop's extent a multiple of 4, so the four share
+// every other index; input j is read as one 4-vector (kind EW_LD_VEC:
+// contiguous along the last loop and 4-element aligned), as one value for
+// all four (EW_LD_BCAST: broadcast along it) or element by element, and the
+// output is stored as one 4-vector).  The same evaluation order and
+// rounding as the interpreter (k_ewise): an instruction's operands are read
+// before its destination is written, and `rnd` rounds every instruction's
+// value once to binary32.
+std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, const int* kind) {
+  const std::string I = narrow ? "unsigned int" : "long long";
+  auto icon = [&](int64_t v) {
+    char buf[48];
+    snprintf(buf, sizeof buf, "((%s)(%" PRId64 "LL))", I.c_str(), v);
+    return std::string(buf);
+  };
+  auto R = [](int r, int k) { return "r" + std::to_string(r) + "_" + std::to_string(k); };
+  const int last = p.ndims - 1;
+  std::string s = "#include <hip/hip_runtime.h>\n";
+  s += kJsMathSrc;
+  s += "\nstruct EwJitPtrs { const void* in[" + std::to_string(Q8_EW_MAX_INPUTS) + "]; void* out; };\n";
+  s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(EW_NT) +
+       ") void q8_ew_jit(EwJitPtrs ptr, long long n) {\n";
+  s += "  const long long G = (long long)gridDim.x * " + std::to_string(EW_NT) + ";\n";
+  s += "  for (long long t = (long long)blockIdx.x * " + std::to_string(EW_NT) + " + threadIdx.x; t < n / " +
+       std::to_string(V) + "; t += G) {\n";
+  s += "    const long long e = t * " + std::to_string(V) + ";\n";
+  s += "    " + I + " rem = (" + I + ")e;\n";
+  for (int d = last; d >= 0; --d) {
+    const std::string x = icon(p.extent[d]);
+    s += "    const " + I + " i" + std::to_string(d) + " = rem % " + x + "; rem /= " + x + ";\n";
+  }
+  s += "    (void)rem;\n";
+  for (int r = 0; r < Q8_EW_MAX_REGS; ++r) {
+    s += "    double";
+    for (int k = 0; k < V; ++k) s += std::string(k ? "," : "") + " " + R(r, k) + " = 0.0";
+    s += ";\n";
+  }
+  static const char* cmp_ops[] = {"==", "!=", "<", "<=", ">", ">="};
+  static const char* lanes[] = {"x", "y", "z", "w"};
+  auto put = [&](const q8_ew_instr& in, int k, const std::string& v) {
+    s += "    { double v = " + v + ";";
+    if (in.rnd) s += " v = (double)(float)v;";
+    s += " " + R(in.dst, k) + " = v; }\n";
+  };
+  for (int pc = 0; pc < p.ncode; ++pc) {
+    const q8_ew_instr& in = p.code[pc];
+    if (in.op == Q8_EW_LOAD) {
+      const int j = in.aux;
+      std::string off = icon(p.in_coef[j][Q8_EW_MAX_DIMS]);
+      for (int d = 0; d < p.ndims; ++d)
+        if (p.in_coef[j][d] != 0) off += " + " + icon(p.in_coef[j][d]) + " * i" + std::to_string(d);
+      const std::string base = std::string("((const ") + ew_ctype(p.in_dtype[j]) + "*)ptr.in[" + std::to_string(j) + "])";
+      const int kd = V == 1 ? EW_LD_EACH : kind[j];
+      if (kd == EW_LD_VEC && p.in_dtype[j] == Q8_F64) {
+        s += "    { const double2 q0 = *(const double2*)(" + base + " + " + off + "), q1 = *(const double2*)(" + base +
+             " + " + off + " + 2);\n";
+        for (int k = 0; k < V; ++k) put(in, k, std::string(k < 2 ? "q0." : "q1.") + lanes[k & 1]);
+        s += "    }\n";
+      } else if (kd == EW_LD_VEC) {
+        s += std::string("    { const ") + ew_ctype4(p.in_dtype[j]) + " q = *(const " + ew_ctype4(p.in_dtype[j]) +
+             "*)(" + base + " + " + off + ");\n";
+        for (int k = 0; k < V; ++k) put(in, k, std::string("(double)q.") + lanes[k]);
+        s += "    }\n";
+      } else if (kd == EW_LD_BCAST) {
+        s += "    { const double q = (double)" + base + "[" + off + "];\n";
+        for (int k = 0; k < V; ++k) put(in, k, "q");
+        s += "    }\n";
+      } else {
+        for (int k = 0; k < V; ++k)
+          put(in, k, "(double)" + base + "[" + off + (k ? " + " + icon(p.in_coef[j][last] * k) : "") + "]");
+      }
+      continue;
+    }
+    for (int k = 0; k < V; ++k) {
+      const std::string a = R(in.a, k), b = R(in.b, k), c = R(in.c, k);
+      std::string v;
+      switch (in.op) {
+        case Q8_EW_CONST: v = ew_lit(p.konst[in.aux]); break;
+        case Q8_EW_INDEX:
+          v = "(double)(i" + std::to_string(in.aux) + (in.aux == last && k ? " + " + icon(k) : "") + ")";
+          break;
+        case Q8_EW_ADD: v = a + " + " + b; break;
+        case Q8_EW_SUB: v = a + " - " + b; break;
+        case Q8_EW_MUL: v = a + " * " + b; break;
+        case Q8_EW_DIV: v = a + " / " + b; break;
+        case Q8_EW_IDIV: v = "trunc(" + a + " / " + b + ")"; break;
+        case Q8_EW_MOD: case Q8_EW_FMOD: v = "js_rem(js_rem(" + a + ", " + b + ") + " + b + ", " + b + ")"; break;
+        case Q8_EW_FLOORDIV: v = "floor(" + a + " / " + b + ")"; break;
+        case Q8_EW_TMOD: v = "js_rem(" + a + ", " + b + ")"; break;
+        case Q8_EW_TDIV: v = "(double)js_to_int32(" + a + " / " + b + ")"; break;
+        case Q8_EW_NEG: v = "-" + a; break;
+        case Q8_EW_CMP: v = "((" + a + " " + cmp_ops[in.aux <= 5 ? in.aux : 5] + " " + b + ") ? 1.0 : 0.0)"; break;
+        case Q8_EW_SELECT: v = "(truthy(" + a + ") ? " + b + " : " + c + ")"; break;
+        case Q8_EW_TOINT32: v = "(double)js_to_int32(" + a + ")"; break;
+        case Q8_EW_TOBOOL: v = "(truthy(" + a + ") ? 1.0 : 0.0)"; break;
+        case Q8_EW_MAX: v = "js_max(" + a + ", " + b + ")"; break;
+        case Q8_EW_MIN: v = "js_min(" + a + ", " + b + ")"; break;
+        case Q8_EW_ABS: v = "fabs(" + a + ")"; break;
+        case Q8_EW_FLOOR: v = "floor(" + a + ")"; break;
+        case Q8_EW_CEIL: v = "ceil(" + a + ")"; break;
+        case Q8_EW_ROUND: v = "js_round_full(" + a + ")"; break;
+        case Q8_EW_SIGN: v = "js_sign(" + a + ")"; break;
+        case Q8_EW_SQRT: v = "sqrt(" + a + ")"; break;
+        case Q8_EW_EXP: v = "exp(" + a + ")"; break;
+        case Q8_EW_LOG: v = "log(" + a + ")"; break;
+        case Q8_EW_TANH: v = "tanh(" + a + ")"; break;
+        case Q8_EW_RSQRT: v = "1.0 / sqrt(" + a + ")"; break;
+        case Q8_EW_POW: v = "pow(" + a + ", " + b + ")"; break;
+        default: v = a; break;
+      }
+      put(in, k, v);
+    }
+  }
+  // the store: Float32Array / Float64Array conversion, ToInt32 and its low bits
+  auto conv = [&](int k) {
+    const std::string r = R(p.result, k);
+    switch (p.out_dtype) {
+      case Q8_F32: return "(float)" + r;
+      case Q8_F64: return r;
+      case Q8_I32: return "js_to_int32(" + r + ")";
+      case Q8_I8: return "(signed char)(unsigned char)(unsigned int)js_to_int32(" + r + ")";
+      default: return "(unsigned char)(unsigned int)js_to_int32(" + r + ")";
+    }
+  };
+  if (V == 4 && p.out_dtype == Q8_F64) {
+    s += "    ((double2*)ptr.out)[e / 2] = make_double2(" + conv(0) + ", " + conv(1) + ");\n";
+    s += "    ((double2*)ptr.out)[e / 2 + 1] = make_double2(" + conv(2) + ", " + conv(3) + ");\n";
+  } else if (V == 4) {
+    const char* t4 = p.out_dtype == Q8_F32 ? "float4" : p.out_dtype == Q8_I32 ? "int4"
+                     : p.out_dtype == Q8_I8 ? "char4" : "uchar4";
+    const char* mk = p.out_dtype == Q8_F32 ? "make_float4" : p.out_dtype == Q8_I32 ? "make_int4"
+                     : p.out_dtype == Q8_I8 ? "make_char4" : "make_uchar4";
+    s += std::string("    ((") + t4 + "*)ptr.out)[e / 4] = " + mk + "(" + conv(0) + ", " + conv(1) + ", " + conv(2) +
+         ", " + conv(3) + ");\n";
+  } else {
+    s += std::string("    ((") + ew_ctype(p.out_dtype) + "*)ptr.out)[e] = " + conv(0) + ";\n";
+  }
+  s += "  }\n}\n";
+  return s;
+}
+
+// The compiled kernel of a program source on the current device (nullptr
+// if hiprtc or the module load failed; the failure is cached too).
+hipFunction_t ewise_jit_kernel(const std::string& src) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  static std::mutex mu;
+  static std::unordered_map<std::string, hipFunction_t> cache;
+  const std::string key = std::to_string(dev) + "\n" + src;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  if (cache.size() >= EW_JIT_MAX_PROGRAMS) return nullptr;
+  hipFunction_t fn = nullptr;
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "q8_ew_jit.hip", 0, nullptr, nullptr) == HIPRTC_SUCCESS) {
+    // the library's own arithmetic flags: IEEE, no contraction, no packed FP32
+    const char* opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-fno-fast-math",
+                          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+    if (hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts) == HIPRTC_SUCCESS) {
+      size_t sz = 0;
+      if (hiprtcGetCodeSize(prog, &sz) == HIPRTC_SUCCESS && sz > 0) {
+        std::vector<char> code(sz);
+        hipModule_t mod;
+        if (hiprtcGetCode(prog, code.data()) == HIPRTC_SUCCESS &&
+            hipModuleLoadData(&mod, code.data()) == hipSuccess &&
+            hipModuleGetFunction(&fn, mod, "q8_ew_jit") != hipSuccess)
+          fn = nullptr;
+      }
+    }
+    hiprtcDestroyProgram(&prog);
+  }
+  (void)hipGetLastError();   // a failed load must not surface at the next launch
+  cache.emplace(key, fn);
+  if (fn) g_ewise_jit_compiled.fetch_add(1, std::memory_order_relaxed);
+  return fn;
+}
+
+}  // namespace
+
 hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* out, int64_t n,
                         hipStream_t st) {
   if (n == 0) return hipSuccess;
@@ -324,6 +540,33 @@ hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* ou
   }
   const int64_t blocks = (n + EW_NT - 1) / EW_NT;
   const int grid = (int)(blocks < 16384 ? blocks : 16384);
+  const int mode = g_ewise_jit_mode.load(std::memory_order_relaxed);
+  if (mode == 2 || (mode == 0 && n >= EW_JIT_MIN_ELEMS)) {
+    // four elements per lane when the last loop's extent allows it and the
+    // output is 16-byte aligned (as torch and the addon allocate)
+    int kind[Q8_EW_MAX_INPUTS] = {};
+    const int last = p.ndims - 1;
+    const bool v4 = p.ndims >= 1 && p.extent[last] % 4 == 0 &&
+                    reinterpret_cast<uintptr_t>(out) % (4 * (uintptr_t)ew_size(p.out_dtype) < 16
+                                                            ? 4 * (uintptr_t)ew_size(p.out_dtype) : 16) == 0;
+    for (int j = 0; v4 && j < p.ninputs; ++j) {
+      const int64_t cl = p.in_coef[j][last];
+      bool aligned = cl == 1 && p.in_coef[j][Q8_EW_MAX_DIMS] % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(inputs[j]) % (uintptr_t)(4 * ew_size(p.in_dtype[j]) < 16
+                                                                         ? 4 * ew_size(p.in_dtype[j]) : 16) == 0;
+      for (int d = 0; d < last; ++d) aligned = aligned && p.in_coef[j][d] % 4 == 0;
+      kind[j] = cl == 0 ? EW_LD_BCAST : aligned ? EW_LD_VEC : EW_LD_EACH;
+    }
+    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, kind))) {
+      long long nn = (long long)n;
+      void* args[] = {&ptr, &nn};
+      const int64_t vblocks = (n / (v4 ? 4 : 1) + EW_NT - 1) / EW_NT;
+      const unsigned vgrid = (unsigned)(vblocks < 16384 ? vblocks : 16384);
+      const hipError_t err = hipModuleLaunchKernel(fn, vgrid, 1, 1, EW_NT, 1, 1, 0, st, args, nullptr);
+      if (err == hipSuccess) g_ewise_jit_launches.fetch_add(1, std::memory_order_relaxed);
+      return err;
+    }
+  }
   if (narrow) hipLaunchKernelGGL((k_ewise<true>), dim3(grid), dim3(EW_NT), 0, st, p, ptr, dv, n);
   else hipLaunchKernelGGL((k_ewise<false>), dim3(grid), dim3(EW_NT), 0, st, p, ptr, dv, n);
   return hipGetLastError();

@@ -116,6 +116,10 @@ hipError_t launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, i
 // once; gemm_dq_fits tells beforehand.  g_dq_force_timeout (test hook) makes
 // every launch's grid-wide wait run out.
 extern std::atomic<int> g_dq_force_timeout;
+// q8_ewise's route (q8_debug_ewise_jit): 0 by size, 1 interpreter, 2 compiled;
+// programs compiled and compiled launches so far
+extern std::atomic<int> g_ewise_jit_mode;
+extern std::atomic<long long> g_ewise_jit_compiled, g_ewise_jit_launches;
 bool gemm_dq_fits(int64_t M, int64_t N);
 size_t gemm_dq_ws_bytes(int64_t M);
 hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
