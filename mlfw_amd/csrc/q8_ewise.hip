@@ -17,19 +17,17 @@
 // magic numbers and the offsets from 32-bit multiply-adds, else from int64
 // division.  The externs with long f64 code paths are out of line.
 //
-// Measured on [4096, 4096] (bench.py's `ewise_*` lines: a per-channel
-// dequant with bias, ReLU fused with quantize, a dequantize feeding an add):
-// 187 / 272 / 181 us, 6-10% of HBM -- the interpreter is instruction-bound,
-// not memory-bound.  Counters on the dequant-add program (5 instructions)
-// show ~145 VALU and ~170 SALU instructions per element per lane: operand
-// fetch and dispatch per program instruction, not the arithmetic.  Keeping
-// the registers in VGPRs instead (uniform register numbers, GPR index mode,
-// 2-4 elements per lane) measured slower (294 / 342 / 306 us): each indexed
-// access costs a mode switch, and the register files cut occupancy.
-// 32-bit indexing and the out-of-line externs gave 5-8% over int64
-// indexing with every extern inlined (201 / 286 / 195 us).  These are the
-// elementwise PrimFuncs the GEMM chain fusion does not absorb; a program
-// that matters for speed belongs in a fused epilogue.
+// The interpreter is instruction-bound, not memory-bound: counters on a
+// 5-instruction program show ~145 VALU and ~170 SALU instructions per
+// element per lane, operand fetch and dispatch per program instruction, not
+// the arithmetic; on bench.py's [4096, 4096] programs (a per-channel
+// dequant with bias, ReLU fused with quantize, a dequantize feeding an add)
+// it takes 187 / 272 / 182 us, 6-10% of HBM.  Keeping its registers in
+// VGPRs instead (uniform register numbers, GPR index mode, 2-4 elements per
+// lane) measured slower (294 / 342 / 306 us).  So a call over 2^20 elements
+// or more runs the program compiled instead (hiprtc, once per program and
+// device, below): 26 / 30 / 30 us on the same programs, the first and the
+// last at 62-64% of HBM, the quantize bound by its f64 division.
 //
 // Value semantics (all f64, like JS numbers):
 //   * f32-typed arithmetic and non-exact externs round once to binary32

@@ -13,7 +13,8 @@ through the C ABI: q8_ewise with the one-instruction program a JS
 PrimFunc `out[i] = exp(in[i])` translates to (LOAD, then EXP / LOG / TANH
 rounded to binary32), and the same hashes are taken on the device.  Equal
 hashes on all 256 chunks: the device's bits equal V8's (any NaN counted as
-one NaN) for every input."""
+one NaN) for every input, on both of q8_ewise's routes (the interpreter and
+the hiprtc-compiled program)."""
 import ctypes as C
 import json
 import os
@@ -81,8 +82,9 @@ def chunk_hash(h, w):
     return [s1, s2]
 
 
+@pytest.mark.parametrize("route", [1, 2], ids=["interpreted", "compiled"])
 @pytest.mark.parametrize("name,op", [("exp", EW_EXP), ("log", EW_LOG), ("tanh", EW_TANH)])
-def test_ewise_extern_bits_equal_v8_on_every_input(lib, name, op):
+def test_ewise_extern_bits_equal_v8_on_every_input(lib, name, op, route):
     with open(GOLDEN) as f:
         golden = json.load(f)[name]
     assert len(golden) == 256
@@ -92,7 +94,16 @@ def test_ewise_extern_bits_equal_v8_on_every_input(lib, name, op):
     bits = torch.arange(n, dtype=torch.int64, device=DEV)
     out = torch.empty(n, dtype=torch.float32, device=DEV)
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lib.call("q8_debug_ewise_jit", route, None, None)      # q8_ewise's interpreter, or the compiled program
     bad = []
+    try:
+        chunks(lib, prog, bits, out, w, golden, n, stream, bad, name)
+    finally:
+        lib.call("q8_debug_ewise_jit", 0, None, None)
+    assert not bad, f"{name}: {len(bad)} of 256 chunks differ from V8: {bad[:16]}"
+
+
+def chunks(lib, prog, bits, out, w, golden, n, stream, bad, name):
     for c in range(256):
         x = ((bits + c * n) & M32)
         x = torch.where(x >= 1 << 31, x - (1 << 32), x).to(torch.int32).view(torch.float32)
@@ -104,4 +115,3 @@ def test_ewise_extern_bits_equal_v8_on_every_input(lib, name, op):
             bad.append(c)
         if c % 64 == 63:
             print(f"{name} exhaustive: chunks 0..{c} done, {len(bad)} differ", flush=True)
-    assert not bad, f"{name}: {len(bad)} of 256 chunks differ from V8: {bad[:16]}"
