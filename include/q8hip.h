@@ -607,6 +607,13 @@ int q8_ewise(const q8_ew_prog* prog, const void* const* inputs, const int64_t* i
  * (either pointer may be NULL).  For tests and diagnosis. */
 int q8_debug_ewise_jit(int mode, int64_t* compiled, int64_t* launches);
 
+/* Why the last program hiprtc could not take fell back to the interpreter:
+ * the failing step (hiprtc compile, code object load ...), its error string
+ * and the compiler log, copied into buf (cap bytes, truncated and
+ * NUL-terminated; "" if no compile has failed); *len (may be NULL) gets the
+ * message's full length.  No counterpart in the reference; for diagnosis. */
+int q8_debug_ewise_jit_error(char* buf, size_t cap, size_t* len);
+
 /* ------------------------------------------------------------ calibration */
 
 /* An observer is a device buffer of q8_observer_state_bytes(num_bins) bytes

@@ -90,6 +90,7 @@ SIGNATURES = {
     "q8_gemm_requant_dynamic_status": [_vp, _i64, _vp, _vp],
     "q8_debug_dq_force_timeout": [_int],
     "q8_debug_ewise_jit": [_int, _vp, _vp],
+    "q8_debug_ewise_jit_error": [_vp, C.c_size_t, _vp],
     "q8_quantized_dot_workspace": [_i64, _i64, _i64, _int, _int, C.c_int32, C.c_int32, _vp],
     "q8_quantized_dot": [_vp, _int, _vp, _int, _i64, _i64, _i64, C.c_int32, C.c_int32, _vp, C.c_size_t,
                          _vp, _vp],

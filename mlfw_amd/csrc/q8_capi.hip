@@ -791,6 +791,12 @@ int q8_debug_ewise_jit(int mode, int64_t* compiled, int64_t* launches) {
   return Q8_OK;
 }
 
+int q8_debug_ewise_jit_error(char* buf, size_t cap, size_t* len) {
+  const size_t n = q8::ewise_jit_error(buf, cap);
+  if (len) *len = n;
+  return Q8_OK;
+}
+
 int q8_debug_dq_force_timeout(int on) {
   q8::g_dq_force_timeout.store(on ? 1 : 0, std::memory_order_relaxed);
   return Q8_OK;

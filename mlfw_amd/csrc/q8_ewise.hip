@@ -345,8 +345,10 @@ std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, const int*
   };
   auto R = [](int r, int k) { return "r" + std::to_string(r) + "_" + std::to_string(k); };
   const int last = p.ndims - 1;
-  std::string s = "#include <hip/hip_runtime.h>\n";
-  s += kJsMathSrc;
+  // No #include: hiprtc declares the HIP built-ins, vector types and math
+  // functions itself, and an included header is found only where comgr
+  // locates the ROCm tree (not under every launcher, e.g. a profiler's).
+  std::string s = kJsMathSrc;
   s += "\nstruct EwJitPtrs { const void* in[" + std::to_string(Q8_EW_MAX_INPUTS) + "]; void* out; };\n";
   s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(EW_NT) +
        ") void q8_ew_jit(EwJitPtrs ptr, long long n) {\n";
@@ -469,37 +471,59 @@ std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, const int*
   return s;
 }
 
+// Guards the compile cache and g_jit_error: why the last failed compile
+// failed (the failing step, its error string, the hiprtc log), "" if none has.
+std::mutex g_jit_mu;
+std::string g_jit_error;
+
 // The compiled kernel of a program source on the current device (nullptr
 // if hiprtc or the module load failed; the failure is cached too).
 hipFunction_t ewise_jit_kernel(const std::string& src) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  static std::mutex mu;
   static std::unordered_map<std::string, hipFunction_t> cache;
   const std::string key = std::to_string(dev) + "\n" + src;
-  std::lock_guard<std::mutex> lock(mu);
+  std::lock_guard<std::mutex> lock(g_jit_mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   if (cache.size() >= EW_JIT_MAX_PROGRAMS) return nullptr;
   hipFunction_t fn = nullptr;
+  std::string why;
   hiprtcProgram prog;
-  if (hiprtcCreateProgram(&prog, src.c_str(), "q8_ew_jit.hip", 0, nullptr, nullptr) == HIPRTC_SUCCESS) {
+  hiprtcResult rc = hiprtcCreateProgram(&prog, src.c_str(), "q8_ew_jit.hip", 0, nullptr, nullptr);
+  if (rc != HIPRTC_SUCCESS) {
+    why = std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(rc);
+  } else {
     // the library's own arithmetic flags: IEEE, no contraction, no packed FP32
     const char* opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-fno-fast-math",
                           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
-    if (hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts) == HIPRTC_SUCCESS) {
-      size_t sz = 0;
-      if (hiprtcGetCodeSize(prog, &sz) == HIPRTC_SUCCESS && sz > 0) {
-        std::vector<char> code(sz);
-        hipModule_t mod;
-        if (hiprtcGetCode(prog, code.data()) == HIPRTC_SUCCESS &&
-            hipModuleLoadData(&mod, code.data()) == hipSuccess &&
-            hipModuleGetFunction(&fn, mod, "q8_ew_jit") != hipSuccess)
-          fn = nullptr;
+    rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+    size_t sz = 0;
+    if (rc != HIPRTC_SUCCESS) {
+      why = std::string("hiprtcCompileProgram: ") + hiprtcGetErrorString(rc);
+      size_t ln = 0;
+      if (hiprtcGetProgramLogSize(prog, &ln) == HIPRTC_SUCCESS && ln > 1) {
+        std::string log(ln, '\0');
+        if (hiprtcGetProgramLog(prog, &log[0]) == HIPRTC_SUCCESS) why += "\n" + log;
+      }
+    } else if ((rc = hiprtcGetCodeSize(prog, &sz)) != HIPRTC_SUCCESS || sz == 0) {
+      why = std::string("hiprtcGetCodeSize: ") + hiprtcGetErrorString(rc);
+    } else {
+      std::vector<char> code(sz);
+      hipModule_t mod;
+      hipError_t he;
+      if ((rc = hiprtcGetCode(prog, code.data())) != HIPRTC_SUCCESS)
+        why = std::string("hiprtcGetCode: ") + hiprtcGetErrorString(rc);
+      else if ((he = hipModuleLoadData(&mod, code.data())) != hipSuccess)
+        why = std::string("hipModuleLoadData: ") + hipGetErrorString(he);
+      else if ((he = hipModuleGetFunction(&fn, mod, "q8_ew_jit")) != hipSuccess) {
+        why = std::string("hipModuleGetFunction: ") + hipGetErrorString(he);
+        fn = nullptr;
       }
     }
     hiprtcDestroyProgram(&prog);
   }
+  if (!fn) g_jit_error = why;
   (void)hipGetLastError();   // a failed load must not surface at the next launch
   cache.emplace(key, fn);
   if (fn) g_ewise_jit_compiled.fetch_add(1, std::memory_order_relaxed);
@@ -507,6 +531,12 @@ hipFunction_t ewise_jit_kernel(const std::string& src) {
 }
 
 }  // namespace
+
+size_t ewise_jit_error(char* buf, size_t cap) {
+  std::lock_guard<std::mutex> lock(g_jit_mu);
+  if (buf && cap > 0) snprintf(buf, cap, "%s", g_jit_error.c_str());
+  return g_jit_error.size();
+}
 
 hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* out, int64_t n,
                         hipStream_t st) {

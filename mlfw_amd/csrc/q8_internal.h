@@ -120,6 +120,9 @@ extern std::atomic<int> g_dq_force_timeout;
 // programs compiled and compiled launches so far
 extern std::atomic<int> g_ewise_jit_mode;
 extern std::atomic<long long> g_ewise_jit_compiled, g_ewise_jit_launches;
+// Copies why the last failed ewise compile failed into buf (truncated,
+// NUL-terminated; "" if none has) and returns the message's full length.
+size_t ewise_jit_error(char* buf, size_t cap);
 bool gemm_dq_fits(int64_t M, int64_t N);
 size_t gemm_dq_ws_bytes(int64_t M);
 hipError_t launch_gemm_dq(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,

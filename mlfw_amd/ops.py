@@ -721,3 +721,12 @@ def ewise(prog: EwProg, inputs, out: torch.Tensor) -> torch.Tensor:
     _call("q8_ewise", C.c_void_p(C.addressof(prog)), C.cast(ins, C.c_void_p), C.cast(nums, C.c_void_p),
           _ptr(out), out.numel(), _stream(), keep=(prog, ins, nums))
     return out
+
+
+def ewise_jit_error() -> str:
+    """Why the last program that hiprtc could not compile fell back to the
+    interpreter ("" if none has)."""
+    n = C.c_size_t(0)
+    buf = C.create_string_buffer(4096)
+    _call("q8_debug_ewise_jit_error", C.cast(buf, C.c_void_p), C.sizeof(buf), C.byref(n))
+    return buf.value.decode(errors="replace")

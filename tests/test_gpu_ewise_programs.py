@@ -109,7 +109,7 @@ def test_large_programs_run_compiled(ops, oracle):
     ops.ewise(prog, [x], a)
     torch.cuda.synchronize()
     c1, l1 = jit_counts()
-    assert l1 == l0 + 1, "a 2^20-element call should launch the compiled kernel"
+    assert l1 == l0 + 1, f"a 2^20-element call should launch the compiled kernel: {ops.ewise_jit_error()!r}"
     set_jit(1)
     try:
         b = torch.empty_like(a)
