@@ -25,8 +25,9 @@ calibration), or null when that file is absent.
 secondary: the HBM-bound kernels of C5 (per-token quantize and dequantize
 of [16384,4096], GEMVs M in {1,4,16} x N in {4096,11008}, and the same
 GEMVs for M <= 4 with 4-bit per-group weights, and the one-call dynamic
-qlinear), the C4 projection set, and quantized_conv on ResNet-style
-layers at batch 32 (synthetic int8 data).  Each is captured R times in a
+qlinear), the C4 projection set, quantized_conv on ResNet-style layers at
+batch 32 (synthetic int8 data), and three elementwise programs through
+q8_ewise.  Each is captured R times in a
 HIP graph (rotating input buffers so the 256 MB Infinity Cache cannot
 serve repeats, except conv, whose inputs are a few MB) and the graph is
 replayed between two events: per-launch host overhead would otherwise
@@ -249,9 +250,10 @@ def bench_c5_quant():
 
 
 def bench_ewise():
-    """q8_ewise, the device interpreter of the elementwise PrimFuncs the
-    GEMM chain fusion does not absorb, on [4096, 4096]: graph replays over
-    3 rotating input sets (> the MALL)."""
+    """q8_ewise on the elementwise PrimFuncs the GEMM chain fusion does not
+    absorb, on [4096, 4096] (2^24 elements: the hiprtc-compiled route):
+    graph replays over 4 rotating input and output sets (320-576 MiB, more
+    than the 256 MB MALL)."""
     import torch
     from mlfw_amd import ops as O
     M = N = 4096
@@ -259,7 +261,7 @@ def bench_ewise():
     g = torch.Generator(device="cuda").manual_seed(11)
     from mlfw_amd import configs as C
     for name, (prog, ins, odt, nbytes) in C.ewise_programs(M, N).items():
-        n = 3
+        n = 4
         sets = []
         for _ in range(n):
             ts = []

@@ -26,8 +26,10 @@
 // VGPRs instead (uniform register numbers, GPR index mode, 2-4 elements per
 // lane) measured slower (294 / 342 / 306 us).  So a call over 2^20 elements
 // or more runs the program compiled instead (hiprtc, once per program and
-// device, below): 26 / 30 / 30 us on the same programs, the first and the
-// last at 62-64% of HBM, the quantize bound by its f64 division.
+// device, below): 27 / 23 / 30 us on the same programs, the first and the
+// last at 62% of HBM (a plain streaming kernel of the same bytes takes
+// 28 us for the last), the quantize at 46% (the same bytes stream in 16 us;
+// its rounded division, round and clamps are what remains).
 //
 // Value semantics (all f64, like JS numbers):
 //   * f32-typed arithmetic and non-exact externs round once to binary32
@@ -327,23 +329,54 @@ int ew_size(int dt) {
 // Load kinds of an input in the 4-element form
 enum { EW_LD_EACH = 0, EW_LD_VEC = 1, EW_LD_BCAST = 2 };
 
+// An exact C literal of a binary32 value v.
+std::string ew_litf(double v) {
+  if (v != v) return "__builtin_nanf(\"\")";
+  if (__builtin_isinf(v)) return v > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+  char buf[64];
+  snprintf(buf, sizeof buf, "(%af)", v);
+  return buf;
+}
+
+bool ew_is_f32(double v) { return v != v || (double)(float)v == v; }
+
+// Static types of the compiled kernels' values: TF a binary32 value held as
+// float, TI an int32 value (ToInt32's result, an i32 load) held as int, TD
+// any other number, held as double.
+enum { EW_TF = 0, EW_TI = 1, EW_TD = 2 };
+
 // The kernel source of program p over V = 1 or 4 consecutive elements per
 // lane (V = 4: the last loop's extent a multiple of 4, so the four share
 // every other index; input j is read as one 4-vector (kind EW_LD_VEC:
 // contiguous along the last loop and 4-element aligned), as one value for
 // all four (EW_LD_BCAST: broadcast along it) or element by element, and the
-// output is stored as one 4-vector).  The same evaluation order and
-// rounding as the interpreter (k_ewise): an instruction's operands are read
-// before its destination is written, and `rnd` rounds every instruction's
-// value once to binary32.
-std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, const int* kind) {
+// output is stored as one 4-vector).  Each lane takes U such groups a
+// grid stride apart and issues the loads of all U groups (every input the
+// program reads) before any arithmetic, so that a lane has U loads in
+// flight per input; a group past the end loads the last group again
+// (clamped, so the loads stay unconditional) and is not stored.
+//
+// The program is straight-line code, so every instruction's value becomes a
+// constant of its own (operands are read before the destination register
+// names the new value, as in the interpreter), with a static type.  A value
+// is float when it is exactly binary32: f32, i8 and u8 loads, binary32
+// constants, loop indices below 2^24, comparisons, and every rounded
+// (`rnd`) value.  Operations on float operands run in binary32 where that
+// gives the f64 evaluation's bits: max, min, abs, neg, floor, ceil, round,
+// sign, comparisons and ToInt32 are exact; fround(a + b), fround(a - b),
+// fround(a * b) and fround(a / b) of binary32 a and b are the binary32
+// operations themselves (53 >= 2 * 24 + 2: rounding the f64 result to
+// binary32 gives the correctly rounded binary32 result).  fround(a / c) by a
+// constant c that is not binary32 goes through js_fround_div_const (through
+// js_fround_div_const_f, without a division, when a is binary32).  Every
+// other operation runs in f64 on the operands converted exactly.
+std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, int U, const int* kind) {
   const std::string I = narrow ? "unsigned int" : "long long";
   auto icon = [&](int64_t v) {
     char buf[48];
     snprintf(buf, sizeof buf, "((%s)(%" PRId64 "LL))", I.c_str(), v);
     return std::string(buf);
   };
-  auto R = [](int r, int k) { return "r" + std::to_string(r) + "_" + std::to_string(k); };
   const int last = p.ndims - 1;
   // No #include: hiprtc declares the HIP built-ins, vector types and math
   // functions itself, and an included header is found only where comgr
@@ -352,120 +385,238 @@ std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, const int*
   s += "\nstruct EwJitPtrs { const void* in[" + std::to_string(Q8_EW_MAX_INPUTS) + "]; void* out; };\n";
   s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(EW_NT) +
        ") void q8_ew_jit(EwJitPtrs ptr, long long n) {\n";
-  s += "  const long long G = (long long)gridDim.x * " + std::to_string(EW_NT) + ";\n";
-  s += "  for (long long t = (long long)blockIdx.x * " + std::to_string(EW_NT) + " + threadIdx.x; t < n / " +
-       std::to_string(V) + "; t += G) {\n";
-  s += "    const long long e = t * " + std::to_string(V) + ";\n";
-  s += "    " + I + " rem = (" + I + ")e;\n";
-  for (int d = last; d >= 0; --d) {
-    const std::string x = icon(p.extent[d]);
-    s += "    const " + I + " i" + std::to_string(d) + " = rem % " + x + "; rem /= " + x + ";\n";
+  const std::string Vs = std::to_string(V);
+  s += "  const long long G = (long long)gridDim.x * " + std::to_string(EW_NT) + ", nv = n / " + Vs + ";\n";
+  s += "  for (long long t = (long long)blockIdx.x * " + std::to_string(EW_NT) + " + threadIdx.x; t < nv; t += G * " +
+       std::to_string(U) + ") {\n";
+  for (int u = 0; u < U; ++u) {
+    const std::string us = std::to_string(u);
+    if (u == 0) s += "    const long long t0 = t;\n";
+    else s += "    const long long t" + us + " = t + " + us + " * G < nv ? t + " + us + " * G : nv - 1;\n";
+    s += "    const long long e" + us + " = t" + us + " * " + Vs + ";\n";
+    s += "    " + I + " rem" + us + " = (" + I + ")e" + us + ";\n";
+    for (int d = last; d >= 0; --d) {
+      const std::string x = icon(p.extent[d]);
+      s += "    const " + I + " i" + std::to_string(d) + "_" + us + " = rem" + us + " % " + x + "; rem" + us +
+           " /= " + x + ";\n";
+    }
+    s += "    (void)rem" + us + ";\n";
   }
-  s += "    (void)rem;\n";
-  for (int r = 0; r < Q8_EW_MAX_REGS; ++r) {
-    s += "    double";
-    for (int k = 0; k < V; ++k) s += std::string(k ? "," : "") + " " + R(r, k) + " = 0.0";
-    s += ";\n";
-  }
+
+  // register state: the type of the value it names, the value's variable
+  // (per lane: name + "_" + lane) or a literal, and the constant if known
+  struct Reg { int t = EW_TF; std::string name = "0.0f"; bool lit = true; bool known = true; double k = 0.0; };
+  Reg reg[Q8_EW_MAX_REGS];
+  const int NL = U * V;   // lane L: group L / V, element L % V of it
+  auto X = [&](int r, int k) { return reg[r].lit ? reg[r].name : reg[r].name + "_" + std::to_string(k); };
+  auto D = [&](int r, int k) { return reg[r].t == EW_TD ? X(r, k) : "(double)" + X(r, k); };
+  static const char* ctype[] = {"float", "int", "double"};
   static const char* cmp_ops[] = {"==", "!=", "<", "<=", ">", ">="};
   static const char* lanes[] = {"x", "y", "z", "w"};
-  auto put = [&](const q8_ew_instr& in, int k, const std::string& v) {
-    s += "    { double v = " + v + ";";
-    if (in.rnd) s += " v = (double)(float)v;";
-    s += " " + R(in.dst, k) + " = v; }\n";
+  // defines instruction pc's value from per-lane expressions of type t,
+  // rounded to binary32 when rnd is set
+  auto define = [&](int pc, const q8_ew_instr& in, int t, const std::vector<std::string>& ex) {
+    const bool rnd = in.rnd && t != EW_TF;
+    const int tt = rnd ? EW_TF : t;
+    const std::string name = "v" + std::to_string(pc);
+    for (int L = 0; L < NL; ++L)
+      s += std::string("    const ") + ctype[tt] + " " + name + "_" + std::to_string(L) + " = " +
+           (rnd ? "(float)(" + ex[L] + ")" : ex[L]) + ";\n";
+    Reg& r = reg[in.dst];
+    r.t = tt;
+    r.name = name;
+    r.lit = false;
+    r.known = false;
   };
+  // every load first: per LOAD instruction, its values per lane
+  std::vector<std::vector<std::string>> ld(p.ncode);
   for (int pc = 0; pc < p.ncode; ++pc) {
     const q8_ew_instr& in = p.code[pc];
-    if (in.op == Q8_EW_LOAD) {
-      const int j = in.aux;
+    if (in.op != Q8_EW_LOAD) continue;
+    const int j = in.aux;
+    const int dt = p.in_dtype[j];
+    const int t = dt == Q8_F64 ? EW_TD : dt == Q8_I32 ? EW_TI : EW_TF;
+    const std::string base = std::string("((const ") + ew_ctype(dt) + "*)ptr.in[" + std::to_string(j) + "])";
+    const std::string cv = std::string("(") + ctype[t] + ")";
+    const int kd = V == 1 ? EW_LD_EACH : kind[j];
+    ld[pc].resize(NL);
+    for (int u = 0; u < U; ++u) {
+      const std::string us = std::to_string(u);
       std::string off = icon(p.in_coef[j][Q8_EW_MAX_DIMS]);
       for (int d = 0; d < p.ndims; ++d)
-        if (p.in_coef[j][d] != 0) off += " + " + icon(p.in_coef[j][d]) + " * i" + std::to_string(d);
-      const std::string base = std::string("((const ") + ew_ctype(p.in_dtype[j]) + "*)ptr.in[" + std::to_string(j) + "])";
-      const int kd = V == 1 ? EW_LD_EACH : kind[j];
-      if (kd == EW_LD_VEC && p.in_dtype[j] == Q8_F64) {
-        s += "    { const double2 q0 = *(const double2*)(" + base + " + " + off + "), q1 = *(const double2*)(" + base +
-             " + " + off + " + 2);\n";
-        for (int k = 0; k < V; ++k) put(in, k, std::string(k < 2 ? "q0." : "q1.") + lanes[k & 1]);
-        s += "    }\n";
+        if (p.in_coef[j][d] != 0) off += " + " + icon(p.in_coef[j][d]) + " * i" + std::to_string(d) + "_" + us;
+      const std::string q = "q" + std::to_string(pc) + "_" + us;
+      for (int k = 0; k < V; ++k) {
+        std::string& e = ld[pc][u * V + k];
+        if (kd == EW_LD_VEC && dt == Q8_F64) e = q + (k < 2 ? "a." : "b.") + lanes[k & 1];
+        else if (kd == EW_LD_VEC) e = cv + q + "." + lanes[k];
+        else if (kd == EW_LD_BCAST) e = q;
+        else e = q + "_" + std::to_string(k);
+      }
+      if (kd == EW_LD_VEC && dt == Q8_F64) {
+        s += "    const double2 " + q + "a = *(const double2*)(" + base + " + " + off + "), " + q +
+             "b = *(const double2*)(" + base + " + " + off + " + 2);\n";
       } else if (kd == EW_LD_VEC) {
-        s += std::string("    { const ") + ew_ctype4(p.in_dtype[j]) + " q = *(const " + ew_ctype4(p.in_dtype[j]) +
-             "*)(" + base + " + " + off + ");\n";
-        for (int k = 0; k < V; ++k) put(in, k, std::string("(double)q.") + lanes[k]);
-        s += "    }\n";
+        s += std::string("    const ") + ew_ctype4(dt) + " " + q + " = *(const " + ew_ctype4(dt) + "*)(" + base +
+             " + " + off + ");\n";
       } else if (kd == EW_LD_BCAST) {
-        s += "    { const double q = (double)" + base + "[" + off + "];\n";
-        for (int k = 0; k < V; ++k) put(in, k, "q");
-        s += "    }\n";
+        s += std::string("    const ") + ctype[t] + " " + q + " = " + cv + base + "[" + off + "];\n";
       } else {
         for (int k = 0; k < V; ++k)
-          put(in, k, "(double)" + base + "[" + off + (k ? " + " + icon(p.in_coef[j][last] * k) : "") + "]");
+          s += std::string("    const ") + ctype[t] + " " + q + "_" + std::to_string(k) + " = " + cv + base + "[" +
+               off + (k ? " + " + icon(p.in_coef[j][last] * k) : "") + "];\n";
       }
-      continue;
-    }
-    for (int k = 0; k < V; ++k) {
-      const std::string a = R(in.a, k), b = R(in.b, k), c = R(in.c, k);
-      std::string v;
-      switch (in.op) {
-        case Q8_EW_CONST: v = ew_lit(p.konst[in.aux]); break;
-        case Q8_EW_INDEX:
-          v = "(double)(i" + std::to_string(in.aux) + (in.aux == last && k ? " + " + icon(k) : "") + ")";
-          break;
-        case Q8_EW_ADD: v = a + " + " + b; break;
-        case Q8_EW_SUB: v = a + " - " + b; break;
-        case Q8_EW_MUL: v = a + " * " + b; break;
-        case Q8_EW_DIV: v = a + " / " + b; break;
-        case Q8_EW_IDIV: v = "trunc(" + a + " / " + b + ")"; break;
-        case Q8_EW_MOD: case Q8_EW_FMOD: v = "js_rem(js_rem(" + a + ", " + b + ") + " + b + ", " + b + ")"; break;
-        case Q8_EW_FLOORDIV: v = "floor(" + a + " / " + b + ")"; break;
-        case Q8_EW_TMOD: v = "js_rem(" + a + ", " + b + ")"; break;
-        case Q8_EW_TDIV: v = "(double)js_to_int32(" + a + " / " + b + ")"; break;
-        case Q8_EW_NEG: v = "-" + a; break;
-        case Q8_EW_CMP: v = "((" + a + " " + cmp_ops[in.aux <= 5 ? in.aux : 5] + " " + b + ") ? 1.0 : 0.0)"; break;
-        case Q8_EW_SELECT: v = "(truthy(" + a + ") ? " + b + " : " + c + ")"; break;
-        case Q8_EW_TOINT32: v = "(double)js_to_int32(" + a + ")"; break;
-        case Q8_EW_TOBOOL: v = "(truthy(" + a + ") ? 1.0 : 0.0)"; break;
-        case Q8_EW_MAX: v = "js_max(" + a + ", " + b + ")"; break;
-        case Q8_EW_MIN: v = "js_min(" + a + ", " + b + ")"; break;
-        case Q8_EW_ABS: v = "fabs(" + a + ")"; break;
-        case Q8_EW_FLOOR: v = "floor(" + a + ")"; break;
-        case Q8_EW_CEIL: v = "ceil(" + a + ")"; break;
-        case Q8_EW_ROUND: v = "js_round_full(" + a + ")"; break;
-        case Q8_EW_SIGN: v = "js_sign(" + a + ")"; break;
-        case Q8_EW_SQRT: v = "sqrt(" + a + ")"; break;
-        case Q8_EW_EXP: v = "exp(" + a + ")"; break;
-        case Q8_EW_LOG: v = "log(" + a + ")"; break;
-        case Q8_EW_TANH: v = "tanh(" + a + ")"; break;
-        case Q8_EW_RSQRT: v = "1.0 / sqrt(" + a + ")"; break;
-        case Q8_EW_POW: v = "pow(" + a + ", " + b + ")"; break;
-        default: v = a; break;
-      }
-      put(in, k, v);
     }
   }
+  for (int pc = 0; pc < p.ncode; ++pc) {
+    const q8_ew_instr& in = p.code[pc];
+    std::vector<std::string> ex(NL);
+    if (in.op == Q8_EW_LOAD) {
+      const int dt = p.in_dtype[in.aux];
+      define(pc, in, dt == Q8_F64 ? EW_TD : dt == Q8_I32 ? EW_TI : EW_TF, ld[pc]);
+      continue;
+    }
+    if (in.op == Q8_EW_CONST) {
+      double v = p.konst[in.aux];
+      if (in.rnd) v = (double)(float)v;
+      Reg& r = reg[in.dst];
+      r.t = ew_is_f32(v) ? EW_TF : EW_TD;
+      r.name = r.t == EW_TF ? ew_litf(v) : ew_lit(v);
+      r.lit = true;
+      r.known = true;
+      r.k = v;
+      continue;
+    }
+    const int ta = reg[in.a].t, tb = reg[in.b].t, tc = reg[in.c].t;
+    const bool ff = ta == EW_TF && tb == EW_TF, ii = ta == EW_TI && tb == EW_TI;
+    int t = EW_TD;
+    for (int L = 0; L < NL; ++L) {
+      const int k = L % V;
+      const std::string us = std::to_string(L / V);
+      const std::string a = X(in.a, L), b = X(in.b, L), c = X(in.c, L);
+      const std::string da = D(in.a, L), db = D(in.b, L), dc = D(in.c, L);
+      std::string v;
+      switch (in.op) {
+        case Q8_EW_INDEX:
+          t = p.extent[in.aux] <= ((int64_t)1 << 24) ? EW_TF : EW_TD;
+          v = std::string("(") + ctype[t] + ")(i" + std::to_string(in.aux) + "_" + us +
+              (in.aux == last && k ? " + " + icon(k) : "") + ")";
+          break;
+        case Q8_EW_ADD: case Q8_EW_SUB: case Q8_EW_MUL: case Q8_EW_DIV: {
+          const char* o = in.op == Q8_EW_ADD ? " + " : in.op == Q8_EW_SUB ? " - " : in.op == Q8_EW_MUL ? " * " : " / ";
+          const Reg& rb = reg[in.b];
+          const double cb = rb.k;
+          if (in.rnd && ff) {
+            t = EW_TF;
+            v = a + o + b;
+          } else if (in.rnd && in.op == Q8_EW_DIV && rb.known && cb == cb && !__builtin_isinf(cb) &&
+                     __builtin_fabs(cb) >= 0x1p-1000 && __builtin_fabs(cb) <= 0x1p1000) {
+            t = EW_TF;
+            const double ac = __builtin_fabs(cb);
+            if (ta == EW_TF && ac >= 0x1p-800 && ac <= 0x1p800)
+              v = "js_fround_div_const_f(" + a + ", " + ew_lit(ac) + ", " + ew_lit(1.0 / ac) + ", " +
+                  (cb < 0 ? "true" : "false") + ")";
+            else
+              v = "js_fround_div_const(" + da + ", " + ew_lit(cb) + ", " + ew_lit(1.0 / cb) + ")";
+          } else {
+            v = da + o + db;
+          }
+          break;
+        }
+        case Q8_EW_IDIV: v = "trunc(" + da + " / " + db + ")"; break;
+        case Q8_EW_MOD: case Q8_EW_FMOD: v = "js_rem(js_rem(" + da + ", " + db + ") + " + db + ", " + db + ")"; break;
+        case Q8_EW_FLOORDIV: v = "floor(" + da + " / " + db + ")"; break;
+        case Q8_EW_TMOD: v = "js_rem(" + da + ", " + db + ")"; break;
+        case Q8_EW_TDIV: t = EW_TI; v = "js_to_int32(" + da + " / " + db + ")"; break;
+        case Q8_EW_NEG:
+          if (ta == EW_TF) { t = EW_TF; v = "-" + a; } else { v = "-" + da; }
+          break;
+        case Q8_EW_CMP: {
+          const char* o = cmp_ops[in.aux <= 5 ? in.aux : 5];
+          t = EW_TF;
+          v = (ff || ii ? "((" + a + " " + o + " " + b + ")" : "((" + da + " " + o + " " + db + ")") + " ? 1.0f : 0.0f)";
+          break;
+        }
+        case Q8_EW_SELECT: {
+          const std::string cond = ta == EW_TF ? "truthyf(" + a + ")" : ta == EW_TI ? "(" + a + " != 0)"
+                                                                                    : "truthy(" + a + ")";
+          if (tb == tc) { t = tb; v = "(" + cond + " ? " + b + " : " + c + ")"; }
+          else { v = "(" + cond + " ? " + db + " : " + dc + ")"; }
+          break;
+        }
+        case Q8_EW_TOINT32:
+          t = EW_TI;
+          v = ta == EW_TF ? "js_to_int32f(" + a + ")" : ta == EW_TI ? a : "js_to_int32(" + a + ")";
+          break;
+        case Q8_EW_TOBOOL:
+          t = EW_TF;
+          v = (ta == EW_TF ? "(truthyf(" + a + ")" : ta == EW_TI ? "((" + a + " != 0)" : "(truthy(" + a + ")") +
+              " ? 1.0f : 0.0f)";
+          break;
+        case Q8_EW_MAX: case Q8_EW_MIN: {
+          const bool mx = in.op == Q8_EW_MAX;
+          if (ff) { t = EW_TF; v = std::string(mx ? "js_maxf(" : "js_minf(") + a + ", " + b + ")"; }
+          else if (ii) { t = EW_TI; v = "(" + a + (mx ? " > " : " < ") + b + " ? " + a + " : " + b + ")"; }
+          else { v = std::string(mx ? "js_max(" : "js_min(") + da + ", " + db + ")"; }
+          break;
+        }
+        case Q8_EW_ABS:
+          if (ta == EW_TF) { t = EW_TF; v = "__builtin_fabsf(" + a + ")"; } else { v = "fabs(" + da + ")"; }
+          break;
+        case Q8_EW_FLOOR: case Q8_EW_CEIL: case Q8_EW_ROUND: {
+          const char* ff32 = in.op == Q8_EW_FLOOR ? "__builtin_floorf(" : in.op == Q8_EW_CEIL ? "__builtin_ceilf(" : "js_roundf(";
+          const char* ff64 = in.op == Q8_EW_FLOOR ? "floor(" : in.op == Q8_EW_CEIL ? "ceil(" : "js_round_full(";
+          if (ta == EW_TF) { t = EW_TF; v = ff32 + a + ")"; }
+          else if (ta == EW_TI) { t = EW_TI; v = a; }
+          else { v = ff64 + a + ")"; }
+          break;
+        }
+        case Q8_EW_SIGN:
+          if (ta == EW_TF) { t = EW_TF; v = "js_signf(" + a + ")"; } else { v = "js_sign(" + da + ")"; }
+          break;
+        case Q8_EW_SQRT: v = "sqrt(" + da + ")"; break;
+        case Q8_EW_EXP: v = "exp(" + da + ")"; break;
+        case Q8_EW_LOG: v = "log(" + da + ")"; break;
+        case Q8_EW_TANH: v = "tanh(" + da + ")"; break;
+        case Q8_EW_RSQRT: v = "1.0 / sqrt(" + da + ")"; break;
+        case Q8_EW_POW: v = "pow(" + da + ", " + db + ")"; break;
+        default: t = ta; v = a; break;
+      }
+      ex[L] = v;
+    }
+    define(pc, in, t, ex);
+  }
   // the store: Float32Array / Float64Array conversion, ToInt32 and its low bits
+  const int rt = reg[p.result].t;
   auto conv = [&](int k) {
-    const std::string r = R(p.result, k);
+    const std::string r = X(p.result, k);
+    const std::string i32 = rt == EW_TI ? r : rt == EW_TF ? "js_to_int32f(" + r + ")" : "js_to_int32(" + r + ")";
     switch (p.out_dtype) {
-      case Q8_F32: return "(float)" + r;
-      case Q8_F64: return r;
-      case Q8_I32: return "js_to_int32(" + r + ")";
-      case Q8_I8: return "(signed char)(unsigned char)(unsigned int)js_to_int32(" + r + ")";
-      default: return "(unsigned char)(unsigned int)js_to_int32(" + r + ")";
+      case Q8_F32: return rt == EW_TF ? r : "(float)" + r;
+      case Q8_F64: return rt == EW_TD ? r : "(double)" + r;
+      case Q8_I32: return i32;
+      case Q8_I8: return "(signed char)(unsigned char)(unsigned int)" + i32;
+      default: return "(unsigned char)(unsigned int)" + i32;
     }
   };
-  if (V == 4 && p.out_dtype == Q8_F64) {
-    s += "    ((double2*)ptr.out)[e / 2] = make_double2(" + conv(0) + ", " + conv(1) + ");\n";
-    s += "    ((double2*)ptr.out)[e / 2 + 1] = make_double2(" + conv(2) + ", " + conv(3) + ");\n";
-  } else if (V == 4) {
-    const char* t4 = p.out_dtype == Q8_F32 ? "float4" : p.out_dtype == Q8_I32 ? "int4"
-                     : p.out_dtype == Q8_I8 ? "char4" : "uchar4";
-    const char* mk = p.out_dtype == Q8_F32 ? "make_float4" : p.out_dtype == Q8_I32 ? "make_int4"
-                     : p.out_dtype == Q8_I8 ? "make_char4" : "make_uchar4";
-    s += std::string("    ((") + t4 + "*)ptr.out)[e / 4] = " + mk + "(" + conv(0) + ", " + conv(1) + ", " + conv(2) +
-         ", " + conv(3) + ");\n";
-  } else {
-    s += std::string("    ((") + ew_ctype(p.out_dtype) + "*)ptr.out)[e] = " + conv(0) + ";\n";
+  for (int u = 0; u < U; ++u) {
+    const std::string us = std::to_string(u), e = "e" + us;
+    const int L0 = u * V;
+    std::string st;
+    if (V == 4 && p.out_dtype == Q8_F64) {
+      st = "((double2*)ptr.out)[" + e + " / 2] = make_double2(" + conv(L0) + ", " + conv(L0 + 1) + "); " +
+           "((double2*)ptr.out)[" + e + " / 2 + 1] = make_double2(" + conv(L0 + 2) + ", " + conv(L0 + 3) + ");";
+    } else if (V == 4) {
+      const char* t4 = p.out_dtype == Q8_F32 ? "float4" : p.out_dtype == Q8_I32 ? "int4"
+                       : p.out_dtype == Q8_I8 ? "char4" : "uchar4";
+      const char* mk = p.out_dtype == Q8_F32 ? "make_float4" : p.out_dtype == Q8_I32 ? "make_int4"
+                       : p.out_dtype == Q8_I8 ? "make_char4" : "make_uchar4";
+      st = std::string("((") + t4 + "*)ptr.out)[" + e + " / 4] = " + mk + "(" + conv(L0) + ", " + conv(L0 + 1) +
+           ", " + conv(L0 + 2) + ", " + conv(L0 + 3) + ");";
+    } else {
+      st = std::string("((") + ew_ctype(p.out_dtype) + "*)ptr.out)[" + e + "] = " + conv(L0) + ";";
+    }
+    s += u == 0 ? "    " + st + "\n" : "    if (t + " + us + " * G < nv) { " + st + " }\n";
   }
   s += "  }\n}\n";
   return s;
@@ -585,10 +736,25 @@ hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* ou
       for (int d = 0; d < last; ++d) aligned = aligned && p.in_coef[j][d] % 4 == 0;
       kind[j] = cl == 0 ? EW_LD_BCAST : aligned ? EW_LD_VEC : EW_LD_EACH;
     }
-    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, kind))) {
+    // groups per lane: 2 when the program has arithmetic enough for the
+    // second group's loads to overlap the first group's work (measured on
+    // [4096, 4096]: a 7-operation ReLU + quantize 22.6 -> 21.5 us), else 1
+    // (a 2-operation dequant + add, bound by HBM, 28.3 -> 29.3 us with 2);
+    // 1 as well for the externs with long f64 code paths, whose copies
+    // would grow the kernel's code
+    bool slow = false;
+    int arith = 0;
+    for (int i = 0; i < p.ncode; ++i) {
+      const int op = p.code[i].op;
+      slow = slow || op == Q8_EW_EXP || op == Q8_EW_LOG || op == Q8_EW_TANH || op == Q8_EW_POW ||
+             op == Q8_EW_MOD || op == Q8_EW_FMOD || op == Q8_EW_TMOD || op == Q8_EW_RSQRT;
+      arith += op != Q8_EW_LOAD && op != Q8_EW_CONST;
+    }
+    const int U = !slow && arith >= 6 ? 2 : 1;
+    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, U, kind))) {
       long long nn = (long long)n;
       void* args[] = {&ptr, &nn};
-      const int64_t vblocks = (n / (v4 ? 4 : 1) + EW_NT - 1) / EW_NT;
+      const int64_t vblocks = (n / (v4 ? 4 : 1) + (int64_t)EW_NT * U - 1) / ((int64_t)EW_NT * U);
       const unsigned vgrid = (unsigned)(vblocks < 16384 ? vblocks : 16384);
       const hipError_t err = hipModuleLaunchKernel(fn, vgrid, 1, 1, EW_NT, 1, 1, 0, st, args, nullptr);
       if (err == hipSuccess) g_ewise_jit_launches.fetch_add(1, std::memory_order_relaxed);
