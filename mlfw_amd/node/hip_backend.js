@@ -647,8 +647,19 @@ function constSet(kernel) {
  *    later call replays the graph (device_plan.ts:178-218).  The graph is
  *    dropped and re-captured when a buffer it names changes (a slot group
  *    grows, a constant buffer is marked dirty).
+ *  - runPlan enqueues the plan's uploads and launches on the addon's stream
+ *    and returns; its promise settles once the device has finished
+ *    (syncAsync: the wait runs on a worker thread, so the JS thread is free
+ *    meanwhile) and the outputs are downloaded.  The reference's CUDA
+ *    runner blocks the JS thread for the whole plan instead (devSync in
+ *    device_plan.ts:254,276 inside the async runCudaPlan, :288-299).  All
+ *    plans share one stream, and a plan's downloads must read its own
+ *    results, so an asynchronous run waits for the previous one to settle
+ *    before it uploads anything; runPlanSync and releasePlan throw while
+ *    an asynchronous run of the plan is in flight.
  */
 const _planState = new WeakMap();
+let _planTail = null;        // the last asynchronous plan run, settled or not; null when none is in flight
 let _useHipGraph = false;
 /** The reference's setCudaGraphEnabled / isCudaGraphEnabled (device_plan.ts:40-42). */
 function setHipGraphEnabled(on) { _useHipGraph = !!on; }
@@ -679,6 +690,7 @@ function planStateOf(plan) {
 function releasePlan(plan) {
   const st = _planState.get(plan);
   if (!st) return;
+  need(!st.inFlight, 'releasePlan: an asynchronous runPlan of this plan is still in flight; await it first');
   dropGraph(st);
   for (const b of st.gbuf) if (b) q8().free(b);
   st.dev.release();
@@ -706,6 +718,39 @@ function checkStepArgs(s, inst, slots) {
 }
 
 function runPlanOnDevice(plan, slots, steps, opts) {
+  need(!(_planState.get(plan) || {}).inFlight,
+       'runPlanSync: an asynchronous runPlan of this plan is still in flight; await it first');
+  const finish = enqueuePlan(plan, slots, steps, opts);
+  q8().sync();
+  finish();
+}
+
+/** runPlan's promise form: the plan's work is enqueued when no earlier
+ * asynchronous run is in flight, else when that run settles. */
+function runPlanAsync(plan, slots, steps, opts) {
+  const start = () => {
+    const st = planStateOf(plan);
+    need(!st.inFlight, 'runPlan: the plan is still in flight');
+    const finish = enqueuePlan(plan, slots, steps, opts);
+    st.inFlight = true;
+    return q8().syncAsync().then(() => { st.inFlight = false; finish(); },
+                                 (e) => { st.inFlight = false; throw e; });
+  };
+  let p;
+  if (_planTail === null) {
+    try { p = start(); } catch (e) { return Promise.reject(e); }
+  } else {
+    p = _planTail.then(start);
+  }
+  const tail = p.then(() => {}, () => {});
+  _planTail = tail;
+  tail.then(() => { if (_planTail === tail) _planTail = null; });
+  return p;
+}
+
+/** Checks, uploads and launches a plan on the addon's stream; returns the
+ * function that downloads its outputs once the stream has finished. */
+function enqueuePlan(plan, slots, steps, opts) {
   const st = planStateOf(plan);
   const dev = st.dev;
   const instOf = (kernel) => {
@@ -853,8 +898,9 @@ function runPlanOnDevice(plan, slots, steps, opts) {
     A.graphLaunch(g);
     stats.graphReplays++;
   }
-  q8().sync();
-  for (const s of hostNeeds) if (slots[s] && slots[s].data) download(slots[s].data, slotBuf(s));
+  return () => {
+    for (const s of hostNeeds) if (slots[s] && slots[s].data) download(slots[s].data, slotBuf(s));
+  };
 }
 
 /**
@@ -974,16 +1020,10 @@ function createHipRuntimeBackend() {
     runAsync(inst, tensorArgs, shapeValues) {
       return Promise.resolve().then(() => this.runSync(inst, tensorArgs, shapeValues));
     },
-    // runs the plan before returning (the device work is ordered on one
-    // stream and its outputs are already downloaded); the promise is the
-    // registry's contract (backend_registry.ts:19)
+    // enqueues the plan and settles when its outputs are downloaded
+    // (runPlanAsync); argument errors reject the promise
     runPlan(plan, slots, steps, opts) {
-      try {
-        runPlanOnDevice(plan, slots, steps, opts);
-        return Promise.resolve();
-      } catch (e) {
-        return Promise.reject(e);
-      }
+      return runPlanAsync(plan, slots, steps, opts);
     },
     isAsync() { return false; },
   };

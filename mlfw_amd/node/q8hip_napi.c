@@ -15,7 +15,8 @@
  *   - host memory stays owned by JS: upload()/download() copy between a
  *     typed array (or ArrayBuffer) and a device buffer and block;
  *   - ops enqueue on the addon's one stream (created by init()) and return
- *     immediately; sync() waits; captureBegin() / captureEnd() record a
+ *     immediately; sync() waits, syncAsync() returns a promise of the same
+ *     wait made on a worker thread; captureBegin() / captureEnd() record a
  *     launch sequence on it as a graph that graphLaunch() replays;
  *   - every device buffer an op names is checked against the bytes its
  *     shape arguments imply before the C ABI is called;
@@ -422,6 +423,62 @@ static napi_value js_sync(napi_env env, napi_callback_info info) {
   (void)info;
   Q8_CHECK(env, q8_stream_sync(g_stream));
   return undefined(env);
+}
+
+/* syncAsync(): a promise that settles when the stream's work has finished.
+ * The wait runs on a libuv worker thread (napi_async_work), so the JS thread
+ * stays free while the device works; the promise rejects with the coded
+ * error of a failed wait.  The error text is the worker thread's own
+ * (q8_last_error is thread-local), copied before the thread moves on. */
+typedef struct {
+  napi_async_work work;
+  napi_deferred deferred;
+  int rc;
+  char msg[1024];
+} SyncWork;
+
+static void sync_execute(napi_env env, void* data) {
+  (void)env;
+  SyncWork* w = (SyncWork*)data;
+  w->rc = q8_stream_sync(g_stream);
+  if (w->rc != Q8_OK) snprintf(w->msg, sizeof(w->msg), "%s", q8_last_error());
+}
+
+static void sync_complete(napi_env env, napi_status status, void* data) {
+  SyncWork* w = (SyncWork*)data;
+  if (status == napi_ok && w->rc == Q8_OK) {
+    napi_resolve_deferred(env, w->deferred, undefined(env));
+  } else {
+    char code[16];
+    snprintf(code, sizeof(code), "Q8_ERR_%d", w->rc != Q8_OK ? w->rc : Q8_ERR_DEVICE);
+    napi_value c, m, e;
+    napi_create_string_utf8(env, code, NAPI_AUTO_LENGTH, &c);
+    napi_create_string_utf8(env, w->rc != Q8_OK && w->msg[0] ? w->msg : "q8hip.syncAsync: the wait did not run",
+                            NAPI_AUTO_LENGTH, &m);
+    napi_create_error(env, c, m, &e);
+    napi_reject_deferred(env, w->deferred, e);
+  }
+  napi_delete_async_work(env, w->work);
+  free(w);
+}
+
+static napi_value js_sync_async(napi_env env, napi_callback_info info) {
+  (void)info;
+  SyncWork* w = (SyncWork*)calloc(1, sizeof(SyncWork));
+  napi_value promise, name;
+  if (!w) {
+    napi_throw_error(env, NULL, "q8hip.syncAsync: out of host memory");
+    return NULL;
+  }
+  if (napi_create_promise(env, &w->deferred, &promise) != napi_ok ||
+      napi_create_string_utf8(env, "q8hip.syncAsync", NAPI_AUTO_LENGTH, &name) != napi_ok ||
+      napi_create_async_work(env, NULL, name, sync_execute, sync_complete, w, &w->work) != napi_ok ||
+      napi_queue_async_work(env, w->work) != napi_ok) {
+    free(w);
+    napi_throw_error(env, NULL, "q8hip.syncAsync: could not queue the wait");
+    return NULL;
+  }
+  return promise;
 }
 
 /* ---------------------------------------------------------------- ops */
@@ -905,6 +962,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"upload", js_upload},
       {"download", js_download},
       {"sync", js_sync},
+      {"syncAsync", js_sync_async},
       {"fillNormal", js_fill_normal},
       {"fillUniform", js_fill_uniform},
       {"quantizeStatic", js_quantize_static},

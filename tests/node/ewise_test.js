@@ -553,6 +553,29 @@ function gpuTests() {
     hip.releasePlan(t.plan);
   });
 
+  testAsync('GPU: runPlan (the promise form) downloads when the device has finished, queues overlapping calls on one plan', () => {
+    const be = hip.createHipRuntimeBackend();
+    const t = linearRun('fused', true);
+    // a second call on the same plan (the same device buffers) with another
+    // x and its own output, made before the first has settled
+    const x2 = normal(91, M * K, 1.5);
+    const out2 = new Float32Array(M * N);
+    const slots2 = t.slots.map((sl, i) => ({ ...sl, data: i === 0 ? x2 : i === 6 ? out2 : sl.data.slice() }));
+    const p1 = be.runPlan(t.plan, t.slots, t.steps);
+    assert.ok(p1 instanceof Promise);
+    assert.ok(t.out.every((v) => v === 0), 'the output is downloaded when the promise settles, not before');
+    assert.throws(() => hip.runPlanSync(t.plan, t.slots, t.steps), /still in flight/);
+    assert.throws(() => hip.releasePlan(t.plan), /still in flight/);
+    const p2 = be.runPlan(t.plan, slots2, t.steps);
+    return Promise.all([p1, p2]).then(() => {
+      sameBits(t.out, t.want, 'first call');
+      sameBits(out2, oracleLinear(t.L, 'fused', x2, t.bD), 'second call, queued behind the first');
+      hip.runPlanSync(t.plan, t.slots, t.steps);             // settled: the plan runs synchronously again
+      sameBits(t.out, t.want, 'runPlanSync after the promises');
+      hip.releasePlan(t.plan);
+    });
+  });
+
   for (const [which, fuse] of [['fused', true], ['unfused', false], ['requant', true]]) {
     test(`GPU: runPlan in graph mode (${which}, fusion ${fuse ? 'on' : 'off'}): eager, captured, replayed, fresh x every call`, () => {
       const t = linearRun(which, fuse);
