@@ -628,8 +628,10 @@ std::mutex g_jit_mu;
 std::string g_jit_error;
 
 // The compiled kernel of a program source on the current device (nullptr
-// if hiprtc or the module load failed; the failure is cached too).
-hipFunction_t ewise_jit_kernel(const std::string& src) {
+// if hiprtc or the module load failed; the failure is cached too).  With
+// may_compile false only a kernel already compiled is returned, and a miss
+// is not cached.
+hipFunction_t ewise_jit_kernel(const std::string& src, bool may_compile) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   static std::unordered_map<std::string, hipFunction_t> cache;
@@ -637,7 +639,7 @@ hipFunction_t ewise_jit_kernel(const std::string& src) {
   std::lock_guard<std::mutex> lock(g_jit_mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  if (cache.size() >= EW_JIT_MAX_PROGRAMS) return nullptr;
+  if (!may_compile || cache.size() >= EW_JIT_MAX_PROGRAMS) return nullptr;
   hipFunction_t fn = nullptr;
   std::string why;
   hiprtcProgram prog;
@@ -751,7 +753,13 @@ hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* ou
       arith += op != Q8_EW_LOAD && op != Q8_EW_CONST;
     }
     const int U = !slow && arith >= 6 ? 2 : 1;
-    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, U, kind))) {
+    // no compile while the stream is captured into a graph: a module load
+    // there may be refused, and a refusal must not stick to the program;
+    // a program compiled before launches the same way captured or not
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const bool may_compile = hipStreamIsCapturing(st, &cap) != hipSuccess || cap == hipStreamCaptureStatusNone;
+    (void)hipGetLastError();
+    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, U, kind), may_compile)) {
       long long nn = (long long)n;
       void* args[] = {&ptr, &nn};
       const int64_t vblocks = (n / (v4 ? 4 : 1) + (int64_t)EW_NT * U - 1) / ((int64_t)EW_NT * U);

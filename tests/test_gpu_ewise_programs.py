@@ -121,6 +121,39 @@ def test_large_programs_run_compiled(ops, oracle):
     same_bits(host(a), host(b), "compiled vs interpreted")
 
 
+def test_program_first_seen_under_graph_capture(ops):
+    """A program first called while its stream is captured into a HIP graph
+    is not compiled there (the capture records the interpreter); the next
+    eager call compiles it.  Every replay, with eager work between them,
+    gives the compiled kernel's bits."""
+    from mlfw_amd import configs as C
+    set_jit(0)
+    M = N = 1024
+    prog, _, _, _ = C.ewise_programs(M, N, s_q=0.0371)["relu_quantize"]    # a scale no other test uses
+    x = torch.randn((M, N), device=DEV)
+    c0, l0 = jit_counts()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out_g = torch.empty((M, N), dtype=torch.int8, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ops.ewise(prog, [x], out_g)
+    torch.cuda.synchronize()
+    assert jit_counts() == (c0, l0), "no compile and no compiled launch while capturing"
+    out_e = torch.empty_like(out_g)
+    ops.ewise(prog, [x], out_e)
+    torch.cuda.synchronize()
+    c1, l1 = jit_counts()
+    assert (c1, l1) == (c0 + 1, l0 + 1), ops.ewise_jit_error()
+    for r in range(3):
+        out_g.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        same_bits(host(out_g), host(out_e), f"replay {r} (interpreter) vs eager (compiled)")
+        ops.ewise(prog, [x], out_e)       # eager work between the replays
+        torch.cuda.synchronize()
+
+
 ALL_OPS = ["add", "sub", "mul", "div", "idiv", "mod", "floordiv", "tmod", "tdiv", "neg", "cmp", "select",
            "toint32", "tobool", "max", "min", "abs", "floor", "ceil", "round", "sign", "sqrt", "fmod", "exp",
            "log", "tanh", "rsqrt", "pow", "index", "const"]
