@@ -249,6 +249,14 @@ def bench_c5_quant():
     return res
 
 
+def _ewise_compiled_launches():
+    import ctypes
+    from mlfw_amd import _lib
+    n = ctypes.c_int64(0)
+    _lib.call("q8_debug_ewise_jit", -1, None, ctypes.byref(n))
+    return n.value
+
+
 def bench_ewise():
     """q8_ewise on the elementwise PrimFuncs the GEMM chain fusion does not
     absorb, on [4096, 4096] (2^24 elements: the hiprtc-compiled route):
@@ -272,10 +280,16 @@ def bench_ewise():
                     ts.append(torch.randint(-1000 if dt == torch.int32 else -128, 1000 if dt == torch.int32 else 128,
                                             shape, dtype=dt, device="cuda", generator=g))
             sets.append((ts, torch.empty((M, N), dtype=odt, device="cuda")))
+        l0 = _ewise_compiled_launches()
         us, how = graph_time_us(lambda i: O.ewise(prog, sets[i][0], sets[i][1]), n)
         gbs = nbytes / (us * 1e-6) / 1e9
+        # which of q8_ewise's routes ran: compiled launches counted by the library
+        compiled = _ewise_compiled_launches() > l0
         res[f"ewise_{name}_4096x4096"] = {"avg_us": us, "bytes": nbytes, "GB/s": gbs,
-                                           "frac_hbm": gbs / PEAK_HBM_GBS, "timing": how}
+                                           "frac_hbm": gbs / PEAK_HBM_GBS, "timing": how,
+                                           "route": "compiled" if compiled else "interpreted"}
+        if not compiled:
+            res[f"ewise_{name}_4096x4096"]["compile_error"] = O.ewise_jit_error()[:400]
         del sets
     return res
 
