@@ -576,6 +576,19 @@ function gpuTests() {
     });
   });
 
+  testAsync('GPU: runPlan (the promise form) in graph mode: eager, captured and replayed runs queue and match', () => {
+    const be = hip.createHipRuntimeBackend();
+    const t = linearRun('fused', true);
+    const xs = [normal(101, M * K, 1.5), normal(102, M * K, 1.5), normal(103, M * K, 1.5), normal(104, M * K, 1.5)];
+    const outs = xs.map(() => new Float32Array(M * N));
+    const runs = xs.map((x, i) => be.runPlan(t.plan, t.slots.map((sl, j) => ({ ...sl, data: j === 0 ? x : j === 6 ? outs[i] : sl.data.slice() })),
+                                             t.steps, { graph: true }));
+    return Promise.all(runs).then(() => {
+      xs.forEach((x, i) => sameBits(outs[i], oracleLinear(t.L, 'fused', x, t.bD), `graph-mode run ${i}`));
+      hip.releasePlan(t.plan);
+    });
+  });
+
   for (const [which, fuse] of [['fused', true], ['unfused', false], ['requant', true]]) {
     test(`GPU: runPlan in graph mode (${which}, fusion ${fuse ? 'on' : 'off'}): eager, captured, replayed, fresh x every call`, () => {
       const t = linearRun(which, fuse);
