@@ -26,10 +26,10 @@
 // VGPRs instead (uniform register numbers, GPR index mode, 2-4 elements per
 // lane) measured slower (294 / 342 / 306 us).  So a call over 2^20 elements
 // or more runs the program compiled instead (hiprtc, once per program and
-// device, below): 27 / 23 / 30 us on the same programs, the first and the
-// last at 62% of HBM (a plain streaming kernel of the same bytes takes
-// 28 us for the last), the quantize at 46% (the same bytes stream in 16 us;
-// its rounded division, round and clamps are what remains).
+// device, below): 21 / 23 / 27 us on the same programs, the first at 78% of
+// HBM and the last at 69% (their 64 MiB outputs stored non-temporally), the
+// quantize at 45% (the same bytes stream in 16 us; its rounded division,
+// round and clamps are what remains).
 //
 // Value semantics (all f64, like JS numbers):
 //   * f32-typed arithmetic and non-exact externs round once to binary32
@@ -350,7 +350,7 @@ enum { EW_TF = 0, EW_TI = 1, EW_TD = 2 };
 // every other index; input j is read as one 4-vector (kind EW_LD_VEC:
 // contiguous along the last loop and 4-element aligned), as one value for
 // all four (EW_LD_BCAST: broadcast along it) or element by element, and the
-// output is stored as one 4-vector).  Each lane takes U such groups a
+// output is stored as one 4-vector, non-temporally when nts).  Each lane takes U such groups a
 // grid stride apart and issues the loads of all U groups (every input the
 // program reads) before any arithmetic, so that a lane has U loads in
 // flight per input; a group past the end loads the last group again
@@ -370,7 +370,7 @@ enum { EW_TF = 0, EW_TI = 1, EW_TD = 2 };
 // constant c that is not binary32 goes through js_fround_div_const (through
 // js_fround_div_const_f, without a division, when a is binary32).  Every
 // other operation runs in f64 on the operands converted exactly.
-std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, int U, const int* kind) {
+std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, int U, const int* kind, bool nts) {
   const std::string I = narrow ? "unsigned int" : "long long";
   auto icon = [&](int64_t v) {
     char buf[48];
@@ -382,6 +382,10 @@ std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, int U, con
   // functions itself, and an included header is found only where comgr
   // locates the ROCm tree (not under every launcher, e.g. a profiler's).
   std::string s = kJsMathSrc;
+  if (nts)   // native vectors: the non-temporal store builtin takes no HIP vector structs
+    s += "\ntypedef float ew_f4 __attribute__((ext_vector_type(4)));\n"
+         "typedef int ew_i4 __attribute__((ext_vector_type(4)));\n"
+         "typedef double ew_d2 __attribute__((ext_vector_type(2)));\n";
   s += "\nstruct EwJitPtrs { const void* in[" + std::to_string(Q8_EW_MAX_INPUTS) + "]; void* out; };\n";
   s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(EW_NT) +
        ") void q8_ew_jit(EwJitPtrs ptr, long long n) {\n";
@@ -604,15 +608,31 @@ std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, int U, con
     const int L0 = u * V;
     std::string st;
     if (V == 4 && p.out_dtype == Q8_F64) {
-      st = "((double2*)ptr.out)[" + e + " / 2] = make_double2(" + conv(L0) + ", " + conv(L0 + 1) + "); " +
-           "((double2*)ptr.out)[" + e + " / 2 + 1] = make_double2(" + conv(L0 + 2) + ", " + conv(L0 + 3) + ");";
+      if (nts)
+        st = "__builtin_nontemporal_store((ew_d2){" + conv(L0) + ", " + conv(L0 + 1) + "}, (ew_d2*)ptr.out + " + e +
+             " / 2); __builtin_nontemporal_store((ew_d2){" + conv(L0 + 2) + ", " + conv(L0 + 3) +
+             "}, (ew_d2*)ptr.out + " + e + " / 2 + 1);";
+      else
+        st = "((double2*)ptr.out)[" + e + " / 2] = make_double2(" + conv(L0) + ", " + conv(L0 + 1) + "); " +
+             "((double2*)ptr.out)[" + e + " / 2 + 1] = make_double2(" + conv(L0 + 2) + ", " + conv(L0 + 3) + ");";
     } else if (V == 4) {
       const char* t4 = p.out_dtype == Q8_F32 ? "float4" : p.out_dtype == Q8_I32 ? "int4"
                        : p.out_dtype == Q8_I8 ? "char4" : "uchar4";
       const char* mk = p.out_dtype == Q8_F32 ? "make_float4" : p.out_dtype == Q8_I32 ? "make_int4"
                        : p.out_dtype == Q8_I8 ? "make_char4" : "make_uchar4";
-      st = std::string("((") + t4 + "*)ptr.out)[" + e + " / 4] = " + mk + "(" + conv(L0) + ", " + conv(L0 + 1) +
-           ", " + conv(L0 + 2) + ", " + conv(L0 + 3) + ");";
+      const std::string val = std::string(mk) + "(" + conv(L0) + ", " + conv(L0 + 1) + ", " + conv(L0 + 2) + ", " +
+                              conv(L0 + 3) + ")";
+      if (nts) {
+        // the four values as one native vector (f32, i32) or one 32-bit word (i8, u8)
+        const char* nt = p.out_dtype == Q8_F32 ? "ew_f4" : p.out_dtype == Q8_I32 ? "ew_i4" : "int";
+        st = std::string("{ const ") + t4 + " t_ = " + val + "; __builtin_nontemporal_store(*(const " + nt +
+             "*)&t_, (" + nt + "*)((" + t4 + "*)ptr.out + " + e + " / 4)); }";
+      } else {
+        st = std::string("((") + t4 + "*)ptr.out)[" + e + " / 4] = " + val + ";";
+      }
+    } else if (nts) {
+      st = std::string("__builtin_nontemporal_store((") + ew_ctype(p.out_dtype) + ")(" + conv(L0) + "), (" +
+           ew_ctype(p.out_dtype) + "*)ptr.out + " + e + ");";
     } else {
       st = std::string("((") + ew_ctype(p.out_dtype) + "*)ptr.out)[" + e + "] = " + conv(L0) + ";";
     }
@@ -759,7 +779,12 @@ hipError_t launch_ewise(const q8_ew_prog& p, const void* const* inputs, void* ou
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     const bool may_compile = hipStreamIsCapturing(st, &cap) != hipSuccess || cap == hipStreamCaptureStatusNone;
     (void)hipGetLastError();
-    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, U, kind), may_compile)) {
+    // non-temporal stores above 32 MiB of output: smaller outputs stay in
+    // the MALL for the kernel that reads them next (the rule the quantize
+    // kernels follow); measured on [4096, 4096] dequant + add, 64 MiB of
+    // f32 out: 28.3 -> 26.6 us
+    const bool nts = n * (int64_t)ew_size(p.out_dtype) > ((int64_t)32 << 20);
+    if (hipFunction_t fn = ewise_jit_kernel(ewise_jit_source(p, narrow, v4 ? 4 : 1, U, kind, nts), may_compile)) {
       long long nn = (long long)n;
       void* args[] = {&ptr, &nn};
       const int64_t vblocks = (n / (v4 ? 4 : 1) + (int64_t)EW_NT * U - 1) / ((int64_t)EW_NT * U);
