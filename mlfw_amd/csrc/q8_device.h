@@ -100,7 +100,6 @@ __device__ __forceinline__ int key4(float4 v) {
   return a > c ? a : c;
 }
 
-// Symmetric int8 codes of four values (R1 with zp = 0), packed.
 // Symmetric int8 codes of four values (R1 with zp = 0), packed; one branch
 // to the exact path for the four.
 __device__ __forceinline__ int quant4_sym(float4 v, bool fast, float r32, double s) {
