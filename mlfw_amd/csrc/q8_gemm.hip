@@ -1936,6 +1936,45 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
       xf[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
     }
   };
+  if constexpr (KB <= 8) {
+    if (passes == 1 && (int)gridDim.x >= nblk) {
+      // One pass covers K and every workgroup has one row block: straight
+      // line, the activation and weight loads issued together before the
+      // first MFMA (0.3-0.5 us less than the block loop below on the same
+      // launch at N = 4096, K = 1024..4096).  With several blocks per
+      // workgroup the loop below stays: walking balanced row ranges, or
+      // issuing the next block's weights before this block's MFMAs, was
+      // slower there (N = 11008, M <= 8: 12.0 -> 12.5-13.5 us).
+      load_x(0);
+      const int n0 = (int)blockIdx.x * 16;
+      const int rows = N - n0 < 16 ? N - n0 : 16;
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(B + (int64_t)n0 * K, (uint32_t)rows * (uint32_t)K);
+      const uint32_t wo = (uint32_t)(r16 * K + wave * 64 * KB + 16 * g);
+      v4i w[KB];
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 64 * j, 0, 0));
+      __builtin_amdgcn_sched_barrier(0);
+      v4i acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < KB; j += 2) {
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], xf[j], acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j + 1], xf[j + 1], acc2, 0, 0, 0);
+      }
+      acc += acc2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[0][wave][r16 * 16 + 4 * g + r] = acc[r];
+      __syncthreads();
+      const int t = tid >> 4, i = tid & 15, n = n0 + i;
+      if (tid < 256 && t < M && n < N) {
+        uint32_t su = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) su += (uint32_t)red[0][w2][tid];
+        store_out(out, (int64_t)t * N + n, (int)su, t, n, e);
+      }
+      return;
+    }
+  }
   if (passes == 1) load_x(0);
   int rb = 0;
   for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x, rb ^= 1) {
