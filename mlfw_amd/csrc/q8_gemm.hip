@@ -1900,18 +1900,17 @@ void k_qlinear_dot4(const float* __restrict__ x, int M, int K, int per_tensor,
 // rows x 64 K-bytes x all 16 tokens.  Weights are the A operand (lane l:
 // row l%16, K bytes 16*(l/16) of each 64-byte block), the tokens the B
 // operand in the same lane layout (rows >= M zero), so both operands
-// pair the same K bytes.  The workgroup's 4 waves split K into quarters of
-// KB blocks; each wave keeps its activation fragments in registers for
-// all the weight-row blocks it visits (grid-stride over blocks of 16 rows),
-// and the 4 partial 16x16 results meet in LDS (double-buffered: one
-// barrier per block).  Output element (row n0 + 4*(l/16) + r, token l%16)
+// pair the same K bytes.  The workgroup's NW waves split each pass over K
+// into NW slices of KB 64-byte blocks; each wave keeps its activation
+// fragments in registers for all the weight-row blocks it visits
+// (grid-stride over blocks of 16 rows), and the NW partial 16x16 results
+// meet in LDS (double-buffered: one barrier per block).  Output element (row n0 + 4*(l/16) + r, token l%16)
 // is accumulator r of lane l.  NW = 4: at most 168 VGPRs (3 waves per
 // SIMD), so 3 workgroups per CU are resident (K < 4096).  NW = 16 (KB = 4):
 // a 1024-lane workgroup, each wave a sixteenth of K with 32 VGPRs of
 // operands; one per row block while the blocks fit the CUs, else one per CU
 // walking several row blocks (N = 11008, M = 16: 14.8 -> 13.3 us against
-// three 4-wave workgroups per CU).  NW = 8 (KB = 8): two per CU, for up to
-// 8 tokens and more row blocks than CUs.
+// three 4-wave workgroups per CU, unstaged).
 template <int KB, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 3 : 4)))
 void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K,
@@ -1936,6 +1935,48 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
       xf[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
     }
   };
+  // Weight fragments.  Fragment j of lane (g, r16) is K chunk 4 j + g (16
+  // bytes) of the wave's K slice of row r16, as the activation fragments.
+  // Loaded straight into that layout, each load instruction reads 64 bytes
+  // of each of 16 rows.  The staged forms instead copy the wave's 16 rows x
+  // 64 KB bytes into LDS (direct-to-LDS buffer loads), 4 rows x 256
+  // contiguous bytes per instruction, then read the fragments from LDS.
+  // The slice is kept as KB / 4 regions of 16 rows x 256 bytes; in a
+  // region, row r's chunk c sits in slot c ^ r, so a row still arrives as
+  // one contiguous run and the 16 lanes of a fragment read fall in 16
+  // different bank groups.  Each wave reads back only its own copies (its
+  // vmcnt, no barrier).  Staged where the copies fit beside the workgroups
+  // a CU holds: 16 waves (one per CU, 64 KiB) and 4 waves with KB <= 8
+  // (three per CU, up to 32 KiB each); N = 11008, M = 16: 13.3 -> 12.4 us.
+  constexpr bool STAGE = (NW == 16 && KB == 4) || (NW == 4 && KB <= 8);
+  __shared__ __align__(16) int8_t wst[STAGE ? NW * KB * 1024 : 16];
+  auto load_w = [&](v4i* w, const __amdgpu_buffer_rsrc_t& rw, uint32_t kpass) {
+    if constexpr (STAGE) {
+      int8_t* base = wst + KB * 1024 * __builtin_amdgcn_readfirstlane(wave);
+      const int rl = lane >> 4, q = lane & 15;
+      // the previous fragment reads from this region have returned
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int h = 0; h < KB / 4; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = 4 * j + rl;
+          copy16_to_lds(rw, base + 4096 * h + 1024 * j,
+                        (uint32_t)(row * K) + kpass + (uint32_t)(wave * 64 * KB + 256 * h + 16 * (q ^ row)));
+        }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        const int c = 4 * j + g;
+        w[j] = *reinterpret_cast<const v4i*>(base + 4096 * (c >> 4) + 256 * r16 + 16 * ((c & 15) ^ r16));
+      }
+    } else {
+      const uint32_t wo = (uint32_t)(r16 * K) + kpass + (uint32_t)(wave * 64 * KB + 16 * g);
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 64 * j, 0, 0));
+    }
+  };
   if constexpr (KB <= 8) {
     if (passes == 1 && (int)gridDim.x >= nblk) {
       // One pass covers K and every workgroup has one row block: straight
@@ -1949,11 +1990,8 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
       const int n0 = (int)blockIdx.x * 16;
       const int rows = N - n0 < 16 ? N - n0 : 16;
       const __amdgpu_buffer_rsrc_t rw = make_rsrc(B + (int64_t)n0 * K, (uint32_t)rows * (uint32_t)K);
-      const uint32_t wo = (uint32_t)(r16 * K + wave * 64 * KB + 16 * g);
       v4i w[KB];
-#pragma unroll
-      for (int j = 0; j < KB; ++j)
-        w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 64 * j, 0, 0));
+      load_w(w, rw, 0u);
       __builtin_amdgcn_sched_barrier(0);
       v4i acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
 #pragma unroll
@@ -1984,11 +2022,8 @@ void k_gemv_mfma(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int
     v4i acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};     // two chains of dependent MFMAs
     for (int pass = 0; pass < passes; ++pass) {
       if (passes > 1) load_x(pass);
-      const uint32_t wo = (uint32_t)(r16 * K + pass * 64 * NW * KB + wave * 64 * KB + 16 * g);
       v4i w[KB];
-#pragma unroll
-      for (int j = 0; j < KB; ++j)
-        w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 64 * j, 0, 0));
+      load_w(w, rw, (uint32_t)(pass * 64 * NW * KB));
       // all KB weight loads in flight before the first MFMA waits on one
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -2026,21 +2061,17 @@ static hipError_t launch_gemv_mt(const int8_t* A, const int8_t* B, int M, int N,
 
 static hipError_t launch_gemv_mfma(const int8_t* A, const int8_t* B, int M, int N, int K,
                                    const GemmEpi& e, void* out, hipStream_t st) {
-  // K >= 4096 (one pass of 16 x 4 or 8 x 8 waves x 64 bytes covers 4096):
-  // one 16-wave workgroup per row block while the blocks fit the CUs, then
-  // 8-wave workgroups (two per CU) up to 8 tokens and 16-wave ones (one per
-  // CU) above.  Measured on M 5..16 x N 1024..12288 at K = 4096 against the
-  // three-per-CU 4-wave form: 2-9% faster where they differ, never slower
-  // by more than 1%.
+  // K >= 4096 (one pass of 16 waves x 4 x 64 bytes covers 4096): one
+  // 16-wave workgroup per row block while the blocks fit the CUs, else one
+  // per CU walking several blocks.  With its weights staged through LDS
+  // this form beats two 8-wave workgroups per CU (unstaged: they would not
+  // fit their copies beside each other) at every token count: N = 11008,
+  // M = 8: 12.2 -> 11.6 us; N = 14336: 16.1 -> 14.6 us.
   const int nblk = (N + 15) / 16;
   const int cus = cu_count() > 0 ? cu_count() : 256;
   if (K >= 4096) {
-    if (nblk <= cus || M > 8)
-      hipLaunchKernelGGL((k_gemv_mfma<4, 16>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(1024), 0,
-                         st, A, B, M, N, K, e, out);
-    else
-      hipLaunchKernelGGL((k_gemv_mfma<8, 8>), dim3((unsigned)(nblk < 2 * cus ? nblk : 2 * cus)), dim3(512),
-                         0, st, A, B, M, N, K, e, out);
+    hipLaunchKernelGGL((k_gemv_mfma<4, 16>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(1024), 0, st,
+                       A, B, M, N, K, e, out);
     return hipGetLastError();
   }
   // every workgroup resident at once (3 per CU): weight loads of all row
