@@ -26,10 +26,12 @@
 // VGPRs instead (uniform register numbers, GPR index mode, 2-4 elements per
 // lane) measured slower (294 / 342 / 306 us).  So a call over 2^20 elements
 // or more runs the program compiled instead (hiprtc, once per program and
-// device, below): 21 / 23 / 27 us on the same programs, the first at 78% of
-// HBM and the last at 69% (their 64 MiB outputs stored non-temporally), the
-// quantize at 45% (the same bytes stream in 16 us; its rounded division,
-// round and clamps are what remains).
+// device, below): 21 / 17.5 / 27 us on the same programs, the first at 78%
+// of HBM and the last at 69% (their 64 MiB outputs stored non-temporally),
+// the quantize at 60% (the same bytes stream in 16 us).  The compiled form
+// runs a symmetric int8 quantize chain as the library's quantize fast path
+// (js_quant_i8): with the division, round and clamps as separate steps the
+// ReLU + quantize program took 23 us.
 //
 // Value semantics (all f64, like JS numbers):
 //   * f32-typed arithmetic and non-exact externs round once to binary32
@@ -472,9 +474,85 @@ std::string ewise_jit_source(const q8_ew_prog& p, bool narrow, int V, int U, con
       }
     }
   }
+  // The symmetric int8 quantize chain, as QuantizationPass's expression
+  // leaves it: DIV(a, c) rounded to binary32, ROUND, MAX with -128, MIN
+  // with 127, TOINT32 (constants may sit between them), with a binary32 a
+  // and a constant c in [2^-100, 2^100], and every intermediate register
+  // read by the next step only.  It is emitted at the DIV as one
+  // js_quant_i8 per element (the library's quantize fast path) and bound to
+  // the TOINT32's register when that instruction is reached.
+  auto reads_later = [&](int r, int from) {   // r read at or after `from` before it is redefined
+    for (int q = from; q < p.ncode; ++q) {
+      const q8_ew_instr& x = p.code[q];
+      const bool src = x.op != Q8_EW_LOAD && x.op != Q8_EW_CONST && x.op != Q8_EW_INDEX;
+      if (src && (x.a == r || x.b == r || x.c == r)) return true;
+      if (x.dst == r) return false;
+    }
+    return r == p.result;
+  };
+  std::vector<int> qchain(p.ncode, -1);        // at the DIV: pc of its TOINT32; at the rest: -2
+  std::string qname;                          // the fused value awaiting its TOINT32
+  auto match_quant = [&](int pc) {
+    const q8_ew_instr& dv = p.code[pc];
+    if (dv.op != Q8_EW_DIV || !dv.rnd || reg[dv.a].t != EW_TF || !reg[dv.b].known) return -1;
+    const double c = reg[dv.b].k;
+    if (!(c >= 0x1p-100 && c <= 0x1p100)) return -1;
+    // constants as they will stand at each step
+    bool kn[Q8_EW_MAX_REGS];
+    double kv[Q8_EW_MAX_REGS];
+    for (int r = 0; r < Q8_EW_MAX_REGS; ++r) { kn[r] = reg[r].known; kv[r] = reg[r].k; }
+    const int want[4] = {Q8_EW_ROUND, Q8_EW_MAX, Q8_EW_MIN, Q8_EW_TOINT32};
+    int cur = dv.dst, q = pc + 1;
+    std::vector<int> steps;
+    for (int k = 0; k < 4; ++k) {
+      while (q < p.ncode && p.code[q].op == Q8_EW_CONST) {
+        const q8_ew_instr& x = p.code[q];
+        if (x.dst == cur) return -1;
+        kn[x.dst] = true;
+        kv[x.dst] = x.rnd ? (double)(float)p.konst[x.aux] : p.konst[x.aux];
+        ++q;
+      }
+      if (q >= p.ncode || p.code[q].op != want[k]) return -1;
+      const q8_ew_instr& x = p.code[q];
+      if (k == 0 || k == 3) {
+        if (x.a != cur) return -1;
+      } else {
+        const double bound = k == 1 ? -128.0 : 127.0;
+        const int other = x.a == cur ? x.b : x.b == cur ? x.a : -1;
+        if (other < 0 || other == cur || !kn[other] || kv[other] != bound) return -1;
+      }
+      if (reads_later(cur, q + 1)) return -1;
+      steps.push_back(q);
+      cur = x.dst;
+      ++q;
+    }
+    for (int st : steps) qchain[st] = -2;
+    return steps.back();
+  };
   for (int pc = 0; pc < p.ncode; ++pc) {
     const q8_ew_instr& in = p.code[pc];
     std::vector<std::string> ex(NL);
+    if (qchain[pc] == -2) {                     // a step of a fused quantize chain
+      if (in.op == Q8_EW_TOINT32) {
+        Reg& r = reg[in.dst];
+        r.t = EW_TI;
+        r.name = qname;
+        r.lit = false;
+        r.known = false;
+      }
+      continue;
+    }
+    if (in.op == Q8_EW_DIV) {
+      const int end = match_quant(pc);
+      if (end >= 0) {
+        const double c = reg[in.b].k;
+        qname = "v" + std::to_string(pc);
+        for (int L = 0; L < NL; ++L)
+          s += "    const int " + qname + "_" + std::to_string(L) + " = js_quant_i8(" + X(in.a, L) + ", " +
+               ew_litf((double)(float)(1.0 / c)) + ", " + ew_lit(c) + ");\n";
+        continue;
+      }
+    }
     if (in.op == Q8_EW_LOAD) {
       const int dt = p.in_dtype[in.aux];
       define(pc, in, dt == Q8_F64 ? EW_TD : dt == Q8_I32 ? EW_TI : EW_TF, ld[pc]);

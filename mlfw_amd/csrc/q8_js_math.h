@@ -52,6 +52,18 @@
 // division remains.  In both functions the empty asm statement on the
 // dividend keeps the division inside its branch: without it the compiler
 // evaluates the division for every element and selects the result.
+//
+// js_quant_i8(a, r32, c) is ToInt32(Math.min(Math.max(Math.round(
+// Math.fround(a / c)), -128), 127)) for a binary32 a and a constant c in
+// [2^-100, 2^100], r32 = (float)(1 / c): the symmetric int8 quantize
+// (quant_math.ts:16-27) as QuantizationPass's expression writes it, NaN
+// giving 0.  It is the library's int8 quantize fast path: t = a * r32 in
+// binary32 is within 2^-15 of the quotient for every |quotient| < 256, and
+// the fround within 2^-17, so Math.round can differ from the one of t only
+// when t's fraction lies within 2^-13 of 1/2; those inputs (and NaN and
+// infinite t, whose fraction is NaN) take js_quant_i8_exact, the
+// expression's own steps in f64.  |t| >= 256 clamps: floor(t) saturates at
+// +-256 before the integer clamp.
 Q8_JS_MATH_BODY(
 __device__ __forceinline__ int js_to_int32(double x) {
   if (!(x == x) || __builtin_isinf(x)) return 0;
@@ -137,5 +149,17 @@ __device__ __forceinline__ float js_fround_div_const_f(float a, double c, double
     r = (float)(d / c);
   }
   return __builtin_signbit(a) != neg ? -r : r;
+}
+__device__ __noinline__ int js_quant_i8_exact(float a, double c) {
+  const double r = js_round_full((double)(float)((double)a / c));
+  return js_to_int32(js_min(js_max(r, -128.0), 127.0));
+}
+__device__ __forceinline__ int js_quant_i8(float a, float r32, double c) {
+  const float t = a * r32;
+  const float fl = __builtin_floorf(t);
+  const float fr = t - fl;
+  int r = (int)__builtin_amdgcn_fmed3f(fl, -256.0f, 256.0f) + (fr > 0.5f ? 1 : 0);
+  r = r < -128 ? -128 : (r > 127 ? 127 : r);
+  return __builtin_fabsf(fr - 0.5f) > 0x1p-13f ? r : js_quant_i8_exact(a, c);
 }
 )

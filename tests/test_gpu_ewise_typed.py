@@ -115,6 +115,32 @@ def test_relu_quantize_program(ops):
     compare_all_inputs(ops, code, (0.0, 0.05, -128.0, 127.0), torch.int8, "relu_quantize")
 
 
+QUANT_CHAIN = [("const", 1, 0, 0, 0, 0, 0), ("div", 2, 0, 1, 0, 0, 1), ("round", 3, 2, 0, 0, 0, 0),
+               ("const", 4, 0, 0, 0, 1, 0), ("max", 5, 3, 4, 0, 0, 0), ("const", 6, 0, 0, 0, 2, 0),
+               ("min", 7, 5, 6, 0, 0, 0), ("toint32", 8, 7, 0, 0, 0, 0)]
+
+
+@pytest.mark.parametrize("s", [1e-3, 0.1, 1.0 / 3.0, 7.0, 2.0 ** -100, 2.0 ** 100, 6e-31])
+def test_quantize_chain(ops, s):
+    """QuantizationPass's int8 quantize, (min(max(Math.round(Math.fround(x /
+    s)), -128), 127) | 0): the compiled kernels run the chain as the
+    library's quantize fast path (binary32 product with 1/s, exact f64 steps
+    near rounding ties) for s in [2^-100, 2^100] -- both ends included --
+    and as the separate steps for s outside it (6e-31)."""
+    print(f"quantize chain s={s!r} over every binary32 x", flush=True)
+    compare_all_inputs(ops, QUANT_CHAIN, (s, -128.0, 127.0), torch.int8, f"quantize s={s!r}")
+
+
+def test_quantize_chain_not_fused(ops):
+    """Chains the fusion must leave alone, on every binary32 x: the rounded
+    quotient read again after the chain (added to the code), and a clamp to
+    [0, 255] (a u8 range, not the int8 one)."""
+    print("quantize chain variants over every binary32 x", flush=True)
+    reused = QUANT_CHAIN[:-1] + [("toint32", 8, 7, 0, 0, 0, 0), ("add", 9, 8, 2, 0, 0, 0)]
+    compare_all_inputs(ops, reused, (0.05, -128.0, 127.0), torch.int32, "quantize + quotient")
+    compare_all_inputs(ops, QUANT_CHAIN, (0.05, 0.0, 255.0), torch.uint8, "quantize to [0, 255]")
+
+
 @pytest.mark.parametrize("op", ["round", "floor", "ceil", "sign", "abs", "neg"])
 def test_exact_unary_ops(ops, op):
     """Exact unary ops on binary32 values, stored as f32 (-0 and NaN kept)."""
