@@ -69,6 +69,7 @@ int init_device(int dev) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   e = q8::setup_kernel_attributes();
+  if (e == hipSuccess) e = q8::setup_w4_attributes();
   (void)q8::cu_count();
   void* sp = nullptr;
   if (e == hipSuccess) e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));

@@ -220,6 +220,7 @@ hipError_t launch_obs_update(ObsState* st, const float* x, int64_t n, hipStream_
 
 // One-time per-device kernel attribute set-up (dynamic LDS limits).
 hipError_t setup_kernel_attributes();
+hipError_t setup_w4_attributes();   // the 4-bit GEMV kernels' dynamic LDS limits
 
 // Compute units of the current device (cached per device).
 int cu_count();

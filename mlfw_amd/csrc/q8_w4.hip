@@ -104,6 +104,19 @@ __device__ __forceinline__ void w4_lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// 16 bytes per lane from buffer offset voff to LDS dst + 16 * lane.
+__device__ __forceinline__ void w4_copy16_to_lds(__amdgpu_buffer_rsrc_t r, int8_t* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
+// Slot of 16-byte unit u of staged row r (LPR units per row): a bijection
+// of the row's units, chosen so that the 16 rows' reads of one unit fall in
+// 16 different bank groups.
+template <int LPR>
+__device__ __forceinline__ int w4_slot(int u, int r) {
+  return u ^ (LPR == 8 ? (r >> 1) & 7 : r & 15);
+}
+
 // A block of rows is P passes of RPP rows: a row's K / 32 chunks (NCP =
 // that count rounded up to a power of two, <= 256) map to consecutive
 // lanes, and every lane keeps the same chunk -- one load of its activations
@@ -397,6 +410,21 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
   int gacc = 0, pieces = 0, gdone = 0;                  // groups split over spans
   const int P = group > PS ? group / PS : 1;            // spans per group
   int* const win0 = reinterpret_cast<int*>(lds);
+  // Weight staging: each round, the wave copies its 16 rows x 64 RS packed
+  // bytes (its span) into LDS after the windows with direct-to-LDS buffer
+  // loads, RPC rows of LPR contiguous 16-byte units per instruction, and
+  // reads its fragments back (unit u of row r in slot w4_slot(u, r)).
+  // Loaded straight into the fragment layout, each instruction reads 64
+  // bytes of each of 16 rows.  Units outside the span or K, and rows past
+  // N, read zero.  Staged where the 32 KiB of copies keep the workgroups a
+  // CU holds: 16 waves (one per CU), and 8 waves for up to 8 tokens (small
+  // windows); for 16 tokens, and with 4 waves, they would cost a resident
+  // workgroup per CU and run slower (N = 11008, M = 16: 12.6 -> 13.1 us).
+  constexpr bool STAGE = NW == 16 || (NW == 8 && XH);
+  constexpr int LPR = 4 * RS, RPC = 64 / LPR;
+  const int nwin = (ONE || rounds == 1) ? 1 : 2;
+  int8_t* const stg = reinterpret_cast<int8_t*>(lds) + ((nwin * win * 4 + 15) & ~15) +
+                      RS * 1024 * __builtin_amdgcn_readfirstlane(wave);
   // ONE: a single round (K <= NW * PS), known at compile time: no loop, and
   // the registers of the round are allocated as straight-line code
   for (int r = 0; r < (ONE ? 1 : rounds); ++r) {
@@ -406,6 +434,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
     const int gfirst = (NW * r * PS) / group;           // first group that can end in round r
     v4i wv[RS], xv[RS][2];
     double scv[NSC];
+    if constexpr (STAGE) {
+      // the previous round's fragment reads from the staging have returned
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int c = 0; c < RS; ++c) {
+        const int row = RPC * c + lane / LPR, u = w4_slot<LPR>(lane % LPR, row);
+        const bool ok = 32 * u < PS && k0 + 32 * u < K;
+        w4_copy16_to_lds(rw, stg + 1024 * c,
+                         ok ? (uint32_t)row * (uint32_t)KB + (uint32_t)(k0 / 2 + 16 * u) : 0x80000000u);
+      }
+    }
 #pragma unroll
     for (int s = 0; s < RS; ++s) {
       const int kc = k0 + 128 * s + 32 * q;             // the lane's chunk
@@ -414,7 +453,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
       const bool ok = 128 * s + 32 * q < PS && kc < K;
       const uint32_t kk = ok ? (uint32_t)kc : 0u;
       const uint32_t wr = ok ? wrow : rows, xt = ok ? xtok : (uint32_t)MB;
-      wv[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wr * (uint32_t)KB + kk / 2, 0, 0));
+      if constexpr (!STAGE)
+        wv[s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wr * (uint32_t)KB + kk / 2, 0, 0));
       const uint32_t xo = xt * (uint32_t)K + kk;
       if constexpr (XH) {
         xv[s][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16u * (uint32_t)(r16 >> 3), 0, 0));
@@ -428,6 +468,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_w4_mfma(const int8_t* __restri
       const int g = gfirst + sc_g[u2] < G ? gfirst + sc_g[u2] : G;          // G: past the row
       scv[u2] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(
                     rs, (sc_off[u2] + (uint32_t)g) * 8u, 0, 0));
+    }
+    if constexpr (STAGE) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int s = 0; s < RS; ++s)
+        wv[s] = *reinterpret_cast<const v4i*>(stg + r16 * (16 * LPR) + 16 * w4_slot<LPR>(4 * s + q, r16));
     }
     // an unconditional use of every loaded value: the compiler would
     // otherwise sink a step's loads into the branch that consumes them,
@@ -600,6 +646,8 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int n
   pl->lds = (size_t)lds_of(PS, pl->segw, pl->ng);
   pl->one = K <= NW * PS;
   if (!(pl->ng <= 64 && pl->lds <= 65536)) return false;
+  if (nw == 16 || (nw == 8 && M <= 8))   // the kernels that stage their weights (XH: M <= 8)
+    pl->lds = ((pl->lds + 15) & ~(size_t)15) + (size_t)NW * pl->rs * 1024;
   // Waves per workgroup by the number of (row, token) blocks: 16 while
   // every block has a CU to itself, 4 when they outnumber the resident
   // 8-wave workgroups.  Measured with groups of 128 at K = 4096, M 3..16:
@@ -743,6 +791,27 @@ hipError_t launch_gemv_w4(const int8_t* xq, const double* sx, int sx_stride, con
   else Q8_W4(4);
 #undef Q8_W4
   return hipGetLastError();
+}
+
+// The MFMA kernel's dynamic LDS (windows of up to 64 KiB plus 32 KiB of
+// weight staging) can pass 64 KiB, which needs each launched
+// instantiation's limit raised; done once per device at set-up.
+hipError_t setup_w4_attributes() {
+  hipError_t err;
+#define Q8_W4M_LDS(NW, RS, TR, ONE, XH)                                                            \
+  err = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_w4_mfma<NW, RS, TR, ONE, XH>),    \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024 + 16);          \
+  if (err != hipSuccess) return err;
+#define Q8_W4M_LDS4(NW, RS, TR)                                                                    \
+  Q8_W4M_LDS(NW, RS, TR, true, true) Q8_W4M_LDS(NW, RS, TR, true, false)                          \
+  Q8_W4M_LDS(NW, RS, TR, false, true) Q8_W4M_LDS(NW, RS, TR, false, false)
+  Q8_W4M_LDS4(4, 8, false)
+  Q8_W4M_LDS4(16, 2, false)
+  Q8_W4M_LDS4(8, 4, true)
+  Q8_W4M_LDS4(8, 4, false)
+#undef Q8_W4M_LDS4
+#undef Q8_W4M_LDS
+  return hipSuccess;
 }
 
 }  // namespace q8
