@@ -652,14 +652,17 @@ bool w4m_plan(int64_t M, int64_t N, int64_t K, int64_t group, W4MPlan* pl, int n
   // every block has a CU to itself, 4 when they outnumber the resident
   // 8-wave workgroups.  Measured with groups of 128 at K = 4096, M 3..16:
   // N = 4096 (256 blocks) 5.5 / 6.7 us at M = 4 / 16 with 16 waves against
-  // 6.0 / 7.1 with 8; N = 11008 (688 blocks) 8 waves, 16 being 3-5% slower.
+  // 6.0 / 7.1 with 8; N = 11008 (688 blocks) 8 waves up to 8 tokens (16
+  // are 4-5% slower there), and 16 above: with its weights staged the
+  // 16-wave form beats the 8-wave one, which cannot stage at 16 tokens
+  // (M = 16: 12.5 -> 12.0 us).
   if (nw == 8 && !pl->tr) {
     const int64_t blocks = ((N + 15) / 16) * ((M + 15) / 16);
     const int64_t cus = cu_count() > 0 ? cu_count() : 256;
     if (blocks > (pl->one ? 3 : 2) * cus) {
       W4MPlan p4;
       if (w4m_plan(M, N, K, group, &p4, 4)) *pl = p4;
-    } else if (blocks <= cus) {
+    } else if (blocks <= cus || M > 8) {
       W4MPlan p16;
       if (w4m_plan(M, N, K, group, &p16, 16)) *pl = p16;
     }
